@@ -1,0 +1,372 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused tile-local Strassen GEMM on one MI355X.
+
+Workload (one "step"): the GEMM sites of one Qwen3-32B-shaped decoder block
+at 8 x 1024 tokens, each with its fused epilogue, on synthetic bf16 data
+already resident in HBM:
+
+  q     X[8192,5120]  . Wq[5120,8192]   + per-head RMSNorm + RoPE (qk_norm_rope)
+  k     X[8192,5120]  . Wk[5120,1024]   + qk_norm_rope
+  v     X[8192,5120]  . Wv[5120,1024]
+  o     O[8192,8192]  . Wo[8192,5120]   + residual (residual_add)
+  gate|up Y[8192,5120] . Wgu[5120,51200] -> silu(gate)*up (swiglu) -> H[8192,25600]
+  down  H[8192,25600] . Wd[25600,5120]  + residual (residual_add)
+
+7.989 TFLOP per step (2*M*N*K summed over the sites, the classical count for
+every arm). Arms: "strassen" (7-product kernel), "cubic" (matched 8-product
+kernel, identical tiling and epilogues) and "hipblaslt" (torch.matmul, with
+the epilogues as separate torch ops). Printed value: effective TFLOP/s of the
+Strassen arm. The pure GEMMs at the same shapes (no epilogue) are reported in
+"pure_gemm".
+
+One JSON line on stdout; progress on stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+METRIC = "block ms + effective TFLOP/s vs matched cubic MFMA, Qwen3-32B shapes, 8x1024 tok"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (AMD spec)
+
+TOKENS, HIDDEN, FFN = 8192, 5120, 25600
+HEADS, KV_HEADS, HEAD_DIM = 64, 8, 128
+BATCH, SEQ = 8, 1024
+THETA, EPS = 1e6, 1e-6
+TILE = (1024, 1024, 512)
+
+
+def log(*args):
+    print(*args, file=sys.stderr, flush=True)
+
+
+def site_shapes():
+    q, kv = HEADS * HEAD_DIM, KV_HEADS * HEAD_DIM
+    return {
+        "q": (TOKENS, HIDDEN, q),
+        "k": (TOKENS, HIDDEN, kv),
+        "v": (TOKENS, HIDDEN, kv),
+        "o": (TOKENS, q, HIDDEN),
+        "gate_up": (TOKENS, HIDDEN, 2 * FFN),
+        "down": (TOKENS, FFN, HIDDEN),
+    }
+
+
+def flops(shape):
+    m, k, n = shape
+    return 2.0 * m * n * k
+
+
+def make_block(torch, dev, seed=0):
+    """Random-init weights and activations of the block's GEMM sites."""
+    import strassen_tpu_amd as smx
+
+    bm, bn, bk = TILE
+    g = torch.Generator(device=dev).manual_seed(seed)
+
+    def randn(*shape, std=1.0):
+        return (torch.randn(*shape, device=dev, generator=g) * std).to(torch.bfloat16)
+
+    d = {}
+    d["x"] = randn(TOKENS, HIDDEN)            # normalised attention input
+    d["attn"] = randn(TOKENS, HEADS * HEAD_DIM)
+    d["y"] = randn(TOKENS, HIDDEN)            # normalised MLP input
+    d["res1"] = randn(TOKENS, HIDDEN)
+    d["res2"] = randn(TOKENS, HIDDEN)
+    # Weights stored [out, in]; the GEMM's B operand is the [in, out] view.
+    for name, (out_f, in_f) in {"wq": (HEADS * HEAD_DIM, HIDDEN), "wk": (KV_HEADS * HEAD_DIM, HIDDEN),
+                                "wv": (KV_HEADS * HEAD_DIM, HIDDEN), "wo": (HIDDEN, HEADS * HEAD_DIM),
+                                "wgu": (2 * FFN, HIDDEN), "wd": (HIDDEN, FFN)}.items():
+        d[name] = randn(out_f, in_f, std=0.02).t()
+    gamma_q = (1.0 + 0.1 * torch.randn(HEAD_DIM, device=dev, generator=g)).to(torch.bfloat16)
+    gamma_k = (1.0 + 0.1 * torch.randn(HEAD_DIM, device=dev, generator=g)).to(torch.bfloat16)
+    pos = torch.arange(SEQ, dtype=torch.float32, device=dev)[:, None]
+    inv = 1.0 / (THETA ** (torch.arange(0, HEAD_DIM, 2, dtype=torch.float32, device=dev) / HEAD_DIM))
+    ang = torch.cat([pos * inv[None, :]] * 2, dim=-1)
+    cos, sin = torch.cos(ang).to(torch.bfloat16), torch.sin(ang).to(torch.bfloat16)
+    d["cos"], d["sin"], d["gamma_q"], d["gamma_k"] = cos, sin, gamma_q, gamma_k
+    # Offline relayouts (strassen_pallas.py:1315-1411), done once.
+    d["wq_laid"] = smx.rope_weight_layout(d["wq"], bn, HEAD_DIM)
+    d["wk_laid"] = smx.rope_weight_layout(d["wk"], bn, HEAD_DIM)
+    d["wgu_laid"] = smx.swiglu_weight_layout(d["wgu"], bn)
+    tcos, tsin = smx.rope_layout_tables(cos.repeat(BATCH, 1), sin.repeat(BATCH, 1), bn // 2, HEAD_DIM)
+    d["tcos"], d["tsin"] = tcos, tsin
+    d["scale_q"] = smx.rope_scale_layout(gamma_q, bn, HEAD_DIM)
+    d["scale_k"] = smx.rope_scale_layout(gamma_k, bn, HEAD_DIM)
+    return d
+
+
+def fused_sites(torch, d, algo):
+    """Callables for the fused Strassen or cubic arm, keyed by site."""
+    import strassen_tpu_amd as smx
+
+    bm, bn, bk = TILE
+    fn = smx.strassen_matmul if algo == "strassen" else smx.cubic_matmul
+    kw = dict(bm=bm, bn=bn, bk=bk)
+    if algo == "strassen":
+        kw["interleave_products"] = True
+    qk = dict(epilogue="qk_norm_rope", rope_cos=d["tcos"], rope_sin=d["tsin"], rope_head_dim=HEAD_DIM,
+              rope_eps=EPS)
+    out = {}
+    out["q"] = lambda: fn(d["x"], d["wq_laid"], rope_scale=d["scale_q"], **qk, **kw)
+    out["k"] = lambda: fn(d["x"], d["wk_laid"], rope_scale=d["scale_k"], **qk, **kw)
+    out["v"] = lambda: fn(d["x"], d["wv"], **kw)
+    out["o"] = lambda: fn(d["attn"], d["wo"], epilogue="residual_add", residual=d["res1"], **kw)
+
+    def gate_up():
+        d["h"] = fn(d["y"], d["wgu_laid"], epilogue="swiglu", **kw)
+        return d["h"]
+
+    out["gate_up"] = gate_up
+    out["down"] = lambda: fn(d["h"], d["wd"], epilogue="residual_add", residual=d["res2"], **kw)
+    return out
+
+
+def vendor_sites(torch, d):
+    """hipBLASLt GEMMs with the same epilogues as separate torch ops."""
+    f32 = torch.float32
+
+    def qk_norm_rope(y, gamma, heads):
+        t = y.view(TOKENS, heads, HEAD_DIM).float()
+        t = t * torch.rsqrt(t.pow(2).mean(-1, keepdim=True) + EPS) * gamma.float()
+        c = d["cos"].float().repeat(BATCH, 1)[:, None, :]
+        s = d["sin"].float().repeat(BATCH, 1)[:, None, :]
+        x1, x2 = t.chunk(2, dim=-1)
+        return (t * c + torch.cat([-x2, x1], dim=-1) * s).to(torch.bfloat16)
+
+    out = {}
+    out["q"] = lambda: qk_norm_rope(torch.matmul(d["x"], d["wq"]), d["gamma_q"], HEADS)
+    out["k"] = lambda: qk_norm_rope(torch.matmul(d["x"], d["wk"]), d["gamma_k"], KV_HEADS)
+    out["v"] = lambda: torch.matmul(d["x"], d["wv"])
+    out["o"] = lambda: (torch.matmul(d["attn"], d["wo"]).to(f32) + d["res1"].to(f32)).to(torch.bfloat16)
+
+    def gate_up():
+        gu = torch.matmul(d["y"], d["wgu"])
+        g, u = gu.chunk(2, dim=-1)
+        d["h_v"] = (torch.nn.functional.silu(g.float()) * u.float()).to(torch.bfloat16)
+        return d["h_v"]
+
+    out["gate_up"] = gate_up
+    out["down"] = lambda: (torch.matmul(d["h_v"], d["wd"]).to(f32) + d["res2"].to(f32)).to(torch.bfloat16)
+    return out
+
+
+def pure_sites(torch, d, algo):
+    """the pure GEMMs (no epilogue) at gate/up, down and o."""
+    import strassen_tpu_amd as smx
+
+    bm, bn, bk = TILE
+    a_up, w_up = d["y"], d["wgu"][:, :FFN]
+    if algo == "hipblaslt":
+        fn = lambda a, b: torch.matmul(a, b)
+    else:
+        base = smx.strassen_matmul if algo == "strassen" else smx.cubic_matmul
+        fn = lambda a, b: base(a, b, bm=bm, bn=bn, bk=bk)
+    return {
+        "gate_up": lambda: fn(a_up, w_up),
+        "down": lambda: fn(d["h_any"], d["wd"]),
+        "o": lambda: fn(d["attn"], d["wo"]),
+    }
+
+
+def time_steps(torch, step, steps, warmup):
+    """Warm up, then time exactly `steps` calls between two synchronisations.
+    Returns (total wall ms, per-step event ms list)."""
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for e0, e1 in events:
+        e0.record()
+        step()
+        e1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3
+    return wall, [e0.elapsed_time(e1) for e0, e1 in events]
+
+
+def run_block(sites):
+    order = ("q", "k", "v", "o", "gate_up", "down")
+
+    def step():
+        for name in order:
+            sites[name]()
+    return step
+
+
+def cpu_baseline(seconds):
+    """The oracle's Strassen restatement timed on host cores over a bounded
+    sample: 1024x1024 output tiles of the gate|up site (K=5120), repeated for
+    about `seconds`."""
+    import numpy as np
+
+    import oracle as o
+
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+    except Exception:  # pragma: no cover - informational only
+        cores = os.cpu_count() or 1
+    rng = np.random.default_rng(0)
+    bm, bn, bk = TILE
+    a = o.bf16_round(rng.standard_normal((bm, HIDDEN)).astype(np.float32))
+    b = o.bf16_round(rng.standard_normal((HIDDEN, bn)).astype(np.float32) * np.float32(0.02))
+    o.strassen_matmul(a, b, bm=bm, bn=bn, bk=bk, interleave_products=True)  # warm-up
+    tiles, t0 = 0, time.perf_counter()
+    while True:
+        o.strassen_matmul(a, b, bm=bm, bn=bn, bk=bk, interleave_products=True)
+        tiles += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    tflops = tiles * 2.0 * bm * bn * HIDDEN / elapsed / 1e12
+    return {
+        "value": tflops, "unit": "TFLOP/s", "cores": int(cores), "kind": "port",
+        "sample": f"{tiles} output tiles of 1024x1024 (K=5120) of the gate|up site, "
+                  f"numpy oracle Strassen restatement, {elapsed:.1f} s",
+        "ms_per_tile": elapsed * 1e3 / tiles,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", default=None, help="time only this arm:site (profiling runs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: the Strassen GEMM path runs on one MI355X "
+              "(no collectives). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import strassen_tpu_amd as smx  # noqa: F401  (loads the HIP library; fails loudly if missing)
+    from strassen_tpu_amd import _lib
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    torch.backends.cuda.matmul.allow_tf32 = False
+    log(f"device: {torch.cuda.get_device_name(0)}, CUs {torch.cuda.get_device_properties(0).multi_processor_count}")
+    d = make_block(torch, dev)
+    shapes = site_shapes()
+    block_flops = sum(flops(s) for s in shapes.values())
+
+    arms = {"strassen": fused_sites(torch, d, "strassen"), "cubic": fused_sites(torch, d, "cubic"),
+            "hipblaslt": vendor_sites(torch, d)}
+    # H for the pure down GEMM (any bf16 activations of the right shape).
+    arms["strassen"]["gate_up"]()
+    d["h_any"] = d["h"]
+    arms["hipblaslt"]["gate_up"]()
+    torch.cuda.synchronize()
+
+    if args.only:
+        arm, site = args.only.split(":")
+        table = arms[arm] if site in arms[arm] and not site.startswith("pure_") else \
+            pure_sites(torch, d, arm)
+        fn = table[site.replace("pure_", "")]
+        wall, ev = time_steps(torch, fn, args.steps, args.warmup)
+        log(f"{args.only}: {statistics.mean(ev):.3f} ms/call")
+        return
+
+    # Headline: exactly `steps` Strassen block steps between synchronisations.
+    log("timing strassen block")
+    wall_s, ev_s = time_steps(torch, run_block(arms["strassen"]), args.steps, args.warmup)
+    results = {"strassen": statistics.median(ev_s)}
+    for arm in ("cubic", "hipblaslt"):
+        log(f"timing {arm} block")
+        _, ev = time_steps(torch, run_block(arms[arm]), args.steps, args.warmup)
+        results[arm] = statistics.median(ev)
+    # Interleaved rounds (rotated arm order) to check the comparison is not
+    # an ordering artefact.
+    rounds = {a: [] for a in results}
+    names = list(results)
+    for r in range(3):
+        order = names[r % 3:] + names[:r % 3]
+        for arm in order:
+            _, ev = time_steps(torch, run_block(arms[arm]), max(3, args.steps // 4), 1)
+            rounds[arm].append(statistics.median(ev))
+
+    # Per-site times (events on the launching stream) for every arm.
+    per_site = {}
+    for arm, sites in arms.items():
+        per_site[arm] = {}
+        for name in ("q", "k", "v", "o", "gate_up", "down"):
+            _, ev = time_steps(torch, sites[name], args.steps, 2)
+            per_site[arm][name] = statistics.median(ev)
+    pure = {}
+    for arm in ("strassen", "cubic", "hipblaslt"):
+        table = pure_sites(torch, d, arm)
+        pure[arm] = {}
+        for name, fn in table.items():
+            _, ev = time_steps(torch, fn, args.steps, 2)
+            pure[arm][name] = statistics.median(ev)
+    pure_shapes = {"gate_up": (TOKENS, HIDDEN, FFN), "down": (TOKENS, FFN, HIDDEN),
+                   "o": (TOKENS, HEADS * HEAD_DIM, HIDDEN)}
+
+    # Roofline of the dominant kernel: the fused gate|up SwiGLU Strassen launch.
+    gu_ms = per_site["strassen"]["gate_up"]
+    gu_tflops = flops(shapes["gate_up"]) / (gu_ms * 1e-3) / 1e12
+    roofline = {
+        "bound": "mfma", "achieved": round(gu_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+        "frac": round(gu_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+        "kernel": "gemm_kernel<Cfg<7,...>, SMX_EPI_SWIGLU> (gate|up, M=8192 K=5120 N=51200)",
+        "mfma_executed_frac": round(gu_tflops * 7 / 8 / PEAK_BF16_TFLOPS, 4),
+        "avg_launch_ms": round(gu_ms, 4),
+    }
+
+    ms = results["strassen"]
+    value = block_flops / (ms * 1e-3) / 1e12
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "wall_ms_per_step": round(wall_s / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init bf16 weights ~N(0,0.02), activations ~N(0,1))",
+        "config": {
+            "workload": "qwen3_32b_block_gemm_sites_fused",
+            "tokens": TOKENS, "batch": BATCH, "seq": SEQ, "hidden": HIDDEN, "ffn": FFN,
+            "heads": HEADS, "kv_heads": KV_HEADS, "head_dim": HEAD_DIM,
+            "tile_bm_bn_bk": list(TILE), "block_tflop": round(block_flops / 1e12, 4),
+            "sites": {k: list(v) for k, v in shapes.items()},
+        },
+        "arms_ms": {k: round(v, 4) for k, v in results.items()},
+        "arms_interleaved_ms": {k: [round(x, 4) for x in v] for k, v in rounds.items()},
+        "speedup_vs_cubic": round(results["cubic"] / ms, 4),
+        "speedup_vs_hipblaslt": round(results["hipblaslt"] / ms, 4),
+        "sites_ms": {arm: {k: round(v, 4) for k, v in s.items()} for arm, s in per_site.items()},
+        "sites_tflops": {arm: {k: round(flops(shapes[k]) / (v * 1e-3) / 1e12, 1) for k, v in s.items()}
+                         for arm, s in per_site.items()},
+        "pure_gemm_ms": {arm: {k: round(v, 4) for k, v in s.items()} for arm, s in pure.items()},
+        "pure_gemm_tflops": {arm: {k: round(flops(pure_shapes[k]) / (v * 1e-3) / 1e12, 1) for k, v in s.items()}
+                             for arm, s in pure.items()},
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        log("timing CPU baseline (oracle)")
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,500 @@
+"""Numpy restatement of the reference's tile-local one-level Strassen path.
+
+Test infrastructure only (see ``oracle/__init__.py``). Matrices are carried
+as float32 arrays whose values are exactly representable in bfloat16 (the
+"bf16 value" convention); ``bf16_round`` performs every bf16 rounding the
+reference performs, and nothing else rounds.
+
+File:line citations are relative to the reference checkout.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+__all__ = [
+    "bf16_round", "bf16_bits", "bits_to_f32", "silu",
+    "strassen_matmul", "cubic_blocked_matmul", "native_matmul",
+    "high_precision_reference", "device_error", "host_uniform_inputs",
+    "swiglu_weight_layout_order", "swiglu_weight_layout",
+    "rope_weight_layout_order", "rope_weight_layout", "rope_layout_tables",
+    "rope_scale_layout", "rope_layout_to_heads", "rope_values", "rms_norm",
+    "apply_rope", "strassen_products", "PRODUCT_UPDATES",
+]
+
+
+# ---------------------------------------------------------------------------
+# bf16 helpers
+# ---------------------------------------------------------------------------
+
+def bf16_bits(x):
+    """Round float32 values to bfloat16 (ties to even) and return uint16 bits.
+
+    Same rounding as ``x.astype(jnp.bfloat16)`` used throughout
+    ``strassen_pallas.py`` (e.g. ``:327-329``): round-to-nearest-even on the
+    upper 16 bits. NaN stays NaN (quiet bit set); +-inf and overflow to inf
+    follow IEEE rounding.
+    """
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    u = x.view(np.uint32)
+    rounding_bias = np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))
+    rounded = ((u + rounding_bias) >> np.uint32(16)).astype(np.uint16)
+    nan = np.isnan(x)
+    if nan.any():
+        rounded = np.where(nan, ((u >> np.uint32(16)) | np.uint32(0x0040)).astype(np.uint16), rounded)
+    return rounded
+
+
+def bits_to_f32(bits):
+    """Widen uint16 bfloat16 bit patterns to float32 (exact)."""
+    b = np.asarray(bits, dtype=np.uint16).astype(np.uint32) << np.uint32(16)
+    return b.view(np.float32)
+
+
+def bf16_round(x):
+    """Round to the nearest bfloat16 value, returned as float32."""
+    return bits_to_f32(bf16_bits(x))
+
+
+def silu(x):
+    """float32 ``x * sigmoid(x)`` -- ``jax.nn.silu`` (``strassen_pallas.py:153``)."""
+    x = np.asarray(x, dtype=np.float32)
+    with np.errstate(over="ignore"):
+        return (x / (np.float32(1.0) + np.exp(-x))).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# Strassen algebra
+# ---------------------------------------------------------------------------
+
+# Classical products and the quadrant updates each one makes,
+# ``strassen_pallas.py:324-379``. Quadrants: 0=(top,left) 1=(top,right)
+# 2=(bottom,left) 3=(bottom,right); a0..a3 / b0..b3 use the same numbering
+# over (row half, K half) and (K half, column half), ``:193-204``.
+PRODUCT_UPDATES = {
+    1: ((0, +1), (3, +1)),   # P1=(A0+A3)(B0+B3)
+    2: ((2, +1), (3, -1)),   # P2=(A2+A3)B0
+    3: ((1, +1), (3, +1)),   # P3=A0(B1-B3)
+    4: ((0, +1), (2, +1)),   # P4=A3(B2-B0)
+    5: ((0, -1), (1, +1)),   # P5=(A0+A1)B3
+    6: ((3, +1),),           # P6=(A2-A0)(B0+B1)
+    7: ((0, +1),),           # P7=(A1-A3)(B2+B3)
+}
+
+PLAIN_ORDER = (1, 2, 3, 4, 5, 6, 7)                 # ``:566-573``
+INTERLEAVED_ORDER = (4, 6, 5, 2, 7, 3, 1)           # ``:556-565``
+PA_SWIGLU_TOP = (4, 5, 7, 3, 1)                     # ``:627-631``
+PA_SWIGLU_BOTTOM = (6, 2)                           # ``:633-634``
+PA_RESIDUAL_FINAL = (4, 6, 5, 2, 7, 3, 1)           # ``:679-687``
+
+
+def strassen_products(a_q, b_q):
+    """The seven classical operand pairs, each sum rounded once to bf16.
+
+    ``a_q``/``b_q`` are the four quadrants (bf16 values in float32). Every
+    add/sub is ``(x.astype(cd) + y.astype(cd)).astype(cd)`` with cd=bf16 in
+    the reference (``:324-379``): the exact sum of two bf16 values rounded
+    once to bf16. float32 holds that sum either exactly or within half an
+    ulp of float32, and float32 precision (24 bits) >= 2*8+2, so rounding the
+    float32 sum to bf16 is the correctly rounded bf16 sum.
+    """
+    a0, a1, a2, a3 = a_q
+    b0, b1, b2, b3 = b_q
+    r = bf16_round
+    return {
+        1: (r(a0 + a3), r(b0 + b3)),
+        2: (r(a2 + a3), b0),
+        3: (a0, r(b1 - b3)),
+        4: (a3, r(b2 - b0)),
+        5: (r(a0 + a1), b3),
+        6: (r(a2 - a0), r(b0 + b1)),
+        7: (r(a1 - a3), r(b2 + b3)),
+    }
+
+
+def _split_a(a, bm, bk, step):
+    """Quadrants of every A tile in K panel ``step`` stacked over row tiles.
+
+    Returns four (M/2, bk/2) arrays whose row index is (row tile, local row).
+    Quadrant slicing follows ``strassen_pallas.py:193-198``.
+    """
+    m = a.shape[0]
+    hm, hk = bm // 2, bk // 2
+    panel = a[:, step * bk:(step + 1) * bk].reshape(m // bm, 2, hm, 2, hk)
+    return tuple(
+        np.ascontiguousarray(panel[:, r, :, c, :].reshape(m // 2, hk))
+        for r in range(2) for c in range(2))
+
+
+def _split_b(b, bn, bk, step):
+    """Quadrants of every B tile in K panel ``step`` stacked over column tiles.
+
+    Returns four (bk/2, N/2) arrays (``strassen_pallas.py:199-204``).
+    """
+    n = b.shape[1]
+    hn, hk = bn // 2, bk // 2
+    panel = b[step * bk:(step + 1) * bk, :].reshape(2, hk, n // bn, 2, hn)
+    return tuple(
+        np.ascontiguousarray(panel[r, :, :, c, :].reshape(hk, n // 2))
+        for r in range(2) for c in range(2))
+
+
+def _quadrants_of(x, bm, bn):
+    """Split an (M, N) output-shaped array into its four quadrant planes."""
+    m, n = x.shape
+    hm, hn = bm // 2, bn // 2
+    v = x.reshape(m // bm, 2, hm, n // bn, 2, hn)
+    return tuple(
+        np.ascontiguousarray(v[:, r, :, :, c, :].reshape(m // 2, n // 2))
+        for r in range(2) for c in range(2))
+
+
+def _assemble(quads, m, n, bm, bn):
+    """Inverse of ``_quadrants_of``: four (M/2, N/2) planes -> (M, N)."""
+    hm, hn = bm // 2, bn // 2
+    out = np.empty((m // bm, 2, hm, n // bn, 2, hn), dtype=np.float32)
+    for q in range(4):
+        r, c = divmod(q, 2)
+        out[:, r, :, :, c, :] = quads[q].reshape(m // bm, hm, n // bn, hn)
+    return out.reshape(m, n)
+
+
+def _column_vector_quadrants(v, bn):
+    """Split a length-N per-column vector into its (left, right) halves."""
+    n = v.shape[0]
+    hn = bn // 2
+    w = v.reshape(n // bn, 2, hn)
+    return (np.ascontiguousarray(w[:, 0, :].reshape(n // 2)),
+            np.ascontiguousarray(w[:, 1, :].reshape(n // 2)))
+
+
+def _check_common(a, b, bm, bn, bk):
+    if a.ndim != 2 or b.ndim != 2:
+        raise ValueError("strassen_matmul expects two rank-2 matrices")
+    m, k = a.shape
+    k2, n = b.shape
+    if k != k2:
+        raise ValueError(f"inner dimensions disagree: {k} vs {k2}")
+    for name, dimension, block in (("M", m, bm), ("N", n, bn), ("K", k, bk)):
+        if dimension % block:
+            raise ValueError(f"{name}={dimension} is not divisible by {block}")
+    if bm % 2 or bn % 2 or bk % 2:
+        raise ValueError("tile dimensions must be even")
+    return m, k, n
+
+
+def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
+                    epilogue=None, residual=None, bias=None, rope_cos=None,
+                    rope_sin=None, rope_scale=None, rope_head_dim=128,
+                    rope_eps=1e-6, product_aware_swiglu=False,
+                    product_aware_residual=False, output_dtype="bfloat16"):
+    """``a @ b`` with one tile-local classical Strassen level.
+
+    Restates ``_classical_strassen_kernel`` (``strassen_pallas.py:156-879``)
+    for ``formula_variant="classical"``, ``block_permutation=0`` and no exact
+    panels, under the plumbing of ``strassen_matmul`` (``:882-1221``):
+
+    * grid ``(M/bm, N/bn, K/bk)``; per K panel the seven half-size products
+      update four FP32 quadrant accumulators in the reference's order
+      (plain ``:566-573`` or interleaved ``:556-565``; product-aware final
+      panels ``:593-689``);
+    * the epilogue runs on the FP32 accumulators after the last panel and
+      the result is rounded once to bf16 (``:739-879``);
+    * ``output_dtype="float32"`` returns the accumulators unrounded
+      (the reference's output-as-accumulator mode ``:1054-1057`` sums the
+      same values in the same order).
+
+    Inputs must hold bf16 values (use ``bf16_round`` first). Returns float32
+    arrays holding bf16 values (or raw FP32 for ``output_dtype="float32"``).
+    """
+    a = np.asarray(a, dtype=np.float32)
+    b = np.asarray(b, dtype=np.float32)
+    m, k, n = _check_common(a, b, bm, bn, bk)
+    nk = k // bk
+    hm, hn = bm // 2, bn // 2
+    if product_aware_swiglu and epilogue not in ("swiglu",):
+        raise ValueError("product_aware_swiglu is only valid with epilogue='swiglu'")
+    if product_aware_residual and epilogue != "residual_add":
+        raise ValueError("product_aware_residual is only valid with epilogue='residual_add'")
+    order = INTERLEAVED_ORDER if interleave_products else PLAIN_ORDER
+
+    acc = [np.zeros((m // 2, n // 2), dtype=np.float32) for _ in range(4)]
+
+    def run(products, sequence):
+        for p in sequence:
+            s, t = products[p]
+            value = np.matmul(s, t, dtype=np.float32)
+            for q, sign in PRODUCT_UPDATES[p]:
+                if sign > 0:
+                    acc[q] += value
+                else:
+                    acc[q] -= value
+
+    for step in range(nk):
+        products = strassen_products(_split_a(a, bm, bk, step),
+                                     _split_b(b, bn, bk, step))
+        last = step == nk - 1
+        if last and product_aware_swiglu:
+            run(products, PA_SWIGLU_TOP)
+            run(products, PA_SWIGLU_BOTTOM)
+        elif last and product_aware_residual:
+            run(products, PA_RESIDUAL_FINAL)
+        else:
+            run(products, order)
+    return _epilogue(acc, m, n, bm, bn, epilogue=epilogue, residual=residual,
+                     bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
+                     rope_scale=rope_scale, rope_head_dim=rope_head_dim,
+                     rope_eps=rope_eps, output_dtype=output_dtype)
+
+
+def cubic_blocked_matmul(a, b, *, bm, bn, bk, epilogue=None, residual=None,
+                         bias=None, rope_cos=None, rope_sin=None,
+                         rope_scale=None, rope_head_dim=128, rope_eps=1e-6,
+                         output_dtype="bfloat16"):
+    """The matched cubic control: eight half-size products per K panel.
+
+    ``_cubic_blocked_kernel`` (``experiments/qwen3/benchmark_cubic_control.py
+    :76-113``): same quadrant split and four FP32 accumulators as Strassen,
+    products (a0b0, a0b1, a2b0, a2b1, a1b2, a1b3, a3b2, a3b3) into quadrants
+    (0, 1, 2, 3, 0, 1, 2, 3), no operand pre-adds. The reference control has
+    no epilogues; the same epilogue code as Strassen is applied here so the
+    fused sites can be compared against an identical cubic arm.
+    """
+    a = np.asarray(a, dtype=np.float32)
+    b = np.asarray(b, dtype=np.float32)
+    m, k, n = _check_common(a, b, bm, bn, bk)
+    acc = [np.zeros((m // 2, n // 2), dtype=np.float32) for _ in range(4)]
+    pairs = ((0, 0, 0), (0, 1, 1), (2, 0, 2), (2, 1, 3),
+             (1, 2, 0), (1, 3, 1), (3, 2, 2), (3, 3, 3))
+    for step in range(k // bk):
+        aq = _split_a(a, bm, bk, step)
+        bq = _split_b(b, bn, bk, step)
+        for ia, ib, q in pairs:
+            acc[q] += np.matmul(aq[ia], bq[ib], dtype=np.float32)
+    return _epilogue(acc, m, n, bm, bn, epilogue=epilogue, residual=residual,
+                     bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
+                     rope_scale=rope_scale, rope_head_dim=rope_head_dim,
+                     rope_eps=rope_eps, output_dtype=output_dtype)
+
+
+def _epilogue(acc, m, n, bm, bn, *, epilogue, residual, bias, rope_cos,
+              rope_sin, rope_scale, rope_head_dim, rope_eps, output_dtype):
+    """Epilogues on the FP32 accumulators, then one bf16 rounding.
+
+    ``strassen_pallas.py:739-879``: swiglu ``:762-777``, residual_add
+    ``:778-792``, qk_norm_rope ``:793-835``, bias_add ``:867-874``, plain
+    store ``:875-879``.
+    """
+    hm, hn = bm // 2, bn // 2
+    to_out = (lambda x: x.astype(np.float32)) if output_dtype == "float32" else bf16_round
+    if epilogue is None:
+        return to_out(_assemble(acc, m, n, bm, bn))
+    if epilogue == "swiglu":
+        top = silu(acc[0]) * acc[1]
+        bottom = silu(acc[2]) * acc[3]
+        # Output tile (bm, bn/2): rows [0,hm) from the top pair, [hm,bm) bottom.
+        out = np.empty((m // bm, 2, hm, n // bn, hn), dtype=np.float32)
+        out[:, 0] = top.reshape(m // bm, hm, n // bn, hn)
+        out[:, 1] = bottom.reshape(m // bm, hm, n // bn, hn)
+        return to_out(out.reshape(m, n // 2))
+    if epilogue == "residual_add":
+        res = _quadrants_of(np.asarray(residual, dtype=np.float32), bm, bn)
+        return to_out(_assemble([acc[q] + res[q] for q in range(4)], m, n, bm, bn))
+    if epilogue == "bias_add":
+        left, right = _column_vector_quadrants(np.asarray(bias, dtype=np.float32), bn)
+        quads = [acc[0] + left, acc[1] + right, acc[2] + left, acc[3] + right]
+        return to_out(_assemble(quads, m, n, bm, bn))
+    if epilogue == "qk_norm_rope":
+        return to_out(_qk_norm_rope(acc, m, n, bm, bn, rope_cos, rope_sin,
+                                    rope_scale, rope_head_dim, rope_eps))
+    raise ValueError(f"unknown epilogue {epilogue!r}")
+
+
+def _qk_norm_rope(acc, m, n, bm, bn, cos, sin, scale, head_dim, eps):
+    """Per-head RMSNorm then RoPE on laid-out quadrants (``:793-835``).
+
+    Within each (bm, bn) tile, quadrants 0/2 hold each head's first-half
+    channels and 1/3 the matching second halves (``rope_weight_layout``), in
+    contiguous head_dim/2-wide segments. Per row and head:
+    ``sums = sum(a^2) + sum(b^2)`` over the segment (two separate segmented
+    sums, ``:815-820``), ``recip = rsqrt(sums/head_dim + eps)``,
+    ``a' = a*recip*gamma_a``, ``b' = b*recip*gamma_b``,
+    ``out_a = a'cos - b'sin``, ``out_b = b'cos + a'sin`` with cos/sin read
+    by output row (``:812-827``).
+    """
+    hm, hn = bm // 2, bn // 2
+    seg = head_dim // 2
+    cos = np.asarray(cos, dtype=np.float32)
+    sin = np.asarray(sin, dtype=np.float32)
+    scale = np.asarray(scale, dtype=np.float32)
+    scale_a, scale_b = scale[:hn], scale[hn:]
+    inverse_width = np.float32(1.0 / head_dim)
+    eps = np.float32(eps)
+    # Row-indexed tables for the top / bottom quadrant rows of every tile.
+    rows = cos.reshape(m // bm, 2, hm, hn)
+    srows = sin.reshape(m // bm, 2, hm, hn)
+    outs = []
+    for half in range(2):
+        first = acc[2 * half].reshape(m // bm, hm, n // bn, hn)
+        second = acc[2 * half + 1].reshape(m // bm, hm, n // bn, hn)
+        c = rows[:, half][:, :, None, :]
+        s = srows[:, half][:, :, None, :]
+        fsq = (first * first).reshape(m // bm, hm, n // bn, hn // seg, seg)
+        ssq = (second * second).reshape(m // bm, hm, n // bn, hn // seg, seg)
+        sums = fsq.sum(axis=-1, dtype=np.float32) + ssq.sum(axis=-1, dtype=np.float32)
+        recip = (np.float32(1.0) / np.sqrt(sums * inverse_width + eps)).astype(np.float32)
+        recip = np.repeat(recip, seg, axis=-1)
+        na = first * recip * scale_a
+        nb = second * recip * scale_b
+        out_a = na * c - nb * s
+        out_b = nb * c + na * s
+        outs.append((out_a.reshape(m // 2, n // 2), out_b.reshape(m // 2, n // 2)))
+    quads = [outs[0][0], outs[0][1], outs[1][0], outs[1][1]]
+    return _assemble(quads, m, n, bm, bn)
+
+
+def native_matmul(a, b):
+    """bf16 x bf16 with FP32 accumulation, one bf16 rounding.
+
+    ``strassen_pallas.py:1414-1421`` / ``benchmark_common.py:17-24``.
+    """
+    return bf16_round(np.matmul(np.asarray(a, np.float32), np.asarray(b, np.float32)))
+
+
+def high_precision_reference(a, b):
+    """The FP32 HIGHEST oracle of ``benchmark_common.py:27-33``.
+
+    Computed in float64 and rounded to float32 (at least as accurate as an
+    FP32 HIGHEST product of the same bf16-valued inputs).
+    """
+    return np.matmul(np.asarray(a, np.float64), np.asarray(b, np.float64)).astype(np.float32)
+
+
+def device_error(got, reference):
+    """Error metrics of ``benchmark_common.py:36-60``."""
+    got = np.asarray(got, dtype=np.float64)
+    reference = np.asarray(reference, dtype=np.float64)
+    delta = got - reference
+    tiny = float(np.finfo(np.float32).tiny)
+    max_abs = float(np.max(np.abs(delta))) if delta.size else 0.0
+    return {
+        "max_abs": max_abs,
+        "rmse": float(np.sqrt(np.mean(delta * delta))) if delta.size else 0.0,
+        "maxnorm_relative": max_abs / max(float(np.max(np.abs(reference))) if delta.size else 0.0, tiny),
+        "l2_relative": float(np.linalg.norm(delta)) / max(float(np.linalg.norm(reference)), tiny),
+    }
+
+
+def host_uniform_inputs(shape, seed):
+    """uniform[-1, 1] inputs of ``benchmark_common.py:63-69``, rounded to bf16
+    as ``jnp.asarray(..., dtype=bfloat16)`` does (``:72-74``)."""
+    m, k, n = shape
+    rng = np.random.default_rng(seed)
+    a = rng.uniform(-1.0, 1.0, (m, k)).astype(np.float32)
+    b = rng.uniform(-1.0, 1.0, (k, n)).astype(np.float32)
+    return bf16_round(a), bf16_round(b)
+
+
+# ---------------------------------------------------------------------------
+# Relayouts (pure column permutations) and unfused Qwen3 semantics
+# ---------------------------------------------------------------------------
+
+def swiglu_weight_layout_order(two_i, bn):
+    """Column order of ``swiglu_weight_layout`` (``strassen_pallas.py:1381-1411``)."""
+    if two_i % 2:
+        raise ValueError(f"combined gate/up width {two_i} is not even")
+    intermediate = two_i // 2
+    half = bn // 2
+    if intermediate % half:
+        raise ValueError(f"intermediate {intermediate} is not divisible by bn//2={half}")
+    order = []
+    for block in range(intermediate // half):
+        start = block * half
+        order.extend(range(start, start + half))
+        order.extend(range(intermediate + start, intermediate + start + half))
+    return np.asarray(order, dtype=np.int64)
+
+
+def swiglu_weight_layout(gate_up, bn):
+    return np.asarray(gate_up)[:, swiglu_weight_layout_order(np.asarray(gate_up).shape[1], bn)]
+
+
+def rope_weight_layout_order(n, bn, head_dim=128):
+    """Column order of ``rope_weight_layout`` (``strassen_pallas.py:1315-1349``)."""
+    if n % head_dim:
+        raise ValueError(f"width {n} is not a multiple of head_dim {head_dim}")
+    if bn % (2 * head_dim):
+        raise ValueError(f"bn={bn} must be a multiple of 2*head_dim={2 * head_dim}")
+    half_head = head_dim // 2
+    heads = n // head_dim
+    a_cols = [h * head_dim + j for h in range(heads) for j in range(half_head)]
+    b_cols = [h * head_dim + half_head + j for h in range(heads) for j in range(half_head)]
+    half = bn // 2
+    if (n // 2) % half:
+        raise ValueError(f"half width {n // 2} is not divisible by bn//2={half}")
+    order = []
+    for block in range((n // 2) // half):
+        lo, hi = block * half, (block + 1) * half
+        order.extend(a_cols[lo:hi])
+        order.extend(b_cols[lo:hi])
+    return np.asarray(order, dtype=np.int64)
+
+
+def rope_weight_layout(weight, bn, head_dim=128):
+    weight = np.asarray(weight)
+    return weight[:, rope_weight_layout_order(weight.shape[1], bn, head_dim)]
+
+
+def rope_layout_tables(cos, sin, half_width, head_dim=128):
+    """``strassen_pallas.py:1352-1368``."""
+    half_head = head_dim // 2
+    if half_width % half_head:
+        raise ValueError(f"half_width {half_width} is not a multiple of {half_head}")
+    repeats = half_width // half_head
+    return (np.tile(np.asarray(cos)[:, :half_head], (1, repeats)),
+            np.tile(np.asarray(sin)[:, :half_head], (1, repeats)))
+
+
+def rope_scale_layout(scale, bn, head_dim=128):
+    """``strassen_pallas.py:1371-1378``."""
+    half_head = head_dim // 2
+    repeats = (bn // 2) // half_head
+    scale = np.asarray(scale)
+    return np.concatenate((np.tile(scale[:half_head], repeats),
+                           np.tile(scale[half_head:], repeats)))
+
+
+def rope_layout_to_heads(flat, heads, bn, batch, seq, head_dim=128):
+    """Inverse regroup of a qk_norm_rope output
+    (``experiments/qwen3/benchmark_qwen3_32b_layer.py:322-341``)."""
+    half_head = head_dim // 2
+    heads_per_half = (bn // 2) // half_head
+    blocks = (heads * head_dim) // bn
+    tokens = batch * seq
+    return (np.asarray(flat).reshape(tokens, blocks, 2, heads_per_half, half_head)
+            .transpose(0, 1, 3, 2, 4).reshape(batch, seq, heads, head_dim))
+
+
+def rope_values(seq, head_dim=128, theta=1e6):
+    """bf16 cos/sin tables (``benchmark_qwen3_32b_layer.py:258-267``)."""
+    positions = np.arange(seq, dtype=np.float32)[:, None]
+    inverse = (np.float32(1.0) / (np.float32(theta) ** (np.arange(0, head_dim, 2, dtype=np.float32) / np.float32(head_dim)))).astype(np.float32)
+    angles = np.concatenate((positions * inverse[None, :],) * 2, axis=-1).astype(np.float32)
+    return bf16_round(np.cos(angles)), bf16_round(np.sin(angles))
+
+
+def rms_norm(x, scale, eps=1e-6):
+    """``benchmark_qwen3_32b_layer.py:270-276`` (FP32 math, bf16 output)."""
+    x32 = np.asarray(x, dtype=np.float32)
+    mean = np.mean(x32 * x32, axis=-1, keepdims=True, dtype=np.float32)
+    return bf16_round(x32 * (np.float32(1.0) / np.sqrt(mean + np.float32(eps))) * np.asarray(scale, np.float32))
+
+
+def apply_rope(x, cos, sin):
+    """``benchmark_qwen3_32b_layer.py:279-284``: x (B,S,H,D), cos/sin (S,D)."""
+    x32 = np.asarray(x, dtype=np.float32)
+    first, second = np.split(x32, 2, axis=-1)
+    rotated = np.concatenate((-second, first), axis=-1)
+    c = np.asarray(cos, np.float32)[None, :, None, :]
+    s = np.asarray(sin, np.float32)[None, :, None, :]
+    return bf16_round(x32 * c + rotated * s)

@@ -1,0 +1,107 @@
+"""ctypes binding of ``libstrassen_mi355x.so`` (the C ABI in
+``include/strassen_mi355x.h``).
+
+The library links the HIP runtime by SONAME ``libamdhip64.so.7``; importing
+torch first makes it bind to the runtime torch already loaded, so both share
+one HIP context and torch's streams are valid handles here.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (load torch's HIP runtime before the library)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY = os.path.join(HERE, "libstrassen_mi355x.so")
+
+SMX_OK = 0
+SMX_ERR_INVALID = 1
+SMX_ERR_UNSUPPORTED = 2
+SMX_ERR_LAUNCH = 3
+
+SMX_ALGO_STRASSEN = 7
+SMX_ALGO_CUBIC = 8
+
+SMX_EPI = {
+    None: 0,
+    "swiglu": 1,
+    "residual_add": 2,
+    "bias_add": 3,
+    "qk_norm_rope": 4,
+}
+
+SMX_B_KCONTIG = 1
+SMX_AUX_BIAS_F32 = 1
+SMX_AUX_SCALE_F32 = 2
+
+EXPORTS = ("smx_gemm", "smx_tile_requirements", "smx_last_error", "smx_version")
+
+
+class SmxGemmDesc(ctypes.Structure):
+    _fields_ = [
+        ("m", ctypes.c_int64), ("n", ctypes.c_int64), ("k", ctypes.c_int64),
+        ("lda", ctypes.c_int64), ("ldb", ctypes.c_int64), ("ldc", ctypes.c_int64),
+        ("ldr", ctypes.c_int64),
+        ("bm", ctypes.c_int32), ("bn", ctypes.c_int32), ("bk", ctypes.c_int32),
+        ("algo", ctypes.c_int32), ("epilogue", ctypes.c_int32),
+        ("b_layout", ctypes.c_int32), ("rope_head_dim", ctypes.c_int32),
+        ("rope_eps", ctypes.c_float), ("aux_f32", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
+    ]
+
+
+_lib = None
+
+
+def load():
+    """Load the built library, or raise: there is no fallback path."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIBRARY):
+        raise RuntimeError(
+            f"{LIBRARY} is missing: build it with `python -m strassen_tpu_amd.build` "
+            "(the Strassen GEMM has no CPU or fallback implementation)")
+    lib = ctypes.CDLL(LIBRARY)
+    vp = ctypes.c_void_p
+    lib.smx_gemm.argtypes = [ctypes.POINTER(SmxGemmDesc), vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.smx_gemm.restype = ctypes.c_int
+    lib.smx_tile_requirements.argtypes = [ctypes.c_int32, ctypes.c_int32,
+                                          ctypes.POINTER(ctypes.c_int32),
+                                          ctypes.POINTER(ctypes.c_int32),
+                                          ctypes.POINTER(ctypes.c_int32)]
+    lib.smx_tile_requirements.restype = ctypes.c_int
+    lib.smx_last_error.argtypes = []
+    lib.smx_last_error.restype = ctypes.c_char_p
+    lib.smx_version.argtypes = []
+    lib.smx_version.restype = ctypes.c_int
+    _lib = lib
+    return lib
+
+
+def last_error():
+    return load().smx_last_error().decode("utf-8", "replace")
+
+
+def tile_requirements(algo, epilogue):
+    lib = load()
+    tm, tn, tk = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    rc = lib.smx_tile_requirements(algo, SMX_EPI[epilogue], ctypes.byref(tm), ctypes.byref(tn), ctypes.byref(tk))
+    if rc != SMX_OK:
+        raise ValueError(last_error())
+    return tm.value, tn.value, tk.value
+
+
+def check(rc):
+    if rc == SMX_OK:
+        return
+    message = last_error()
+    if rc in (SMX_ERR_INVALID, SMX_ERR_UNSUPPORTED):
+        raise ValueError(message)
+    raise RuntimeError(message)
+
+
+def ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())

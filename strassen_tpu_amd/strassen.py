@@ -1,0 +1,380 @@
+"""Drop-in surface of the reference's ``strassen_pallas`` GEMM path on gfx950.
+
+``strassen_matmul`` keeps the keyword surface, argument meaning and error
+messages of ``strassen_pallas.strassen_matmul`` (``strassen_pallas.py:882-1221``)
+and runs the hand-written HIP kernel in ``csrc/strassen_gemm.hip`` through
+the C ABI of ``include/strassen_mi355x.h``. Tensors are torch bf16 tensors on
+the HIP device; the result is a new bf16 tensor, computed asynchronously on
+torch's current stream.
+
+Differences a caller can observe, all raised as exceptions (never silent):
+
+* Research formula knobs that the tuned dispatcher never selects
+  (``formula_variant != "classical"``, ``block_permutation``,
+  ``classical_panels``, ``panel_schedule``) and the ``geglu`` /
+  ``norm_residual_add`` epilogues, FP32 inputs and FP32 output raise
+  ``NotImplementedError``.
+* TPU-only knobs (``dot_precision``, ``allow_input_fusion`` after its
+  validation, ``vmem_limit_bytes``) are accepted and have no effect;
+  ``interpret=True`` raises ``NotImplementedError`` (there is no CPU path).
+* The kernel keeps seven persistent FP32 product accumulators and combines
+  the quadrants once after the last K panel, so ``interleave_products`` and
+  the ``product_aware_*`` schedules (which only reorder FP32 additions in
+  the reference) are validated and accepted but select the same kernel.
+* Tiles must additionally satisfy the gfx950 kernel's divisibility rule
+  (``smx_tile_requirements``): bm % 256, bn % 128, bk % 64 == 0.
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+
+from . import _lib
+from .layouts import is_k_contiguous
+
+__all__ = [
+    "strassen_matmul", "cubic_matmul", "native_matmul", "check_tiling",
+    "TUNED_BM", "TUNED_BN", "TUNED_BK", "VMEM_PROFILE", "PROFILE_INFO",
+]
+
+LANE = 128
+SUBLANE = 8
+
+# The reference's default tile (``compact16``, strassen_pallas.py:20-24).
+TUNED_BM, TUNED_BN, TUNED_BK = 1024, 1024, 512
+VMEM_PROFILE = "compact16"
+PROFILE_INFO = {
+    "profile": VMEM_PROFILE,
+    "tile": (TUNED_BM, TUNED_BN, TUNED_BK),
+    "device": "gfx950",
+}
+
+_EPILOGUES = ("swiglu", "geglu", "residual_add", "bias_add", "qk_norm_rope", "norm_residual_add")
+
+
+def check_tiling(bm, bn, bk):
+    """The reference's alignment rule (``strassen_pallas.py:127-140``)."""
+    requirements = (
+        ("bm", bm, 2 * SUBLANE),
+        ("bn", bn, 2 * LANE),
+        ("bk", bk, 2 * LANE),
+    )
+    errors = [
+        f"{name}={value} must be a multiple of {multiple}"
+        for name, value, multiple in requirements
+        if value % multiple
+    ]
+    if errors:
+        raise ValueError("tile breaks TPU v5e alignment:\n  " + "\n  ".join(errors))
+
+
+def _check_device_tiling(algo, epilogue, bm, bn, bk):
+    tm, tn, tk = _lib.tile_requirements(algo, epilogue)
+    errors = [
+        f"{name}={value} must be a multiple of {multiple}"
+        for name, value, multiple in (("bm", bm, 2 * tm), ("bn", bn, 2 * tn), ("bk", bk, 2 * tk))
+        if value % multiple
+    ]
+    if errors:
+        raise ValueError("tile breaks the gfx950 kernel tiling:\n  " + "\n  ".join(errors))
+
+
+def _is_dtype(x, dtype):
+    return x.dtype == dtype
+
+
+def _validate(a, b, *, bm, bn, bk, block_permutation, formula_variant,
+              classical_panels, panel_schedule, epilogue, residual, bias,
+              rope_cos, rope_sin, rope_scale, rope_head_dim, norm_scale,
+              output_dtype, allow_input_fusion, product_aware_swiglu,
+              product_aware_residual):
+    """Argument checks in the order and wording of ``strassen_pallas.py:927-1047``."""
+    if a.dim() != 2 or b.dim() != 2:
+        raise ValueError("strassen_matmul expects two rank-2 matrices")
+    m, k = a.shape
+    k2, n = b.shape
+    if k != k2:
+        raise ValueError(f"inner dimensions disagree: {k} vs {k2}")
+    if a.dtype != b.dtype:
+        raise ValueError(f"input dtypes disagree: {a.dtype} vs {b.dtype}")
+    if a.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("inputs must be BF16 or FP32")
+    if not isinstance(block_permutation, int) or not 0 <= block_permutation < 8:
+        raise ValueError("block_permutation must be an integer from 0 through 7")
+    if formula_variant not in ("classical", "dual", "powers"):
+        raise ValueError("formula_variant must be 'classical', 'dual', or 'powers'")
+    classical_panels = tuple(sorted({int(p) for p in classical_panels}))
+    if epilogue is not None:
+        if epilogue not in _EPILOGUES:
+            raise ValueError(
+                f"unknown epilogue {epilogue!r}; choose 'swiglu' or "
+                "'residual_add' or 'bias_add'")
+        if formula_variant == "powers":
+            raise ValueError("fused epilogues require a quadrant-basis formula")
+        if output_dtype is not None and output_dtype != torch.bfloat16:
+            raise ValueError("fused epilogues write a BF16 output tile")
+        if epilogue in ("swiglu", "geglu") and bn % 2:
+            raise ValueError(f"{epilogue} epilogue needs an even bn, got {bn}")
+        if epilogue == "residual_add" and residual is None:
+            raise ValueError("residual_add epilogue requires residual=")
+        if epilogue == "bias_add" and bias is None:
+            raise ValueError("bias_add epilogue requires bias=")
+    if residual is not None and epilogue not in ("residual_add", "norm_residual_add"):
+        raise ValueError(
+            "residual= is only used by the residual_add and "
+            "norm_residual_add epilogues")
+    if bias is not None and epilogue != "bias_add":
+        raise ValueError("bias= is only used by the bias_add epilogue")
+    if epilogue == "norm_residual_add":
+        if residual is None or norm_scale is None:
+            raise ValueError("norm_residual_add requires residual= and norm_scale=")
+        if bn != n:
+            raise ValueError(
+                "norm_residual_add normalises over the whole output row, so "
+                f"the tile must span it: bn={bn} must equal n={n}")
+    if epilogue == "qk_norm_rope":
+        if rope_cos is None or rope_sin is None or rope_scale is None:
+            raise ValueError(
+                "qk_norm_rope epilogue requires rope_cos=, rope_sin= and "
+                "rope_scale= (use rope_layout_tables and rope_scale_layout)")
+        if bn % (2 * rope_head_dim):
+            raise ValueError(
+                f"qk_norm_rope needs bn a multiple of 2*head_dim="
+                f"{2 * rope_head_dim} so a tile half holds whole heads, "
+                f"got bn={bn}")
+        if tuple(rope_cos.shape) != (m, bn // 2) or tuple(rope_sin.shape) != (m, bn // 2):
+            raise ValueError(
+                f"rope tables must be {(m, bn // 2)}, got "
+                f"{tuple(rope_cos.shape)} and {tuple(rope_sin.shape)}")
+        if tuple(rope_scale.shape) != (bn,):
+            raise ValueError(
+                f"rope_scale must be laid out to {(bn,)}, got "
+                f"{tuple(rope_scale.shape)}")
+    if rope_cos is not None and epilogue != "qk_norm_rope":
+        raise ValueError("rope_* are only used by the qk_norm_rope epilogue")
+    if product_aware_swiglu and epilogue not in ("swiglu", "geglu"):
+        raise ValueError(
+            "product_aware_swiglu is only valid with epilogue='swiglu' or 'geglu'")
+    if product_aware_residual and epilogue != "residual_add":
+        raise ValueError(
+            "product_aware_residual is only valid with epilogue='residual_add'")
+    if epilogue == "bias_add" and tuple(bias.shape) != (n,):
+        raise ValueError(f"bias shape {tuple(bias.shape)} != output width {(n,)}")
+    operand_count = 3 if epilogue in ("residual_add", "bias_add") else 2
+    if epilogue == "norm_residual_add":
+        operand_count = 4
+    if epilogue == "qk_norm_rope":
+        operand_count = 6
+    if allow_input_fusion is not None:
+        allow_input_fusion = tuple(allow_input_fusion)
+        if len(allow_input_fusion) != operand_count:
+            raise ValueError(
+                "allow_input_fusion must contain one boolean per operand: "
+                f"expected {operand_count}, got {len(allow_input_fusion)}")
+        if not all(isinstance(value, bool) for value in allow_input_fusion):
+            raise TypeError("allow_input_fusion entries must be bool")
+    if panel_schedule is not None and classical_panels:
+        raise ValueError(
+            "pass either classical_panels (static) or panel_schedule "
+            "(prefetched), not both")
+    if classical_panels:
+        if formula_variant == "powers":
+            raise ValueError("classical_panels requires a quadrant-basis formula")
+        if classical_panels[0] < 0 or classical_panels[-1] >= k // bk:
+            raise ValueError(f"classical_panels {classical_panels} outside 0..{k // bk - 1}")
+    for name, dimension, block in (("M", m, bm), ("N", n, bn), ("K", k, bk)):
+        if dimension % block:
+            raise ValueError(f"{name}={dimension} is not divisible by {block}")
+    check_tiling(bm, bn, bk)
+    out = a.dtype if output_dtype is None else output_dtype
+    if out not in (torch.bfloat16, torch.float32):
+        raise ValueError("output_dtype must be BF16 or FP32")
+    if residual is not None and epilogue == "residual_add" and tuple(residual.shape) != (m, n):
+        raise ValueError(f"residual shape {tuple(residual.shape)} != output shape {(m, n)}")
+    return m, k, n, classical_panels, out
+
+
+def _unsupported(formula_variant, block_permutation, classical_panels, panel_schedule,
+                 epilogue, dtype, out_dtype, interpret):
+    if interpret:
+        raise NotImplementedError("interpret=True: the gfx950 kernel has no CPU interpreter path")
+    if formula_variant != "classical":
+        raise NotImplementedError(f"formula_variant={formula_variant!r} is not implemented on gfx950")
+    if block_permutation:
+        raise NotImplementedError("block_permutation is not implemented on gfx950")
+    if classical_panels or panel_schedule is not None:
+        raise NotImplementedError("exact-panel policies are not implemented on gfx950")
+    if epilogue in ("geglu", "norm_residual_add"):
+        raise NotImplementedError(f"epilogue {epilogue!r} is not implemented on gfx950")
+    if dtype != torch.bfloat16:
+        raise NotImplementedError("FP32 inputs are not implemented on gfx950 (bf16 MFMA path)")
+    if out_dtype != torch.bfloat16:
+        raise NotImplementedError("FP32 output is not implemented on gfx950")
+
+
+def _require_device(*tensors):
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise ValueError("the gfx950 kernel needs tensors on the HIP device "
+                             f"(got a tensor on {t.device})")
+
+
+def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
+         rope_cos=None, rope_sin=None, rope_scale=None, rope_head_dim=128,
+         rope_eps=1e-6):
+    lib = _lib.load()
+    m, k = a.shape
+    n = b.shape[1]
+    _check_device_tiling(algo, epilogue, bm, bn, bk)
+    _require_device(a, b, residual, bias, rope_cos, rope_sin, rope_scale)
+    if a.stride(1) != 1:
+        a = a.contiguous()
+    if not is_k_contiguous(b):
+        b = b.t().contiguous().t()
+    bt = b.t()  # [N, K], rows contiguous
+    out_cols = n // 2 if epilogue == "swiglu" else n
+    c = torch.empty((m, out_cols), dtype=torch.bfloat16, device=a.device)
+    desc = _lib.SmxGemmDesc()
+    desc.m, desc.n, desc.k = m, n, k
+    desc.lda, desc.ldb, desc.ldc = a.stride(0), bt.stride(0), c.stride(0)
+    desc.bm, desc.bn, desc.bk = bm, bn, bk
+    desc.algo = algo
+    desc.epilogue = _lib.SMX_EPI[epilogue]
+    desc.b_layout = _lib.SMX_B_KCONTIG
+    desc.rope_head_dim = rope_head_dim
+    desc.rope_eps = rope_eps
+    aux = 0
+    if residual is not None:
+        residual = residual.to(torch.bfloat16)
+        if residual.stride(1) != 1:
+            residual = residual.contiguous()
+        desc.ldr = residual.stride(0)
+    if bias is not None:
+        bias = bias.contiguous()
+        if bias.dtype == torch.float32:
+            aux |= _lib.SMX_AUX_BIAS_F32
+        elif bias.dtype != torch.bfloat16:
+            bias = bias.to(torch.float32)
+            aux |= _lib.SMX_AUX_BIAS_F32
+    if rope_cos is not None:
+        rope_cos = rope_cos.to(torch.bfloat16).contiguous()
+        rope_sin = rope_sin.to(torch.bfloat16).contiguous()
+        rope_scale = rope_scale.contiguous()
+        if rope_scale.dtype == torch.float32:
+            aux |= _lib.SMX_AUX_SCALE_F32
+        elif rope_scale.dtype != torch.bfloat16:
+            rope_scale = rope_scale.to(torch.float32)
+            aux |= _lib.SMX_AUX_SCALE_F32
+    desc.aux_f32 = aux
+    stream = torch.cuda.current_stream(a.device).cuda_stream
+    rc = lib.smx_gemm(desc, _lib.ptr(a), _lib.ptr(bt), _lib.ptr(c), _lib.ptr(residual),
+                      _lib.ptr(bias), _lib.ptr(rope_cos), _lib.ptr(rope_sin),
+                      _lib.ptr(rope_scale), stream)
+    _lib.check(rc)
+    return c
+
+
+def strassen_matmul(
+    a,
+    b,
+    *,
+    bm=TUNED_BM,
+    bn=TUNED_BN,
+    bk=TUNED_BK,
+    dot_precision=None,
+    interleave_products=False,
+    block_permutation=0,
+    formula_variant="classical",
+    classical_panels=(),
+    panel_schedule=None,
+    epilogue=None,
+    residual=None,
+    bias=None,
+    rope_cos=None,
+    rope_sin=None,
+    rope_scale=None,
+    rope_head_dim=128,
+    rope_eps=1e-6,
+    norm_scale=None,
+    norm_eps=1e-6,
+    output_dtype=None,
+    allow_input_fusion=None,
+    product_aware_swiglu=False,
+    product_aware_residual=False,
+    interpret=False,
+    vmem_limit_bytes=None,
+):
+    """Compute ``a @ b`` with one tile-local classical Strassen level.
+
+    ``a`` is ``[M, K]`` and ``b`` is ``[K, N]``, both bf16 on the HIP device.
+    ``b`` is read directly when K-contiguous (``w.t()`` of a ``[N, K]``
+    weight, see ``layouts.k_contiguous``); otherwise it is transposed on each
+    call. Epilogues and their operands follow ``strassen_pallas.py:739-879``:
+    ``swiglu`` returns ``[M, N/2]`` from a ``swiglu_weight_layout`` weight,
+    ``residual_add`` adds ``residual`` ``[M, N]``, ``bias_add`` adds
+    ``bias`` ``[N]``, ``qk_norm_rope`` applies per-head RMSNorm and RoPE with
+    ``rope_layout_tables`` / ``rope_scale_layout`` operands.
+    """
+    m, k, n, classical_panels, out_dtype = _validate(
+        a, b, bm=bm, bn=bn, bk=bk, block_permutation=block_permutation,
+        formula_variant=formula_variant, classical_panels=classical_panels,
+        panel_schedule=panel_schedule, epilogue=epilogue, residual=residual,
+        bias=bias, rope_cos=rope_cos, rope_sin=rope_sin, rope_scale=rope_scale,
+        rope_head_dim=rope_head_dim, norm_scale=norm_scale,
+        output_dtype=output_dtype, allow_input_fusion=allow_input_fusion,
+        product_aware_swiglu=product_aware_swiglu,
+        product_aware_residual=product_aware_residual)
+    _unsupported(formula_variant, block_permutation, classical_panels, panel_schedule,
+                 epilogue, a.dtype, out_dtype, interpret)
+    return _run(_lib.SMX_ALGO_STRASSEN, a, b, bm=bm, bn=bn, bk=bk, epilogue=epilogue,
+                residual=residual, bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
+                rope_scale=rope_scale, rope_head_dim=rope_head_dim, rope_eps=rope_eps)
+
+
+def cubic_matmul(a, b, *, variant="blocked", bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_BK,
+                 dot_precision=None, allow_input_fusion=None, interpret=False,
+                 vmem_limit_bytes=None, epilogue=None, residual=None, bias=None,
+                 rope_cos=None, rope_sin=None, rope_scale=None, rope_head_dim=128,
+                 rope_eps=1e-6):
+    """Matched cubic control (``experiments/qwen3/benchmark_cubic_control.py:116-177``).
+
+    Eight half-size products per K panel into four FP32 quadrant
+    accumulators, with the Strassen kernel's tiling, LDS staging and
+    epilogues. ``variant="full"`` (one full-tile product per panel) computes
+    the same cubic GEMM and runs the same kernel. The fused epilogues are an
+    extension of the reference control, used to time fused sites against an
+    identical cubic arm.
+    """
+    if variant not in ("full", "blocked"):
+        raise ValueError(f"unknown cubic variant {variant!r}")
+    if a.dim() != 2 or b.dim() != 2:
+        raise ValueError("cubic_matmul expects two rank-2 matrices")
+    m, k = a.shape
+    k2, n = b.shape
+    if k != k2:
+        raise ValueError(f"inner dimensions disagree: {k} vs {k2}")
+    if allow_input_fusion is not None:
+        allow_input_fusion = tuple(allow_input_fusion)
+        if len(allow_input_fusion) != 2:
+            raise ValueError("allow_input_fusion must contain one boolean per operand")
+        if not all(isinstance(value, bool) for value in allow_input_fusion):
+            raise TypeError("allow_input_fusion entries must be bool")
+    for name, dimension, block in (("M", m, bm), ("N", n, bn), ("K", k, bk)):
+        if dimension % block:
+            raise ValueError(f"{name}={dimension} is not divisible by {block}")
+    check_tiling(bm, bn, bk)
+    if interpret:
+        raise NotImplementedError("interpret=True: the gfx950 kernel has no CPU interpreter path")
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        raise NotImplementedError("the gfx950 cubic control takes bf16 inputs")
+    return _run(_lib.SMX_ALGO_CUBIC, a, b, bm=bm, bn=bn, bk=bk, epilogue=epilogue,
+                residual=residual, bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
+                rope_scale=rope_scale, rope_head_dim=rope_head_dim, rope_eps=rope_eps)
+
+
+def native_matmul(a, b):
+    """Vendor arm: hipBLASLt bf16 GEMM with FP32 accumulation and bf16 output
+    (``strassen_pallas.py:1414-1421``)."""
+    return torch.matmul(a, b)

@@ -1,0 +1,116 @@
+"""The C-ABI library loads and exports every function include/*.h declares;
+argument errors come back as status codes without touching the GPU."""
+
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+from strassen_tpu_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = set()
+    for header in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(header).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names.update(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(smx_\w+)\s*\(", text, flags=re.M))
+    return sorted(names)
+
+
+def test_header_declares_expected_entry_points():
+    assert set(_lib.EXPORTS) == set(declared_functions())
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_version_and_macros_match_header():
+    header = open(os.path.join(ROOT, "include", "strassen_mi355x.h")).read()
+    version = int(re.search(r"#define SMX_VERSION (\d+)", header).group(1))
+    assert _lib.load().smx_version() == version
+    for name in ("SMX_OK", "SMX_ERR_INVALID", "SMX_ERR_UNSUPPORTED", "SMX_ERR_LAUNCH",
+                 "SMX_ALGO_STRASSEN", "SMX_ALGO_CUBIC", "SMX_B_KCONTIG",
+                 "SMX_AUX_BIAS_F32", "SMX_AUX_SCALE_F32"):
+        value = int(re.search(rf"#define {name} (\d+)", header).group(1))
+        assert getattr(_lib, name) == value, name
+    for epi, code in _lib.SMX_EPI.items():
+        if epi is not None:
+            macro = "SMX_EPI_" + epi.upper()
+            assert int(re.search(rf"#define {macro} (\d+)", header).group(1)) == code
+
+
+def test_descriptor_layout_matches_header_order():
+    header = open(os.path.join(ROOT, "include", "strassen_mi355x.h")).read()
+    body = re.search(r"typedef struct smx_gemm_desc \{(.*?)\} smx_gemm_desc;", header, re.S).group(1)
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    fields = []
+    for line in body.splitlines():
+        line = line.strip().rstrip(";")
+        if not line:
+            continue
+        ctype, names = line.split(None, 1)
+        fields += [(n.strip(), ctype) for n in names.split(",")]
+    kinds = {"int64_t": ctypes.c_int64, "int32_t": ctypes.c_int32, "float": ctypes.c_float}
+    assert [(n, kinds[t]) for n, t in fields] == list(_lib.SmxGemmDesc._fields_)
+
+
+def _desc(**kw):
+    d = _lib.SmxGemmDesc()
+    d.m, d.n, d.k = 256, 256, 128
+    d.lda, d.ldb, d.ldc, d.ldr = 128, 128, 256, 256
+    d.bm, d.bn, d.bk = 256, 256, 128
+    d.algo = _lib.SMX_ALGO_STRASSEN
+    d.epilogue = 0
+    d.b_layout = _lib.SMX_B_KCONTIG
+    d.rope_head_dim = 128
+    d.rope_eps = 1e-6
+    for key, value in kw.items():
+        setattr(d, key, value)
+    return d
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("algo", 5, _lib.SMX_ERR_INVALID),
+    ("m", 0, _lib.SMX_ERR_INVALID),
+    ("bm", 100, _lib.SMX_ERR_INVALID),
+    ("bm", 128, _lib.SMX_ERR_UNSUPPORTED),
+    ("bn", 64, _lib.SMX_ERR_UNSUPPORTED),
+    ("bk", 32, _lib.SMX_ERR_UNSUPPORTED),
+    ("b_layout", 0, _lib.SMX_ERR_UNSUPPORTED),
+    ("lda", 100, _lib.SMX_ERR_INVALID),
+    ("epilogue", 9, _lib.SMX_ERR_INVALID),
+])
+def test_invalid_descriptors_are_rejected_before_any_launch(field, value, code):
+    lib = _lib.load()
+    buf = (ctypes.c_uint8 * 16)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    rc = lib.smx_gemm(_desc(**{field: value}), p, p, p, None, None, None, None, None, None)
+    assert rc == code
+    assert _lib.last_error()
+
+
+def test_null_pointers_and_missing_epilogue_operands():
+    lib = _lib.load()
+    assert lib.smx_gemm(None, None, None, None, None, None, None, None, None, None) == _lib.SMX_ERR_INVALID
+    buf = (ctypes.c_uint8 * 16)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    assert lib.smx_gemm(_desc(), None, p, p, None, None, None, None, None, None) == _lib.SMX_ERR_INVALID
+    rc = lib.smx_gemm(_desc(epilogue=_lib.SMX_EPI["residual_add"]), p, p, p, None, None, None, None, None, None)
+    assert rc == _lib.SMX_ERR_INVALID and "residual" in _lib.last_error()
+    rc = lib.smx_gemm(_desc(epilogue=_lib.SMX_EPI["qk_norm_rope"]), p, p, p, None, None, None, None, None, None)
+    assert rc == _lib.SMX_ERR_INVALID and "rope" in _lib.last_error()
+
+
+def test_tile_requirements():
+    tm, tn, tk = _lib.tile_requirements(_lib.SMX_ALGO_STRASSEN, None)
+    assert tm > 0 and tn > 0 and tk % 16 == 0
+    with pytest.raises(ValueError):
+        _lib.tile_requirements(3, None)

@@ -1,0 +1,330 @@
+"""GPU parity of the gfx950 Strassen / cubic kernels against the CPU oracle.
+
+Bars:
+* exact-integer operands: bit-exact equality with A @ B (rounded once to bf16);
+* random bf16 operands: the same bf16 operand sums as the oracle, so outputs
+  agree to within one bf16 ulp everywhere (FP32 summation order differs), with
+  at most a small fraction of elements not bit-identical;
+* against the FP32 product: relative Frobenius error <= 1e-2 and <= 1.5x the
+  oracle Strassen's own error on the same inputs;
+* full Qwen3-32B shapes: sampled (bm, bn) output tiles recomputed by the
+  oracle (a Strassen tile depends only on its own A rows and B columns), plus
+  the whole-output error bound against an FP32 product.
+"""
+
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as o
+import strassen_tpu_amd as smx
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+DEV = torch.device("cuda:0")
+
+
+def say(*args):
+    print(*args, flush=True)
+
+
+def dev(x):
+    """float32 numpy (bf16 values) -> bf16 device tensor."""
+    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(DEV).to(torch.bfloat16)
+
+
+def dev_weight(b):
+    """[K, N] numpy -> K-contiguous [K, N] bf16 device view of [N, K] storage."""
+    return dev(np.ascontiguousarray(np.asarray(b, np.float32).T)).t()
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+def bf16_ulp(v):
+    bits = np.abs(np.asarray(v, np.float32)).view(np.uint32)
+    exponent = ((bits >> 23) & 0xFF).astype(np.int32)
+    exponent = np.maximum(exponent, 1)
+    return np.ldexp(np.float32(1.0), exponent - 127 - 7).astype(np.float32)
+
+
+def fp32_floor(want, k):
+    """Absolute FP32 summation-error allowance for outputs near zero.
+
+    The kernel and the oracle sum the same bf16 products in different FP32
+    orders; the kernel keeps seven product accumulators over K/2 terms and
+    combines them at the end, so its absolute error grows like
+    eps_f32 * sqrt(K) * |output scale|. Elements much smaller than that scale
+    can then differ by several of their own (tiny) bf16 ulps. The allowance
+    8 * 2^-24 * sqrt(K) * rms(want) stays far below one bf16 ulp at typical
+    magnitudes, so algebra or rounding mistakes still fail.
+    """
+    rms = float(np.sqrt(np.mean(np.asarray(want, np.float64) ** 2)))
+    return 8.0 * 2.0 ** -24 * np.sqrt(k) * rms
+
+
+def assert_ulp_close(got, want, *, k, max_mismatch_frac=0.02):
+    """|got - want| <= 1 bf16 ulp of want (or the FP32 summation allowance
+    near zero), and most elements bit-identical."""
+    got = np.asarray(got, np.float32)
+    want = np.asarray(want, np.float32)
+    assert got.shape == want.shape
+    assert np.isfinite(got).all()
+    floor = fp32_floor(want, k)
+    diff = np.abs(got - want)
+    bad = diff > np.maximum(bf16_ulp(want), floor)
+    assert not bad.any(), (
+        f"{int(bad.sum())} elements beyond 1 ulp; worst {float(diff.max())} at "
+        f"{np.unravel_index(int(np.argmax(diff)), diff.shape)}")
+    frac = float(np.mean(diff > 0))
+    assert frac <= max_mismatch_frac, f"{frac:.4f} of elements differ"
+
+
+def rel_l2(got, ref):
+    return float(np.linalg.norm(np.asarray(got, np.float64) - ref) / np.linalg.norm(ref))
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    say(f"\n[gpu] {request.node.nodeid}")
+    yield
+    torch.cuda.synchronize()
+
+
+# ---------------------------------------------------------------------------
+# Exact-integer known answers
+# ---------------------------------------------------------------------------
+
+INT_CASES = [
+    ((256, 512, 256), (256, 256, 512)),
+    ((512, 1024, 512), (256, 256, 256)),
+    ((1024, 2048, 768), (512, 256, 512)),
+]
+
+
+@pytest.mark.parametrize("shape,tile", INT_CASES)
+@pytest.mark.parametrize("algo", ["strassen", "cubic"])
+def test_integer_kat_bit_exact(shape, tile, algo):
+    m, k, n = shape
+    bm, bn, bk = tile
+    rng = np.random.default_rng(187)
+    a = rng.integers(-2, 3, (m, k)).astype(np.float32)
+    b = rng.integers(-2, 3, (k, n)).astype(np.float32)
+    fn = smx.strassen_matmul if algo == "strassen" else smx.cubic_matmul
+    say(f"  {algo} shape={shape} tile={tile}")
+    got = host(fn(dev(a), dev_weight(b), bm=bm, bn=bn, bk=bk))
+    assert np.array_equal(got, o.bf16_round(a @ b))
+
+
+def test_integer_kat_row_major_weight():
+    """A row-major [K, N] weight is transposed by the surface and gives the
+    same exact answer."""
+    rng = np.random.default_rng(190)
+    a = rng.integers(-2, 3, (256, 512)).astype(np.float32)
+    b = rng.integers(-2, 3, (512, 256)).astype(np.float32)
+    got = host(smx.strassen_matmul(dev(a), dev(b), bm=256, bn=256, bk=512))
+    assert np.array_equal(got, o.bf16_round(a @ b))
+
+
+# ---------------------------------------------------------------------------
+# Random bf16 operands vs the oracle
+# ---------------------------------------------------------------------------
+
+def _gaussian(seed, m, k, n, a_std=1.0, b_std=0.02):
+    rng = np.random.default_rng(seed)
+    a = o.bf16_round(rng.standard_normal((m, k)).astype(np.float32) * np.float32(a_std))
+    b = o.bf16_round(rng.standard_normal((k, n)).astype(np.float32) * np.float32(b_std))
+    return rng, a, b
+
+
+def test_config1_1024_cube_seed0():
+    """A[1024,1024] ~ N(0,1), B ~ N(0, 1/32), seed 0, reference default tile
+    (1024, 1024, 512), bf16 out, vs FP32 cubic."""
+    gen = torch.Generator().manual_seed(0)
+    a = o.bf16_round(torch.randn(1024, 1024, generator=gen).numpy())
+    b = o.bf16_round((torch.randn(1024, 1024, generator=gen) / 32).numpy())
+    ref = o.high_precision_reference(a, b).astype(np.float64)
+    want = o.strassen_matmul(a, b, bm=1024, bn=1024, bk=512, interleave_products=True)
+    got = host(smx.strassen_matmul(dev(a), dev_weight(b), bm=1024, bn=1024, bk=512,
+                                   interleave_products=True))
+    assert_ulp_close(got, want, k=1024)
+    e_got, e_want = rel_l2(got, ref), rel_l2(want, ref)
+    say(f"  strassen rel err gpu={e_got:.4e} oracle={e_want:.4e}")
+    assert e_got <= 1e-2 and e_got <= 1.5 * e_want
+    cubic = host(smx.cubic_matmul(dev(a), dev_weight(b), bm=1024, bn=1024, bk=512))
+    assert_ulp_close(cubic, o.cubic_blocked_matmul(a, b, bm=1024, bn=1024, bk=512), k=1024)
+
+
+@pytest.mark.parametrize("shape,tile", [
+    ((512, 2048, 1024), (256, 256, 512)),
+    ((768, 1536, 512), (256, 512, 256)),
+])
+def test_random_matches_oracle(shape, tile):
+    m, k, n = shape
+    _, a, b = _gaussian(42, m, k, n)
+    bm, bn, bk = tile
+    for fn, ofn in ((smx.strassen_matmul, o.strassen_matmul), (smx.cubic_matmul, o.cubic_blocked_matmul)):
+        got = host(fn(dev(a), dev_weight(b), bm=bm, bn=bn, bk=bk))
+        assert_ulp_close(got, ofn(a, b, bm=bm, bn=bn, bk=bk), k=k)
+
+
+def test_repeated_calls_reset_accumulators():
+    _, a, b = _gaussian(3, 256, 1024, 256)
+    first = host(smx.strassen_matmul(dev(a), dev_weight(b), bm=256, bn=256, bk=512))
+    second = host(smx.strassen_matmul(dev(-a), dev_weight(b), bm=256, bn=256, bk=512))
+    want = o.strassen_matmul(a, b, bm=256, bn=256, bk=512)
+    assert_ulp_close(first, want, k=1024)
+    assert_ulp_close(second, o.strassen_matmul(-a, b, bm=256, bn=256, bk=512), k=1024)
+
+
+def test_real_qwen3_weight_slice():
+    """Real Qwen3-0.6B layer-0 q_proj weights (reference test data) as B."""
+    data = np.load(os.path.join(GOLDEN, "qwen3_0p6b_q_proj_slice.npz"))
+    w_bits = data["weight_bits"]  # [out=256, in=512] bf16 bits
+    w = o.bits_to_f32(w_bits)     # [N, K]
+    b = np.ascontiguousarray(w.T)  # [K, N]
+    rng = np.random.default_rng(2026)
+    a = o.bf16_round(rng.standard_normal((256, 512)).astype(np.float32))
+    b_dev = torch.from_numpy(w_bits.view(np.int16)).view(torch.bfloat16).to(DEV).t()
+    ref = o.high_precision_reference(a, b).astype(np.float64)
+    for fn, ofn in ((smx.strassen_matmul, o.strassen_matmul), (smx.cubic_matmul, o.cubic_blocked_matmul)):
+        got = host(fn(dev(a), b_dev, bm=256, bn=256, bk=256))
+        want = ofn(a, b, bm=256, bn=256, bk=256)
+        assert_ulp_close(got, want, k=512)
+        assert rel_l2(got, ref) <= 1.5 * max(rel_l2(want, ref), 1e-4)
+
+
+@pytest.mark.slow
+def test_published_accuracy_gate_on_gpu():
+    """The reference's accuracy gate, regenerated: Strassen error vs FP32 on
+    the GPU matches the published TPU value (4.6988e-3) and the oracle."""
+    spec = json.load(open(os.path.join(GOLDEN, "accuracy_gate_reference.json")))
+    a, b = o.host_uniform_inputs(tuple(spec["shape_mkn"]), spec["seed"])
+    bm, bn, bk = spec["tile_bm_bn_bk"]
+    ref_t = torch.matmul(dev(a).float(), dev(b).float())  # FP32 product on the GPU
+    got = smx.strassen_matmul(dev(a), dev_weight(b), bm=bm, bn=bn, bk=bk).float()
+    cub = smx.cubic_matmul(dev(a), dev_weight(b), bm=bm, bn=bn, bk=bk).float()
+    e_s = float(torch.linalg.norm(got - ref_t) / torch.linalg.norm(ref_t))
+    e_c = float(torch.linalg.norm(cub - ref_t) / torch.linalg.norm(ref_t))
+    published = spec["errors_vs_reference"]
+    say(f"  strassen {e_s:.6e} (published {published['strassen']['l2_relative']:.6e}); "
+        f"cubic {e_c:.6e} (published {published['cubic_blocked']['l2_relative']:.6e})")
+    assert e_s == pytest.approx(published["strassen"]["l2_relative"], rel=5e-3)
+    assert e_c == pytest.approx(published["cubic_blocked"]["l2_relative"], rel=5e-3)
+    assert e_s <= 1.5 * published["strassen"]["l2_relative"]
+
+
+# ---------------------------------------------------------------------------
+# Epilogues
+# ---------------------------------------------------------------------------
+
+def test_swiglu_epilogue():
+    _, a, b = _gaussian(318, 512, 1024, 2048)
+    bm, bn, bk = 256, 512, 512
+    laid = o.swiglu_weight_layout(b, bn)
+    laid_dev = smx.swiglu_weight_layout(dev_weight(b), bn)
+    assert np.array_equal(host(laid_dev), laid)
+    for fn, ofn in ((smx.strassen_matmul, o.strassen_matmul), (smx.cubic_matmul, o.cubic_blocked_matmul)):
+        got = host(fn(dev(a), laid_dev, bm=bm, bn=bn, bk=bk, epilogue="swiglu"))
+        assert got.shape == (512, 1024)
+        assert_ulp_close(got, ofn(a, laid, bm=bm, bn=bn, bk=bk, epilogue="swiglu"), k=1024)
+    # product-aware flag is accepted and selects the same kernel
+    got = host(smx.strassen_matmul(dev(a), laid_dev, bm=bm, bn=bn, bk=bk, epilogue="swiglu",
+                                   interleave_products=True, product_aware_swiglu=True))
+    assert_ulp_close(got, o.strassen_matmul(a, laid, bm=bm, bn=bn, bk=bk, epilogue="swiglu",
+                                            interleave_products=True, product_aware_swiglu=True), k=1024)
+
+
+def test_residual_add_epilogue():
+    rng, a, b = _gaussian(319, 512, 2048, 1024)
+    r = o.bf16_round(rng.standard_normal((512, 1024)).astype(np.float32))
+    for fn, ofn in ((smx.strassen_matmul, o.strassen_matmul), (smx.cubic_matmul, o.cubic_blocked_matmul)):
+        got = host(fn(dev(a), dev_weight(b), bm=256, bn=512, bk=512, epilogue="residual_add", residual=dev(r)))
+        assert_ulp_close(got, ofn(a, b, bm=256, bn=512, bk=512, epilogue="residual_add", residual=r), k=2048)
+
+
+@pytest.mark.parametrize("bias_dtype", [torch.bfloat16, torch.float32])
+def test_bias_add_epilogue(bias_dtype):
+    rng, a, b = _gaussian(321, 256, 1024, 1024)
+    bias = rng.standard_normal(1024).astype(np.float32)
+    if bias_dtype == torch.bfloat16:
+        bias = o.bf16_round(bias)
+    bias_dev = torch.from_numpy(bias).to(DEV).to(bias_dtype)
+    got = host(smx.strassen_matmul(dev(a), dev_weight(b), bm=256, bn=256, bk=512,
+                                   epilogue="bias_add", bias=bias_dev))
+    assert_ulp_close(got, o.strassen_matmul(a, b, bm=256, bn=256, bk=512, epilogue="bias_add", bias=bias), k=1024)
+
+
+def _qk_problem(seed, batch, seq, heads, k, bn, hd=128):
+    rng = np.random.default_rng(seed)
+    tokens, n = batch * seq, heads * hd
+    x = o.bf16_round(rng.standard_normal((tokens, k)).astype(np.float32))
+    w = o.bf16_round(rng.standard_normal((k, n)).astype(np.float32) * np.float32(0.02))
+    gamma = o.bf16_round((1.0 + 0.1 * rng.standard_normal(hd)).astype(np.float32))
+    cos, sin = o.rope_values(seq, hd, 1e6)
+    laid = o.rope_weight_layout(w, bn, hd)
+    tcos, tsin = o.rope_layout_tables(np.tile(cos, (batch, 1)), np.tile(sin, (batch, 1)), bn // 2, hd)
+    scale = o.rope_scale_layout(gamma, bn, hd)
+    return x, w, laid, tcos, tsin, scale
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.bfloat16, torch.float32])
+def test_qk_norm_rope_epilogue(scale_dtype):
+    batch, seq, heads, k, bn = 2, 256, 8, 1024, 512
+    x, w, laid, tcos, tsin, scale = _qk_problem(11, batch, seq, heads, k, bn)
+    kw = dict(bm=256, bn=bn, bk=512, epilogue="qk_norm_rope", rope_head_dim=128, rope_eps=1e-6)
+    laid_dev = smx.rope_weight_layout(dev_weight(w), bn)
+    assert np.array_equal(host(laid_dev), laid)
+    for fn, ofn in ((smx.strassen_matmul, o.strassen_matmul), (smx.cubic_matmul, o.cubic_blocked_matmul)):
+        got = host(fn(dev(x), laid_dev, rope_cos=dev(tcos), rope_sin=dev(tsin),
+                      rope_scale=torch.from_numpy(scale).to(DEV).to(scale_dtype), **kw))
+        want = ofn(x, laid, rope_cos=tcos, rope_sin=tsin, rope_scale=scale, **kw)
+        assert_ulp_close(got, want, k=k)
+
+
+# ---------------------------------------------------------------------------
+# Full Qwen3-32B shapes (8 x 1024 tokens)
+# ---------------------------------------------------------------------------
+
+QWEN_SHAPES = {
+    "gate_up": (8192, 5120, 25600),
+    "down": (8192, 25600, 5120),
+    "o": (8192, 8192, 5120),
+}
+
+
+@pytest.mark.parametrize("site", sorted(QWEN_SHAPES))
+def test_qwen3_32b_shapes_sampled_tiles(site):
+    m, k, n = QWEN_SHAPES[site]
+    bm, bn, bk = 1024, 1024, 512
+    gen = torch.Generator(device=DEV).manual_seed(7)
+    a = torch.randn(m, k, device=DEV, generator=gen).to(torch.bfloat16)
+    w = (torch.randn(n, k, device=DEV, generator=gen) * 0.02).to(torch.bfloat16)
+    b = w.t()  # [K, N], K-contiguous
+    say(f"  {site} m={m} k={k} n={n}")
+    got = smx.strassen_matmul(a, b, bm=bm, bn=bn, bk=bk, interleave_products=True)
+    cub = smx.cubic_matmul(a, b, bm=bm, bn=bn, bk=bk)
+    torch.cuda.synchronize()
+    # Whole-output bound against an FP32 product computed on the GPU.
+    ref = torch.matmul(a.float(), b.float())
+    e_s = float(torch.linalg.norm(got.float() - ref) / torch.linalg.norm(ref))
+    e_c = float(torch.linalg.norm(cub.float() - ref) / torch.linalg.norm(ref))
+    say(f"  whole-output rel err strassen={e_s:.4e} cubic={e_c:.4e}")
+    assert e_s <= 1e-2 and e_c <= 1e-2 and e_c < e_s
+    # Sampled tiles recomputed by the oracle from their own rows / columns.
+    rng = np.random.default_rng(1)
+    a_h, b_h = host(a), host(b)
+    for _ in range(2):
+        i = int(rng.integers(m // bm))
+        j = int(rng.integers(n // bn))
+        rows, cols = slice(i * bm, (i + 1) * bm), slice(j * bn, (j + 1) * bn)
+        want = o.strassen_matmul(a_h[rows], b_h[:, cols], bm=bm, bn=bn, bk=bk, interleave_products=True)
+        assert_ulp_close(host(got[rows, cols]), want, k=k)
+        ref_tile = o.high_precision_reference(a_h[rows], b_h[:, cols]).astype(np.float64)
+        assert rel_l2(host(got[rows, cols]), ref_tile) <= 1.5 * rel_l2(want, ref_tile)
+        want_c = o.cubic_blocked_matmul(a_h[rows], b_h[:, cols], bm=bm, bn=bn, bk=bk)
+        assert_ulp_close(host(cub[rows, cols]), want_c, k=k)

@@ -1,0 +1,313 @@
+"""Pins for the CPU oracle (oracle/strassen_ref.py).
+
+Each check is chosen so that a plausible mistake in the oracle fails it:
+bf16 rounding against torch's conversion; Strassen/cubic algebra against
+exact-integer products (reference technique,
+Strassen_MM_Focus/tests/test_kernels_v001.py:59-80); operand-sum and output
+rounding against the reference's published accuracy-gate errors on
+regenerated inputs (archive/initial-snapshot/evidence/strassen_cubic_control.jsonl:7);
+epilogues against closed forms and the unfused Qwen3 semantics.
+"""
+
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as o
+from oracle import strassen_ref as ref
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+# ---------------------------------------------------------------------------
+# bf16 rounding
+# ---------------------------------------------------------------------------
+
+def test_bf16_round_matches_torch_conversion():
+    rng = np.random.default_rng(5)
+    x = np.concatenate([
+        rng.standard_normal(100000).astype(np.float32) * np.float32(10.0) ** rng.integers(-30, 30, 100000).astype(np.float32),
+        np.array([0.0, -0.0, 1.0, -1.0, np.inf, -np.inf, 3.3895314e38, -3.3895314e38, 1e-40, -1e-40], np.float32),
+    ])
+    # exact ties: bf16 value + half ulp, both parities of the kept mantissa
+    base = o.bf16_round(rng.standard_normal(1000).astype(np.float32))
+    ties = (base.view(np.uint32) | np.uint32(0x8000)).view(np.float32)
+    x = np.concatenate([x, ties]).astype(np.float32)
+    expected = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    got = o.bf16_bits(x)
+    assert np.array_equal(got, expected)
+
+
+def test_bf16_round_ties_to_even_closed_form():
+    # 1 + 2^-8 is exactly halfway between 1 and 1 + 2^-7: ties to even -> 1.
+    assert o.bf16_round(np.float32(1.0 + 2.0 ** -8)) == np.float32(1.0)
+    # 1 + 3*2^-8 is halfway between 1+2^-7 (odd) and 1+2^-6 (even) -> 1+2^-6.
+    assert o.bf16_round(np.float32(1.0 + 3 * 2.0 ** -8)) == np.float32(1.0 + 2.0 ** -6)
+    assert np.isnan(o.bf16_round(np.float32(np.nan)))
+
+
+# ---------------------------------------------------------------------------
+# Algebra: exact-integer known answers
+# ---------------------------------------------------------------------------
+
+KAT_CASES = [
+    # (m, k, n), (bm, bn, bk): several row/column tiles and K panels
+    ((16, 256, 256), (16, 256, 256)),
+    ((64, 1024, 512), (32, 256, 256)),
+    ((48, 768, 768), (16, 256, 256)),
+]
+
+
+@pytest.mark.parametrize("shape,tile", KAT_CASES)
+@pytest.mark.parametrize("interleave", [False, True])
+def test_strassen_exact_integer_kat(shape, tile, interleave):
+    rng = np.random.default_rng(187)
+    m, k, n = shape
+    bm, bn, bk = tile
+    a = rng.integers(-2, 3, (m, k)).astype(np.float32)
+    b = rng.integers(-2, 3, (k, n)).astype(np.float32)
+    got = o.strassen_matmul(a, b, bm=bm, bn=bn, bk=bk, interleave_products=interleave,
+                            output_dtype="float32")
+    assert np.array_equal(got, a @ b)
+    got16 = o.strassen_matmul(a, b, bm=bm, bn=bn, bk=bk, interleave_products=interleave)
+    assert np.array_equal(got16, o.bf16_round(a @ b))
+
+
+@pytest.mark.parametrize("shape,tile", KAT_CASES)
+def test_cubic_exact_integer_kat(shape, tile):
+    rng = np.random.default_rng(188)
+    m, k, n = shape
+    a = rng.integers(-2, 3, (m, k)).astype(np.float32)
+    b = rng.integers(-2, 3, (k, n)).astype(np.float32)
+    got = o.cubic_blocked_matmul(a, b, bm=tile[0], bn=tile[1], bk=tile[2], output_dtype="float32")
+    assert np.array_equal(got, a @ b)
+
+
+def test_kat_detects_planted_sign_error(monkeypatch):
+    """A wrong sign in one operand sum must fail the integer KAT."""
+    original = ref.strassen_products
+
+    def broken(a_q, b_q):
+        products = original(a_q, b_q)
+        s, t = products[6]
+        a0, a1, a2, a3 = a_q
+        products[6] = (o.bf16_round(a2 + a0), t)  # should be A2 - A0
+        return products
+
+    monkeypatch.setattr(ref, "strassen_products", broken)
+    rng = np.random.default_rng(187)
+    a = rng.integers(-2, 3, (16, 256)).astype(np.float32)
+    b = rng.integers(-2, 3, (256, 256)).astype(np.float32)
+    got = o.strassen_matmul(a, b, bm=16, bn=256, bk=256, output_dtype="float32")
+    assert not np.array_equal(got, a @ b)
+
+
+def test_kat_detects_planted_quadrant_swap(monkeypatch):
+    """Routing a product to the wrong quadrant must fail the integer KAT."""
+    table = dict(ref.PRODUCT_UPDATES)
+    table[3] = ((2, +1), (3, +1))  # P3 belongs to C1 and C3
+    monkeypatch.setattr(ref, "PRODUCT_UPDATES", table)
+    rng = np.random.default_rng(187)
+    a = rng.integers(-2, 3, (16, 256)).astype(np.float32)
+    b = rng.integers(-2, 3, (256, 256)).astype(np.float32)
+    got = o.strassen_matmul(a, b, bm=16, bn=256, bk=256, output_dtype="float32")
+    assert not np.array_equal(got, a @ b)
+
+
+def test_bounded_nonzero_rounding_error():
+    """Reference ``test_kernels_v001.py:82-96``: Gaussian bf16 operands give a
+    Strassen error that is nonzero (operand sums are rounded) and < 0.02."""
+    rng = np.random.default_rng(23)
+    a = o.bf16_round(rng.normal(size=(16, 256)).astype(np.float32))
+    b = o.bf16_round(rng.normal(size=(256, 256)).astype(np.float32))
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    got = o.strassen_matmul(a, b, bm=16, bn=256, bk=256, output_dtype="float32").astype(np.float64)
+    rel = np.linalg.norm(got - exact) / np.linalg.norm(exact)
+    assert 0.0 < rel < 0.02
+    cubic = o.cubic_blocked_matmul(a, b, bm=16, bn=256, bk=256, output_dtype="float32").astype(np.float64)
+    assert np.linalg.norm(cubic - exact) / np.linalg.norm(exact) < 1e-6 < rel
+
+
+# ---------------------------------------------------------------------------
+# Rounding: the reference's published accuracy gate on regenerated inputs
+# ---------------------------------------------------------------------------
+
+@pytest.fixture(scope="module")
+def accuracy_gate_inputs():
+    spec = json.load(open(os.path.join(GOLDEN, "accuracy_gate_reference.json")))
+    a, b = o.host_uniform_inputs(tuple(spec["shape_mkn"]), spec["seed"])
+    return spec, a, b, o.high_precision_reference(a, b)
+
+
+@pytest.mark.slow
+def test_oracle_reproduces_published_accuracy_gate(accuracy_gate_inputs):
+    spec, a, b, reference = accuracy_gate_inputs
+    bm, bn, bk = spec["tile_bm_bn_bk"]
+    published = spec["errors_vs_reference"]
+    strassen = o.device_error(o.strassen_matmul(a, b, bm=bm, bn=bn, bk=bk), reference)
+    cubic = o.device_error(o.cubic_blocked_matmul(a, b, bm=bm, bn=bn, bk=bk), reference)
+    native = o.device_error(o.native_matmul(a, b), reference)
+    # Same inputs, same operand roundings: only FP32 dot accumulation order
+    # differs from the TPU, so the metrics agree to ~5 significant digits.
+    for got, want in ((strassen, published["strassen"]), (cubic, published["cubic_blocked"]),
+                      (native, published["native"])):
+        assert got["l2_relative"] == pytest.approx(want["l2_relative"], rel=2e-4)
+        assert got["rmse"] == pytest.approx(want["rmse"], rel=2e-4)
+        assert got["maxnorm_relative"] == pytest.approx(want["maxnorm_relative"], rel=2e-3)
+
+
+@pytest.mark.slow
+def test_accuracy_gate_detects_planted_unrounded_sums(accuracy_gate_inputs, monkeypatch):
+    """Dropping the bf16 rounding of the operand sums (a plausible mistake)
+    moves the Strassen error far from the published value."""
+    spec, a, b, reference = accuracy_gate_inputs
+    monkeypatch.setattr(ref, "bf16_round", lambda x: np.asarray(x, np.float32))
+    m, k, n = spec["shape_mkn"]
+    a_small, b_small, r_small = a[:256], b[:, :256], reference[:256, :256]
+    got = ref.strassen_matmul(a_small, b_small, bm=256, bn=256, bk=512, output_dtype="float32")
+    err = o.device_error(got, r_small)["l2_relative"]
+    assert err < 0.5 * spec["errors_vs_reference"]["strassen"]["l2_relative"]
+
+
+# ---------------------------------------------------------------------------
+# Epilogues
+# ---------------------------------------------------------------------------
+
+def _int_problem(seed, m, k, n, lo=-1, hi=2):
+    rng = np.random.default_rng(seed)
+    a = rng.integers(lo, hi, (m, k)).astype(np.float32)
+    b = rng.integers(lo, hi, (k, n)).astype(np.float32)
+    return rng, a, b
+
+
+def test_residual_add_closed_form():
+    rng, a, b = _int_problem(319, 32, 512, 512)
+    r = rng.integers(-3, 4, (32, 512)).astype(np.float32)
+    for pa in (False, True):
+        got = o.strassen_matmul(a, b, bm=16, bn=256, bk=256, interleave_products=True,
+                                epilogue="residual_add", residual=r, product_aware_residual=pa)
+        assert np.array_equal(got, o.bf16_round(a @ b + r))
+
+
+def test_bias_add_closed_form():
+    rng, a, b = _int_problem(321, 32, 512, 512)
+    bias = rng.integers(-3, 4, (512,)).astype(np.float32)
+    got = o.strassen_matmul(a, b, bm=16, bn=256, bk=256, epilogue="bias_add", bias=bias)
+    assert np.array_equal(got, o.bf16_round(a @ b + bias[None, :]))
+
+
+def test_swiglu_closed_form_with_layout():
+    """silu(gate) * up of the un-laid-out projection equals the fused
+    epilogue on the laid-out weight (within one bf16 rounding of float32
+    silu, evaluated here in float64)."""
+    rng, a, b = _int_problem(318, 32, 512, 1024)
+    bn = 256
+    laid = o.swiglu_weight_layout(b, bn)
+    exact = (a @ b).astype(np.float64)
+    gate, up = np.split(exact, 2, axis=1)
+    expected = gate / (1.0 + np.exp(-gate)) * up
+    for pa in (False, True):
+        got = o.strassen_matmul(a, laid, bm=16, bn=bn, bk=256, interleave_products=True,
+                                epilogue="swiglu", product_aware_swiglu=pa)
+        assert got.shape == (32, 512)
+        np.testing.assert_allclose(got, expected, rtol=2 ** -7, atol=1e-6)
+
+
+def test_product_aware_residual_bitwise_identical_to_interleaved():
+    """strassen_pallas.py:640-643: same FP32 order, bitwise identical."""
+    rng = np.random.default_rng(7)
+    a = o.bf16_round(rng.standard_normal((64, 1024)).astype(np.float32))
+    b = o.bf16_round(rng.standard_normal((1024, 512)).astype(np.float32) * np.float32(0.02))
+    r = o.bf16_round(rng.standard_normal((64, 512)).astype(np.float32))
+    std = o.strassen_matmul(a, b, bm=32, bn=256, bk=256, interleave_products=True,
+                            epilogue="residual_add", residual=r)
+    pa = o.strassen_matmul(a, b, bm=32, bn=256, bk=256, interleave_products=True,
+                           epilogue="residual_add", residual=r, product_aware_residual=True)
+    assert np.array_equal(std, pa)
+
+
+def test_product_aware_swiglu_within_reference_gate():
+    """benchmark_qwen3_32b_product_aware_inference.py:149-151: product-aware
+    l2 <= standard fused l2 + 1e-3 against the unfused FP32 result."""
+    rng = np.random.default_rng(20260904)
+    a = o.bf16_round(rng.standard_normal((64, 1024)).astype(np.float32))
+    b = o.bf16_round(rng.standard_normal((1024, 1024)).astype(np.float32) * np.float32(0.02))
+    laid = o.swiglu_weight_layout(b, 256)
+    exact = (a.astype(np.float64) @ b.astype(np.float64))
+    gate, up = np.split(exact, 2, axis=1)
+    expected = gate / (1.0 + np.exp(-gate)) * up
+    std = o.strassen_matmul(a, laid, bm=32, bn=256, bk=256, interleave_products=True, epilogue="swiglu")
+    pa = o.strassen_matmul(a, laid, bm=32, bn=256, bk=256, interleave_products=True, epilogue="swiglu",
+                           product_aware_swiglu=True)
+    e_std = o.device_error(std, expected)["l2_relative"]
+    e_pa = o.device_error(pa, expected)["l2_relative"]
+    assert e_pa <= e_std + 1e-3
+    assert e_std < 2e-2
+
+
+def test_qk_norm_rope_matches_unfused_semantics():
+    """Fused per-head RMSNorm+RoPE on the rope layout equals the reference's
+    unfused path (projection -> rms_norm per head -> apply_rope,
+    benchmark_qwen3_32b_layer.py:270-284, 354-366) after rope_layout_to_heads,
+    up to the bf16 roundings the unfused path adds."""
+    rng = np.random.default_rng(11)
+    batch, seq, heads, hd = 2, 16, 4, 128
+    tokens, n, k, bn = batch * seq, heads * hd, 512, 256
+    x = o.bf16_round(rng.standard_normal((tokens, k)).astype(np.float32))
+    w = o.bf16_round(rng.standard_normal((k, n)).astype(np.float32) * np.float32(0.05))
+    gamma = o.bf16_round((1.0 + 0.1 * rng.standard_normal(hd)).astype(np.float32))
+    cos, sin = o.rope_values(seq, hd, 1e6)
+    laid = o.rope_weight_layout(w, bn, hd)
+    tcos, tsin = o.rope_layout_tables(np.tile(cos, (batch, 1)), np.tile(sin, (batch, 1)), bn // 2, hd)
+    scale = o.rope_scale_layout(gamma, bn, hd)
+    fused = o.strassen_matmul(x, laid, bm=16, bn=bn, bk=256, epilogue="qk_norm_rope",
+                              rope_cos=tcos, rope_sin=tsin, rope_scale=scale,
+                              rope_head_dim=hd, rope_eps=1e-6)
+    fused_heads = o.rope_layout_to_heads(fused, heads, bn, batch, seq, hd)
+    # Unfused: the same Strassen projection in natural order, then the model ops.
+    proj = o.strassen_matmul(x, w, bm=16, bn=bn, bk=256).reshape(batch, seq, heads, hd)
+    unfused = o.apply_rope(o.rms_norm(proj, gamma), cos, sin)
+    err = o.device_error(fused_heads, unfused)
+    assert err["l2_relative"] < 1e-2
+    # With no intermediate roundings the two paths differ by a few bf16 ulps.
+    assert err["maxnorm_relative"] < 3e-2
+
+
+# ---------------------------------------------------------------------------
+# Relayouts: brute force and round trips
+# ---------------------------------------------------------------------------
+
+def test_swiglu_layout_brute_force():
+    two_i, bn = 24, 8
+    order = o.swiglu_weight_layout_order(two_i, bn)
+    half, inter = bn // 2, two_i // 2
+    for pos, src in enumerate(order):
+        block, within = divmod(pos, bn)
+        if within < half:
+            assert src == block * half + within
+        else:
+            assert src == inter + block * half + within - half
+    assert sorted(order) == list(range(two_i))
+
+
+def test_rope_layout_round_trip_restores_heads():
+    batch, seq, heads, hd, bn = 2, 3, 8, 16, 64
+    tokens = batch * seq
+    natural = np.arange(tokens * heads * hd, dtype=np.float32).reshape(tokens, heads * hd)
+    laid = o.rope_weight_layout(natural, bn, hd)  # permute columns like a weight
+    back = o.rope_layout_to_heads(laid, heads, bn, batch, seq, hd)
+    assert np.array_equal(back, natural.reshape(batch, seq, heads, hd))
+
+
+def test_rope_tables_and_scale_layout():
+    cos = np.arange(5 * 16, dtype=np.float32).reshape(5, 16)
+    sin = -cos
+    tc, ts = o.rope_layout_tables(cos, sin, 32, 16)
+    assert tc.shape == (5, 32) and np.array_equal(tc[:, 8:16], cos[:, :8])
+    assert np.array_equal(ts, -tc)
+    gamma = np.arange(16, dtype=np.float32)
+    s = o.rope_scale_layout(gamma, 64, 16)
+    assert np.array_equal(s, np.concatenate([np.tile(gamma[:8], 4), np.tile(gamma[8:], 4)]))

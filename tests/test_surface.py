@@ -1,0 +1,119 @@
+"""Host-side behaviour of the drop-in surface: the reference's argument
+checks (strassen_pallas.py:927-1047) raise the same exception types and
+messages, and unsupported research options fail loudly. No GPU is used: every
+case is rejected before a launch."""
+
+import pytest
+import torch
+
+import strassen_tpu_amd as smx
+
+
+def t(*shape, dtype=torch.bfloat16):
+    return torch.zeros(*shape, dtype=dtype)
+
+
+@pytest.mark.parametrize("kwargs,args,exc,match", [
+    ({}, (t(4), t(4, 4)), ValueError, "two rank-2 matrices"),
+    ({}, (t(256, 512), t(256, 256)), ValueError, "inner dimensions disagree: 512 vs 256"),
+    ({}, (t(256, 512), t(512, 256, dtype=torch.float32)), ValueError, "input dtypes disagree"),
+    ({}, (t(256, 512, dtype=torch.float16), t(512, 256, dtype=torch.float16)), ValueError, "BF16 or FP32"),
+    ({"block_permutation": 9}, None, ValueError, "block_permutation must be"),
+    ({"formula_variant": "fancy"}, None, ValueError, "formula_variant must be"),
+    ({"epilogue": "gelu"}, None, ValueError, "unknown epilogue"),
+    ({"epilogue": "swiglu", "formula_variant": "powers"}, None, ValueError, "quadrant-basis formula"),
+    ({"epilogue": "swiglu", "output_dtype": torch.float32}, None, ValueError, "BF16 output tile"),
+    ({"epilogue": "residual_add"}, None, ValueError, "requires residual="),
+    ({"epilogue": "bias_add"}, None, ValueError, "requires bias="),
+    ({"residual": t(256, 256)}, None, ValueError, "residual= is only used"),
+    ({"bias": t(256)}, None, ValueError, "bias= is only used"),
+    ({"epilogue": "qk_norm_rope"}, None, ValueError, "requires rope_cos="),
+    ({"epilogue": "qk_norm_rope", "bn": 128, "rope_cos": t(256, 64), "rope_sin": t(256, 64),
+      "rope_scale": t(128)}, None, ValueError, "multiple of 2\\*head_dim"),
+    ({"epilogue": "qk_norm_rope", "rope_cos": t(256, 64), "rope_sin": t(256, 64),
+      "rope_scale": t(256)}, None, ValueError, "rope tables must be"),
+    ({"epilogue": "qk_norm_rope", "rope_cos": t(256, 128), "rope_sin": t(256, 128),
+      "rope_scale": t(128)}, None, ValueError, "rope_scale must be laid out"),
+    ({"rope_cos": t(256, 128)}, None, ValueError, "rope_\\* are only used"),
+    ({"product_aware_swiglu": True}, None, ValueError, "product_aware_swiglu is only valid"),
+    ({"product_aware_residual": True}, None, ValueError, "product_aware_residual is only valid"),
+    ({"epilogue": "bias_add", "bias": t(128)}, None, ValueError, "bias shape"),
+    ({"allow_input_fusion": (True,)}, None, ValueError, "one boolean per operand"),
+    ({"allow_input_fusion": (1, 0)}, None, TypeError, "must be bool"),
+    ({"classical_panels": (0,), "panel_schedule": [0]}, None, ValueError, "not both"),
+    ({"classical_panels": (5,)}, None, ValueError, "outside 0..0"),
+    ({"bm": 96}, None, ValueError, "M=256 is not divisible by 96"),
+    ({"bm": 8, "bn": 128, "bk": 128}, (t(256, 512), t(512, 256)), ValueError, "TPU v5e alignment"),
+    ({"output_dtype": torch.float16}, None, ValueError, "output_dtype must be"),
+])
+def test_reference_argument_errors(kwargs, args, exc, match):
+    a, b = args if args is not None else (t(256, 512), t(512, 256))
+    base = {"bm": 256, "bn": 256, "bk": 512}
+    base.update(kwargs)
+    with pytest.raises(exc, match=match):
+        smx.strassen_matmul(a, b, **base)
+
+
+@pytest.mark.parametrize("kwargs", [
+    {"formula_variant": "dual"},
+    {"formula_variant": "powers"},
+    {"block_permutation": 3},
+    {"classical_panels": (0,)},
+    {"panel_schedule": [0]},
+    {"epilogue": "geglu"},
+    {"output_dtype": torch.float32},
+    {"interpret": True},
+])
+def test_unported_options_raise_not_implemented(kwargs):
+    a, b = t(256, 512), t(512, 256)
+    with pytest.raises(NotImplementedError):
+        smx.strassen_matmul(a, b, bm=256, bn=256, bk=512, **kwargs)
+
+
+def test_fp32_inputs_not_implemented():
+    a, b = t(256, 512, dtype=torch.float32), t(512, 256, dtype=torch.float32)
+    with pytest.raises(NotImplementedError):
+        smx.strassen_matmul(a, b, bm=256, bn=256, bk=512)
+
+
+def test_gfx950_tile_rule_and_device_check():
+    a, b = t(256, 512), t(512, 256)
+    with pytest.raises(ValueError, match="gfx950 kernel tiling"):
+        smx.strassen_matmul(a, b, bm=16, bn=256, bk=256)
+    with pytest.raises(ValueError, match="HIP device"):
+        smx.strassen_matmul(a, b, bm=256, bn=256, bk=512)
+    with pytest.raises(ValueError, match="HIP device"):
+        smx.cubic_matmul(a, b, bm=256, bn=256, bk=512)
+
+
+def test_cubic_surface_checks():
+    a, b = t(256, 512), t(512, 256)
+    with pytest.raises(ValueError, match="unknown cubic variant"):
+        smx.cubic_matmul(a, b, variant="sparse")
+    with pytest.raises(ValueError, match="not divisible"):
+        smx.cubic_matmul(a, b, bm=96, bn=256, bk=512)
+
+
+def test_torch_relayouts_match_oracle():
+    import numpy as np
+
+    import oracle as o
+
+    w = torch.arange(64 * 1024, dtype=torch.float32).reshape(64, 1024)
+    assert np.array_equal(smx.swiglu_weight_layout(w, 256).numpy(), o.swiglu_weight_layout(w.numpy(), 256))
+    assert np.array_equal(smx.rope_weight_layout(w, 256).numpy(), o.rope_weight_layout(w.numpy(), 256))
+    # K-contiguous weights keep their layout through the permutation.
+    wk = w.t().contiguous().t()
+    laid = smx.swiglu_weight_layout(wk, 256)
+    assert smx.is_k_contiguous(laid)
+    assert torch.equal(laid, smx.swiglu_weight_layout(w, 256))
+    cos = torch.randn(32, 128)
+    sin = torch.randn(32, 128)
+    tc, ts = smx.rope_layout_tables(cos, sin, 128)
+    oc, os_ = o.rope_layout_tables(cos.numpy(), sin.numpy(), 128)
+    assert np.array_equal(tc.numpy(), oc) and np.array_equal(ts.numpy(), os_)
+    g = torch.randn(128)
+    assert np.array_equal(smx.rope_scale_layout(g, 256).numpy(), o.rope_scale_layout(g.numpy(), 256))
+    flat = torch.randn(2 * 4 * 1024).reshape(8, 1024)
+    assert np.array_equal(smx.rope_layout_to_heads(flat, 8, 256, 2, 4).numpy(),
+                          o.rope_layout_to_heads(flat.numpy(), 8, 256, 2, 4))
