@@ -99,32 +99,40 @@ def make_block(torch, dev, seed=0):
     d["tcos"], d["tsin"] = tcos, tsin
     d["scale_q"] = smx.rope_scale_layout(gamma_q, bn, HEAD_DIM)
     d["scale_k"] = smx.rope_scale_layout(gamma_k, bn, HEAD_DIM)
+    # Pre-summed Strassen weights (offline, like the relayouts above).
+    for name in ("wq_laid", "wk_laid", "wv", "wo", "wgu_laid", "wd"):
+        d[name + "_sw"] = smx.strassen_weight_layout(d[name], bn, bk)
+    d["wup"] = d["wgu"][:, :FFN]
+    d["wup_sw"] = smx.strassen_weight_layout(d["wup"], bn, bk)
     return d
 
 
 def fused_sites(torch, d, algo):
-    """Callables for the fused Strassen or cubic arm, keyed by site."""
+    """Callables for a fused arm, keyed by site. algo: "strassen" (pre-summed
+    weights), "strassen_plain" (plain weights, both operand sums formed in
+    the kernel) or "cubic" (matched control)."""
     import strassen_tpu_amd as smx
 
     bm, bn, bk = TILE
-    fn = smx.strassen_matmul if algo == "strassen" else smx.cubic_matmul
+    fn = smx.cubic_matmul if algo == "cubic" else smx.strassen_matmul
+    sw = "_sw" if algo == "strassen" else ""
     kw = dict(bm=bm, bn=bn, bk=bk)
-    if algo == "strassen":
+    if algo != "cubic":
         kw["interleave_products"] = True
     qk = dict(epilogue="qk_norm_rope", rope_cos=d["tcos"], rope_sin=d["tsin"], rope_head_dim=HEAD_DIM,
               rope_eps=EPS)
     out = {}
-    out["q"] = lambda: fn(d["x"], d["wq_laid"], rope_scale=d["scale_q"], **qk, **kw)
-    out["k"] = lambda: fn(d["x"], d["wk_laid"], rope_scale=d["scale_k"], **qk, **kw)
-    out["v"] = lambda: fn(d["x"], d["wv"], **kw)
-    out["o"] = lambda: fn(d["attn"], d["wo"], epilogue="residual_add", residual=d["res1"], **kw)
+    out["q"] = lambda: fn(d["x"], d["wq_laid" + sw], rope_scale=d["scale_q"], **qk, **kw)
+    out["k"] = lambda: fn(d["x"], d["wk_laid" + sw], rope_scale=d["scale_k"], **qk, **kw)
+    out["v"] = lambda: fn(d["x"], d["wv" + sw], **kw)
+    out["o"] = lambda: fn(d["attn"], d["wo" + sw], epilogue="residual_add", residual=d["res1"], **kw)
 
     def gate_up():
-        d["h"] = fn(d["y"], d["wgu_laid"], epilogue="swiglu", **kw)
+        d["h"] = fn(d["y"], d["wgu_laid" + sw], epilogue="swiglu", **kw)
         return d["h"]
 
     out["gate_up"] = gate_up
-    out["down"] = lambda: fn(d["h"], d["wd"], epilogue="residual_add", residual=d["res2"], **kw)
+    out["down"] = lambda: fn(d["h"], d["wd" + sw], epilogue="residual_add", residual=d["res2"], **kw)
     return out
 
 
@@ -162,16 +170,16 @@ def pure_sites(torch, d, algo):
     import strassen_tpu_amd as smx
 
     bm, bn, bk = TILE
-    a_up, w_up = d["y"], d["wgu"][:, :FFN]
+    sw = "_sw" if algo == "strassen" else ""
     if algo == "hipblaslt":
         fn = lambda a, b: torch.matmul(a, b)
     else:
-        base = smx.strassen_matmul if algo == "strassen" else smx.cubic_matmul
+        base = smx.cubic_matmul if algo == "cubic" else smx.strassen_matmul
         fn = lambda a, b: base(a, b, bm=bm, bn=bn, bk=bk)
     return {
-        "gate_up": lambda: fn(a_up, w_up),
-        "down": lambda: fn(d["h_any"], d["wd"]),
-        "o": lambda: fn(d["attn"], d["wo"]),
+        "gate_up": lambda: fn(d["y"], d["wup" + sw]),
+        "down": lambda: fn(d["h_any"], d["wd" + sw]),
+        "o": lambda: fn(d["attn"], d["wo" + sw]),
     }
 
 
@@ -263,7 +271,7 @@ def main():
     block_flops = sum(flops(s) for s in shapes.values())
 
     arms = {"strassen": fused_sites(torch, d, "strassen"), "cubic": fused_sites(torch, d, "cubic"),
-            "hipblaslt": vendor_sites(torch, d)}
+            "hipblaslt": vendor_sites(torch, d), "strassen_plain": fused_sites(torch, d, "strassen_plain")}
     # H for the pure down GEMM (any bf16 activations of the right shape).
     arms["strassen"]["gate_up"]()
     d["h_any"] = d["h"]
@@ -283,14 +291,14 @@ def main():
     log("timing strassen block")
     wall_s, ev_s = time_steps(torch, run_block(arms["strassen"]), args.steps, args.warmup)
     results = {"strassen": statistics.median(ev_s)}
-    for arm in ("cubic", "hipblaslt"):
+    for arm in ("cubic", "hipblaslt", "strassen_plain"):
         log(f"timing {arm} block")
         _, ev = time_steps(torch, run_block(arms[arm]), args.steps, args.warmup)
         results[arm] = statistics.median(ev)
     # Interleaved rounds (rotated arm order) to check the comparison is not
     # an ordering artefact.
-    rounds = {a: [] for a in results}
-    names = list(results)
+    names = ["strassen", "cubic", "hipblaslt"]
+    rounds = {a: [] for a in names}
     for r in range(3):
         order = names[r % 3:] + names[:r % 3]
         for arm in order:
@@ -305,7 +313,7 @@ def main():
             _, ev = time_steps(torch, sites[name], args.steps, 2)
             per_site[arm][name] = statistics.median(ev)
     pure = {}
-    for arm in ("strassen", "cubic", "hipblaslt"):
+    for arm in ("strassen", "strassen_plain", "cubic", "hipblaslt"):
         table = pure_sites(torch, d, arm)
         pure[arm] = {}
         for name, fn in table.items():
@@ -320,7 +328,7 @@ def main():
     roofline = {
         "bound": "mfma", "achieved": round(gu_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
         "frac": round(gu_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
-        "kernel": "gemm_kernel<Cfg<7,...>, SMX_EPI_SWIGLU> (gate|up, M=8192 K=5120 N=51200)",
+        "kernel": "smx::v2::gemm_v2<7, SMX_EPI_SWIGLU> (gate|up, M=8192 K=5120 N=51200, pre-summed weight)",
         "mfma_executed_frac": round(gu_tflops * 7 / 8 / PEAK_BF16_TFLOPS, 4),
         "avg_launch_ms": round(gu_ms, 4),
     }

@@ -19,7 +19,8 @@ __all__ = [
     "swiglu_weight_layout_order", "swiglu_weight_layout",
     "rope_weight_layout_order", "rope_weight_layout", "rope_layout_tables",
     "rope_scale_layout", "rope_layout_to_heads", "rope_values", "rms_norm",
-    "apply_rope", "strassen_products", "PRODUCT_UPDATES",
+    "apply_rope", "strassen_products", "strassen_a_operands", "strassen_b_operands",
+    "strassen_weight_layout", "PRODUCT_UPDATES",
 ]
 
 
@@ -88,28 +89,33 @@ PA_SWIGLU_BOTTOM = (6, 2)                           # ``:633-634``
 PA_RESIDUAL_FINAL = (4, 6, 5, 2, 7, 3, 1)           # ``:679-687``
 
 
-def strassen_products(a_q, b_q):
-    """The seven classical operand pairs, each sum rounded once to bf16.
+def strassen_a_operands(a_q):
+    """The A operands of P1..P7 (``strassen_pallas.py:324-379``): A0+A3,
+    A2+A3, A0, A3, A0+A1, A2-A0, A1-A3, every sum rounded once to bf16.
 
-    ``a_q``/``b_q`` are the four quadrants (bf16 values in float32). Every
-    add/sub is ``(x.astype(cd) + y.astype(cd)).astype(cd)`` with cd=bf16 in
-    the reference (``:324-379``): the exact sum of two bf16 values rounded
-    once to bf16. float32 holds that sum either exactly or within half an
-    ulp of float32, and float32 precision (24 bits) >= 2*8+2, so rounding the
-    float32 sum to bf16 is the correctly rounded bf16 sum.
+    Each add/sub is ``(x.astype(cd) + y.astype(cd)).astype(cd)`` with cd=bf16
+    in the reference: the exact sum of two bf16 values rounded once to bf16.
+    float32 holds that sum exactly or within half a float32 ulp, and float32
+    precision (24 bits) >= 2*8+2, so rounding the float32 sum to bf16 is the
+    correctly rounded bf16 sum.
     """
     a0, a1, a2, a3 = a_q
+    r = bf16_round
+    return (r(a0 + a3), r(a2 + a3), a0, a3, r(a0 + a1), r(a2 - a0), r(a1 - a3))
+
+
+def strassen_b_operands(b_q):
+    """The B operands of P1..P7: B0+B3, B0, B1-B3, B2-B0, B3, B0+B1, B2+B3."""
     b0, b1, b2, b3 = b_q
     r = bf16_round
-    return {
-        1: (r(a0 + a3), r(b0 + b3)),
-        2: (r(a2 + a3), b0),
-        3: (a0, r(b1 - b3)),
-        4: (a3, r(b2 - b0)),
-        5: (r(a0 + a1), b3),
-        6: (r(a2 - a0), r(b0 + b1)),
-        7: (r(a1 - a3), r(b2 + b3)),
-    }
+    return (r(b0 + b3), b0, r(b1 - b3), r(b2 - b0), b3, r(b0 + b1), r(b2 + b3))
+
+
+def strassen_products(a_q, b_q):
+    """The seven classical operand pairs {p: (S_p, T_p)}."""
+    sa = strassen_a_operands(a_q)
+    tb = strassen_b_operands(b_q)
+    return {p: (sa[p - 1], tb[p - 1]) for p in range(1, 8)}
 
 
 def _split_a(a, bm, bk, step):
@@ -166,6 +172,22 @@ def _column_vector_quadrants(v, bn):
     w = v.reshape(n // bn, 2, hn)
     return (np.ascontiguousarray(w[:, 0, :].reshape(n // 2)),
             np.ascontiguousarray(w[:, 1, :].reshape(n // 2)))
+
+
+def strassen_weight_layout(b, bn, bk):
+    """Pre-summed B operands of every (bk, bn) tile as [N/2 * 7, K/2]:
+    row ``p*7 + o`` = operand ``o`` (order of ``strassen_b_operands``) of
+    product-space column ``p`` (tile j, column c < bn/2) over product-space
+    depth (panel s, k < bk/2). The layout of ``smx_strassen_weight_layout``."""
+    b = np.asarray(b, dtype=np.float32)
+    k, n = b.shape
+    hk = bk // 2
+    out = np.empty((n // 2, 7, k // 2), dtype=np.float32)
+    for step in range(k // bk):
+        ops = strassen_b_operands(_split_b(b, bn, bk, step))  # each (hk, N/2)
+        for o, t in enumerate(ops):
+            out[:, o, step * hk:(step + 1) * hk] = t.T
+    return out.reshape(n // 2 * 7, k // 2)
 
 
 def _check_common(a, b, bm, bn, bk):

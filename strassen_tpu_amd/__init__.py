@@ -15,4 +15,6 @@ from .strassen import (  # noqa: F401
     cubic_matmul, native_matmul, strassen_matmul,
 )
 
-__version__ = "0.1.0"
+from .weights import StrassenWeight, strassen_weight_layout  # noqa: F401
+
+__version__ = "0.2.0"

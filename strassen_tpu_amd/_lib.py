@@ -33,10 +33,12 @@ SMX_EPI = {
 }
 
 SMX_B_KCONTIG = 1
+SMX_B_PRESUMMED = 2
+SMX_FLAG_COMPACT_TILE = 1
 SMX_AUX_BIAS_F32 = 1
 SMX_AUX_SCALE_F32 = 2
 
-EXPORTS = ("smx_gemm", "smx_tile_requirements", "smx_last_error", "smx_version")
+EXPORTS = ("smx_gemm", "smx_tile_requirements", "smx_strassen_weight_layout", "smx_last_error", "smx_version")
 
 
 class SmxGemmDesc(ctypes.Structure):
@@ -68,11 +70,14 @@ def load():
     vp = ctypes.c_void_p
     lib.smx_gemm.argtypes = [ctypes.POINTER(SmxGemmDesc), vp, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.smx_gemm.restype = ctypes.c_int
-    lib.smx_tile_requirements.argtypes = [ctypes.c_int32, ctypes.c_int32,
+    lib.smx_tile_requirements.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                           ctypes.POINTER(ctypes.c_int32),
                                           ctypes.POINTER(ctypes.c_int32),
                                           ctypes.POINTER(ctypes.c_int32)]
     lib.smx_tile_requirements.restype = ctypes.c_int
+    i64, i32 = ctypes.c_int64, ctypes.c_int32
+    lib.smx_strassen_weight_layout.argtypes = [i64, i64, vp, i64, i32, i32, vp, i64, vp]
+    lib.smx_strassen_weight_layout.restype = ctypes.c_int
     lib.smx_last_error.argtypes = []
     lib.smx_last_error.restype = ctypes.c_char_p
     lib.smx_version.argtypes = []
@@ -85,10 +90,11 @@ def last_error():
     return load().smx_last_error().decode("utf-8", "replace")
 
 
-def tile_requirements(algo, epilogue):
+def tile_requirements(algo, epilogue, b_layout=SMX_B_KCONTIG, flags=0):
     lib = load()
     tm, tn, tk = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
-    rc = lib.smx_tile_requirements(algo, SMX_EPI[epilogue], ctypes.byref(tm), ctypes.byref(tn), ctypes.byref(tk))
+    rc = lib.smx_tile_requirements(algo, SMX_EPI[epilogue], b_layout, flags,
+                                   ctypes.byref(tm), ctypes.byref(tn), ctypes.byref(tk))
     if rc != SMX_OK:
         raise ValueError(last_error())
     return tm.value, tn.value, tk.value

@@ -8,9 +8,11 @@ this file. hipcc cross-compiles for gfx950 without a GPU.
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
+import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
@@ -42,17 +44,65 @@ def compile_command(output=LIBRARY, extra=()):
     ]
 
 
+# The pre-summed Strassen kernel issues its MFMAs through inline asm (to pin
+# accumulators to AGPRs / VGPRs), so the compiler does not insert the wait
+# states an MFMA result needs before a VALU, VMEM or v_accvgpr read. Such a
+# kernel only reads accumulators after an explicit s_nop drain; any spill,
+# AGPR copy or read the compiler places between the first MFMA and that
+# drain would read a stale value. This check finds every kernel with an
+# inline-asm MFMA and rejects such code.
+_FUNCTION = re.compile(r"^(_Z\w+):", re.M)
+_ASM_MFMA = re.compile(r";;#ASMSTART\s*\n\s*v_mfma")
+_DRAIN = "s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+_FORBIDDEN = re.compile(r"^\s*(scratch_\w+|buffer_store\w*|v_accvgpr_read\w*|v_accvgpr_mov\w*)\b", re.M)
+
+
+def verify_inline_asm_kernels(asm_text):
+    """Raise if a kernel with inline-asm MFMAs touches accumulators before its
+    drain; returns the number of such kernels (at least one is expected)."""
+    checked = 0
+    for m in _FUNCTION.finditer(asm_text):
+        name = m.group(1)
+        end = asm_text.find("s_endpgm", m.end())
+        body = asm_text[m.end():end if end >= 0 else len(asm_text)]
+        if not _ASM_MFMA.search(body):
+            continue
+        checked += 1
+        drain = body.find(_DRAIN)
+        first_mfma = body.find("v_mfma")
+        if drain < 0:
+            raise RuntimeError(f"{name}: inline-asm MFMAs without the drain sequence")
+        # Between the first MFMA and the drain nothing may read, copy or
+        # spill registers (before the first MFMA no accumulator holds an
+        # MFMA result yet).
+        bad = _FORBIDDEN.search(body[first_mfma:drain])
+        if bad:
+            raise RuntimeError(f"{name}: '{bad.group(1)}' before the MFMA drain "
+                               "(accumulators spilled or copied); refusing to build")
+    if not checked:
+        raise RuntimeError("no inline-asm MFMA kernels found in the device assembly")
+    return checked
+
+
 def build(verbose=False):
     """Compile the library; returns its path. Always recompiles."""
     tmp = LIBRARY + ".tmp"
-    cmd = compile_command(tmp)
-    result = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "packed-fp32-ops"
-    stderr = "\n".join(l for l in result.stderr.splitlines() if noise not in l)
-    if result.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + " ".join(cmd) + "\n" + stderr)
-    if verbose and stderr.strip():
-        print(stderr, file=sys.stderr)
+    with tempfile.TemporaryDirectory() as scratch:
+        # --save-temps keeps the device assembly for the inline-asm check.
+        cmd = compile_command(tmp, extra=("-save-temps",))
+        result = subprocess.run(cmd, capture_output=True, text=True, cwd=scratch)
+        noise = "packed-fp32-ops"
+        stderr = "\n".join(l for l in result.stderr.splitlines() if noise not in l)
+        if result.returncode != 0:
+            raise RuntimeError("hipcc failed:\n" + " ".join(cmd) + "\n" + stderr)
+        if verbose and stderr.strip():
+            print(stderr, file=sys.stderr)
+        asm = [f for f in os.listdir(scratch) if f.endswith("gfx950.s")]
+        if len(asm) != 1:
+            raise RuntimeError(f"expected one gfx950 assembly file from -save-temps, found {asm}")
+        checked = verify_inline_asm_kernels(open(os.path.join(scratch, asm[0])).read())
+    if verbose:
+        print(f"verified {checked} inline-asm MFMA kernels", file=sys.stderr)
     os.replace(tmp, LIBRARY)
     return LIBRARY
 

@@ -1,0 +1,326 @@
+// Shared device helpers for the gfx950 Strassen / cubic GEMM kernels:
+// bf16 packing, kernel parameters, workgroup-to-tile mapping and the fused
+// epilogues (strassen_pallas.py:739-879).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/strassen_mi355x.h"
+
+namespace smx {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 256;  // 4 waves of 64
+
+// ---------------------------------------------------------------------------
+// bf16 helpers
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float lo_f32(uint32_t x) { return __uint_as_float(x << 16); }
+__device__ __forceinline__ float hi_f32(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
+
+// Round two floats to bf16 (ties to even) and pack: v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  bf16x2 v;
+  v[0] = (__bf16)lo;
+  v[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t x) { return __uint_as_float(((uint32_t)x) << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float x) {
+  __bf16 v = (__bf16)x;
+  return __builtin_bit_cast(uint16_t, v);
+}
+
+// Eight bf16 values unpacked to float.
+struct F8 {
+  float v[8];
+};
+
+__device__ __forceinline__ F8 unpack8(u32x4 x) {
+  F8 f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f.v[2 * i] = lo_f32(x[i]);
+    f.v[2 * i + 1] = hi_f32(x[i]);
+  }
+  return f;
+}
+
+// bf16(x + y) or bf16(x - y) per element. Two bf16 values sum exactly or
+// within half a float ulp in float, and float keeps >= 2*8+2 bits, so
+// rounding the float sum to bf16 gives the correctly rounded bf16 sum.
+template <bool kSub>
+__device__ __forceinline__ u32x4 sum8(const F8& x, const F8& y) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float s0 = kSub ? x.v[2 * i] - y.v[2 * i] : x.v[2 * i] + y.v[2 * i];
+    float s1 = kSub ? x.v[2 * i + 1] - y.v[2 * i + 1] : x.v[2 * i + 1] + y.v[2 * i + 1];
+    r[i] = pack_bf16(s0, s1);
+  }
+  return r;
+}
+
+// The seven classical A operands of P1..P7 (strassen_pallas.py:324-379) from
+// the four raw A quadrants: A0+A3, A2+A3, A0, A3, A0+A1, A2-A0, A1-A3.
+__device__ __forceinline__ void strassen_a_ops(const u32x4 (&q)[4], u32x4 (&ops)[7]) {
+  const F8 a0 = unpack8(q[0]), a1 = unpack8(q[1]), a2 = unpack8(q[2]), a3 = unpack8(q[3]);
+  ops[0] = sum8<false>(a0, a3);
+  ops[1] = sum8<false>(a2, a3);
+  ops[2] = q[0];
+  ops[3] = q[3];
+  ops[4] = sum8<false>(a0, a1);
+  ops[5] = sum8<true>(a2, a0);
+  ops[6] = sum8<true>(a1, a3);
+}
+
+// The seven classical B operands of P1..P7 from the four raw B quadrants:
+// B0+B3, B0, B1-B3, B2-B0, B3, B0+B1, B2+B3.
+__device__ __forceinline__ void strassen_b_ops(const u32x4 (&q)[4], u32x4 (&ops)[7]) {
+  const F8 b0 = unpack8(q[0]), b1 = unpack8(q[1]), b2 = unpack8(q[2]), b3 = unpack8(q[3]);
+  ops[0] = sum8<false>(b0, b3);
+  ops[1] = q[0];
+  ops[2] = sum8<true>(b1, b3);
+  ops[3] = sum8<true>(b2, b0);
+  ops[4] = q[3];
+  ops[5] = sum8<false>(b0, b1);
+  ops[6] = sum8<false>(b2, b3);
+}
+
+// ---------------------------------------------------------------------------
+// Parameters and tile mapping
+// ---------------------------------------------------------------------------
+
+struct Params {
+  const uint16_t* a;
+  const uint16_t* b;  // B^T [N, K] (plain) or the pre-summed operands [N/2*7, K/2]
+  uint16_t* c;
+  const uint16_t* residual;
+  const void* bias;
+  const uint16_t* rope_cos;
+  const uint16_t* rope_sin;
+  const void* rope_scale;
+  int64_t m, n, k;
+  int64_t lda, ldb, ldc, ldr;
+  int32_t bm, bn, bk;
+  int32_t bias_f32, scale_f32;
+  int32_t head_dim;
+  float eps;
+  int32_t tiles_m, tiles_n;  // product-space workgroup grid
+};
+
+// Workgroup id -> product-space tile. Workgroups are dispatched round-robin
+// over the 8 XCDs; consecutive logical tiles are gathered on one XCD so that
+// neighbouring tiles share its L2, and inside an XCD tiles walk column groups
+// of kGroupM rows (an A row panel is reused across the group's columns).
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  int logical = bid;
+  if (total % 8 == 0) {
+    const int per_xcd = total / 8;
+    logical = (bid % 8) * per_xcd + bid / 8;
+  }
+  constexpr int kGroupM = 8;
+  const int group_size = kGroupM * tiles_n;
+  const int group = logical / group_size;
+  const int first_m = group * kGroupM;
+  const int rows_in_group = min(tiles_m - first_m, kGroupM);
+  const int in_group = logical - group * group_size;
+  tm = first_m + in_group % rows_in_group;
+  tn = in_group / rows_in_group;
+}
+
+// Physical origin of a product-space workgroup tile (prow0, pcol0).
+struct TileOrigin {
+  int64_t ti, tr;  // row tile index and row inside the half
+  int64_t tj, tc;  // column tile index and column inside the half
+};
+
+__device__ __forceinline__ TileOrigin tile_origin(const Params& p, int64_t prow0, int64_t pcol0) {
+  const int hm = p.bm / 2, hn = p.bn / 2;
+  TileOrigin o;
+  o.ti = prow0 / hm;
+  o.tr = prow0 % hm;
+  o.tj = pcol0 / hn;
+  o.tc = pcol0 % hn;
+  return o;
+}
+
+// ---------------------------------------------------------------------------
+// Epilogue
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float load_vec(const void* v, int is_f32, int64_t i) {
+  return is_f32 ? reinterpret_cast<const float*>(v)[i] : bf16_to_f32(reinterpret_cast<const uint16_t*>(v)[i]);
+}
+
+// Sum over the 32 lanes of a half-wave (lanes sharing lane>>5).
+__device__ __forceinline__ float half_wave_sum(float x) {
+#pragma unroll
+  for (int s = 16; s >= 1; s >>= 1) x += __shfl_xor(x, s, 64);
+  return x;
+}
+
+// Combines the accumulator sets into the four quadrants, applies the
+// epilogue and stores bf16. acc has kNacc sets (7 Strassen products P1..P7,
+// or the 4 quadrants for the cubic) of kMB x kNB 32x32 blocks; the wave's
+// block (i, j) sits at product-space rows row0 + 32 i and columns
+// col0 + 32 j, relative to the tile origin o.
+// Accumulator lane layout (v_mfma_f32_32x32x16_bf16): column lane%32, row
+// 8*(r/4) + 4*(lane/32) + r%4 for register r.
+// Addresses are a per-wave 64-bit base plus 32-bit element offsets (the host
+// checks that (bm/2 + 128) * max(ldc, ldr) < 2^31), which keeps the
+// epilogue's register footprint small.
+template <int kAlgo, int kMB, int kNB, int kEpi, int kNacc>
+__device__ __forceinline__ void epilogue(const Params& p, const TileOrigin& o, int row0, int col0,
+                                         f32x16 (&acc)[kNacc][kMB][kNB]) {
+  const int lane = threadIdx.x & 63;
+  const int hm = p.bm / 2, hn = p.bn / 2;
+  const int lcol = lane & 31;
+  const int lrow4 = (lane >> 5) * 4;
+  const int ldc = (int)p.ldc, ldr = (int)p.ldr;
+  // Top-left output element of this wave (quadrant 0) and its column inside
+  // the tile half.
+  const int64_t row_base = o.ti * p.bm + o.tr + row0;
+  const int64_t cc_base = o.tc + col0;
+  const int64_t col_base = o.tj * p.bn + cc_base;
+  const int64_t ocol_base = o.tj * hn + cc_base;  // SwiGLU output column
+  uint16_t* const cw = p.c + row_base * p.ldc + (kEpi == SMX_EPI_SWIGLU ? ocol_base : col_base);
+  const uint16_t* const rw = kEpi == SMX_EPI_RESIDUAL_ADD ? p.residual + row_base * p.ldr + col_base : nullptr;
+  const int hm_c = hm * ldc, hm_r = hm * ldr;
+#pragma unroll
+  for (int i = 0; i < kMB; ++i) {
+#pragma unroll
+    for (int j = 0; j < kNB; ++j) {
+      const int cj = j * 32 + lcol;  // column offset inside the wave
+      float bl = 0.f, br = 0.f;
+      if constexpr (kEpi == SMX_EPI_BIAS_ADD) {
+        bl = load_vec(p.bias, p.bias_f32, col_base + cj);
+        br = load_vec(p.bias, p.bias_f32, col_base + cj + hn);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int ri = i * 32 + 8 * (r >> 2) + lrow4 + (r & 3);  // row offset inside the wave
+        float q0, q1, q2, q3;
+        if constexpr (kAlgo == 7) {
+          const float p1 = acc[0][i][j][r], p2 = acc[1][i][j][r], p3 = acc[2][i][j][r];
+          const float p4 = acc[3][i][j][r], p5 = acc[4][i][j][r], p6 = acc[5][i][j][r];
+          const float p7 = acc[6][i][j][r];
+          q0 = ((p4 - p5) + p7) + p1;
+          q1 = p5 + p3;
+          q2 = p4 + p2;
+          q3 = ((p6 - p2) + p3) + p1;
+        } else {
+          q0 = acc[0][i][j][r];
+          q1 = acc[1][i][j][r];
+          q2 = acc[2][i][j][r];
+          q3 = acc[3][i][j][r];
+        }
+        if constexpr (kEpi == SMX_EPI_SWIGLU) {
+          // Quadrants 0/2 are gate, 1/3 up; output [M, N/2].
+          const int off = ri * ldc + cj;
+          cw[off] = f32_to_bf16(silu_f32(q0) * q1);
+          cw[off + hm_c] = f32_to_bf16(silu_f32(q2) * q3);
+        } else if constexpr (kEpi == SMX_EPI_QK_NORM_ROPE) {
+          // Normalisation needs whole head segments: keep the quadrant
+          // values and finish below.
+          acc[0][i][j][r] = q0;
+          acc[1][i][j][r] = q1;
+          acc[2][i][j][r] = q2;
+          acc[3][i][j][r] = q3;
+        } else {
+          const int off = ri * ldc + cj;
+          if constexpr (kEpi == SMX_EPI_RESIDUAL_ADD) {
+            const int roff = ri * ldr + cj;
+            q0 += bf16_to_f32(rw[roff]);
+            q1 += bf16_to_f32(rw[roff + hn]);
+            q2 += bf16_to_f32(rw[roff + hm_r]);
+            q3 += bf16_to_f32(rw[roff + hm_r + hn]);
+          } else if constexpr (kEpi == SMX_EPI_BIAS_ADD) {
+            q0 += bl;
+            q1 += br;
+            q2 += bl;
+            q3 += br;
+          }
+          cw[off] = f32_to_bf16(q0);
+          cw[off + hn] = f32_to_bf16(q1);
+          cw[off + hm_c] = f32_to_bf16(q2);
+          cw[off + hm_c + hn] = f32_to_bf16(q3);
+        }
+      }
+      // One 32x32 block at a time keeps the epilogue's live set small.
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  if constexpr (kEpi == SMX_EPI_QK_NORM_ROPE) {
+    // Per-head RMSNorm then RoPE (strassen_pallas.py:793-835). A head owns
+    // head_dim/2 = 64 consecutive columns of a tile half: the wave's column
+    // blocks j = 2h, 2h+1 (the caller guarantees kNB % 2 == 0 and 64-aligned
+    // wave columns). Quadrants 0/2 hold the a half, 1/3 the b half.
+    static_assert(kEpi != SMX_EPI_QK_NORM_ROPE || kNB % 2 == 0, "qk epilogue needs 64-column waves");
+    const float inv_width = 1.0f / (float)p.head_dim;
+    // rope tables are [M, hn], indexed by output row and column inside the half
+    const uint16_t* const cos_w = p.rope_cos + row_base * hn + cc_base;
+    const uint16_t* const sin_w = p.rope_sin + row_base * hn + cc_base;
+    const int hm_t = hm * hn;
+#pragma unroll
+    for (int i = 0; i < kMB; ++i) {
+#pragma unroll
+      for (int h = 0; h < kNB / 2; ++h) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int ri = i * 32 + 8 * (r >> 2) + lrow4 + (r & 3);
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const int sa = 2 * half, sb = 2 * half + 1;  // a / b quadrant sets
+            const float a0 = acc[sa][i][2 * h][r], a1 = acc[sa][i][2 * h + 1][r];
+            const float b0 = acc[sb][i][2 * h][r], b1 = acc[sb][i][2 * h + 1][r];
+            const float ssa = half_wave_sum(a0 * a0 + a1 * a1);
+            const float ssb = half_wave_sum(b0 * b0 + b1 * b1);
+            const float recip = 1.0f / sqrtf((ssa + ssb) * inv_width + p.eps);
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+              const int j = 2 * h + jj;
+              const int cj = j * 32 + lcol;
+              const float ga = load_vec(p.rope_scale, p.scale_f32, cc_base + cj);
+              const float gb = load_vec(p.rope_scale, p.scale_f32, hn + cc_base + cj);
+              const int toff = ri * hn + cj + half * hm_t;
+              const float cs = bf16_to_f32(cos_w[toff]);
+              const float sn = bf16_to_f32(sin_w[toff]);
+              const float na = acc[sa][i][j][r] * recip * ga;
+              const float nbv = acc[sb][i][j][r] * recip * gb;
+              const int off = ri * ldc + cj + half * hm_c;
+              cw[off] = f32_to_bf16(na * cs - nbv * sn);
+              cw[off + hn] = f32_to_bf16(nbv * cs + na * sn);
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int kNacc, int kMB, int kNB>
+__device__ __forceinline__ void zero_acc(f32x16 (&acc)[kNacc][kMB][kNB]) {
+#pragma unroll
+  for (int s = 0; s < kNacc; ++s)
+#pragma unroll
+    for (int i = 0; i < kMB; ++i)
+#pragma unroll
+      for (int j = 0; j < kNB; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[s][i][j][r] = 0.0f;
+}
+
+}  // namespace smx

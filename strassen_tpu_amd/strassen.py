@@ -21,8 +21,10 @@ Differences a caller can observe, all raised as exceptions (never silent):
   the quadrants once after the last K panel, so ``interleave_products`` and
   the ``product_aware_*`` schedules (which only reorder FP32 additions in
   the reference) are validated and accepted but select the same kernel.
-* Tiles must additionally satisfy the gfx950 kernel's divisibility rule
-  (``smx_tile_requirements``): bm % 256, bn % 128, bk % 64 == 0.
+* Tiles must additionally satisfy the gfx950 kernels' divisibility rule
+  (``smx_tile_requirements``): bm % 256 == 0 always; bn % 128 and bk % 64 for
+  a plain weight; bn % 256 and bk % 32 for a ``StrassenWeight`` and for the
+  cubic control.
 """
 
 from __future__ import annotations
@@ -33,6 +35,7 @@ import torch
 
 from . import _lib
 from .layouts import is_k_contiguous
+from .weights import StrassenWeight
 
 __all__ = [
     "strassen_matmul", "cubic_matmul", "native_matmul", "check_tiling",
@@ -70,8 +73,8 @@ def check_tiling(bm, bn, bk):
         raise ValueError("tile breaks TPU v5e alignment:\n  " + "\n  ".join(errors))
 
 
-def _check_device_tiling(algo, epilogue, bm, bn, bk):
-    tm, tn, tk = _lib.tile_requirements(algo, epilogue)
+def _check_device_tiling(algo, epilogue, bm, bn, bk, b_layout, flags):
+    tm, tn, tk = _lib.tile_requirements(algo, epilogue, b_layout, flags)
     errors = [
         f"{name}={value} must be a multiple of {multiple}"
         for name, value, multiple in (("bm", bm, 2 * tm), ("bn", bn, 2 * tn), ("bk", bk, 2 * tk))
@@ -223,17 +226,25 @@ def _require_device(*tensors):
 
 def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
          rope_cos=None, rope_sin=None, rope_scale=None, rope_head_dim=128,
-         rope_eps=1e-6):
+         rope_eps=1e-6, flags=0):
     lib = _lib.load()
     m, k = a.shape
     n = b.shape[1]
-    _check_device_tiling(algo, epilogue, bm, bn, bk)
-    _require_device(a, b, residual, bias, rope_cos, rope_sin, rope_scale)
-    if a.stride(1) != 1:
+    presummed = isinstance(b, StrassenWeight)
+    b_layout = _lib.SMX_B_PRESUMMED if presummed else _lib.SMX_B_KCONTIG
+    if presummed and (b.bn, b.bk) != (bn, bk):
+        raise ValueError(f"StrassenWeight was laid out for (bn={b.bn}, bk={b.bk}), "
+                         f"called with (bn={bn}, bk={bk})")
+    _check_device_tiling(algo, epilogue, bm, bn, bk, b_layout, flags)
+    _require_device(a, b.data if presummed else b, residual, bias, rope_cos, rope_sin, rope_scale)
+    if a.stride(1) != 1 or a.stride(0) % 8 or a.data_ptr() % 16:
         a = a.contiguous()
-    if not is_k_contiguous(b):
-        b = b.t().contiguous().t()
-    bt = b.t()  # [N, K], rows contiguous
+    if presummed:
+        bt = b.data  # [N/2*7, K/2]
+    else:
+        if not is_k_contiguous(b) or b.stride(1) % 8 or b.data_ptr() % 16:
+            b = b.t().contiguous().t()
+        bt = b.t()  # [N, K], rows contiguous
     out_cols = n // 2 if epilogue == "swiglu" else n
     c = torch.empty((m, out_cols), dtype=torch.bfloat16, device=a.device)
     desc = _lib.SmxGemmDesc()
@@ -242,7 +253,8 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
     desc.bm, desc.bn, desc.bk = bm, bn, bk
     desc.algo = algo
     desc.epilogue = _lib.SMX_EPI[epilogue]
-    desc.b_layout = _lib.SMX_B_KCONTIG
+    desc.b_layout = b_layout
+    desc.flags = flags
     desc.rope_head_dim = rope_head_dim
     desc.rope_eps = rope_eps
     aux = 0
@@ -309,9 +321,11 @@ def strassen_matmul(
     """Compute ``a @ b`` with one tile-local classical Strassen level.
 
     ``a`` is ``[M, K]`` and ``b`` is ``[K, N]``, both bf16 on the HIP device.
-    ``b`` is read directly when K-contiguous (``w.t()`` of a ``[N, K]``
-    weight, see ``layouts.k_contiguous``); otherwise it is transposed on each
-    call. Epilogues and their operands follow ``strassen_pallas.py:739-879``:
+    ``b`` is either a tensor, read directly when K-contiguous (``w.t()`` of a
+    ``[N, K]`` weight, see ``layouts.k_contiguous``; otherwise transposed on
+    each call) and served by the kernel that forms both operand sums in
+    registers; or a ``StrassenWeight`` from ``strassen_weight_layout(b, bn,
+    bk)`` (pre-summed B operands, the faster pipelined kernel). Epilogues and their operands follow ``strassen_pallas.py:739-879``:
     ``swiglu`` returns ``[M, N/2]`` from a ``swiglu_weight_layout`` weight,
     ``residual_add`` adds ``residual`` ``[M, N]``, ``bias_add`` adds
     ``bias`` ``[N]``, ``qk_norm_rope`` applies per-head RMSNorm and RoPE with
@@ -337,7 +351,7 @@ def cubic_matmul(a, b, *, variant="blocked", bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_
                  dot_precision=None, allow_input_fusion=None, interpret=False,
                  vmem_limit_bytes=None, epilogue=None, residual=None, bias=None,
                  rope_cos=None, rope_sin=None, rope_scale=None, rope_head_dim=128,
-                 rope_eps=1e-6):
+                 rope_eps=1e-6, compact=False):
     """Matched cubic control (``experiments/qwen3/benchmark_cubic_control.py:116-177``).
 
     Eight half-size products per K panel into four FP32 quadrant
@@ -345,8 +359,11 @@ def cubic_matmul(a, b, *, variant="blocked", bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_
     epilogues. ``variant="full"`` (one full-tile product per panel) computes
     the same cubic GEMM and runs the same kernel. The fused epilogues are an
     extension of the reference control, used to time fused sites against an
-    identical cubic arm.
+    identical cubic arm. ``compact=True`` selects the compact-tile kernel that
+    matches ``strassen_matmul`` with a plain (not pre-summed) weight.
     """
+    if isinstance(b, StrassenWeight):
+        raise ValueError("cubic_matmul takes a plain weight, not a StrassenWeight")
     if variant not in ("full", "blocked"):
         raise ValueError(f"unknown cubic variant {variant!r}")
     if a.dim() != 2 or b.dim() != 2:
@@ -371,7 +388,8 @@ def cubic_matmul(a, b, *, variant="blocked", bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_
         raise NotImplementedError("the gfx950 cubic control takes bf16 inputs")
     return _run(_lib.SMX_ALGO_CUBIC, a, b, bm=bm, bn=bn, bk=bk, epilogue=epilogue,
                 residual=residual, bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
-                rope_scale=rope_scale, rope_head_dim=rope_head_dim, rope_eps=rope_eps)
+                rope_scale=rope_scale, rope_head_dim=rope_head_dim, rope_eps=rope_eps,
+                flags=_lib.SMX_FLAG_COMPACT_TILE if compact else 0)
 
 
 def native_matmul(a, b):

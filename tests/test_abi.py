@@ -37,8 +37,8 @@ def test_version_and_macros_match_header():
     version = int(re.search(r"#define SMX_VERSION (\d+)", header).group(1))
     assert _lib.load().smx_version() == version
     for name in ("SMX_OK", "SMX_ERR_INVALID", "SMX_ERR_UNSUPPORTED", "SMX_ERR_LAUNCH",
-                 "SMX_ALGO_STRASSEN", "SMX_ALGO_CUBIC", "SMX_B_KCONTIG",
-                 "SMX_AUX_BIAS_F32", "SMX_AUX_SCALE_F32"):
+                 "SMX_ALGO_STRASSEN", "SMX_ALGO_CUBIC", "SMX_B_KCONTIG", "SMX_B_PRESUMMED",
+                 "SMX_FLAG_COMPACT_TILE", "SMX_AUX_BIAS_F32", "SMX_AUX_SCALE_F32"):
         value = int(re.search(rf"#define {name} (\d+)", header).group(1))
         assert getattr(_lib, name) == value, name
     for epi, code in _lib.SMX_EPI.items():
@@ -87,6 +87,7 @@ def _desc(**kw):
     ("b_layout", 0, _lib.SMX_ERR_UNSUPPORTED),
     ("lda", 100, _lib.SMX_ERR_INVALID),
     ("epilogue", 9, _lib.SMX_ERR_INVALID),
+    ("flags", 4, _lib.SMX_ERR_INVALID),
 ])
 def test_invalid_descriptors_are_rejected_before_any_launch(field, value, code):
     lib = _lib.load()
@@ -110,7 +111,66 @@ def test_null_pointers_and_missing_epilogue_operands():
 
 
 def test_tile_requirements():
-    tm, tn, tk = _lib.tile_requirements(_lib.SMX_ALGO_STRASSEN, None)
-    assert tm > 0 and tn > 0 and tk % 16 == 0
+    plain = _lib.tile_requirements(_lib.SMX_ALGO_STRASSEN, None, _lib.SMX_B_KCONTIG)
+    summed = _lib.tile_requirements(_lib.SMX_ALGO_STRASSEN, None, _lib.SMX_B_PRESUMMED)
+    cubic = _lib.tile_requirements(_lib.SMX_ALGO_CUBIC, None)
+    compact = _lib.tile_requirements(_lib.SMX_ALGO_CUBIC, None, flags=_lib.SMX_FLAG_COMPACT_TILE)
+    # The plain-weight Strassen kernel and the compact cubic share a tiling;
+    # the pre-summed Strassen kernel and the default cubic share another.
+    assert plain == compact and summed == cubic
+    for tm, tn, tk in (plain, summed):
+        assert tm > 0 and tn > 0 and tk % 16 == 0
     with pytest.raises(ValueError):
         _lib.tile_requirements(3, None)
+    with pytest.raises(ValueError):
+        _lib.tile_requirements(_lib.SMX_ALGO_CUBIC, None, _lib.SMX_B_PRESUMMED)
+
+
+def test_pre_summed_layout_requires_strassen():
+    lib = _lib.load()
+    buf = (ctypes.c_uint8 * 16)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    d = _desc(algo=_lib.SMX_ALGO_CUBIC, b_layout=_lib.SMX_B_PRESUMMED)
+    assert lib.smx_gemm(d, p, p, p, None, None, None, None, None, None) == _lib.SMX_ERR_INVALID
+
+
+@pytest.mark.parametrize("args", [
+    (0, 512, 512, 256, 512),      # n = 0
+    (512, 512, 512, 256, 500),    # k % bk
+    (512, 512, 512, 255, 512),    # odd bn
+    (512, 512, 512, 256, 24),     # bk % 16
+    (512, 512, 100, 256, 512),    # ldb < k
+])
+def test_weight_layout_rejects_bad_arguments(args):
+    n, k, ldb, bn, bk = args
+    lib = _lib.load()
+    buf = (ctypes.c_uint8 * 16)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    assert lib.smx_strassen_weight_layout(n, k, p, ldb, bn, bk, p, k // 2 if k else 8, None) == _lib.SMX_ERR_INVALID
+    assert _lib.last_error()
+
+
+def test_inline_asm_kernel_check():
+    """The build refuses device code that touches MFMA accumulators between
+    the first inline-asm MFMA and the drain."""
+    from strassen_tpu_amd import build
+
+    drain = "\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n"
+    ok = ("_ZN3smx2v27gemm_v2ILi7ELi0EEEvNS_6ParamsE: ; @x\n\tscratch_store_dword off, v1, off\n"
+          "\t;;#ASMSTART\n\tv_mfma_f32_32x32x16_bf16 a[0:15], v[0:3], v[4:7], a[0:15]\n\t;;#ASMEND\n" + drain +
+          "\tv_accvgpr_read_b32 v0, a0\n\ts_endpgm\n")
+    builtin = ("_ZN3smx2v27gemm_v2ILi8ELi0EEEvNS_6ParamsE:\n"
+               "\tv_mfma_f32_32x32x16_bf16 a[0:15], v[0:3], v[4:7], a[0:15]\n\tv_accvgpr_read_b32 v0, a0\n"
+               "\ts_endpgm\n")
+    assert build.verify_inline_asm_kernels(ok) == 1
+    assert build.verify_inline_asm_kernels(ok + builtin) == 1  # builtin MFMAs are the compiler's business
+    no_drain = ok.replace(drain, "")
+    with pytest.raises(RuntimeError, match="without the drain"):
+        build.verify_inline_asm_kernels(no_drain)
+    for bad in ("\tv_accvgpr_read_b32 v0, a0\n", "\tscratch_store_dwordx4 off, v[0:3], off\n",
+                "\tv_accvgpr_mov_b32 a1, a0\n"):
+        text = ok.replace(drain, bad + drain)
+        with pytest.raises(RuntimeError, match="before the MFMA drain"):
+            build.verify_inline_asm_kernels(text)
+    with pytest.raises(RuntimeError):
+        build.verify_inline_asm_kernels("no kernels here")

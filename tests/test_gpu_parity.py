@@ -88,6 +88,37 @@ def rel_l2(got, ref):
     return float(np.linalg.norm(np.asarray(got, np.float64) - ref) / np.linalg.norm(ref))
 
 
+# The four kernels behind the surface: Strassen with a plain weight (both
+# operand sums in registers), Strassen with a pre-summed weight, the cubic
+# control, and the cubic control on the plain-weight Strassen tiling.
+ARMS = ("strassen_plain", "strassen_presummed", "cubic", "cubic_compact")
+
+
+def run_arm(arm, a, b, *, bm, bn, bk, **kw):
+    """a: [M, K] numpy or device tensor; b: [K, N] numpy or K-contiguous
+    device tensor. Returns the device result."""
+    say(f"  arm {arm} tile=({bm},{bn},{bk}) epilogue={kw.get('epilogue')}")
+    a_dev = a if torch.is_tensor(a) else dev(a)
+    b_dev = b if torch.is_tensor(b) else dev_weight(b)
+    if arm == "strassen_plain":
+        return smx.strassen_matmul(a_dev, b_dev, bm=bm, bn=bn, bk=bk, **kw)
+    if arm == "strassen_presummed":
+        w = smx.strassen_weight_layout(b_dev, bn, bk)
+        return smx.strassen_matmul(a_dev, w, bm=bm, bn=bn, bk=bk, **kw)
+    kw.pop("interleave_products", None)
+    kw.pop("product_aware_swiglu", None)
+    kw.pop("product_aware_residual", None)
+    return smx.cubic_matmul(a_dev, b_dev, bm=bm, bn=bn, bk=bk, compact=(arm == "cubic_compact"), **kw)
+
+
+def oracle_arm(arm, a, b, **kw):
+    if arm.startswith("strassen"):
+        return o.strassen_matmul(a, b, **kw)
+    for key in ("interleave_products", "product_aware_swiglu", "product_aware_residual"):
+        kw.pop(key, None)
+    return o.cubic_blocked_matmul(a, b, **kw)
+
+
 @pytest.fixture(autouse=True)
 def _announce(request):
     say(f"\n[gpu] {request.node.nodeid}")
@@ -107,17 +138,30 @@ INT_CASES = [
 
 
 @pytest.mark.parametrize("shape,tile", INT_CASES)
-@pytest.mark.parametrize("algo", ["strassen", "cubic"])
-def test_integer_kat_bit_exact(shape, tile, algo):
+@pytest.mark.parametrize("arm", ARMS)
+def test_integer_kat_bit_exact(shape, tile, arm):
     m, k, n = shape
     bm, bn, bk = tile
     rng = np.random.default_rng(187)
     a = rng.integers(-2, 3, (m, k)).astype(np.float32)
     b = rng.integers(-2, 3, (k, n)).astype(np.float32)
-    fn = smx.strassen_matmul if algo == "strassen" else smx.cubic_matmul
-    say(f"  {algo} shape={shape} tile={tile}")
-    got = host(fn(dev(a), dev_weight(b), bm=bm, bn=bn, bk=bk))
+    say(f"  {arm} shape={shape} tile={tile}")
+    got = host(run_arm(arm, a, b, bm=bm, bn=bn, bk=bk))
     assert np.array_equal(got, o.bf16_round(a @ b))
+
+
+def test_weight_layout_kernel_matches_oracle():
+    rng = np.random.default_rng(5)
+    for (k, n), (bn, bk) in (((1024, 768), (256, 512)), ((512, 1024), (1024, 256))):
+        b = o.bf16_round(rng.standard_normal((k, n)).astype(np.float32))
+        w = smx.strassen_weight_layout(dev_weight(b), bn, bk)
+        assert tuple(w.data.shape) == (n // 2 * 7, k // 2)
+        assert np.array_equal(host(w.data), o.strassen_weight_layout(b, bn, bk))
+        # a row-major weight gives the same layout
+        w2 = smx.strassen_weight_layout(dev(b), bn, bk)
+        assert torch.equal(w.data, w2.data)
+    with pytest.raises(ValueError, match="does not tile"):
+        smx.strassen_weight_layout(dev(np.zeros((500, 256), np.float32)), 256, 512)
 
 
 def test_integer_kat_row_major_weight():
@@ -148,15 +192,14 @@ def test_config1_1024_cube_seed0():
     a = o.bf16_round(torch.randn(1024, 1024, generator=gen).numpy())
     b = o.bf16_round((torch.randn(1024, 1024, generator=gen) / 32).numpy())
     ref = o.high_precision_reference(a, b).astype(np.float64)
-    want = o.strassen_matmul(a, b, bm=1024, bn=1024, bk=512, interleave_products=True)
-    got = host(smx.strassen_matmul(dev(a), dev_weight(b), bm=1024, bn=1024, bk=512,
-                                   interleave_products=True))
-    assert_ulp_close(got, want, k=1024)
-    e_got, e_want = rel_l2(got, ref), rel_l2(want, ref)
-    say(f"  strassen rel err gpu={e_got:.4e} oracle={e_want:.4e}")
-    assert e_got <= 1e-2 and e_got <= 1.5 * e_want
-    cubic = host(smx.cubic_matmul(dev(a), dev_weight(b), bm=1024, bn=1024, bk=512))
-    assert_ulp_close(cubic, o.cubic_blocked_matmul(a, b, bm=1024, bn=1024, bk=512), k=1024)
+    for arm in ARMS:
+        kw = dict(bm=1024, bn=1024, bk=512, interleave_products=True)
+        want = oracle_arm(arm, a, b, **kw)
+        got = host(run_arm(arm, a, b, **kw))
+        assert_ulp_close(got, want, k=1024)
+        e_got, e_want = rel_l2(got, ref), rel_l2(want, ref)
+        say(f"  {arm} rel err gpu={e_got:.4e} oracle={e_want:.4e}")
+        assert e_got <= 1e-2 and e_got <= 1.5 * e_want
 
 
 @pytest.mark.parametrize("shape,tile", [
@@ -167,18 +210,18 @@ def test_random_matches_oracle(shape, tile):
     m, k, n = shape
     _, a, b = _gaussian(42, m, k, n)
     bm, bn, bk = tile
-    for fn, ofn in ((smx.strassen_matmul, o.strassen_matmul), (smx.cubic_matmul, o.cubic_blocked_matmul)):
-        got = host(fn(dev(a), dev_weight(b), bm=bm, bn=bn, bk=bk))
-        assert_ulp_close(got, ofn(a, b, bm=bm, bn=bn, bk=bk), k=k)
+    for arm in ARMS:
+        got = host(run_arm(arm, a, b, bm=bm, bn=bn, bk=bk))
+        assert_ulp_close(got, oracle_arm(arm, a, b, bm=bm, bn=bn, bk=bk), k=k)
 
 
 def test_repeated_calls_reset_accumulators():
     _, a, b = _gaussian(3, 256, 1024, 256)
-    first = host(smx.strassen_matmul(dev(a), dev_weight(b), bm=256, bn=256, bk=512))
-    second = host(smx.strassen_matmul(dev(-a), dev_weight(b), bm=256, bn=256, bk=512))
-    want = o.strassen_matmul(a, b, bm=256, bn=256, bk=512)
-    assert_ulp_close(first, want, k=1024)
-    assert_ulp_close(second, o.strassen_matmul(-a, b, bm=256, bn=256, bk=512), k=1024)
+    for arm in ARMS:
+        first = host(run_arm(arm, a, b, bm=256, bn=256, bk=512))
+        second = host(run_arm(arm, -a, b, bm=256, bn=256, bk=512))
+        assert_ulp_close(first, oracle_arm(arm, a, b, bm=256, bn=256, bk=512), k=1024)
+        assert_ulp_close(second, oracle_arm(arm, -a, b, bm=256, bn=256, bk=512), k=1024)
 
 
 def test_real_qwen3_weight_slice():
@@ -191,9 +234,9 @@ def test_real_qwen3_weight_slice():
     a = o.bf16_round(rng.standard_normal((256, 512)).astype(np.float32))
     b_dev = torch.from_numpy(w_bits.view(np.int16)).view(torch.bfloat16).to(DEV).t()
     ref = o.high_precision_reference(a, b).astype(np.float64)
-    for fn, ofn in ((smx.strassen_matmul, o.strassen_matmul), (smx.cubic_matmul, o.cubic_blocked_matmul)):
-        got = host(fn(dev(a), b_dev, bm=256, bn=256, bk=256))
-        want = ofn(a, b, bm=256, bn=256, bk=256)
+    for arm in ARMS:
+        got = host(run_arm(arm, a, b_dev, bm=256, bn=256, bk=256))
+        want = oracle_arm(arm, a, b, bm=256, bn=256, bk=256)
         assert_ulp_close(got, want, k=512)
         assert rel_l2(got, ref) <= 1.5 * max(rel_l2(want, ref), 1e-4)
 
@@ -206,16 +249,14 @@ def test_published_accuracy_gate_on_gpu():
     a, b = o.host_uniform_inputs(tuple(spec["shape_mkn"]), spec["seed"])
     bm, bn, bk = spec["tile_bm_bn_bk"]
     ref_t = torch.matmul(dev(a).float(), dev(b).float())  # FP32 product on the GPU
-    got = smx.strassen_matmul(dev(a), dev_weight(b), bm=bm, bn=bn, bk=bk).float()
-    cub = smx.cubic_matmul(dev(a), dev_weight(b), bm=bm, bn=bn, bk=bk).float()
-    e_s = float(torch.linalg.norm(got - ref_t) / torch.linalg.norm(ref_t))
-    e_c = float(torch.linalg.norm(cub - ref_t) / torch.linalg.norm(ref_t))
     published = spec["errors_vs_reference"]
-    say(f"  strassen {e_s:.6e} (published {published['strassen']['l2_relative']:.6e}); "
-        f"cubic {e_c:.6e} (published {published['cubic_blocked']['l2_relative']:.6e})")
-    assert e_s == pytest.approx(published["strassen"]["l2_relative"], rel=5e-3)
-    assert e_c == pytest.approx(published["cubic_blocked"]["l2_relative"], rel=5e-3)
-    assert e_s <= 1.5 * published["strassen"]["l2_relative"]
+    for arm in ARMS:
+        got = run_arm(arm, dev(a), dev_weight(b), bm=bm, bn=bn, bk=bk).float()
+        err = float(torch.linalg.norm(got - ref_t) / torch.linalg.norm(ref_t))
+        want = published["strassen" if arm.startswith("strassen") else "cubic_blocked"]["l2_relative"]
+        say(f"  {arm} {err:.6e} (published {want:.6e})")
+        assert err == pytest.approx(want, rel=5e-3)
+        assert err <= 1.5 * want
 
 
 # ---------------------------------------------------------------------------
@@ -228,10 +269,10 @@ def test_swiglu_epilogue():
     laid = o.swiglu_weight_layout(b, bn)
     laid_dev = smx.swiglu_weight_layout(dev_weight(b), bn)
     assert np.array_equal(host(laid_dev), laid)
-    for fn, ofn in ((smx.strassen_matmul, o.strassen_matmul), (smx.cubic_matmul, o.cubic_blocked_matmul)):
-        got = host(fn(dev(a), laid_dev, bm=bm, bn=bn, bk=bk, epilogue="swiglu"))
+    for arm in ARMS:
+        got = host(run_arm(arm, a, laid_dev, bm=bm, bn=bn, bk=bk, epilogue="swiglu"))
         assert got.shape == (512, 1024)
-        assert_ulp_close(got, ofn(a, laid, bm=bm, bn=bn, bk=bk, epilogue="swiglu"), k=1024)
+        assert_ulp_close(got, oracle_arm(arm, a, laid, bm=bm, bn=bn, bk=bk, epilogue="swiglu"), k=1024)
     # product-aware flag is accepted and selects the same kernel
     got = host(smx.strassen_matmul(dev(a), laid_dev, bm=bm, bn=bn, bk=bk, epilogue="swiglu",
                                    interleave_products=True, product_aware_swiglu=True))
@@ -242,9 +283,10 @@ def test_swiglu_epilogue():
 def test_residual_add_epilogue():
     rng, a, b = _gaussian(319, 512, 2048, 1024)
     r = o.bf16_round(rng.standard_normal((512, 1024)).astype(np.float32))
-    for fn, ofn in ((smx.strassen_matmul, o.strassen_matmul), (smx.cubic_matmul, o.cubic_blocked_matmul)):
-        got = host(fn(dev(a), dev_weight(b), bm=256, bn=512, bk=512, epilogue="residual_add", residual=dev(r)))
-        assert_ulp_close(got, ofn(a, b, bm=256, bn=512, bk=512, epilogue="residual_add", residual=r), k=2048)
+    for arm in ARMS:
+        got = host(run_arm(arm, a, b, bm=256, bn=512, bk=512, epilogue="residual_add", residual=dev(r)))
+        assert_ulp_close(got, oracle_arm(arm, a, b, bm=256, bn=512, bk=512, epilogue="residual_add", residual=r),
+                         k=2048)
 
 
 @pytest.mark.parametrize("bias_dtype", [torch.bfloat16, torch.float32])
@@ -254,9 +296,9 @@ def test_bias_add_epilogue(bias_dtype):
     if bias_dtype == torch.bfloat16:
         bias = o.bf16_round(bias)
     bias_dev = torch.from_numpy(bias).to(DEV).to(bias_dtype)
-    got = host(smx.strassen_matmul(dev(a), dev_weight(b), bm=256, bn=256, bk=512,
-                                   epilogue="bias_add", bias=bias_dev))
-    assert_ulp_close(got, o.strassen_matmul(a, b, bm=256, bn=256, bk=512, epilogue="bias_add", bias=bias), k=1024)
+    for arm in ARMS:
+        got = host(run_arm(arm, a, b, bm=256, bn=256, bk=512, epilogue="bias_add", bias=bias_dev))
+        assert_ulp_close(got, oracle_arm(arm, a, b, bm=256, bn=256, bk=512, epilogue="bias_add", bias=bias), k=1024)
 
 
 def _qk_problem(seed, batch, seq, heads, k, bn, hd=128):
@@ -279,10 +321,10 @@ def test_qk_norm_rope_epilogue(scale_dtype):
     kw = dict(bm=256, bn=bn, bk=512, epilogue="qk_norm_rope", rope_head_dim=128, rope_eps=1e-6)
     laid_dev = smx.rope_weight_layout(dev_weight(w), bn)
     assert np.array_equal(host(laid_dev), laid)
-    for fn, ofn in ((smx.strassen_matmul, o.strassen_matmul), (smx.cubic_matmul, o.cubic_blocked_matmul)):
-        got = host(fn(dev(x), laid_dev, rope_cos=dev(tcos), rope_sin=dev(tsin),
-                      rope_scale=torch.from_numpy(scale).to(DEV).to(scale_dtype), **kw))
-        want = ofn(x, laid, rope_cos=tcos, rope_sin=tsin, rope_scale=scale, **kw)
+    for arm in ARMS:
+        got = host(run_arm(arm, x, laid_dev, rope_cos=dev(tcos), rope_sin=dev(tsin),
+                           rope_scale=torch.from_numpy(scale).to(DEV).to(scale_dtype), **kw))
+        want = oracle_arm(arm, x, laid, rope_cos=tcos, rope_sin=tsin, rope_scale=scale, **kw)
         assert_ulp_close(got, want, k=k)
 
 
@@ -307,8 +349,13 @@ def test_qwen3_32b_shapes_sampled_tiles(site):
     b = w.t()  # [K, N], K-contiguous
     say(f"  {site} m={m} k={k} n={n}")
     got = smx.strassen_matmul(a, b, bm=bm, bn=bn, bk=bk, interleave_products=True)
+    pre = smx.strassen_matmul(a, smx.strassen_weight_layout(b, bn, bk), bm=bm, bn=bn, bk=bk)
     cub = smx.cubic_matmul(a, b, bm=bm, bn=bn, bk=bk)
     torch.cuda.synchronize()
+    # Both Strassen kernels compute the same bf16 operand sums.
+    e_pre = float(torch.linalg.norm(pre.float() - got.float()) / torch.linalg.norm(got.float()))
+    say(f"  plain vs pre-summed weight rel diff {e_pre:.3e}")
+    assert e_pre < 1e-3
     # Whole-output bound against an FP32 product computed on the GPU.
     ref = torch.matmul(a.float(), b.float())
     e_s = float(torch.linalg.norm(got.float() - ref) / torch.linalg.norm(ref))
@@ -324,6 +371,7 @@ def test_qwen3_32b_shapes_sampled_tiles(site):
         rows, cols = slice(i * bm, (i + 1) * bm), slice(j * bn, (j + 1) * bn)
         want = o.strassen_matmul(a_h[rows], b_h[:, cols], bm=bm, bn=bn, bk=bk, interleave_products=True)
         assert_ulp_close(host(got[rows, cols]), want, k=k)
+        assert_ulp_close(host(pre[rows, cols]), want, k=k)
         ref_tile = o.high_precision_reference(a_h[rows], b_h[:, cols]).astype(np.float64)
         assert rel_l2(host(got[rows, cols]), ref_tile) <= 1.5 * rel_l2(want, ref_tile)
         want_c = o.cubic_blocked_matmul(a_h[rows], b_h[:, cols], bm=bm, bn=bn, bk=bk)

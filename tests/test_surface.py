@@ -92,6 +92,43 @@ def test_cubic_surface_checks():
         smx.cubic_matmul(a, b, variant="sparse")
     with pytest.raises(ValueError, match="not divisible"):
         smx.cubic_matmul(a, b, bm=96, bn=256, bk=512)
+    w = smx.StrassenWeight(t(1, 1), 512, 256, 256, 512)
+    with pytest.raises(ValueError, match="plain weight"):
+        smx.cubic_matmul(a, w, bm=256, bn=256, bk=512)
+
+
+def test_strassen_weight_surface():
+    a = t(256, 512)
+    w = smx.StrassenWeight(t(512 // 2 * 7, 256), 512, 512, 512, 512)
+    assert w.shape == (512, 512) and w.dim() == 2 and w.dtype == torch.bfloat16
+    with pytest.raises(ValueError, match="laid out for"):
+        smx.strassen_matmul(a, w, bm=256, bn=256, bk=512)
+    with pytest.raises(ValueError, match="HIP device"):
+        smx.strassen_matmul(a, w, bm=256, bn=512, bk=512)
+    with pytest.raises(ValueError, match="HIP device"):
+        smx.strassen_weight_layout(t(512, 256), 256, 512)
+    with pytest.raises(ValueError, match="bf16"):
+        smx.strassen_weight_layout(t(512, 256, dtype=torch.float32), 256, 512)
+
+
+def test_oracle_weight_layout_brute_force():
+    import numpy as np
+
+    import oracle as o
+
+    rng = np.random.default_rng(0)
+    bn, bk, hn, hk = 16, 32, 8, 16
+    b = o.bf16_round(rng.standard_normal((64, 32)).astype(np.float32))
+    w = o.strassen_weight_layout(b, bn, bk)
+    r = lambda x: o.bf16_round(np.float32(x)).item()
+    for p in range(16):
+        j, c = divmod(p, hn)
+        for kp in range(32):
+            s, kk = divmod(kp, hk)
+            q = [b[s * bk + kh * hk + kk, j * bn + nh * hn + c] for kh in (0, 1) for nh in (0, 1)]
+            b0, b1, b2, b3 = q
+            want = [r(b0 + b3), b0, r(b1 - b3), r(b2 - b0), b3, r(b0 + b1), r(b2 + b3)]
+            assert [w[p * 7 + op, kp] for op in range(7)] == pytest.approx(want, abs=0)
 
 
 def test_torch_relayouts_match_oracle():
