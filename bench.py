@@ -99,40 +99,60 @@ def make_block(torch, dev, seed=0):
     d["tcos"], d["tsin"] = tcos, tsin
     d["scale_q"] = smx.rope_scale_layout(gamma_q, bn, HEAD_DIM)
     d["scale_k"] = smx.rope_scale_layout(gamma_k, bn, HEAD_DIM)
-    # Pre-summed Strassen weights (offline, like the relayouts above).
-    for name in ("wq_laid", "wk_laid", "wv", "wo", "wgu_laid", "wd"):
-        d[name + "_sw"] = smx.strassen_weight_layout(d[name], bn, bk)
+    # Packed weights (offline, like the relayouts above): the seven Strassen
+    # B operand sums ("_sw") and the cubic's four quadrants ("_cw").
     d["wup"] = d["wgu"][:, :FFN]
-    d["wup_sw"] = smx.strassen_weight_layout(d["wup"], bn, bk)
+    for name in ("wq_laid", "wk_laid", "wv", "wo", "wgu_laid", "wd", "wup"):
+        d[name + "_sw"] = smx.strassen_weight_layout(d[name], bn, bk)
+        d[name + "_cw"] = smx.cubic_weight_layout(d[name], bn, bk)
     return d
 
 
+# Weight suffix and algorithm id of each kernel arm.
+ARM_WEIGHTS = {"strassen": ("_sw", 7), "cubic": ("_cw", 8), "strassen_plain": ("", 7), "cubic_plain": ("", 8)}
+
+
 def fused_sites(torch, d, algo):
-    """Callables for a fused arm, keyed by site. algo: "strassen" (pre-summed
-    weights), "strassen_plain" (plain weights, both operand sums formed in
-    the kernel) or "cubic" (matched control)."""
+    """Callables for a fused arm, keyed by site. algo: "strassen" / "cubic"
+    (packed weights; each activation is packed once per step, inside the
+    step, and shared by the GEMMs that read it) or "strassen_plain" /
+    "cubic_plain" (plain weights, the compact kernel forms the operand sums
+    or quadrants from row-major A and B^T)."""
     import strassen_tpu_amd as smx
 
     bm, bn, bk = TILE
-    fn = smx.cubic_matmul if algo == "cubic" else smx.strassen_matmul
-    sw = "_sw" if algo == "strassen" else ""
+    suffix, algo_id = ARM_WEIGHTS[algo]
+    fn = smx.cubic_matmul if algo.startswith("cubic") else smx.strassen_matmul
+    packed = suffix != ""
     kw = dict(bm=bm, bn=bn, bk=bk)
-    if algo != "cubic":
+    if not algo.startswith("cubic"):
         kw["interleave_products"] = True
     qk = dict(epilogue="qk_norm_rope", rope_cos=d["tcos"], rope_sin=d["tsin"], rope_head_dim=HEAD_DIM,
               rope_eps=EPS)
+    act = {}
+
+    def operand(name, fresh):
+        """The activation as the arm consumes it (packed once when fresh)."""
+        if not packed:
+            return d[name]
+        if fresh or name not in act:
+            act[name] = smx.pack_activation(d[name], algo_id, bm, bk)
+        return act[name]
+
     out = {}
-    out["q"] = lambda: fn(d["x"], d["wq_laid" + sw], rope_scale=d["scale_q"], **qk, **kw)
-    out["k"] = lambda: fn(d["x"], d["wk_laid" + sw], rope_scale=d["scale_k"], **qk, **kw)
-    out["v"] = lambda: fn(d["x"], d["wv" + sw], **kw)
-    out["o"] = lambda: fn(d["attn"], d["wo" + sw], epilogue="residual_add", residual=d["res1"], **kw)
+    out["q"] = lambda: fn(operand("x", True), d["wq_laid" + suffix], rope_scale=d["scale_q"], **qk, **kw)
+    out["k"] = lambda: fn(operand("x", False), d["wk_laid" + suffix], rope_scale=d["scale_k"], **qk, **kw)
+    out["v"] = lambda: fn(operand("x", False), d["wv" + suffix], **kw)
+    out["o"] = lambda: fn(operand("attn", True), d["wo" + suffix], epilogue="residual_add", residual=d["res1"],
+                          **kw)
 
     def gate_up():
-        d["h"] = fn(d["y"], d["wgu_laid" + sw], epilogue="swiglu", **kw)
+        d["h"] = fn(operand("y", True), d["wgu_laid" + suffix], epilogue="swiglu", **kw)
         return d["h"]
 
     out["gate_up"] = gate_up
-    out["down"] = lambda: fn(d["h"], d["wd" + sw], epilogue="residual_add", residual=d["res2"], **kw)
+    out["down"] = lambda: fn(operand("h", True), d["wd" + suffix], epilogue="residual_add", residual=d["res2"],
+                             **kw)
     return out
 
 
@@ -166,20 +186,21 @@ def vendor_sites(torch, d):
 
 
 def pure_sites(torch, d, algo):
-    """the pure GEMMs (no epilogue) at gate/up, down and o."""
+    """The pure GEMMs (no epilogue) at gate/up, down and o (activation
+    packing included for the packed arms)."""
     import strassen_tpu_amd as smx
 
     bm, bn, bk = TILE
-    sw = "_sw" if algo == "strassen" else ""
     if algo == "hipblaslt":
-        fn = lambda a, b: torch.matmul(a, b)
+        fn = lambda a, b: torch.matmul(a, d[b])
     else:
-        base = smx.cubic_matmul if algo == "cubic" else smx.strassen_matmul
-        fn = lambda a, b: base(a, b, bm=bm, bn=bn, bk=bk)
+        suffix, _ = ARM_WEIGHTS[algo]
+        base = smx.cubic_matmul if algo.startswith("cubic") else smx.strassen_matmul
+        fn = lambda a, b: base(a, d[b + suffix], bm=bm, bn=bn, bk=bk)
     return {
-        "gate_up": lambda: fn(d["y"], d["wup" + sw]),
-        "down": lambda: fn(d["h_any"], d["wd" + sw]),
-        "o": lambda: fn(d["attn"], d["wo" + sw]),
+        "gate_up": lambda: fn(d["y"], "wup"),
+        "down": lambda: fn(d["h_any"], "wd"),
+        "o": lambda: fn(d["attn"], "wo"),
     }
 
 
@@ -270,8 +291,8 @@ def main():
     shapes = site_shapes()
     block_flops = sum(flops(s) for s in shapes.values())
 
-    arms = {"strassen": fused_sites(torch, d, "strassen"), "cubic": fused_sites(torch, d, "cubic"),
-            "hipblaslt": vendor_sites(torch, d), "strassen_plain": fused_sites(torch, d, "strassen_plain")}
+    arms = {arm: fused_sites(torch, d, arm) for arm in ARM_WEIGHTS}
+    arms["hipblaslt"] = vendor_sites(torch, d)
     # H for the pure down GEMM (any bf16 activations of the right shape).
     arms["strassen"]["gate_up"]()
     d["h_any"] = d["h"]
@@ -291,7 +312,7 @@ def main():
     log("timing strassen block")
     wall_s, ev_s = time_steps(torch, run_block(arms["strassen"]), args.steps, args.warmup)
     results = {"strassen": statistics.median(ev_s)}
-    for arm in ("cubic", "hipblaslt", "strassen_plain"):
+    for arm in ("cubic", "hipblaslt", "strassen_plain", "cubic_plain"):
         log(f"timing {arm} block")
         _, ev = time_steps(torch, run_block(arms[arm]), args.steps, args.warmup)
         results[arm] = statistics.median(ev)
@@ -313,7 +334,7 @@ def main():
             _, ev = time_steps(torch, sites[name], args.steps, 2)
             per_site[arm][name] = statistics.median(ev)
     pure = {}
-    for arm in ("strassen", "strassen_plain", "cubic", "hipblaslt"):
+    for arm in ("strassen", "strassen_plain", "cubic", "cubic_plain", "hipblaslt"):
         table = pure_sites(torch, d, arm)
         pure[arm] = {}
         for name, fn in table.items():
@@ -322,15 +343,30 @@ def main():
     pure_shapes = {"gate_up": (TOKENS, HIDDEN, FFN), "down": (TOKENS, FFN, HIDDEN),
                    "o": (TOKENS, HEADS * HEAD_DIM, HIDDEN)}
 
-    # Roofline of the dominant kernel: the fused gate|up SwiGLU Strassen launch.
-    gu_ms = per_site["strassen"]["gate_up"]
+    # Roofline of the dominant kernel: the fused gate|up SwiGLU Strassen GEMM
+    # launch alone (activation already packed), timed with events on the
+    # stream it is launched on.
+    bm, bn, bk = TILE
+    y_packed = smx.pack_activation(d["y"], 7, bm, bk)
+    gu_fn = lambda: smx.strassen_matmul(y_packed, d["wgu_laid_sw"], bm=bm, bn=bn, bk=bk, epilogue="swiglu",
+                                        interleave_products=True)
+    _, ev = time_steps(torch, gu_fn, args.steps, 2)
+    gu_ms = statistics.mean(ev)
     gu_tflops = flops(shapes["gate_up"]) / (gu_ms * 1e-3) / 1e12
+    yc_packed = smx.pack_activation(d["y"], 8, bm, bk)
+    _, ev = time_steps(torch, lambda: smx.cubic_matmul(yc_packed, d["wgu_laid_cw"], bm=bm, bn=bn, bk=bk,
+                                                       epilogue="swiglu"), args.steps, 2)
+    gu_cubic_ms = statistics.mean(ev)
+    _, ev = time_steps(torch, lambda: smx.pack_activation(d["y"], 7, bm, bk), args.steps, 2)
+    pack_ms = statistics.mean(ev)
     roofline = {
         "bound": "mfma", "achieved": round(gu_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
         "frac": round(gu_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
-        "kernel": "smx::v2::gemm_v2<7, SMX_EPI_SWIGLU> (gate|up, M=8192 K=5120 N=51200, pre-summed weight)",
+        "kernel": "smx::packed::gemm_packed<7, SMX_EPI_SWIGLU> (gate|up, M=8192 K=5120 N=51200, packed operands)",
         "mfma_executed_frac": round(gu_tflops * 7 / 8 / PEAK_BF16_TFLOPS, 4),
         "avg_launch_ms": round(gu_ms, 4),
+        "cubic_same_site_ms": round(gu_cubic_ms, 4),
+        "activation_pack_ms": round(pack_ms, 4),
     }
 
     ms = results["strassen"]

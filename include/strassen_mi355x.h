@@ -18,12 +18,14 @@
  *                strassen_matmul's argument checks (strassen_pallas.py:927-1047).
  *   smx_tile_requirements <- check_tiling (strassen_pallas.py:127-140): the
  *                gfx950 kernel's divisibility rule for (bm, bn, bk).
- *   smx_strassen_weight_layout <- the offline weight relayouts
+ *   smx_pack_operand / smx_packed_bytes <- the offline weight relayouts
  *                (swiglu_weight_layout / rope_weight_layout,
- *                strassen_pallas.py:1315-1411): one more offline transform of a
- *                static weight, which stores the seven classical B operand sums
- *                of every (bk, bn) tile (strassen_pallas.py:324-379) so that
- *                smx_gemm only forms the A sums at run time.
+ *                strassen_pallas.py:1315-1411) and the in-kernel quadrant
+ *                sums (strassen_pallas.py:324-379): a weight is packed once
+ *                (its seven classical B operand sums per (bk, bn) tile, or its
+ *                four quadrants for the cubic) and an activation once per call
+ *                (its A sums / quadrants), into the fragment order the packed
+ *                kernel streams into LDS.
  *   smx_version: no reference counterpart (ABI version query for bindings).
  */
 #ifndef STRASSEN_MI355X_H
@@ -35,7 +37,7 @@
 extern "C" {
 #endif
 
-#define SMX_VERSION 2
+#define SMX_VERSION 3
 
 /* Status codes. */
 #define SMX_OK 0
@@ -54,12 +56,17 @@ extern "C" {
 #define SMX_EPI_BIAS_ADD 3     /* out = acc + bias[col];         :867-874 */
 #define SMX_EPI_QK_NORM_ROPE 4 /* per-head RMSNorm + RoPE;       :793-835 */
 
-/* Layout of B. */
-#define SMX_B_KCONTIG 1   /* B^T stored row-major [N, K] (ldb >= K) */
-#define SMX_B_PRESUMMED 2 /* Strassen weight [N/2 * 7, K/2] from smx_strassen_weight_layout (ldb >= K/2) */
+/* Layout of A. */
+#define SMX_A_ROWMAJOR 0 /* A row-major [M, K] (lda >= K) */
+#define SMX_A_PACKED 1   /* smx_pack_operand(algo, SMX_SIDE_LHS, ...) output */
 
-/* desc.flags bits. */
-#define SMX_FLAG_COMPACT_TILE 1 /* cubic: use the compact-tile (plain-weight Strassen) kernel */
+/* Layout of B. */
+#define SMX_B_KCONTIG 1 /* B^T stored row-major [N, K] (ldb >= K) */
+#define SMX_B_PACKED 2  /* smx_pack_operand(algo, SMX_SIDE_RHS, ...) output */
+
+/* Operand side for smx_pack_operand. */
+#define SMX_SIDE_LHS 0 /* A [M, K] */
+#define SMX_SIDE_RHS 1 /* B^T [N, K] */
 
 /* aux_f32 bits: element type of the small auxiliary vectors. */
 #define SMX_AUX_BIAS_F32 1  /* bias is float32 (else bf16) */
@@ -72,19 +79,22 @@ typedef struct smx_gemm_desc {
   int32_t bm, bn, bk;    /* Strassen quadrant tile: the reference's (bm, bn, bk) */
   int32_t algo;          /* SMX_ALGO_* */
   int32_t epilogue;      /* SMX_EPI_* */
-  int32_t b_layout;      /* SMX_B_KCONTIG or SMX_B_PRESUMMED */
+  int32_t a_layout;      /* SMX_A_ROWMAJOR or SMX_A_PACKED */
+  int32_t b_layout;      /* SMX_B_KCONTIG or SMX_B_PACKED */
   int32_t rope_head_dim; /* qk_norm_rope head width (128) */
   float rope_eps;        /* qk_norm_rope epsilon */
   int32_t aux_f32;       /* SMX_AUX_* bits */
-  int32_t flags;         /* SMX_FLAG_* bits */
+  int32_t flags;         /* reserved, must be 0 */
 } smx_gemm_desc;
 
 /*
- * C = epilogue(A @ B). A: bf16 [m, k] row-major. B: bf16, layout b_layout
- * (SMX_B_PRESUMMED only with SMX_ALGO_STRASSEN, built for the same bn, bk).
- * C: bf16 [m, n] (or [m, n/2] for SwiGLU). residual: bf16 [m, n] (ldr).
- * bias: [n] bf16 or f32. rope_cos / rope_sin: bf16 [m, bn/2] tables indexed
- * by output row (rope_layout_tables). rope_scale: [bn] bf16 or f32
+ * C = epilogue(A @ B). Operands: either A bf16 [m, k] row-major (lda) with
+ * B^T bf16 [n, k] row-major (ldb), served by the compact kernel that forms
+ * the operand sums in registers; or both packed by smx_pack_operand for the
+ * same algo and (bm, bk) / (bn, bk), served by the packed kernel (lda / ldb
+ * ignored). C: bf16 [m, n] (or [m, n/2] for SwiGLU). residual: bf16 [m, n]
+ * (ldr). bias: [n] bf16 or f32. rope_cos / rope_sin: bf16 [m, bn/2] tables
+ * indexed by output row (rope_layout_tables). rope_scale: [bn] bf16 or f32
  * (rope_scale_layout). Unused pointers may be NULL.
  * Returns SMX_OK or an SMX_ERR_* code; smx_last_error() describes it.
  */
@@ -93,20 +103,30 @@ int smx_gemm(const smx_gemm_desc* desc, const void* a, const void* b, void* c, c
              void* stream);
 
 /* Product-space workgroup tile (tm, tn) and K stage (tk) of the kernel that
- * serves (algo, epilogue, b_layout, flags): bm must be a multiple of 2*tm,
- * bn of 2*tn, bk of 2*tk. */
+ * serves (algo, epilogue, b_layout): bm must be a multiple of 2*tm, bn of
+ * 2*tn, bk of 2*tk. */
 int smx_tile_requirements(int32_t algo, int32_t epilogue, int32_t b_layout, int32_t flags, int32_t* tm, int32_t* tn,
                           int32_t* tk);
 
+/* Bytes of the packed form of a [rows, k] operand for algo (rows/2 * k/2 *
+ * nops * 2, nops = 7 for Strassen, 4 for the cubic). */
+int smx_packed_bytes(int32_t algo, int64_t rows, int64_t k, int64_t* bytes);
+
 /*
- * Pre-summed Strassen weight for the (bn, bk) tile: from B^T bf16 [n, k]
- * (row stride ldb) writes out bf16 [n/2 * 7, k/2] (row stride ldo): row
- * (p*7 + o) holds operand T_(o+1) of product-space column p, in order
- * B0+B3, B0, B1-B3, B2-B0, B3, B0+B1, B2+B3, each sum rounded once to bf16.
- * Needs n % bn == 0, k % bk == 0, bk % 16 == 0. Asynchronous on stream.
+ * Packs one operand for the packed kernel. side SMX_SIDE_LHS: src is A bf16
+ * [rows = m, k] and tile_rows = bm; SMX_SIDE_RHS: src is B^T bf16 [rows = n,
+ * k] and tile_rows = bn. Strassen (algo 7) stores the seven operand sums of
+ * P1..P7 (A0+A3, A2+A3, A0, A3, A0+A1, A2-A0, A1-A3; B0+B3, B0, B1-B3,
+ * B2-B0, B3, B0+B1, B2+B3), each rounded once to bf16; the cubic (algo 8)
+ * stores the four quadrants. out (smx_packed_bytes bytes, 16-byte aligned)
+ * is laid out [rows/256][k/32][nops][4][64][8] bf16: fragment (tile of 128
+ * product rows, stage of 16 product k, operand, 32-row block), lane l holding
+ * row l%32, depth 8*(l/32)..+8. Needs rows % tile_rows == 0, k % bk == 0,
+ * tile_rows % 256 == 0, bk % 32 == 0, ld >= k, ld % 8 == 0. Asynchronous on
+ * stream.
  */
-int smx_strassen_weight_layout(int64_t n, int64_t k, const void* bt, int64_t ldb, int32_t bn, int32_t bk, void* out,
-                               int64_t ldo, void* stream);
+int smx_pack_operand(int32_t algo, int32_t side, int64_t rows, int64_t k, const void* src, int64_t ld,
+                     int32_t tile_rows, int32_t bk, void* out, void* stream);
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* smx_last_error(void);

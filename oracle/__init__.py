@@ -31,6 +31,11 @@ Pinning (what checks each function, so a plausible mistake fails a test):
   ``qk_norm_rope``, the unfused RMSNorm+RoPE semantics composed with the
   relayout inverse (``benchmark_qwen3_32b_layer.py:270-284``, ``:322-341``).
 * relayouts -- brute-force index maps on tiny sizes and round trips.
+* ``packed_operand`` (the packed kernel's operand layout, no reference
+  counterpart) -- a per-element index walk over every packed position on
+  small shapes, and the cubic round trip (unpacked quadrants reassemble the
+  input exactly); the operand sums it stores are the ones the known-answer
+  tests above pin.
 
 Parity at the rounding level of XLA/Mosaic internals (dot accumulation order,
 ``jax.nn.silu``/``rsqrt`` ulps) cannot be pinned without JAX, which is absent

@@ -20,7 +20,8 @@ __all__ = [
     "rope_weight_layout_order", "rope_weight_layout", "rope_layout_tables",
     "rope_scale_layout", "rope_layout_to_heads", "rope_values", "rms_norm",
     "apply_rope", "strassen_products", "strassen_a_operands", "strassen_b_operands",
-    "strassen_weight_layout", "PRODUCT_UPDATES",
+    "operand_planes", "packed_operand", "unpack_operand", "PACK_TILE", "PACK_STAGE",
+    "PRODUCT_UPDATES",
 ]
 
 
@@ -174,20 +175,50 @@ def _column_vector_quadrants(v, bn):
             np.ascontiguousarray(w[:, 1, :].reshape(n // 2)))
 
 
-def strassen_weight_layout(b, bn, bk):
-    """Pre-summed B operands of every (bk, bn) tile as [N/2 * 7, K/2]:
-    row ``p*7 + o`` = operand ``o`` (order of ``strassen_b_operands``) of
-    product-space column ``p`` (tile j, column c < bn/2) over product-space
-    depth (panel s, k < bk/2). The layout of ``smx_strassen_weight_layout``."""
-    b = np.asarray(b, dtype=np.float32)
-    k, n = b.shape
-    hk = bk // 2
-    out = np.empty((n // 2, 7, k // 2), dtype=np.float32)
-    for step in range(k // bk):
-        ops = strassen_b_operands(_split_b(b, bn, bk, step))  # each (hk, N/2)
-        for o, t in enumerate(ops):
-            out[:, o, step * hk:(step + 1) * hk] = t.T
-    return out.reshape(n // 2 * 7, k // 2)
+PACK_TILE = 128  # product rows per packed tile (the kernel's workgroup tile)
+PACK_STAGE = 16  # product depth per packed stage (one MFMA k step)
+
+
+def operand_planes(x, algo, side, tile_rows, bk):
+    """The GEMM operands of every tile as (nops, R, K/2) product-space planes.
+
+    ``side="lhs"``: x is A [M, K], R = M/2 product rows (row tile, local row).
+    ``side="rhs"``: x is B [K, N], R = N/2 product columns (column tile,
+    local column). Depth k' = (K panel, local k < bk/2). Strassen (algo 7)
+    gives the seven operand sums of ``strassen_a_operands`` /
+    ``strassen_b_operands``; the cubic (algo 8) the four quadrants.
+    """
+    x = np.asarray(x, dtype=np.float32)
+    if side == "lhs":
+        steps = x.shape[1] // bk
+        quads = [np.concatenate(q, axis=1)
+                 for q in zip(*(_split_a(x, tile_rows, bk, s) for s in range(steps)))]
+        ops = strassen_a_operands(quads) if algo == 7 else quads
+    elif side == "rhs":
+        steps = x.shape[0] // bk
+        quads = [np.concatenate(q, axis=0).T
+                 for q in zip(*(_split_b(x, tile_rows, bk, s) for s in range(steps)))]
+        ops = strassen_b_operands(quads) if algo == 7 else quads
+    else:
+        raise ValueError("side must be 'lhs' or 'rhs'")
+    return np.stack(ops)
+
+
+def packed_operand(x, algo, side, tile_rows, bk):
+    """``smx_pack_operand``'s output as a flat float32 array of bf16 values:
+    ``[R/128][K/32][nops][4][64][8]``, lane l of a fragment holding product
+    row l%32 of its 32-row block and depth 8*(l//32)..+8 of its stage."""
+    planes = operand_planes(x, algo, side, tile_rows, bk)
+    nops, rows, depth = planes.shape
+    v = planes.reshape(nops, rows // PACK_TILE, 4, 32, depth // PACK_STAGE, 2, 8)
+    # (op, tile, block, row32, stage, half, e) -> (tile, stage, op, block, half, row32, e)
+    return np.ascontiguousarray(v.transpose(1, 4, 0, 2, 5, 3, 6)).reshape(-1)
+
+
+def unpack_operand(flat, nops, rows, depth):
+    """Inverse of the packing order: flat -> (nops, R, K/2) planes."""
+    v = np.asarray(flat).reshape(rows // PACK_TILE, depth // PACK_STAGE, nops, 4, 2, 32, 8)
+    return np.ascontiguousarray(v.transpose(2, 0, 3, 5, 1, 4, 6)).reshape(nops, rows, depth)
 
 
 def _check_common(a, b, bm, bn, bk):

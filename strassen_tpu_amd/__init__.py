@@ -15,6 +15,8 @@ from .strassen import (  # noqa: F401
     cubic_matmul, native_matmul, strassen_matmul,
 )
 
-from .weights import StrassenWeight, strassen_weight_layout  # noqa: F401
+from .packing import (  # noqa: F401
+    PackedOperand, cubic_weight_layout, pack_activation, pack_operand, strassen_weight_layout,
+)
 
-__version__ = "0.2.0"
+__version__ = "0.3.0"

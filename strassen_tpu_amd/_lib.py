@@ -32,13 +32,17 @@ SMX_EPI = {
     "qk_norm_rope": 4,
 }
 
+SMX_A_ROWMAJOR = 0
+SMX_A_PACKED = 1
 SMX_B_KCONTIG = 1
-SMX_B_PRESUMMED = 2
-SMX_FLAG_COMPACT_TILE = 1
+SMX_B_PACKED = 2
+SMX_SIDE_LHS = 0
+SMX_SIDE_RHS = 1
 SMX_AUX_BIAS_F32 = 1
 SMX_AUX_SCALE_F32 = 2
 
-EXPORTS = ("smx_gemm", "smx_tile_requirements", "smx_strassen_weight_layout", "smx_last_error", "smx_version")
+EXPORTS = ("smx_gemm", "smx_tile_requirements", "smx_packed_bytes", "smx_pack_operand", "smx_last_error",
+           "smx_version")
 
 
 class SmxGemmDesc(ctypes.Structure):
@@ -48,7 +52,8 @@ class SmxGemmDesc(ctypes.Structure):
         ("ldr", ctypes.c_int64),
         ("bm", ctypes.c_int32), ("bn", ctypes.c_int32), ("bk", ctypes.c_int32),
         ("algo", ctypes.c_int32), ("epilogue", ctypes.c_int32),
-        ("b_layout", ctypes.c_int32), ("rope_head_dim", ctypes.c_int32),
+        ("a_layout", ctypes.c_int32), ("b_layout", ctypes.c_int32),
+        ("rope_head_dim", ctypes.c_int32),
         ("rope_eps", ctypes.c_float), ("aux_f32", ctypes.c_int32),
         ("flags", ctypes.c_int32),
     ]
@@ -76,8 +81,10 @@ def load():
                                           ctypes.POINTER(ctypes.c_int32)]
     lib.smx_tile_requirements.restype = ctypes.c_int
     i64, i32 = ctypes.c_int64, ctypes.c_int32
-    lib.smx_strassen_weight_layout.argtypes = [i64, i64, vp, i64, i32, i32, vp, i64, vp]
-    lib.smx_strassen_weight_layout.restype = ctypes.c_int
+    lib.smx_packed_bytes.argtypes = [i32, i64, i64, ctypes.POINTER(i64)]
+    lib.smx_packed_bytes.restype = ctypes.c_int
+    lib.smx_pack_operand.argtypes = [i32, i32, i64, i64, vp, i64, i32, i32, vp, vp]
+    lib.smx_pack_operand.restype = ctypes.c_int
     lib.smx_last_error.argtypes = []
     lib.smx_last_error.restype = ctypes.c_char_p
     lib.smx_version.argtypes = []
@@ -90,10 +97,10 @@ def last_error():
     return load().smx_last_error().decode("utf-8", "replace")
 
 
-def tile_requirements(algo, epilogue, b_layout=SMX_B_KCONTIG, flags=0):
+def tile_requirements(algo, epilogue, b_layout=SMX_B_KCONTIG):
     lib = load()
     tm, tn, tk = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
-    rc = lib.smx_tile_requirements(algo, SMX_EPI[epilogue], b_layout, flags,
+    rc = lib.smx_tile_requirements(algo, SMX_EPI[epilogue], b_layout, 0,
                                    ctypes.byref(tm), ctypes.byref(tn), ctypes.byref(tk))
     if rc != SMX_OK:
         raise ValueError(last_error())

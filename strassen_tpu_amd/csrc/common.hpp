@@ -115,24 +115,24 @@ struct Params {
   int32_t head_dim;
   float eps;
   int32_t tiles_m, tiles_n;  // product-space workgroup grid
+  int32_t group_m;           // tile rows per rasterization group
 };
 
 // Workgroup id -> product-space tile. Workgroups are dispatched round-robin
 // over the 8 XCDs; consecutive logical tiles are gathered on one XCD so that
 // neighbouring tiles share its L2, and inside an XCD tiles walk column groups
-// of kGroupM rows (an A row panel is reused across the group's columns).
-__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+// of group_m rows (an A row panel is reused across the group's columns).
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
   const int total = tiles_m * tiles_n;
   int logical = bid;
   if (total % 8 == 0) {
     const int per_xcd = total / 8;
     logical = (bid % 8) * per_xcd + bid / 8;
   }
-  constexpr int kGroupM = 8;
-  const int group_size = kGroupM * tiles_n;
+  const int group_size = group_m * tiles_n;
   const int group = logical / group_size;
-  const int first_m = group * kGroupM;
-  const int rows_in_group = min(tiles_m - first_m, kGroupM);
+  const int first_m = group * group_m;
+  const int rows_in_group = min(tiles_m - first_m, group_m);
   const int in_group = logical - group * group_size;
   tm = first_m + in_group % rows_in_group;
   tn = in_group / rows_in_group;

@@ -1,0 +1,315 @@
+// Packed-operand gfx950 kernel: 128x128 product-space workgroup tile, four
+// waves of 64x64, 16 product-space k per stage, both operands streamed from
+// HBM straight into LDS (global_load_lds_dwordx4, no VGPR staging, no VALU in
+// the main loop).
+//
+// Packed operand layout (written by pack_operand below, once per weight and
+// once per call for the activation). An operand of R product rows (M/2 for
+// A, N/2 for B) and K/2 product-space depth is stored as
+//   [R/128 tiles][K/32 stages][nops][4 blocks of 32 rows][64 lanes][8 bf16]
+// where lane l of a 1 KB fragment holds row l%32, depth 8*(l/32)..+8 of the
+// 32x16 MFMA operand, i.e. exactly the order a lane's ds_read_b128 wants.
+// nops is 7 for Strassen (the operand sums of P1..P7, each rounded once to
+// bf16, strassen_pallas.py:324-379) and 4 for the cubic (raw quadrants). One
+// stage of one operand for one workgroup is therefore nops*4 KB contiguous,
+// and every DMA instruction moves one contiguous 1 KB fragment.
+//
+// Pipeline: a ring of kASlots A stages and three B stages in LDS. At stage s
+// a wave issues the DMA of A stage s+kASlots-1 and B stage s+2, runs its
+// MFMAs on stage s and meets the other waves at one barrier that waits for
+// everything but the newest prefetches.
+#pragma once
+
+#include "common.hpp"
+
+namespace smx {
+namespace packed {
+
+constexpr int TM = 128, TN = 128, TK = 16;
+constexpr int kFrag = 1024;  // one 32x16 bf16 operand fragment in lane order
+constexpr int kBlocks = 4;   // 32-row blocks per 128-row tile
+constexpr int kPackStages = 4;  // stages one pack wave handles (128 B per source row)
+
+__host__ __device__ constexpr int nops_of(int algo) { return algo == 7 ? 7 : 4; }
+
+// Byte offset of fragment (tile, stage, op, block) in a packed operand.
+__host__ __device__ inline int64_t frag_offset(int64_t tile, int64_t stage, int64_t nstages, int op, int nops,
+                                               int block) {
+  return (((tile * nstages + stage) * nops + op) * kBlocks + block) * (int64_t)kFrag;
+}
+
+template <int kAlgo>
+struct Lay {
+  static constexpr int nops = nops_of(kAlgo);
+  static constexpr int kStage = nops * kBlocks * kFrag;  // one operand, one stage
+  // Strassen's 28 KB stages allow two A slots next to three B slots.
+  static constexpr int kASlots = kAlgo == 7 ? 2 : 3;
+  static constexpr int kBSlots = 3;
+  static constexpr int kLds = (kASlots + kBSlots) * kStage;
+  static constexpr int kDmaPerWave = nops;  // nops*4 fragments over 4 waves
+  // VMEM operations a wave may leave in flight at the stage barrier: the
+  // prefetches that target stages after s+1.
+  static constexpr int kPending = (kASlots == 3 ? kDmaPerWave : 0) + kDmaPerWave;
+  static_assert(kLds <= 160 * 1024, "LDS budget");
+  static_assert(kPending < 64, "vmcnt range");
+};
+
+// Barrier after this wave's LDS reads and all but its newest kPending VMEM
+// operations have completed. The "memory" clobber keeps the compiler from
+// moving LDS accesses across it.
+template <int kPending>
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"i"(kPending) : "memory");
+}
+
+// v_mfma_f32_32x32x16_bf16 with the accumulator pinned to AGPRs / VGPRs.
+// An accumulator is reused only 4+ MFMAs later and read by VALU only after
+// mfma_drain(), so no MFMA result hazard is left to the compiler.
+__device__ __forceinline__ void mfma_agpr(f32x16& c, const bf16x8& a, const bf16x8& b) {
+  asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_vgpr(f32x16& c, const bf16x8& a, const bf16x8& b) {
+  asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+}
+// Wait states between the last MFMA writes and VALU / v_accvgpr_read reads
+// of the accumulators (more than the longest MFMA result latency). Each
+// accumulator then passes through an empty volatile asm that "defines" it,
+// so no read of it can be scheduled above the s_nops.
+template <int kSets>
+__device__ __forceinline__ void mfma_drain(f32x16 (&acc)[kSets][2][2]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+  for (int s = 0; s < kSets; ++s)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if (s < 4)
+          asm volatile("" : "+a"(acc[s][i][j]));
+        else
+          asm volatile("" : "+v"(acc[s][i][j]));
+      }
+}
+
+__device__ __forceinline__ bf16x8 ld_frag(const uint8_t* p) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(p));
+}
+
+template <int kAlgo, int kEpi>
+__global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
+  using L = Lay<kAlgo>;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  int tile_m, tile_n;
+  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tile_m, tile_n);
+  const TileOrigin o = tile_origin(p, (int64_t)tile_m * TM, (int64_t)tile_n * TN);
+  const int nstages = (int)(p.k / (2 * TK));
+
+  // DMA sources: this workgroup's packed stages are contiguous runs of
+  // L::kStage bytes; wave w moves fragments f = w + 4x of each.
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const uint8_t* const a_src =
+      reinterpret_cast<const uint8_t*>(p.a) + (int64_t)tile_m * nstages * L::kStage + wave_u * kFrag;
+  const uint8_t* const b_src =
+      reinterpret_cast<const uint8_t*>(p.b) + (int64_t)tile_n * nstages * L::kStage + wave_u * kFrag;
+  const uint32_t lane_off = lane * 16;
+  uint8_t* const a_region = lds;
+  uint8_t* const b_region = lds + L::kASlots * L::kStage;
+
+  // Prefetches past the last stage re-load it (in bounds, never read)
+  // instead of branching.
+  auto dma = [&](const uint8_t* src, int stage, uint8_t* slot) {
+    const uint8_t* from = src + (int64_t)min(stage, nstages - 1) * L::kStage + lane_off;
+#pragma unroll
+    for (int x = 0; x < L::kDmaPerWave; ++x)
+      __builtin_amdgcn_global_load_lds(from + x * 4 * kFrag,
+                                       (__attribute__((address_space(3))) void*)(slot + (wave_u + 4 * x) * kFrag), 16,
+                                       0, 0);
+  };
+
+  f32x16 acc[L::nops][2][2];
+  zero_acc(acc);
+
+  // Fragments of one product (Strassen) or one quadrant pair (cubic):
+  // A blocks 2wm, 2wm+1 and B blocks 2wn, 2wn+1.
+  struct Frags {
+    bf16x8 a0, a1, b0, b1;
+  };
+  const int lo = lane * 16;
+  auto load_frags = [&](const uint8_t* sa, const uint8_t* sb, int opa, int opb) {
+    Frags f;
+    f.a0 = ld_frag(sa + opa * kBlocks * kFrag + (2 * wm) * kFrag + lo);
+    f.a1 = ld_frag(sa + opa * kBlocks * kFrag + (2 * wm + 1) * kFrag + lo);
+    f.b0 = ld_frag(sb + opb * kBlocks * kFrag + (2 * wn) * kFrag + lo);
+    f.b1 = ld_frag(sb + opb * kBlocks * kFrag + (2 * wn + 1) * kFrag + lo);
+    return f;
+  };
+  auto mfma4 = [&](const Frags& f, int set) {
+    if constexpr (kAlgo == 8) {
+      // The cubic's 256 accumulator registers fit the AGPR file: compiler
+      // builtins (with the compiler's own hazard handling).
+      acc[set][0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a0, f.b0, acc[set][0][0], 0, 0, 0);
+      acc[set][0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a0, f.b1, acc[set][0][1], 0, 0, 0);
+      acc[set][1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1, f.b0, acc[set][1][0], 0, 0, 0);
+      acc[set][1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1, f.b1, acc[set][1][1], 0, 0, 0);
+      return;
+    }
+    // Strassen: accumulator sets 0-3 live in AGPRs and 4-6 in VGPRs (pinned
+    // through the operand constraint), so 448 accumulator registers never
+    // move between the two files.
+    if (set < 4) {
+      mfma_agpr(acc[set][0][0], f.a0, f.b0);
+      mfma_agpr(acc[set][0][1], f.a0, f.b1);
+      mfma_agpr(acc[set][1][0], f.a1, f.b0);
+      mfma_agpr(acc[set][1][1], f.a1, f.b1);
+    } else {
+      mfma_vgpr(acc[set][0][0], f.a0, f.b0);
+      mfma_vgpr(acc[set][0][1], f.a0, f.b1);
+      mfma_vgpr(acc[set][1][0], f.a1, f.b0);
+      mfma_vgpr(acc[set][1][1], f.a1, f.b1);
+    }
+  };
+  auto mma = [&](const uint8_t* sa, const uint8_t* sb) {
+    if constexpr (kAlgo == 8) {
+      // Cubic (products a0b0 a0b1 a2b0 a2b1 a1b2 a1b3 a3b2 a3b3,
+      // benchmark_cubic_control.py:96-106), one K half at a time: A
+      // quadrants (top, bottom) x B quadrants (left, right), every fragment
+      // feeding two MFMAs. All 16 reads are issued before the first MFMA.
+      const Frags h0t = load_frags(sa, sb, 0, 0), h0b = load_frags(sa, sb, 2, 1);
+      const Frags h1t = load_frags(sa, sb, 1, 2), h1b = load_frags(sa, sb, 3, 3);
+      __builtin_amdgcn_sched_barrier(0);
+      // t: A top quadrant + B left quadrant; b: A bottom + B right.
+      auto half = [&](const Frags& t, const Frags& b) {
+        mfma4(Frags{t.a0, t.a1, t.b0, t.b1}, 0);
+        mfma4(Frags{t.a0, t.a1, b.b0, b.b1}, 1);
+        mfma4(Frags{b.a0, b.a1, t.b0, t.b1}, 2);
+        mfma4(Frags{b.a0, b.a1, b.b0, b.b1}, 3);
+      };
+      half(h0t, h0b);
+      half(h1t, h1b);
+      return;
+    }
+    // Strassen products in issue order P4 P6 P5 P2 P7 P3 P1
+    // (strassen_pallas.py:556-565) as operand / accumulator index p-1; the
+    // next product's fragments load while the current product's MFMAs run.
+    constexpr int kOrder[7] = {3, 5, 4, 1, 6, 2, 0};
+    Frags cur = load_frags(sa, sb, kOrder[0], kOrder[0]);
+#pragma unroll
+    for (int x = 0; x < 7; ++x) {
+      Frags next;
+      if (x + 1 < 7) next = load_frags(sa, sb, kOrder[x + 1], kOrder[x + 1]);
+      mfma4(cur, kOrder[x]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (x + 1 < 7) cur = next;
+    }
+  };
+
+  // Prologue: stages 0..kASlots-2 of A and 0..1 of B.
+  dma(a_src, 0, a_region);
+  dma(b_src, 0, b_region);
+  if constexpr (L::kASlots == 3) dma(a_src, 1, a_region + L::kStage);
+  dma(b_src, 1, b_region + L::kStage);
+  stage_barrier<L::kPending>();
+
+  // Stage s: prefetch, MFMAs on stage s, barrier. The prefetched slots were
+  // last read at stage s-1, which every wave finished before the previous
+  // barrier. The host guarantees nstages >= 1; a do-while leaves no zero-trip
+  // path whose register assignment would need reconciling copies.
+  int s = 0, a_slot = 0, b_slot = 0;
+  do {
+    const int b_next = b_slot == 0 ? 2 : b_slot - 1;  // (s + 2) % 3
+    if constexpr (L::kASlots == 3) {
+      const int a_next = a_slot == 0 ? 2 : a_slot - 1;  // (s + 2) % 3
+      dma(a_src, s + 2, a_region + a_next * L::kStage);
+    } else {
+      dma(a_src, s + 1, a_region + (a_slot ^ 1) * L::kStage);
+    }
+    dma(b_src, s + 2, b_region + b_next * L::kStage);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(a_region + a_slot * L::kStage, b_region + b_slot * L::kStage);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_barrier<L::kPending>();
+    b_slot = b_slot == 2 ? 0 : b_slot + 1;
+    if constexpr (L::kASlots == 3)
+      a_slot = a_slot == 2 ? 0 : a_slot + 1;
+    else
+      a_slot ^= 1;
+  } while (++s < nstages);
+  // Let the (unread) prefetches past the last stage land before the
+  // workgroup can finish.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // The drain also pins every accumulator in its register file up to this
+  // point, so the allocator cannot copy them out early.
+  mfma_drain(acc);
+  epilogue<kAlgo, 2, 2, kEpi>(p, o, wm * 64, wn * 64, acc);
+}
+
+// Packs one operand. kSide 0: A [m, k] row-major, product row R = (tile i,
+// row r < bm/2) -> physical rows i*bm + r (top) and + bm/2 (bottom).
+// kSide 1: B^T [n, k] row-major, product column C = (tile j, c < bn/2) ->
+// rows j*bn + c (left) and + bn/2 (right) of B^T. Product depth k' = (panel
+// s, kk < bk/2) -> columns s*bk + kk and + bk/2. Quadrants: A0 = (top, k
+// left), A1 = (top, k right), A2 = (bottom, k left), A3 = (bottom, k right);
+// B0 = (k top, left), B1 = (k top, right), B2 = (k bottom, left),
+// B3 = (k bottom, right) (strassen_pallas.py:188-204). One wave packs one
+// 32-row product block over kPackStages stages: each lane loads 16 bytes of
+// each quadrant per stage and stores nops 16-byte chunks, so the stores of
+// a wave are whole 1 KB fragments.
+template <int kAlgo, int kSide>
+__global__ __launch_bounds__(256) void pack_operand(const uint16_t* __restrict__ src, int64_t ld, int64_t rows,
+                                                    int64_t k, int32_t tile_rows, int32_t bk,
+                                                    uint8_t* __restrict__ out) {
+  constexpr int nops = nops_of(kAlgo);
+  const int lane = threadIdx.x & 63;
+  const int64_t gwave = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+  const int64_t nstages = k / (2 * TK);
+  const int64_t sgroups = (nstages + kPackStages - 1) / kPackStages;
+  const int64_t rblock = gwave / sgroups;  // 32-row product block
+  if (rblock >= rows / 64) return;
+  const int64_t sg = gwave - rblock * sgroups;
+  const int hr = tile_rows / 2, hk = bk / 2;
+  const int64_t r = rblock * 32 + (lane & 31);
+  const uint16_t* const first = src + ((r / hr) * tile_rows + r % hr) * ld;
+  const uint16_t* const second = first + (int64_t)hr * ld;
+  const int half = lane >> 5;
+  uint8_t* const dst_tile = out + frag_offset(rblock / 4, 0, nstages, 0, nops, (int)(rblock % 4)) + lane * 16;
+#pragma unroll
+  for (int j = 0; j < kPackStages; ++j) {
+    const int64_t st = sg * kPackStages + j;
+    if (st >= nstages) break;
+    const int64_t kp = st * TK + half * 8;
+    const int64_t lo = (kp / hk) * bk + kp % hk, hi = lo + hk;
+    u32x4 q[4];
+    if constexpr (kSide == 0) {
+      q[0] = *reinterpret_cast<const u32x4*>(first + lo);
+      q[1] = *reinterpret_cast<const u32x4*>(first + hi);
+      q[2] = *reinterpret_cast<const u32x4*>(second + lo);
+      q[3] = *reinterpret_cast<const u32x4*>(second + hi);
+    } else {
+      q[0] = *reinterpret_cast<const u32x4*>(first + lo);
+      q[1] = *reinterpret_cast<const u32x4*>(second + lo);
+      q[2] = *reinterpret_cast<const u32x4*>(first + hi);
+      q[3] = *reinterpret_cast<const u32x4*>(second + hi);
+    }
+    uint8_t* const dst = dst_tile + st * (int64_t)(nops * kBlocks * kFrag);
+    if constexpr (kAlgo == 7) {
+      u32x4 ops[7];
+      if constexpr (kSide == 0)
+        strassen_a_ops(q, ops);
+      else
+        strassen_b_ops(q, ops);
+#pragma unroll
+      for (int op = 0; op < 7; ++op) *reinterpret_cast<u32x4*>(dst + op * kBlocks * kFrag) = ops[op];
+    } else {
+#pragma unroll
+      for (int op = 0; op < 4; ++op) *reinterpret_cast<u32x4*>(dst + op * kBlocks * kFrag) = q[op];
+    }
+  }
+}
+
+}  // namespace packed
+}  // namespace smx

@@ -22,23 +22,23 @@
 //   C0 = P1 + P4 - P5 + P7, C1 = P3 + P5, C2 = P2 + P4, C3 = P1 - P2 + P3 + P6.
 //
 // Kernels:
-//   v2 (kernel_v2.hpp): 128x128 product-space tiles, 64x64 waves, pipelined
-//      double-buffered LDS. Strassen reads a pre-summed weight
-//      (smx_strassen_weight_layout) and forms the A sums in registers; the
-//      cubic reads raw B^T. The default for both algorithms.
-//   v1 (kernel_v1.hpp): 128x64 tiles, both operand sums formed in registers;
-//      serves Strassen with a plain weight, and the cubic with
-//      SMX_FLAG_COMPACT_TILE.
+//   packed (kernel_packed.hpp): 128x128 product-space tiles, 64x64 waves,
+//      both operands pre-packed (smx_pack_operand: the Strassen operand sums
+//      or the cubic quadrants, in MFMA fragment order) and streamed into an
+//      LDS ring by DMA. The default for both algorithms.
+//   v1 (kernel_v1.hpp): 128x64 tiles, row-major A and B^T, both operand sums
+//      formed in registers; serves unpacked calls.
 
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "common.hpp"
 #include "kernel_v1.hpp"
-#include "kernel_v2.hpp"
+#include "kernel_packed.hpp"
 
 namespace smx {
 namespace {
@@ -61,6 +61,17 @@ int set_lds(K kern, int bytes) {
   return SMX_OK;
 }
 
+// Tile rows per rasterization group; SMX_GROUP_M overrides the default for
+// tuning sweeps.
+int group_m_setting() {
+  static const int value = [] {
+    const char* env = getenv("SMX_GROUP_M");
+    const int v = env ? atoi(env) : 0;
+    return v > 0 ? v : 8;
+  }();
+  return value;
+}
+
 int check_launch() {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SMX_ERR_LAUNCH, "kernel launch: %s", hipGetErrorString(e));
@@ -71,6 +82,7 @@ template <class C, int kEpi>
 int launch_v1(Params p, hipStream_t stream) {
   p.tiles_m = (int)((p.m / 2) / C::TM);
   p.tiles_n = (int)((p.n / 2) / C::TN);
+  p.group_m = group_m_setting();
   auto kern = v1::gemm_v1<C, kEpi>;
   if (int rc = set_lds(kern, C::kLds)) return rc;
   hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n), dim3(kThreads), C::kLds, stream, p);
@@ -78,12 +90,14 @@ int launch_v1(Params p, hipStream_t stream) {
 }
 
 template <int kAlgo, int kEpi>
-int launch_v2(Params p, hipStream_t stream) {
-  p.tiles_m = (int)((p.m / 2) / v2::TM);
-  p.tiles_n = (int)((p.n / 2) / v2::TN);
-  auto kern = v2::gemm_v2<kAlgo, kEpi>;
-  if (int rc = set_lds(kern, v2::Lay<kAlgo>::kLds)) return rc;
-  hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n), dim3(kThreads), v2::Lay<kAlgo>::kLds, stream, p);
+int launch_packed(Params p, hipStream_t stream) {
+  p.tiles_m = (int)((p.m / 2) / packed::TM);
+  p.tiles_n = (int)((p.n / 2) / packed::TN);
+  p.group_m = group_m_setting();
+  auto kern = packed::gemm_packed<kAlgo, kEpi>;
+  constexpr int lds = packed::Lay<kAlgo>::kLds;
+  if (int rc = set_lds(kern, lds)) return rc;
+  hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n), dim3(kThreads), lds, stream, p);
   return check_launch();
 }
 
@@ -100,31 +114,23 @@ int dispatch_v1(const Params& p, int epilogue, hipStream_t s) {
 }
 
 template <int kAlgo>
-int dispatch_v2(const Params& p, int epilogue, hipStream_t s) {
+int dispatch_packed(const Params& p, int epilogue, hipStream_t s) {
   switch (epilogue) {
-    case SMX_EPI_NONE: return launch_v2<kAlgo, SMX_EPI_NONE>(p, s);
-    case SMX_EPI_SWIGLU: return launch_v2<kAlgo, SMX_EPI_SWIGLU>(p, s);
-    case SMX_EPI_RESIDUAL_ADD: return launch_v2<kAlgo, SMX_EPI_RESIDUAL_ADD>(p, s);
-    case SMX_EPI_BIAS_ADD: return launch_v2<kAlgo, SMX_EPI_BIAS_ADD>(p, s);
-    case SMX_EPI_QK_NORM_ROPE: return launch_v2<kAlgo, SMX_EPI_QK_NORM_ROPE>(p, s);
+    case SMX_EPI_NONE: return launch_packed<kAlgo, SMX_EPI_NONE>(p, s);
+    case SMX_EPI_SWIGLU: return launch_packed<kAlgo, SMX_EPI_SWIGLU>(p, s);
+    case SMX_EPI_RESIDUAL_ADD: return launch_packed<kAlgo, SMX_EPI_RESIDUAL_ADD>(p, s);
+    case SMX_EPI_BIAS_ADD: return launch_packed<kAlgo, SMX_EPI_BIAS_ADD>(p, s);
+    case SMX_EPI_QK_NORM_ROPE: return launch_packed<kAlgo, SMX_EPI_QK_NORM_ROPE>(p, s);
   }
   return fail(SMX_ERR_INVALID, "unknown epilogue %d", epilogue);
 }
 
-// Which kernel serves a call: v2 unless the weight is plain and the
-// algorithm is Strassen, or the caller asked for the compact tile.
-bool uses_v2(int algo, int b_layout, int flags) {
-  if (algo == SMX_ALGO_STRASSEN) return b_layout == SMX_B_PRESUMMED;
-  return !(flags & SMX_FLAG_COMPACT_TILE);
-}
-
-void tile_of_path(bool v2path, int epilogue, int32_t* tm, int32_t* tn, int32_t* tk) {
-  if (v2path) {
-    *tm = v2::TM;
-    *tn = v2::TN;
-    *tk = v2::TK;
-  } else {
-    (void)epilogue;  // both v1 configurations are 128 x 64 x 32
+void tile_of_path(bool packed_path, int32_t* tm, int32_t* tn, int32_t* tk) {
+  if (packed_path) {
+    *tm = packed::TM;
+    *tn = packed::TN;
+    *tk = packed::TK;
+  } else {  // both v1 configurations are 128 x 64 x 32
     *tm = v1::General<7>::TM;
     *tn = v1::General<7>::TN;
     *tk = v1::General<7>::TK;
@@ -133,31 +139,16 @@ void tile_of_path(bool v2path, int epilogue, int32_t* tm, int32_t* tn, int32_t* 
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
-// Pre-summed Strassen weight: out[(pcol*7 + op), kprod] = T_op, the seven B
-// operands of P1..P7 (strassen_b_ops) for product-space column pcol and
-// product-space depth kprod, from B^T [N, K]. One thread per 8 consecutive
-// kprod of one pcol.
-__global__ __launch_bounds__(256) void strassen_weight_kernel(const uint16_t* __restrict__ bt, int64_t n, int64_t k,
-                                                              int64_t ldb, int32_t bn, int32_t bk,
-                                                              uint16_t* __restrict__ out, int64_t ldo) {
-  const int64_t chunks_per_row = (k / 2) / 8;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (n / 2) * chunks_per_row) return;
-  const int64_t pcol = idx / chunks_per_row;
-  const int64_t kprod = (idx % chunks_per_row) * 8;
-  const int hn = bn / 2, hk = bk / 2;
-  const int64_t tj = pcol / hn, c = pcol % hn;
-  const int64_t panel = kprod / hk, kk = kprod % hk;
-  u32x4 q[4];
-#pragma unroll
-  for (int quad = 0; quad < 4; ++quad) {
-    const int kh = quad >> 1, nh = quad & 1;  // b quadrant = (K half, N half)
-    q[quad] = *reinterpret_cast<const u32x4*>(bt + (tj * bn + nh * hn + c) * ldb + panel * bk + kh * hk + kk);
-  }
-  u32x4 ops[7];
-  strassen_b_ops(q, ops);
-#pragma unroll
-  for (int op = 0; op < 7; ++op) *reinterpret_cast<u32x4*>(out + (pcol * 7 + op) * ldo + kprod) = ops[op];
+template <int kAlgo, int kSide>
+int launch_pack(const uint16_t* src, int64_t ld, int64_t rows, int64_t k, int32_t tile_rows, int32_t bk, uint8_t* out,
+                hipStream_t stream) {
+  const int64_t nstages = k / (2 * packed::TK);
+  const int64_t waves = (rows / 64) * ((nstages + packed::kPackStages - 1) / packed::kPackStages);
+  const int64_t blocks = (waves + 3) / 4;
+  if (blocks >= ((int64_t)1 << 31)) return fail(SMX_ERR_UNSUPPORTED, "operand too large to pack");
+  hipLaunchKernelGGL((packed::pack_operand<kAlgo, kSide>), dim3((unsigned)blocks), dim3(256), 0, stream, src, ld, rows,
+                     k, tile_rows, bk, out);
+  return check_launch();
 }
 
 }  // namespace
@@ -174,16 +165,48 @@ const char* smx_last_error(void) { return g_error; }
 int smx_tile_requirements(int32_t algo, int32_t epilogue, int32_t b_layout, int32_t flags, int32_t* tm, int32_t* tn,
                           int32_t* tk) {
   g_error[0] = 0;
+  (void)epilogue;
   if (algo != SMX_ALGO_STRASSEN && algo != SMX_ALGO_CUBIC) return fail(SMX_ERR_INVALID, "algo must be 7 or 8");
-  if (b_layout != SMX_B_KCONTIG && b_layout != SMX_B_PRESUMMED) return fail(SMX_ERR_INVALID, "unknown b_layout");
-  if (algo == SMX_ALGO_CUBIC && b_layout == SMX_B_PRESUMMED)
-    return fail(SMX_ERR_INVALID, "the cubic control takes a plain weight");
+  if (b_layout != SMX_B_KCONTIG && b_layout != SMX_B_PACKED) return fail(SMX_ERR_INVALID, "unknown b_layout");
+  if (flags) return fail(SMX_ERR_INVALID, "flags must be 0");
   int32_t a, b, c;
-  tile_of_path(uses_v2(algo, b_layout, flags), epilogue, &a, &b, &c);
+  tile_of_path(b_layout == SMX_B_PACKED, &a, &b, &c);
   if (tm) *tm = a;
   if (tn) *tn = b;
   if (tk) *tk = c;
   return SMX_OK;
+}
+
+int smx_packed_bytes(int32_t algo, int64_t rows, int64_t k, int64_t* bytes) {
+  g_error[0] = 0;
+  if (algo != SMX_ALGO_STRASSEN && algo != SMX_ALGO_CUBIC) return fail(SMX_ERR_INVALID, "algo must be 7 or 8");
+  if (rows <= 0 || k <= 0 || rows % 2 || k % 2) return fail(SMX_ERR_INVALID, "rows and k must be positive and even");
+  if (!bytes) return fail(SMX_ERR_INVALID, "null output");
+  *bytes = (rows / 2) * (k / 2) * packed::nops_of(algo) * 2;
+  return SMX_OK;
+}
+
+int smx_pack_operand(int32_t algo, int32_t side, int64_t rows, int64_t k, const void* src, int64_t ld,
+                     int32_t tile_rows, int32_t bk, void* out, void* stream) {
+  g_error[0] = 0;
+  if (algo != SMX_ALGO_STRASSEN && algo != SMX_ALGO_CUBIC) return fail(SMX_ERR_INVALID, "algo must be 7 or 8");
+  if (side != SMX_SIDE_LHS && side != SMX_SIDE_RHS) return fail(SMX_ERR_INVALID, "side must be LHS (0) or RHS (1)");
+  if (rows <= 0 || k <= 0 || tile_rows <= 0 || bk <= 0 || rows % tile_rows || k % bk)
+    return fail(SMX_ERR_INVALID, "packing needs rows %% tile_rows == 0 and K %% bk == 0");
+  if (tile_rows % (2 * packed::TM) || bk % (2 * packed::TK))
+    return fail(SMX_ERR_UNSUPPORTED, "packed tiles need %s %% %d == 0 and bk %% %d == 0 (got %d, %d)",
+                side == SMX_SIDE_LHS ? "bm" : "bn", 2 * packed::TM, 2 * packed::TK, tile_rows, bk);
+  if (!src || !out) return fail(SMX_ERR_INVALID, "null pointer");
+  if (!aligned16(src) || !aligned16(out)) return fail(SMX_ERR_INVALID, "pointers must be 16-byte aligned");
+  if (ld < k || ld % 8) return fail(SMX_ERR_INVALID, "ld must be >= K and a multiple of 8");
+  const uint16_t* s16 = (const uint16_t*)src;
+  uint8_t* o8 = (uint8_t*)out;
+  hipStream_t st = (hipStream_t)stream;
+  if (algo == SMX_ALGO_STRASSEN)
+    return side == SMX_SIDE_LHS ? launch_pack<7, 0>(s16, ld, rows, k, tile_rows, bk, o8, st)
+                                : launch_pack<7, 1>(s16, ld, rows, k, tile_rows, bk, o8, st);
+  return side == SMX_SIDE_LHS ? launch_pack<8, 0>(s16, ld, rows, k, tile_rows, bk, o8, st)
+                              : launch_pack<8, 1>(s16, ld, rows, k, tile_rows, bk, o8, st);
 }
 
 int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, const void* residual, const void* bias,
@@ -193,19 +216,21 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
   if (d->algo != SMX_ALGO_STRASSEN && d->algo != SMX_ALGO_CUBIC)
     return fail(SMX_ERR_INVALID, "algo must be %d (Strassen) or %d (cubic), got %d", SMX_ALGO_STRASSEN,
                 SMX_ALGO_CUBIC, d->algo);
-  if (d->b_layout != SMX_B_KCONTIG && d->b_layout != SMX_B_PRESUMMED)
-    return fail(SMX_ERR_UNSUPPORTED, "b_layout must be SMX_B_KCONTIG or SMX_B_PRESUMMED, got %d", d->b_layout);
-  if (d->algo == SMX_ALGO_CUBIC && d->b_layout == SMX_B_PRESUMMED)
-    return fail(SMX_ERR_INVALID, "the cubic control takes a plain weight");
-  if (d->flags & ~SMX_FLAG_COMPACT_TILE) return fail(SMX_ERR_INVALID, "unknown flags 0x%x", d->flags);
+  if (d->a_layout != SMX_A_ROWMAJOR && d->a_layout != SMX_A_PACKED)
+    return fail(SMX_ERR_INVALID, "a_layout must be SMX_A_ROWMAJOR or SMX_A_PACKED, got %d", d->a_layout);
+  if (d->b_layout != SMX_B_KCONTIG && d->b_layout != SMX_B_PACKED)
+    return fail(SMX_ERR_INVALID, "b_layout must be SMX_B_KCONTIG or SMX_B_PACKED, got %d", d->b_layout);
+  const bool packed_path = d->b_layout == SMX_B_PACKED;
+  if (packed_path != (d->a_layout == SMX_A_PACKED))
+    return fail(SMX_ERR_UNSUPPORTED, "A and B must both be packed (smx_pack_operand) or both unpacked");
+  if (d->flags) return fail(SMX_ERR_INVALID, "flags must be 0, got 0x%x", d->flags);
   if (d->m <= 0 || d->n <= 0 || d->k <= 0)
     return fail(SMX_ERR_INVALID, "empty problem m=%lld n=%lld k=%lld", (long long)d->m, (long long)d->n,
                 (long long)d->k);
   if (d->bm <= 0 || d->bn <= 0 || d->bk <= 0 || d->m % d->bm || d->n % d->bn || d->k % d->bk)
     return fail(SMX_ERR_INVALID, "M, N, K must be divisible by bm, bn, bk");
-  const bool v2path = uses_v2(d->algo, d->b_layout, d->flags);
   int32_t tm, tn, tk;
-  tile_of_path(v2path, d->epilogue, &tm, &tn, &tk);
+  tile_of_path(packed_path, &tm, &tn, &tk);
   const int hm = d->bm / 2, hn = d->bn / 2, hk = d->bk / 2;
   if (d->bm % 2 || d->bn % 2 || d->bk % 2 || hm % tm || hn % tn || hk % tk)
     return fail(SMX_ERR_UNSUPPORTED,
@@ -213,10 +238,8 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
                 d->bm, d->bn, d->bk, 2 * tm, 2 * tn, 2 * tk);
   if (!a || !b || !c) return fail(SMX_ERR_INVALID, "null operand pointer");
   if (!aligned16(a) || !aligned16(b)) return fail(SMX_ERR_INVALID, "A and B must be 16-byte aligned");
-  const int64_t b_row = d->b_layout == SMX_B_PRESUMMED ? d->k / 2 : d->k;
-  if (d->lda < d->k || d->ldb < b_row || d->lda % 8 || d->ldb % 8)
-    return fail(SMX_ERR_INVALID, "lda must be >= K, ldb >= %s, both multiples of 8 elements",
-                d->b_layout == SMX_B_PRESUMMED ? "K/2" : "K");
+  if (!packed_path && (d->lda < d->k || d->ldb < d->k || d->lda % 8 || d->ldb % 8))
+    return fail(SMX_ERR_INVALID, "lda and ldb must be >= K and multiples of 8 elements");
   const int64_t out_cols = d->epilogue == SMX_EPI_SWIGLU ? d->n / 2 : d->n;
   if (d->ldc < out_cols) return fail(SMX_ERR_INVALID, "ldc must be >= output width");
   // The epilogue addresses a tile half with 32-bit element offsets.
@@ -270,25 +293,10 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
       return fail(SMX_ERR_INVALID, "unknown epilogue %d", d->epilogue);
   }
   hipStream_t s = (hipStream_t)stream;
-  if (v2path)
-    return d->algo == SMX_ALGO_STRASSEN ? dispatch_v2<7>(p, d->epilogue, s) : dispatch_v2<8>(p, d->epilogue, s);
+  if (packed_path)
+    return d->algo == SMX_ALGO_STRASSEN ? dispatch_packed<7>(p, d->epilogue, s)
+                                        : dispatch_packed<8>(p, d->epilogue, s);
   return d->algo == SMX_ALGO_STRASSEN ? dispatch_v1<7>(p, d->epilogue, s) : dispatch_v1<8>(p, d->epilogue, s);
-}
-
-int smx_strassen_weight_layout(int64_t n, int64_t k, const void* bt, int64_t ldb, int32_t bn, int32_t bk, void* out,
-                               int64_t ldo, void* stream) {
-  g_error[0] = 0;
-  if (n <= 0 || k <= 0 || bn <= 0 || bk <= 0 || bn % 2 || bk % 16 || n % bn || k % bk)
-    return fail(SMX_ERR_INVALID, "weight layout needs N %% bn == 0, K %% bk == 0, bn even, bk %% 16 == 0");
-  if (!bt || !out) return fail(SMX_ERR_INVALID, "null pointer");
-  if (!aligned16(bt) || !aligned16(out)) return fail(SMX_ERR_INVALID, "pointers must be 16-byte aligned");
-  if (ldb < k || ldb % 8 || ldo < k / 2 || ldo % 8)
-    return fail(SMX_ERR_INVALID, "ldb must be >= K and ldo >= K/2, both multiples of 8");
-  const int64_t work = (n / 2) * ((k / 2) / 8);
-  const int64_t blocks = (work + 255) / 256;
-  hipLaunchKernelGGL(strassen_weight_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)bt, n, k, ldb, bn, bk, (uint16_t*)out, ldo);
-  return check_launch();
 }
 
 }  // extern "C"

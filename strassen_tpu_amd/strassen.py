@@ -23,8 +23,7 @@ Differences a caller can observe, all raised as exceptions (never silent):
   the reference) are validated and accepted but select the same kernel.
 * Tiles must additionally satisfy the gfx950 kernels' divisibility rule
   (``smx_tile_requirements``): bm % 256 == 0 always; bn % 128 and bk % 64 for
-  a plain weight; bn % 256 and bk % 32 for a ``StrassenWeight`` and for the
-  cubic control.
+  a plain weight; bn % 256 and bk % 32 for a packed weight.
 """
 
 from __future__ import annotations
@@ -35,7 +34,7 @@ import torch
 
 from . import _lib
 from .layouts import is_k_contiguous
-from .weights import StrassenWeight
+from .packing import PackedOperand, pack_operand
 
 __all__ = [
     "strassen_matmul", "cubic_matmul", "native_matmul", "check_tiling",
@@ -73,8 +72,8 @@ def check_tiling(bm, bn, bk):
         raise ValueError("tile breaks TPU v5e alignment:\n  " + "\n  ".join(errors))
 
 
-def _check_device_tiling(algo, epilogue, bm, bn, bk, b_layout, flags):
-    tm, tn, tk = _lib.tile_requirements(algo, epilogue, b_layout, flags)
+def _check_device_tiling(algo, epilogue, bm, bn, bk, b_layout):
+    tm, tn, tk = _lib.tile_requirements(algo, epilogue, b_layout)
     errors = [
         f"{name}={value} must be a multiple of {multiple}"
         for name, value, multiple in (("bm", bm, 2 * tm), ("bn", bn, 2 * tn), ("bk", bk, 2 * tk))
@@ -224,37 +223,54 @@ def _require_device(*tensors):
                              f"(got a tensor on {t.device})")
 
 
+def _check_packed(x, algo, side, tile_rows, bk):
+    name = "a" if side == "lhs" else "b"
+    if x.algo != algo or x.side != side:
+        raise ValueError(f"{name} was packed as {x!r}, not as the {side} of this algorithm")
+    if (x.tile_rows, x.bk) != (tile_rows, bk):
+        raise ValueError(f"{name} was packed for the tile ({x.tile_rows}, bk={x.bk}), "
+                         f"called with ({tile_rows}, bk={bk})")
+
+
 def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
          rope_cos=None, rope_sin=None, rope_scale=None, rope_head_dim=128,
-         rope_eps=1e-6, flags=0):
+         rope_eps=1e-6):
     lib = _lib.load()
     m, k = a.shape
     n = b.shape[1]
-    presummed = isinstance(b, StrassenWeight)
-    b_layout = _lib.SMX_B_PRESUMMED if presummed else _lib.SMX_B_KCONTIG
-    if presummed and (b.bn, b.bk) != (bn, bk):
-        raise ValueError(f"StrassenWeight was laid out for (bn={b.bn}, bk={b.bk}), "
-                         f"called with (bn={bn}, bk={bk})")
-    _check_device_tiling(algo, epilogue, bm, bn, bk, b_layout, flags)
-    _require_device(a, b.data if presummed else b, residual, bias, rope_cos, rope_sin, rope_scale)
-    if a.stride(1) != 1 or a.stride(0) % 8 or a.data_ptr() % 16:
-        a = a.contiguous()
-    if presummed:
-        bt = b.data  # [N/2*7, K/2]
+    packed = isinstance(b, PackedOperand)
+    if isinstance(a, PackedOperand) and not packed:
+        raise ValueError("a packed activation needs a packed weight (strassen_weight_layout / "
+                         "cubic_weight_layout)")
+    b_layout = _lib.SMX_B_PACKED if packed else _lib.SMX_B_KCONTIG
+    if packed:
+        _check_packed(b, algo, "rhs", bn, bk)
+        if isinstance(a, PackedOperand):
+            _check_packed(a, algo, "lhs", bm, bk)
+    _check_device_tiling(algo, epilogue, bm, bn, bk, b_layout)
+    _require_device(a.data if isinstance(a, PackedOperand) else a, b.data if packed else b,
+                    residual, bias, rope_cos, rope_sin, rope_scale)
+    if packed:
+        if not isinstance(a, PackedOperand):
+            a = pack_operand(a, algo=algo, side="lhs", tile_rows=bm, bk=bk)
+        a_ptr, b_ptr, lda, ldb = a.data, b.data, k, k
     else:
+        if a.stride(1) != 1 or a.stride(0) % 8 or a.data_ptr() % 16:
+            a = a.contiguous()
         if not is_k_contiguous(b) or b.stride(1) % 8 or b.data_ptr() % 16:
             b = b.t().contiguous().t()
         bt = b.t()  # [N, K], rows contiguous
+        a_ptr, b_ptr, lda, ldb = a, bt, a.stride(0), bt.stride(0)
     out_cols = n // 2 if epilogue == "swiglu" else n
     c = torch.empty((m, out_cols), dtype=torch.bfloat16, device=a.device)
     desc = _lib.SmxGemmDesc()
     desc.m, desc.n, desc.k = m, n, k
-    desc.lda, desc.ldb, desc.ldc = a.stride(0), bt.stride(0), c.stride(0)
+    desc.lda, desc.ldb, desc.ldc = lda, ldb, c.stride(0)
     desc.bm, desc.bn, desc.bk = bm, bn, bk
     desc.algo = algo
     desc.epilogue = _lib.SMX_EPI[epilogue]
+    desc.a_layout = _lib.SMX_A_PACKED if packed else _lib.SMX_A_ROWMAJOR
     desc.b_layout = b_layout
-    desc.flags = flags
     desc.rope_head_dim = rope_head_dim
     desc.rope_eps = rope_eps
     aux = 0
@@ -281,7 +297,7 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
             aux |= _lib.SMX_AUX_SCALE_F32
     desc.aux_f32 = aux
     stream = torch.cuda.current_stream(a.device).cuda_stream
-    rc = lib.smx_gemm(desc, _lib.ptr(a), _lib.ptr(bt), _lib.ptr(c), _lib.ptr(residual),
+    rc = lib.smx_gemm(desc, _lib.ptr(a_ptr), _lib.ptr(b_ptr), _lib.ptr(c), _lib.ptr(residual),
                       _lib.ptr(bias), _lib.ptr(rope_cos), _lib.ptr(rope_sin),
                       _lib.ptr(rope_scale), stream)
     _lib.check(rc)
@@ -324,8 +340,11 @@ def strassen_matmul(
     ``b`` is either a tensor, read directly when K-contiguous (``w.t()`` of a
     ``[N, K]`` weight, see ``layouts.k_contiguous``; otherwise transposed on
     each call) and served by the kernel that forms both operand sums in
-    registers; or a ``StrassenWeight`` from ``strassen_weight_layout(b, bn,
-    bk)`` (pre-summed B operands, the faster pipelined kernel). Epilogues and their operands follow ``strassen_pallas.py:739-879``:
+    registers; or a packed weight from ``strassen_weight_layout(b, bn, bk)``
+    (pre-summed B operands), served by the packed kernel after ``a`` is
+    packed with its A sums (or pass ``a`` already packed by
+    ``pack_activation``). Epilogues and their operands follow
+    ``strassen_pallas.py:739-879``:
     ``swiglu`` returns ``[M, N/2]`` from a ``swiglu_weight_layout`` weight,
     ``residual_add`` adds ``residual`` ``[M, N]``, ``bias_add`` adds
     ``bias`` ``[N]``, ``qk_norm_rope`` applies per-head RMSNorm and RoPE with
@@ -351,7 +370,7 @@ def cubic_matmul(a, b, *, variant="blocked", bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_
                  dot_precision=None, allow_input_fusion=None, interpret=False,
                  vmem_limit_bytes=None, epilogue=None, residual=None, bias=None,
                  rope_cos=None, rope_sin=None, rope_scale=None, rope_head_dim=128,
-                 rope_eps=1e-6, compact=False):
+                 rope_eps=1e-6):
     """Matched cubic control (``experiments/qwen3/benchmark_cubic_control.py:116-177``).
 
     Eight half-size products per K panel into four FP32 quadrant
@@ -359,11 +378,11 @@ def cubic_matmul(a, b, *, variant="blocked", bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_
     epilogues. ``variant="full"`` (one full-tile product per panel) computes
     the same cubic GEMM and runs the same kernel. The fused epilogues are an
     extension of the reference control, used to time fused sites against an
-    identical cubic arm. ``compact=True`` selects the compact-tile kernel that
-    matches ``strassen_matmul`` with a plain (not pre-summed) weight.
+    identical cubic arm. A plain ``b`` runs the compact kernel that matches
+    ``strassen_matmul`` with a plain weight; a ``cubic_weight_layout(b, bn,
+    bk)`` weight runs the packed kernel that matches ``strassen_matmul`` with
+    a ``strassen_weight_layout`` weight.
     """
-    if isinstance(b, StrassenWeight):
-        raise ValueError("cubic_matmul takes a plain weight, not a StrassenWeight")
     if variant not in ("full", "blocked"):
         raise ValueError(f"unknown cubic variant {variant!r}")
     if a.dim() != 2 or b.dim() != 2:
@@ -388,8 +407,7 @@ def cubic_matmul(a, b, *, variant="blocked", bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_
         raise NotImplementedError("the gfx950 cubic control takes bf16 inputs")
     return _run(_lib.SMX_ALGO_CUBIC, a, b, bm=bm, bn=bn, bk=bk, epilogue=epilogue,
                 residual=residual, bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
-                rope_scale=rope_scale, rope_head_dim=rope_head_dim, rope_eps=rope_eps,
-                flags=_lib.SMX_FLAG_COMPACT_TILE if compact else 0)
+                rope_scale=rope_scale, rope_head_dim=rope_head_dim, rope_eps=rope_eps)
 
 
 def native_matmul(a, b):

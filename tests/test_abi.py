@@ -37,8 +37,9 @@ def test_version_and_macros_match_header():
     version = int(re.search(r"#define SMX_VERSION (\d+)", header).group(1))
     assert _lib.load().smx_version() == version
     for name in ("SMX_OK", "SMX_ERR_INVALID", "SMX_ERR_UNSUPPORTED", "SMX_ERR_LAUNCH",
-                 "SMX_ALGO_STRASSEN", "SMX_ALGO_CUBIC", "SMX_B_KCONTIG", "SMX_B_PRESUMMED",
-                 "SMX_FLAG_COMPACT_TILE", "SMX_AUX_BIAS_F32", "SMX_AUX_SCALE_F32"):
+                 "SMX_ALGO_STRASSEN", "SMX_ALGO_CUBIC", "SMX_A_ROWMAJOR", "SMX_A_PACKED",
+                 "SMX_B_KCONTIG", "SMX_B_PACKED", "SMX_SIDE_LHS", "SMX_SIDE_RHS",
+                 "SMX_AUX_BIAS_F32", "SMX_AUX_SCALE_F32"):
         value = int(re.search(rf"#define {name} (\d+)", header).group(1))
         assert getattr(_lib, name) == value, name
     for epi, code in _lib.SMX_EPI.items():
@@ -69,6 +70,7 @@ def _desc(**kw):
     d.bm, d.bn, d.bk = 256, 256, 128
     d.algo = _lib.SMX_ALGO_STRASSEN
     d.epilogue = 0
+    d.a_layout = _lib.SMX_A_ROWMAJOR
     d.b_layout = _lib.SMX_B_KCONTIG
     d.rope_head_dim = 128
     d.rope_eps = 1e-6
@@ -84,7 +86,10 @@ def _desc(**kw):
     ("bm", 128, _lib.SMX_ERR_UNSUPPORTED),
     ("bn", 64, _lib.SMX_ERR_UNSUPPORTED),
     ("bk", 32, _lib.SMX_ERR_UNSUPPORTED),
-    ("b_layout", 0, _lib.SMX_ERR_UNSUPPORTED),
+    ("b_layout", 0, _lib.SMX_ERR_INVALID),
+    ("a_layout", 5, _lib.SMX_ERR_INVALID),
+    ("a_layout", _lib.SMX_A_PACKED, _lib.SMX_ERR_UNSUPPORTED),  # packed A needs packed B
+    ("b_layout", _lib.SMX_B_PACKED, _lib.SMX_ERR_UNSUPPORTED),  # and vice versa
     ("lda", 100, _lib.SMX_ERR_INVALID),
     ("epilogue", 9, _lib.SMX_ERR_INVALID),
     ("flags", 4, _lib.SMX_ERR_INVALID),
@@ -112,41 +117,44 @@ def test_null_pointers_and_missing_epilogue_operands():
 
 def test_tile_requirements():
     plain = _lib.tile_requirements(_lib.SMX_ALGO_STRASSEN, None, _lib.SMX_B_KCONTIG)
-    summed = _lib.tile_requirements(_lib.SMX_ALGO_STRASSEN, None, _lib.SMX_B_PRESUMMED)
-    cubic = _lib.tile_requirements(_lib.SMX_ALGO_CUBIC, None)
-    compact = _lib.tile_requirements(_lib.SMX_ALGO_CUBIC, None, flags=_lib.SMX_FLAG_COMPACT_TILE)
-    # The plain-weight Strassen kernel and the compact cubic share a tiling;
-    # the pre-summed Strassen kernel and the default cubic share another.
-    assert plain == compact and summed == cubic
-    for tm, tn, tk in (plain, summed):
-        assert tm > 0 and tn > 0 and tk % 16 == 0
+    packed = _lib.tile_requirements(_lib.SMX_ALGO_STRASSEN, None, _lib.SMX_B_PACKED)
+    # Both algorithms share each kernel's tiling.
+    assert plain == _lib.tile_requirements(_lib.SMX_ALGO_CUBIC, None, _lib.SMX_B_KCONTIG)
+    assert packed == _lib.tile_requirements(_lib.SMX_ALGO_CUBIC, None, _lib.SMX_B_PACKED)
+    assert packed == (128, 128, 16) and plain == (128, 64, 32)
     with pytest.raises(ValueError):
         _lib.tile_requirements(3, None)
     with pytest.raises(ValueError):
-        _lib.tile_requirements(_lib.SMX_ALGO_CUBIC, None, _lib.SMX_B_PRESUMMED)
+        _lib.tile_requirements(_lib.SMX_ALGO_CUBIC, None, 7)
 
 
-def test_pre_summed_layout_requires_strassen():
+def test_packed_bytes():
     lib = _lib.load()
-    buf = (ctypes.c_uint8 * 16)()
-    p = ctypes.cast(buf, ctypes.c_void_p)
-    d = _desc(algo=_lib.SMX_ALGO_CUBIC, b_layout=_lib.SMX_B_PRESUMMED)
-    assert lib.smx_gemm(d, p, p, p, None, None, None, None, None, None) == _lib.SMX_ERR_INVALID
+    out = ctypes.c_int64()
+    assert lib.smx_packed_bytes(7, 512, 256, ctypes.byref(out)) == _lib.SMX_OK
+    assert out.value == 256 * 128 * 7 * 2
+    assert lib.smx_packed_bytes(8, 512, 256, ctypes.byref(out)) == _lib.SMX_OK
+    assert out.value == 512 * 256 * 2
+    assert lib.smx_packed_bytes(5, 512, 256, ctypes.byref(out)) == _lib.SMX_ERR_INVALID
+    assert lib.smx_packed_bytes(7, 511, 256, ctypes.byref(out)) == _lib.SMX_ERR_INVALID
 
 
-@pytest.mark.parametrize("args", [
-    (0, 512, 512, 256, 512),      # n = 0
-    (512, 512, 512, 256, 500),    # k % bk
-    (512, 512, 512, 255, 512),    # odd bn
-    (512, 512, 512, 256, 24),     # bk % 16
-    (512, 512, 100, 256, 512),    # ldb < k
+@pytest.mark.parametrize("args,code", [
+    ((7, 0, 0, 512, 512, 256, 512), _lib.SMX_ERR_INVALID),        # rows = 0
+    ((7, 0, 512, 512, 512, 256, 500), _lib.SMX_ERR_INVALID),      # k % bk
+    ((7, 2, 512, 512, 512, 256, 512), _lib.SMX_ERR_INVALID),      # side
+    ((6, 0, 512, 512, 512, 256, 512), _lib.SMX_ERR_INVALID),      # algo
+    ((7, 0, 512, 512, 512, 128, 512), _lib.SMX_ERR_UNSUPPORTED),  # tile_rows % 256
+    ((8, 1, 512, 512, 512, 256, 48), _lib.SMX_ERR_INVALID),       # k % bk
+    ((8, 1, 512, 480, 480, 256, 48), _lib.SMX_ERR_UNSUPPORTED),   # bk % 32
+    ((7, 0, 512, 512, 100, 256, 512), _lib.SMX_ERR_INVALID),      # ld < k
 ])
-def test_weight_layout_rejects_bad_arguments(args):
-    n, k, ldb, bn, bk = args
+def test_pack_operand_rejects_bad_arguments(args, code):
+    algo, side, rows, k, ld, tile_rows, bk = args
     lib = _lib.load()
     buf = (ctypes.c_uint8 * 16)()
     p = ctypes.cast(buf, ctypes.c_void_p)
-    assert lib.smx_strassen_weight_layout(n, k, p, ldb, bn, bk, p, k // 2 if k else 8, None) == _lib.SMX_ERR_INVALID
+    assert lib.smx_pack_operand(algo, side, rows, k, p, ld, tile_rows, bk, p, None) == code
     assert _lib.last_error()
 
 

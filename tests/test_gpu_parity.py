@@ -88,10 +88,11 @@ def rel_l2(got, ref):
     return float(np.linalg.norm(np.asarray(got, np.float64) - ref) / np.linalg.norm(ref))
 
 
-# The four kernels behind the surface: Strassen with a plain weight (both
-# operand sums in registers), Strassen with a pre-summed weight, the cubic
-# control, and the cubic control on the plain-weight Strassen tiling.
-ARMS = ("strassen_plain", "strassen_presummed", "cubic", "cubic_compact")
+# The four kernels behind the surface: Strassen and the cubic control with a
+# plain weight (the compact kernel: operand sums / quadrants read from
+# row-major A and B^T), and both with packed operands (the packed kernel:
+# weight packed offline, activation packed per call).
+ARMS = ("strassen_plain", "strassen_packed", "cubic_plain", "cubic_packed")
 
 
 def run_arm(arm, a, b, *, bm, bn, bk, **kw):
@@ -102,13 +103,15 @@ def run_arm(arm, a, b, *, bm, bn, bk, **kw):
     b_dev = b if torch.is_tensor(b) else dev_weight(b)
     if arm == "strassen_plain":
         return smx.strassen_matmul(a_dev, b_dev, bm=bm, bn=bn, bk=bk, **kw)
-    if arm == "strassen_presummed":
+    if arm == "strassen_packed":
         w = smx.strassen_weight_layout(b_dev, bn, bk)
         return smx.strassen_matmul(a_dev, w, bm=bm, bn=bn, bk=bk, **kw)
     kw.pop("interleave_products", None)
     kw.pop("product_aware_swiglu", None)
     kw.pop("product_aware_residual", None)
-    return smx.cubic_matmul(a_dev, b_dev, bm=bm, bn=bn, bk=bk, compact=(arm == "cubic_compact"), **kw)
+    if arm == "cubic_packed":
+        b_dev = smx.cubic_weight_layout(b_dev, bn, bk)
+    return smx.cubic_matmul(a_dev, b_dev, bm=bm, bn=bn, bk=bk, **kw)
 
 
 def oracle_arm(arm, a, b, **kw):
@@ -150,15 +153,22 @@ def test_integer_kat_bit_exact(shape, tile, arm):
     assert np.array_equal(got, o.bf16_round(a @ b))
 
 
-def test_weight_layout_kernel_matches_oracle():
+@pytest.mark.parametrize("algo", [7, 8])
+def test_pack_kernel_matches_oracle(algo):
     rng = np.random.default_rng(5)
-    for (k, n), (bn, bk) in (((1024, 768), (256, 512)), ((512, 1024), (1024, 256))):
-        b = o.bf16_round(rng.standard_normal((k, n)).astype(np.float32))
-        w = smx.strassen_weight_layout(dev_weight(b), bn, bk)
-        assert tuple(w.data.shape) == (n // 2 * 7, k // 2)
-        assert np.array_equal(host(w.data), o.strassen_weight_layout(b, bn, bk))
-        # a row-major weight gives the same layout
-        w2 = smx.strassen_weight_layout(dev(b), bn, bk)
+    # (rows x K of the operand, tile_rows, bk): several tiles and K panels,
+    # and a K panel wider than one pack wave's four stages.
+    for (rows, k), (tile, bk) in (((1024, 1024), (512, 512)), ((512, 768), (256, 256)),
+                                  ((768, 4160), (256, 320))):
+        say(f"  algo={algo} rows={rows} k={k} tile={tile} bk={bk}")
+        a = o.bf16_round(rng.standard_normal((rows, k)).astype(np.float32))
+        got = smx.pack_activation(dev(a), algo, tile, bk)
+        assert np.array_equal(host(got.data), o.packed_operand(a, algo, "lhs", tile, bk))
+        b = o.bf16_round(rng.standard_normal((k, rows)).astype(np.float32))
+        w = smx.pack_operand(dev_weight(b), algo=algo, side="rhs", tile_rows=tile, bk=bk)
+        assert np.array_equal(host(w.data), o.packed_operand(b, algo, "rhs", tile, bk))
+        # a row-major weight gives the same packing
+        w2 = smx.pack_operand(dev(b), algo=algo, side="rhs", tile_rows=tile, bk=bk)
         assert torch.equal(w.data, w2.data)
     with pytest.raises(ValueError, match="does not tile"):
         smx.strassen_weight_layout(dev(np.zeros((500, 256), np.float32)), 256, 512)
@@ -350,12 +360,14 @@ def test_qwen3_32b_shapes_sampled_tiles(site):
     say(f"  {site} m={m} k={k} n={n}")
     got = smx.strassen_matmul(a, b, bm=bm, bn=bn, bk=bk, interleave_products=True)
     pre = smx.strassen_matmul(a, smx.strassen_weight_layout(b, bn, bk), bm=bm, bn=bn, bk=bk)
-    cub = smx.cubic_matmul(a, b, bm=bm, bn=bn, bk=bk)
+    cub = smx.cubic_matmul(a, smx.cubic_weight_layout(b, bn, bk), bm=bm, bn=bn, bk=bk)
+    cub_plain = smx.cubic_matmul(a, b, bm=bm, bn=bn, bk=bk)
     torch.cuda.synchronize()
-    # Both Strassen kernels compute the same bf16 operand sums.
+    # The compact and packed kernels compute the same bf16 operand sums.
     e_pre = float(torch.linalg.norm(pre.float() - got.float()) / torch.linalg.norm(got.float()))
-    say(f"  plain vs pre-summed weight rel diff {e_pre:.3e}")
-    assert e_pre < 1e-3
+    e_cub = float(torch.linalg.norm(cub.float() - cub_plain.float()) / torch.linalg.norm(cub.float()))
+    say(f"  compact vs packed rel diff strassen {e_pre:.3e} cubic {e_cub:.3e}")
+    assert e_pre < 1e-3 and e_cub < 1e-3
     # Whole-output bound against an FP32 product computed on the GPU.
     ref = torch.matmul(a.float(), b.float())
     e_s = float(torch.linalg.norm(got.float() - ref) / torch.linalg.norm(ref))

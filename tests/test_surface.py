@@ -92,43 +92,97 @@ def test_cubic_surface_checks():
         smx.cubic_matmul(a, b, variant="sparse")
     with pytest.raises(ValueError, match="not divisible"):
         smx.cubic_matmul(a, b, bm=96, bn=256, bk=512)
-    w = smx.StrassenWeight(t(1, 1), 512, 256, 256, 512)
-    with pytest.raises(ValueError, match="plain weight"):
+    w = smx.PackedOperand(t(1, 1), algo=7, side="rhs", rows=256, k=512, tile_rows=256, bk=512)
+    with pytest.raises(ValueError, match="packed as"):
         smx.cubic_matmul(a, w, bm=256, bn=256, bk=512)
 
 
-def test_strassen_weight_surface():
+def packed_weight(algo=7, n=512, k=512, bn=512, bk=512):
+    return smx.PackedOperand(t(n // 2 * k // 2 * (7 if algo == 7 else 4)), algo=algo, side="rhs",
+                             rows=n, k=k, tile_rows=bn, bk=bk)
+
+
+def test_packed_weight_surface():
     a = t(256, 512)
-    w = smx.StrassenWeight(t(512 // 2 * 7, 256), 512, 512, 512, 512)
+    w = packed_weight()
     assert w.shape == (512, 512) and w.dim() == 2 and w.dtype == torch.bfloat16
-    with pytest.raises(ValueError, match="laid out for"):
+    with pytest.raises(ValueError, match="packed for the tile"):
         smx.strassen_matmul(a, w, bm=256, bn=256, bk=512)
     with pytest.raises(ValueError, match="HIP device"):
         smx.strassen_matmul(a, w, bm=256, bn=512, bk=512)
+    with pytest.raises(ValueError, match="packed as"):
+        smx.strassen_matmul(a, packed_weight(algo=8), bm=256, bn=512, bk=512)
+    with pytest.raises(ValueError, match="needs a packed weight"):
+        pa = smx.PackedOperand(t(1), algo=7, side="lhs", rows=256, k=512, tile_rows=256, bk=512)
+        smx.strassen_matmul(pa, t(512, 512), bm=256, bn=512, bk=512)
     with pytest.raises(ValueError, match="HIP device"):
         smx.strassen_weight_layout(t(512, 256), 256, 512)
     with pytest.raises(ValueError, match="bf16"):
         smx.strassen_weight_layout(t(512, 256, dtype=torch.float32), 256, 512)
 
 
-def test_oracle_weight_layout_brute_force():
+@pytest.mark.parametrize("algo", [7, 8])
+@pytest.mark.parametrize("side", ["lhs", "rhs"])
+def test_oracle_packed_layout_brute_force(algo, side):
+    """Walk every packed position with explicit index arithmetic."""
     import numpy as np
 
     import oracle as o
 
-    rng = np.random.default_rng(0)
-    bn, bk, hn, hk = 16, 32, 8, 16
-    b = o.bf16_round(rng.standard_normal((64, 32)).astype(np.float32))
-    w = o.strassen_weight_layout(b, bn, bk)
-    r = lambda x: o.bf16_round(np.float32(x)).item()
-    for p in range(16):
-        j, c = divmod(p, hn)
-        for kp in range(32):
-            s, kk = divmod(kp, hk)
-            q = [b[s * bk + kh * hk + kk, j * bn + nh * hn + c] for kh in (0, 1) for nh in (0, 1)]
-            b0, b1, b2, b3 = q
-            want = [r(b0 + b3), b0, r(b1 - b3), r(b2 - b0), b3, r(b0 + b1), r(b2 + b3)]
-            assert [w[p * 7 + op, kp] for op in range(7)] == pytest.approx(want, abs=0)
+    rng = np.random.default_rng(1)
+    tile, bk = 512, 64
+    rows, k = 1024, 128  # 2 row tiles, 2 K panels; R = 512, depth 64
+    x = o.bf16_round(rng.standard_normal((rows, k) if side == "lhs" else (k, rows)).astype(np.float32))
+    flat = o.packed_operand(x, algo, side, tile, bk)
+    nops = 7 if algo == 7 else 4
+    assert flat.size == rows // 2 * k // 2 * nops
+    ht, hk = tile // 2, bk // 2
+    r = lambda v: o.bf16_round(np.float32(v)).item()
+    at = lambda row, col: x[row, col] if side == "lhs" else x[col, row]
+    pos = 0
+    for ptile in range(rows // 2 // 128):
+        for stage in range(k // 2 // 16):
+            for op in range(nops):
+                for block in range(4):
+                    for lane in range(64):
+                        prow = ptile * 128 + block * 32 + lane % 32
+                        i, rr = divmod(prow, ht)
+                        first, second = i * tile + rr, i * tile + rr + ht
+                        got = flat[pos:pos + 8]
+                        pos += 8
+                        want = []
+                        for e in range(8):
+                            kp = stage * 16 + (lane // 32) * 8 + e
+                            s_, kk = divmod(kp, hk)
+                            lo, hi = s_ * bk + kk, s_ * bk + kk + hk
+                            if side == "lhs":  # A0 A1 A2 A3 = (top,lo) (top,hi) (bot,lo) (bot,hi)
+                                q0, q1, q2, q3 = at(first, lo), at(first, hi), at(second, lo), at(second, hi)
+                                ops = [r(q0 + q3), r(q2 + q3), q0, q3, r(q0 + q1), r(q2 - q0), r(q1 - q3)]
+                            else:  # B0 B1 B2 B3 = (lo,left) (lo,right) (hi,left) (hi,right)
+                                q0, q1, q2, q3 = at(first, lo), at(second, lo), at(first, hi), at(second, hi)
+                                ops = [r(q0 + q3), q0, r(q1 - q3), r(q2 - q0), q3, r(q0 + q1), r(q2 + q3)]
+                            want.append(ops[op] if algo == 7 else (q0, q1, q2, q3)[op])
+                        assert list(got) == want, (ptile, stage, op, block, lane)
+    assert pos == flat.size
+
+
+def test_oracle_packed_cubic_round_trip():
+    import numpy as np
+
+    import oracle as o
+
+    rng = np.random.default_rng(2)
+    a = o.bf16_round(rng.standard_normal((512, 256)).astype(np.float32))
+    planes = o.unpack_operand(o.packed_operand(a, 8, "lhs", 256, 64), 4, 256, 128)
+    # Reassemble A from its quadrant planes: plane q = (row half q//2, K half q%2).
+    back = np.empty_like(a)
+    for q in range(4):
+        rh, kh = divmod(q, 2)
+        v = planes[q].reshape(2, 128, 4, 32)  # (row tile, row, panel, k)
+        for i in range(2):
+            for s in range(4):
+                back[i * 256 + rh * 128:i * 256 + rh * 128 + 128, s * 64 + kh * 32:s * 64 + kh * 32 + 32] = v[i, :, s, :]
+    assert np.array_equal(back, a)
 
 
 def test_torch_relayouts_match_oracle():
