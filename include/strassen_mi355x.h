@@ -122,7 +122,7 @@ int smx_packed_bytes(int32_t algo, int64_t rows, int64_t k, int64_t* bytes);
  * is laid out [rows/256][k/32][nops][4][64][8] bf16: fragment (tile of 128
  * product rows, stage of 16 product k, operand, 32-row block), lane l holding
  * row l%32, depth 8*(l/32)..+8. Needs rows % tile_rows == 0, k % bk == 0,
- * tile_rows % 256 == 0, bk % 32 == 0, ld >= k, ld % 8 == 0. Asynchronous on
+ * tile_rows % 256 == 0, bk % 64 == 0, ld >= k, ld % 8 == 0. Asynchronous on
  * stream.
  */
 int smx_pack_operand(int32_t algo, int32_t side, int64_t rows, int64_t k, const void* src, int64_t ld,

@@ -26,6 +26,9 @@ namespace smx {
 namespace packed {
 
 constexpr int TM = 128, TN = 128, TK = 16;
+// K granule of the packed kernel: bk % (2 * kKGranule) == 0 keeps the stage
+// count (K/32) even.
+constexpr int kKGranule = 2 * TK;
 constexpr int kFrag = 1024;  // one 32x16 bf16 operand fragment in lane order
 constexpr int kBlocks = 4;   // 32-row blocks per 128-row tile
 constexpr int kPackStages = 4;  // stages one pack wave handles (128 B per source row)
@@ -38,27 +41,37 @@ __host__ __device__ inline int64_t frag_offset(int64_t tile, int64_t stage, int6
   return (((tile * nstages + stage) * nops + op) * kBlocks + block) * (int64_t)kFrag;
 }
 
-template <int kAlgo>
+// kCubicSlots: LDS ring depth of the cubic (both operands); the ring is
+// refilled kCubicSlots-1 stages ahead.
+template <int kAlgo, int kCubicSlots = 3>
 struct Lay {
   static constexpr int nops = nops_of(kAlgo);
   static constexpr int kStage = nops * kBlocks * kFrag;  // one operand, one stage
   // Strassen's 28 KB stages allow two A slots next to three B slots.
-  static constexpr int kASlots = kAlgo == 7 ? 2 : 3;
-  static constexpr int kBSlots = 3;
+  static constexpr int kASlots = kAlgo == 7 ? 2 : kCubicSlots;
+  static constexpr int kBSlots = kAlgo == 7 ? 3 : kCubicSlots;
   static constexpr int kLds = (kASlots + kBSlots) * kStage;
   static constexpr int kDmaPerWave = nops;  // nops*4 fragments over 4 waves
   // VMEM operations a wave may leave in flight at the stage barrier: the
-  // prefetches that target stages after s+1.
-  static constexpr int kPending = (kASlots == 3 ? kDmaPerWave : 0) + kDmaPerWave;
+  // prefetches that target stages after s+1 (Strassen: B stage s+2; cubic:
+  // A and B stages s+2 .. s+kCubicSlots-1).
+  static constexpr int kPending = kAlgo == 7 ? kDmaPerWave : (kCubicSlots - 2) * 2 * kDmaPerWave;
   static_assert(kLds <= 160 * 1024, "LDS budget");
   static_assert(kPending < 64, "vmcnt range");
 };
 
+// s_waitcnt immediate (gfx9 encoding) for vmcnt(vm) lgkmcnt(lgkm), no
+// export-count wait.
+constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8); }
+
 // Barrier after this wave's LDS reads and all but its newest kPending VMEM
-// operations have completed. The "memory" clobber keeps the compiler from
-// moving LDS accesses across it.
+// operations have completed. The wait is issued through the builtin so the
+// compiler's own wait tracking knows the LDS reads are complete (and adds no
+// later wait for them); the asm repeats it next to the barrier, and its
+// "memory" clobber keeps the compiler from moving LDS accesses across.
 template <int kPending>
 __device__ __forceinline__ void stage_barrier() {
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(kPending, 0));
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"i"(kPending) : "memory");
 }
 
@@ -95,9 +108,9 @@ __device__ __forceinline__ bf16x8 ld_frag(const uint8_t* p) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(p));
 }
 
-template <int kAlgo, int kEpi>
+template <int kAlgo, int kEpi, int kCubicSlots = 3>
 __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
-  using L = Lay<kAlgo>;
+  using L = Lay<kAlgo, kCubicSlots>;
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -148,18 +161,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
     return f;
   };
   auto mfma4 = [&](const Frags& f, int set) {
-    if constexpr (kAlgo == 8) {
-      // The cubic's 256 accumulator registers fit the AGPR file: compiler
-      // builtins (with the compiler's own hazard handling).
-      acc[set][0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a0, f.b0, acc[set][0][0], 0, 0, 0);
-      acc[set][0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a0, f.b1, acc[set][0][1], 0, 0, 0);
-      acc[set][1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1, f.b0, acc[set][1][0], 0, 0, 0);
-      acc[set][1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a1, f.b1, acc[set][1][1], 0, 0, 0);
-      return;
-    }
-    // Strassen: accumulator sets 0-3 live in AGPRs and 4-6 in VGPRs (pinned
-    // through the operand constraint), so 448 accumulator registers never
-    // move between the two files.
+    // Accumulator sets 0-3 live in AGPRs and (Strassen) 4-6 in VGPRs, pinned
+    // through the operand constraint, so the accumulators never move between
+    // the two files and the VGPRs stay free for fragments.
     if (set < 4) {
       mfma_agpr(acc[set][0][0], f.a0, f.b0);
       mfma_agpr(acc[set][0][1], f.a0, f.b1);
@@ -172,71 +176,123 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
       mfma_vgpr(acc[set][1][1], f.a1, f.b1);
     }
   };
-  auto mma = [&](const uint8_t* sa, const uint8_t* sb) {
-    if constexpr (kAlgo == 8) {
-      // Cubic (products a0b0 a0b1 a2b0 a2b1 a1b2 a1b3 a3b2 a3b3,
-      // benchmark_cubic_control.py:96-106), one K half at a time: A
-      // quadrants (top, bottom) x B quadrants (left, right), every fragment
-      // feeding two MFMAs. All 16 reads are issued before the first MFMA.
-      const Frags h0t = load_frags(sa, sb, 0, 0), h0b = load_frags(sa, sb, 2, 1);
-      const Frags h1t = load_frags(sa, sb, 1, 2), h1b = load_frags(sa, sb, 3, 3);
-      __builtin_amdgcn_sched_barrier(0);
-      // t: A top quadrant + B left quadrant; b: A bottom + B right.
-      auto half = [&](const Frags& t, const Frags& b) {
-        mfma4(Frags{t.a0, t.a1, t.b0, t.b1}, 0);
-        mfma4(Frags{t.a0, t.a1, b.b0, b.b1}, 1);
-        mfma4(Frags{b.a0, b.a1, t.b0, t.b1}, 2);
-        mfma4(Frags{b.a0, b.a1, b.b0, b.b1}, 3);
-      };
-      half(h0t, h0b);
-      half(h1t, h1b);
-      return;
-    }
-    // Strassen products in issue order P4 P6 P5 P2 P7 P3 P1
-    // (strassen_pallas.py:556-565) as operand / accumulator index p-1; the
-    // next product's fragments load while the current product's MFMAs run.
-    constexpr int kOrder[7] = {3, 5, 4, 1, 6, 2, 0};
-    Frags cur = load_frags(sa, sb, kOrder[0], kOrder[0]);
-#pragma unroll
-    for (int x = 0; x < 7; ++x) {
-      Frags next;
-      if (x + 1 < 7) next = load_frags(sa, sb, kOrder[x + 1], kOrder[x + 1]);
-      mfma4(cur, kOrder[x]);
-      __builtin_amdgcn_sched_barrier(0);
-      if (x + 1 < 7) cur = next;
-    }
-  };
+  // Cubic products a0b0 a0b1 a2b0 a2b1 a1b2 a1b3 a3b2 a3b3
+  // (benchmark_cubic_control.py:96-106) run one K half at a time, A
+  // quadrants (top, bottom) x B quadrants (left, right), every fragment
+  // feeding two MFMAs (the cubic loop below).
+  // Strassen products in issue order P4 P6 P5 P2 P7 P3 P1
+  // (strassen_pallas.py:556-565) as operand / accumulator index p-1.
+  constexpr int kOrder[7] = {3, 5, 4, 1, 6, 2, 0};
 
-  // Prologue: stages 0..kASlots-2 of A and 0..1 of B.
+  // Prologue: stages 0..kASlots-2 of A and 0..kBSlots-2 of B.
   dma(a_src, 0, a_region);
   dma(b_src, 0, b_region);
-  if constexpr (L::kASlots == 3) dma(a_src, 1, a_region + L::kStage);
-  dma(b_src, 1, b_region + L::kStage);
+#pragma unroll
+  for (int st = 1; st + 1 < L::kBSlots; ++st) {
+    if (st + 1 < L::kASlots) dma(a_src, st, a_region + st * L::kStage);
+    dma(b_src, st, b_region + st * L::kStage);
+  }
   stage_barrier<L::kPending>();
+
+  if constexpr (kAlgo == 8) {
+    // Cubic: a whole stage of fragments (16) fits in VGPRs next to the AGPR
+    // accumulators, so the barrier moves to mid-stage and the reads of stage
+    // s+1 run under the second half of stage s's MFMAs:
+    //   DMA stage s+kSlots-1 | MFMAs K half 0 of s | barrier | read s+1 | MFMAs K half 1 of s
+    // The barrier guarantees that every wave's DMA of stage s+1 has landed
+    // (vmcnt leaves only later stages in flight) and that every wave
+    // finished reading stage s (its reads completed before its first MFMA
+    // of s), so stage s's slot may be refilled after it.
+    struct Stage {
+      Frags h0t, h0b, h1t, h1b;  // K half x (A top + B left, A bottom + B right)
+    };
+    auto load_stage = [&](int slot) {
+      const uint8_t* sa = a_region + slot * L::kStage;
+      const uint8_t* sb = b_region + slot * L::kStage;
+      return Stage{load_frags(sa, sb, 0, 0), load_frags(sa, sb, 2, 1), load_frags(sa, sb, 1, 2),
+                   load_frags(sa, sb, 3, 3)};
+    };
+    auto half = [&](const Frags& t, const Frags& b) {
+      mfma4(Frags{t.a0, t.a1, t.b0, t.b1}, 0);
+      mfma4(Frags{t.a0, t.a1, b.b0, b.b1}, 1);
+      mfma4(Frags{b.a0, b.a1, t.b0, t.b1}, 2);
+      mfma4(Frags{b.a0, b.a1, b.b0, b.b1}, 3);
+    };
+    int s = 0, slot = 0;
+    constexpr int kSlots = kCubicSlots;
+    auto body = [&](const Stage& cur) {
+      // Slot of stage s+1, and of stage s+kSlots-1 (the one read at s-1).
+      const int slot1 = slot == kSlots - 1 ? 0 : slot + 1, refill = slot == 0 ? kSlots - 1 : slot - 1;
+      dma(a_src, s + kSlots - 1, a_region + refill * L::kStage);
+      dma(b_src, s + kSlots - 1, b_region + refill * L::kStage);
+      __builtin_amdgcn_sched_barrier(0);
+      half(cur.h0t, cur.h0b);
+      __builtin_amdgcn_sched_barrier(0);
+      stage_barrier<L::kPending>();
+      const Stage next = load_stage(slot1);  // past the last stage: re-reads it, unused
+      __builtin_amdgcn_sched_barrier(0);
+      half(cur.h1t, cur.h1b);
+      __builtin_amdgcn_sched_barrier(0);
+      slot = slot1;
+      return next;
+    };
+    // Unrolled by two so the fragment sets swap roles without copies. The
+    // host guarantees an even stage count (bk % 64 == 0), so the loop is
+    // bottom-tested with no tail: a branch between the two bodies would let
+    // the compiler sink the second body's reads past it (out of the MFMA
+    // shadow), and any path that skips the loop gets its own copy of the
+    // accumulator initialisation.
+    Stage f0 = load_stage(0);
+    do {
+      const Stage f1 = body(f0);
+      ++s;
+      f0 = body(f1);
+      ++s;
+    } while (s < nstages);
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    mfma_drain(acc);
+    epilogue<kAlgo, 2, 2, kEpi>(p, o, wm * 64, wn * 64, acc);
+    return;
+  }
 
   // Stage s: prefetch, MFMAs on stage s, barrier. The prefetched slots were
   // last read at stage s-1, which every wave finished before the previous
   // barrier. The host guarantees nstages >= 1; a do-while leaves no zero-trip
   // path whose register assignment would need reconciling copies.
+  // Strassen: a stage's 28 fragments do not fit next to the 448 accumulator
+  // registers, so fragments stream one product ahead, and the software
+  // pipeline is rotated across the barrier: the barrier sits between the
+  // reads and the MFMAs of the last product, and the first product of stage
+  // s+1 is read right after it, under those MFMAs. The barrier sees every
+  // read of stage s complete (lgkmcnt(0)) and every wave's DMA of stage s+1
+  // landed (vmcnt leaves only the newest prefetch in flight).
   int s = 0, a_slot = 0, b_slot = 0;
+  Frags cur = load_frags(a_region, b_region, kOrder[0], kOrder[0]);
   do {
     const int b_next = b_slot == 0 ? 2 : b_slot - 1;  // (s + 2) % 3
-    if constexpr (L::kASlots == 3) {
-      const int a_next = a_slot == 0 ? 2 : a_slot - 1;  // (s + 2) % 3
-      dma(a_src, s + 2, a_region + a_next * L::kStage);
-    } else {
-      dma(a_src, s + 1, a_region + (a_slot ^ 1) * L::kStage);
-    }
+    const int b_slot1 = b_slot == 2 ? 0 : b_slot + 1;
+    dma(a_src, s + 1, a_region + (a_slot ^ 1) * L::kStage);
     dma(b_src, s + 2, b_region + b_next * L::kStage);
     __builtin_amdgcn_sched_barrier(0);
-    mma(a_region + a_slot * L::kStage, b_region + b_slot * L::kStage);
-    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t* const sa = a_region + a_slot * L::kStage;
+    const uint8_t* const sb = b_region + b_slot * L::kStage;
+#pragma unroll
+    for (int x = 0; x < 6; ++x) {
+      const Frags next = load_frags(sa, sb, kOrder[x + 1], kOrder[x + 1]);
+      mfma4(cur, kOrder[x]);
+      __builtin_amdgcn_sched_barrier(0);
+      cur = next;
+    }
     stage_barrier<L::kPending>();
-    b_slot = b_slot == 2 ? 0 : b_slot + 1;
-    if constexpr (L::kASlots == 3)
-      a_slot = a_slot == 2 ? 0 : a_slot + 1;
-    else
-      a_slot ^= 1;
+    // Stage s+1's first product (past the last stage: a re-loaded copy of
+    // it, never used).
+    const Frags first = load_frags(a_region + (a_slot ^ 1) * L::kStage, b_region + b_slot1 * L::kStage,
+                                   kOrder[0], kOrder[0]);
+    mfma4(cur, kOrder[6]);
+    __builtin_amdgcn_sched_barrier(0);
+    cur = first;
+    b_slot = b_slot1;
+    a_slot ^= 1;
   } while (++s < nstages);
   // Let the (unread) prefetches past the last stage land before the
   // workgroup can finish.

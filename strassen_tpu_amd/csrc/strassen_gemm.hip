@@ -129,7 +129,7 @@ void tile_of_path(bool packed_path, int32_t* tm, int32_t* tn, int32_t* tk) {
   if (packed_path) {
     *tm = packed::TM;
     *tn = packed::TN;
-    *tk = packed::TK;
+    *tk = packed::kKGranule;
   } else {  // both v1 configurations are 128 x 64 x 32
     *tm = v1::General<7>::TM;
     *tn = v1::General<7>::TN;
@@ -193,9 +193,9 @@ int smx_pack_operand(int32_t algo, int32_t side, int64_t rows, int64_t k, const 
   if (side != SMX_SIDE_LHS && side != SMX_SIDE_RHS) return fail(SMX_ERR_INVALID, "side must be LHS (0) or RHS (1)");
   if (rows <= 0 || k <= 0 || tile_rows <= 0 || bk <= 0 || rows % tile_rows || k % bk)
     return fail(SMX_ERR_INVALID, "packing needs rows %% tile_rows == 0 and K %% bk == 0");
-  if (tile_rows % (2 * packed::TM) || bk % (2 * packed::TK))
+  if (tile_rows % (2 * packed::TM) || bk % (2 * packed::kKGranule))
     return fail(SMX_ERR_UNSUPPORTED, "packed tiles need %s %% %d == 0 and bk %% %d == 0 (got %d, %d)",
-                side == SMX_SIDE_LHS ? "bm" : "bn", 2 * packed::TM, 2 * packed::TK, tile_rows, bk);
+                side == SMX_SIDE_LHS ? "bm" : "bn", 2 * packed::TM, 2 * packed::kKGranule, tile_rows, bk);
   if (!src || !out) return fail(SMX_ERR_INVALID, "null pointer");
   if (!aligned16(src) || !aligned16(out)) return fail(SMX_ERR_INVALID, "pointers must be 16-byte aligned");
   if (ld < k || ld % 8) return fail(SMX_ERR_INVALID, "ld must be >= K and a multiple of 8");

@@ -23,7 +23,7 @@ Differences a caller can observe, all raised as exceptions (never silent):
   the reference) are validated and accepted but select the same kernel.
 * Tiles must additionally satisfy the gfx950 kernels' divisibility rule
   (``smx_tile_requirements``): bm % 256 == 0 always; bn % 128 and bk % 64 for
-  a plain weight; bn % 256 and bk % 32 for a packed weight.
+  a plain weight; bn % 256 and bk % 64 for a packed weight.
 """
 
 from __future__ import annotations

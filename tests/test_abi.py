@@ -121,7 +121,7 @@ def test_tile_requirements():
     # Both algorithms share each kernel's tiling.
     assert plain == _lib.tile_requirements(_lib.SMX_ALGO_CUBIC, None, _lib.SMX_B_KCONTIG)
     assert packed == _lib.tile_requirements(_lib.SMX_ALGO_CUBIC, None, _lib.SMX_B_PACKED)
-    assert packed == (128, 128, 16) and plain == (128, 64, 32)
+    assert packed == (128, 128, 32) and plain == (128, 64, 32)
     with pytest.raises(ValueError):
         _lib.tile_requirements(3, None)
     with pytest.raises(ValueError):
@@ -146,7 +146,8 @@ def test_packed_bytes():
     ((6, 0, 512, 512, 512, 256, 512), _lib.SMX_ERR_INVALID),      # algo
     ((7, 0, 512, 512, 512, 128, 512), _lib.SMX_ERR_UNSUPPORTED),  # tile_rows % 256
     ((8, 1, 512, 512, 512, 256, 48), _lib.SMX_ERR_INVALID),       # k % bk
-    ((8, 1, 512, 480, 480, 256, 48), _lib.SMX_ERR_UNSUPPORTED),   # bk % 32
+    ((8, 1, 512, 480, 480, 256, 48), _lib.SMX_ERR_UNSUPPORTED),   # bk % 64
+    ((7, 0, 512, 480, 480, 256, 96), _lib.SMX_ERR_UNSUPPORTED),   # bk % 64
     ((7, 0, 512, 512, 100, 256, 512), _lib.SMX_ERR_INVALID),      # ld < k
 ])
 def test_pack_operand_rejects_bad_arguments(args, code):
