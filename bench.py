@@ -40,6 +40,7 @@ HEADS, KV_HEADS, HEAD_DIM = 64, 8, 128
 BATCH, SEQ = 8, 1024
 THETA, EPS = 1e6, 1e-6
 TILE = (1024, 1024, 512)
+COPY_BYTES = 256 << 20
 
 
 def log(*args):
@@ -204,6 +205,19 @@ def pure_sites(torch, d, algo):
     }
 
 
+def gate_up_gemm(d, algo):
+    """The dominant kernel alone: the fused gate|up SwiGLU GEMM launch on an
+    activation packed beforehand (algo 7 Strassen, 8 cubic)."""
+    import strassen_tpu_amd as smx
+
+    bm, bn, bk = TILE
+    packed = smx.pack_activation(d["y"], algo, bm, bk)
+    if algo == 7:
+        return lambda: smx.strassen_matmul(packed, d["wgu_laid_sw"], bm=bm, bn=bn, bk=bk, epilogue="swiglu",
+                                           interleave_products=True)
+    return lambda: smx.cubic_matmul(packed, d["wgu_laid_cw"], bm=bm, bn=bn, bk=bk, epilogue="swiglu")
+
+
 def time_steps(torch, step, steps, warmup):
     """Warm up, then time exactly `steps` calls between two synchronisations.
     Returns (total wall ms, per-step event ms list)."""
@@ -271,7 +285,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", default=None, help="time only this arm:site (profiling runs)")
+    ap.add_argument("--only", default=None,
+                    help="profiling runs: time only ARM:SITE (ARM strassen|cubic|strassen_plain|cubic_plain|"
+                         "hipblaslt; SITE q|k|v|o|gate_up|down|pure_gate_up|pure_down|pure_o, or gate_up_gemm "
+                         "for the packed GEMM launch alone), or \"copy\" (a 256 MiB copy, counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: the Strassen GEMM path runs on one MI355X "
@@ -286,6 +303,13 @@ def main():
     _lib.load()
     dev = torch.device("cuda:0")
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.only == "copy":
+        # Counter calibration: one 256 MiB device-to-device copy per step.
+        src = torch.ones(COPY_BYTES // 2, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        _, ev = time_steps(torch, lambda: dst.copy_(src), args.steps, args.warmup)
+        log(f"copy {COPY_BYTES >> 20} MiB: {statistics.mean(ev):.3f} ms/call")
+        return
     log(f"device: {torch.cuda.get_device_name(0)}, CUs {torch.cuda.get_device_properties(0).multi_processor_count}")
     d = make_block(torch, dev)
     shapes = site_shapes()
@@ -301,6 +325,11 @@ def main():
 
     if args.only:
         arm, site = args.only.split(":")
+        if site == "gate_up_gemm":
+            fn = gate_up_gemm(d, 7 if arm == "strassen" else 8)
+            _, ev = time_steps(torch, fn, args.steps, args.warmup)
+            log(f"{args.only}: {statistics.mean(ev):.3f} ms/call")
+            return
         table = arms[arm] if site in arms[arm] and not site.startswith("pure_") else \
             pure_sites(torch, d, arm)
         fn = table[site.replace("pure_", "")]
@@ -347,21 +376,24 @@ def main():
     # launch alone (activation already packed), timed with events on the
     # stream it is launched on.
     bm, bn, bk = TILE
-    y_packed = smx.pack_activation(d["y"], 7, bm, bk)
-    gu_fn = lambda: smx.strassen_matmul(y_packed, d["wgu_laid_sw"], bm=bm, bn=bn, bk=bk, epilogue="swiglu",
-                                        interleave_products=True)
-    _, ev = time_steps(torch, gu_fn, args.steps, 2)
+    _, ev = time_steps(torch, gate_up_gemm(d, 7), args.steps, 2)
     gu_ms = statistics.mean(ev)
     gu_tflops = flops(shapes["gate_up"]) / (gu_ms * 1e-3) / 1e12
-    yc_packed = smx.pack_activation(d["y"], 8, bm, bk)
-    _, ev = time_steps(torch, lambda: smx.cubic_matmul(yc_packed, d["wgu_laid_cw"], bm=bm, bn=bn, bk=bk,
-                                                       epilogue="swiglu"), args.steps, 2)
+    _, ev = time_steps(torch, gate_up_gemm(d, 8), args.steps, 2)
     gu_cubic_ms = statistics.mean(ev)
     _, ev = time_steps(torch, lambda: smx.pack_activation(d["y"], 7, bm, bk), args.steps, 2)
     pack_ms = statistics.mean(ev)
+    traffic, traffic_note = None, None
+    measured = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemm_packed_gate_up_traffic.json")
+    if os.path.exists(measured):
+        rec = json.load(open(measured))["strassen"]
+        traffic = round(rec["traffic_bytes"])
+        traffic_note = (f"HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE passes scaled by a copy-kernel "
+                        f"calibration (profiles/gemm_packed_strassen_swiglu_qwen3_32b_gate_up.md); algorithmic "
+                        f"{rec['algorithmic_bytes']} B")
     roofline = {
         "bound": "mfma", "achieved": round(gu_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-        "frac": round(gu_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+        "frac": round(gu_tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic, "traffic_note": traffic_note,
         "kernel": "smx::packed::gemm_packed<7, SMX_EPI_SWIGLU> (gate|up, M=8192 K=5120 N=51200, packed operands)",
         "mfma_executed_frac": round(gu_tflops * 7 / 8 / PEAK_BF16_TFLOPS, 4),
         "avg_launch_ms": round(gu_ms, 4),
