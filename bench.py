@@ -218,6 +218,25 @@ def gate_up_gemm(d, algo):
     return lambda: smx.cubic_matmul(packed, d["wgu_laid_cw"], bm=bm, bn=bn, bk=bk, epilogue="swiglu")
 
 
+def full_block_times(torch, dev, steps, warmup):
+    """Median ms of one whole Qwen3-32B decoder block (RMSNorms, q/k with
+    fused qk_norm_rope, v on hipBLASLt, causal SDPA attention, o + residual,
+    gate|up + SwiGLU, down + residual) per arm, same weights and input."""
+    from strassen_tpu_amd import qwen3_block as qb
+
+    weights = qb.BlockWeights.random_init(qb.QWEN3_32B, dev, seed=1)
+    x = torch.randn(TOKENS, HIDDEN, device=dev, generator=torch.Generator(device=dev).manual_seed(2))
+    x = x.to(torch.bfloat16)
+    out = {}
+    for arm in qb.ARMS:
+        log(f"timing full block, {arm} arm")
+        block = qb.PreparedBlock(weights, qb.QWEN3_32B, arm, batch=BATCH, seq=SEQ, tile=TILE)
+        _, ev = time_steps(torch, lambda: qb.block_forward(x, block), steps, warmup)
+        out[arm] = statistics.median(ev)
+        del block
+    return out
+
+
 def time_steps(torch, step, steps, warmup):
     """Warm up, then time exactly `steps` calls between two synchronisations.
     Returns (total wall ms, per-step event ms list)."""
@@ -401,6 +420,9 @@ def main():
         "activation_pack_ms": round(pack_ms, 4),
     }
 
+    # The whole decoder block (norms, attention, v on hipBLASLt) per arm.
+    full_block = full_block_times(torch, dev, args.steps, args.warmup)
+
     ms = results["strassen"]
     value = block_flops / (ms * 1e-3) / 1e12
     line = {
@@ -435,6 +457,8 @@ def main():
         "pure_gemm_tflops": {arm: {k: round(flops(pure_shapes[k]) / (v * 1e-3) / 1e12, 1) for k, v in s.items()}
                              for arm, s in pure.items()},
         "roofline": roofline,
+        "full_block_ms": {k: round(v, 4) for k, v in full_block.items()},
+        "full_block_speedup_vs_cubic": round(full_block["cubic"] / full_block["strassen"], 4),
     }
     if not args.no_cpu_baseline:
         log("timing CPU baseline (oracle)")
