@@ -49,3 +49,28 @@ def test_block_surface_checks():
     # the native arm needs no relayout and builds on any device
     block = qb.PreparedBlock(w, dims, "hipblaslt", batch=1, seq=256)
     assert tuple(block.cos.shape) == (256, 128)
+
+
+def test_decoder_metrics_on_cpu_tensors():
+    """The streamed decoder's metrics (device-agnostic torch) against numpy."""
+    from strassen_tpu_amd import streamed_decoder as sd
+
+    rng = np.random.default_rng(6)
+    ref = rng.standard_normal((64, 32)).astype(np.float32)
+    got = ref + 1e-3 * rng.standard_normal((64, 32)).astype(np.float32)
+    e = sd.device_error(torch.from_numpy(got), torch.from_numpy(ref))
+    want = o.device_error(got, ref)
+    for key in ("max_abs", "rmse", "maxnorm_relative", "l2_relative"):
+        assert e[key] == pytest.approx(want[key], rel=1e-5), key
+    # logit metrics: identical candidates have zero KL, full agreement, zero delta
+    h = torch.randn(8, 16).to(torch.bfloat16)
+    head = torch.randn(16, 40).to(torch.bfloat16)
+    targets = torch.randint(0, 40, (8,))
+    nl, nsq, nmax, cub, stra, count = sd.logit_chunk_metrics(h, h, h, head, targets, torch.ones(8))
+    assert count == 8 and cub[0] == pytest.approx(nl) and cub[1] == pytest.approx(0, abs=1e-6)
+    assert cub[2] == 8 and cub[3] == 0 and cub[4] == 0
+    # the native loss is the summed negative log-likelihood of the targets
+    logp = torch.log_softmax(torch.matmul(h, head).float(), -1)
+    assert nl == pytest.approx(float(-logp[torch.arange(8), targets].sum()), rel=1e-5)
+    interval = sd.bootstrap_sum_interval([1.0, 2.0, 3.0], seed=0)
+    assert interval["sum_ms"] == 6.0 and interval["ci95_ms"][0] <= 6.0 <= interval["ci95_ms"][1]
