@@ -55,6 +55,7 @@ extern "C" {
 #define SMX_EPI_RESIDUAL_ADD 2 /* out = acc + residual;          :778-792 */
 #define SMX_EPI_BIAS_ADD 3     /* out = acc + bias[col];         :867-874 */
 #define SMX_EPI_QK_NORM_ROPE 4 /* per-head RMSNorm + RoPE;       :793-835 */
+#define SMX_EPI_GEGLU 5        /* out[M, N/2] = gelu_tanh(gate) * up; :143-153 */
 
 /* Layout of A. */
 #define SMX_A_ROWMAJOR 0 /* A row-major [M, K] (lda >= K) */
@@ -67,6 +68,10 @@ extern "C" {
 /* Operand side for smx_pack_operand. */
 #define SMX_SIDE_LHS 0 /* A [M, K] */
 #define SMX_SIDE_RHS 1 /* B^T [N, K] */
+#define SMX_SIDE_LHS_T 2 /* A stored transposed as [K, M] (strassen_matmul_lhs_transposed, :1224-1312) */
+
+/* desc.flags bits. */
+#define SMX_FLAG_OUT_F32 1 /* C is float32 (the unrounded FP32 result, output_dtype=float32, :1048-1057) */
 
 /* aux_f32 bits: element type of the small auxiliary vectors. */
 #define SMX_AUX_BIAS_F32 1  /* bias is float32 (else bf16) */
@@ -84,7 +89,7 @@ typedef struct smx_gemm_desc {
   int32_t rope_head_dim; /* qk_norm_rope head width (128) */
   float rope_eps;        /* qk_norm_rope epsilon */
   int32_t aux_f32;       /* SMX_AUX_* bits */
-  int32_t flags;         /* reserved, must be 0 */
+  int32_t flags;         /* SMX_FLAG_* bits */
 } smx_gemm_desc;
 
 /*
@@ -92,7 +97,8 @@ typedef struct smx_gemm_desc {
  * B^T bf16 [n, k] row-major (ldb), served by the compact kernel that forms
  * the operand sums in registers; or both packed by smx_pack_operand for the
  * same algo and (bm, bk) / (bn, bk), served by the packed kernel (lda / ldb
- * ignored). C: bf16 [m, n] (or [m, n/2] for SwiGLU). residual: bf16 [m, n]
+ * ignored). C: bf16 [m, n] (or [m, n/2] for SwiGLU / GeGLU), float32 with
+ * SMX_FLAG_OUT_F32. residual: bf16 [m, n]
  * (ldr). bias: [n] bf16 or f32. rope_cos / rope_sin: bf16 [m, bn/2] tables
  * indexed by output row (rope_layout_tables). rope_scale: [bn] bf16 or f32
  * (rope_scale_layout). Unused pointers may be NULL.
@@ -114,15 +120,16 @@ int smx_packed_bytes(int32_t algo, int64_t rows, int64_t k, int64_t* bytes);
 
 /*
  * Packs one operand for the packed kernel. side SMX_SIDE_LHS: src is A bf16
- * [rows = m, k] and tile_rows = bm; SMX_SIDE_RHS: src is B^T bf16 [rows = n,
- * k] and tile_rows = bn. Strassen (algo 7) stores the seven operand sums of
+ * [rows = m, k] and tile_rows = bm; SMX_SIDE_LHS_T: src is the same A stored
+ * transposed, bf16 [k, rows = m] with row stride ld >= m; SMX_SIDE_RHS: src
+ * is B^T bf16 [rows = n, k] and tile_rows = bn. Strassen (algo 7) stores the seven operand sums of
  * P1..P7 (A0+A3, A2+A3, A0, A3, A0+A1, A2-A0, A1-A3; B0+B3, B0, B1-B3,
  * B2-B0, B3, B0+B1, B2+B3), each rounded once to bf16; the cubic (algo 8)
  * stores the four quadrants. out (smx_packed_bytes bytes, 16-byte aligned)
  * is laid out [rows/256][k/32][nops][4][64][8] bf16: fragment (tile of 128
  * product rows, stage of 16 product k, operand, 32-row block), lane l holding
  * row l%32, depth 8*(l/32)..+8. Needs rows % tile_rows == 0, k % bk == 0,
- * tile_rows % 256 == 0, bk % 64 == 0, ld >= k, ld % 8 == 0. Asynchronous on
+ * tile_rows % 256 == 0, bk % 64 == 0, ld >= k, ld % 8 == 0 (LHS_T: ld >= m). Asynchronous on
  * stream.
  */
 int smx_pack_operand(int32_t algo, int32_t side, int64_t rows, int64_t k, const void* src, int64_t ld,

@@ -13,8 +13,8 @@ from __future__ import annotations
 import numpy as np
 
 __all__ = [
-    "bf16_round", "bf16_bits", "bits_to_f32", "silu",
-    "strassen_matmul", "cubic_blocked_matmul", "native_matmul",
+    "bf16_round", "bf16_bits", "bits_to_f32", "silu", "gelu_tanh",
+    "strassen_matmul", "strassen_matmul_lhs_transposed", "cubic_blocked_matmul", "native_matmul",
     "high_precision_reference", "device_error", "host_uniform_inputs",
     "swiglu_weight_layout_order", "swiglu_weight_layout",
     "rope_weight_layout_order", "rope_weight_layout", "rope_layout_tables",
@@ -63,6 +63,16 @@ def silu(x):
     x = np.asarray(x, dtype=np.float32)
     with np.errstate(over="ignore"):
         return (x / (np.float32(1.0) + np.exp(-x))).astype(np.float32)
+
+
+def gelu_tanh(x):
+    """float32 tanh-approximate GELU -- ``jax.nn.gelu(approximate=True)``, the
+    GeGLU gate (``strassen_pallas.py:143-153``):
+    0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))."""
+    x = np.asarray(x, dtype=np.float32)
+    k = np.float32(np.sqrt(2.0 / np.pi))
+    inner = k * (x + np.float32(0.044715) * x * x * x)
+    return (np.float32(0.5) * x * (np.float32(1.0) + np.tanh(inner))).astype(np.float32)
 
 
 # ---------------------------------------------------------------------------
@@ -265,8 +275,8 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
     m, k, n = _check_common(a, b, bm, bn, bk)
     nk = k // bk
     hm, hn = bm // 2, bn // 2
-    if product_aware_swiglu and epilogue not in ("swiglu",):
-        raise ValueError("product_aware_swiglu is only valid with epilogue='swiglu'")
+    if product_aware_swiglu and epilogue not in ("swiglu", "geglu"):
+        raise ValueError("product_aware_swiglu is only valid with epilogue='swiglu' or 'geglu'")
     if product_aware_residual and epilogue != "residual_add":
         raise ValueError("product_aware_residual is only valid with epilogue='residual_add'")
     order = INTERLEAVED_ORDER if interleave_products else PLAIN_ORDER
@@ -298,6 +308,16 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
                      bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
                      rope_scale=rope_scale, rope_head_dim=rope_head_dim,
                      rope_eps=rope_eps, output_dtype=output_dtype)
+
+
+def strassen_matmul_lhs_transposed(a_t, b, *, bm, bn, bk, interleave_products=False,
+                                   output_dtype="bfloat16"):
+    """``a_t.T @ b`` (``strassen_pallas.py:1224-1312``): the kernel transposes
+    each resident ``(bk, bm)`` tile of ``a_t`` and runs the ordinary classical
+    Strassen body on it (``:1273-1289``), so the result is ``strassen_matmul``
+    of the transposed matrix."""
+    return strassen_matmul(np.asarray(a_t, dtype=np.float32).T, b, bm=bm, bn=bn, bk=bk,
+                           interleave_products=interleave_products, output_dtype=output_dtype)
 
 
 def cubic_blocked_matmul(a, b, *, bm, bn, bk, epilogue=None, residual=None,
@@ -334,7 +354,8 @@ def _epilogue(acc, m, n, bm, bn, *, epilogue, residual, bias, rope_cos,
               rope_sin, rope_scale, rope_head_dim, rope_eps, output_dtype):
     """Epilogues on the FP32 accumulators, then one bf16 rounding.
 
-    ``strassen_pallas.py:739-879``: swiglu ``:762-777``, residual_add
+    ``strassen_pallas.py:739-879``: swiglu / geglu ``:762-777`` with the gate
+    of ``:143-153``, residual_add
     ``:778-792``, qk_norm_rope ``:793-835``, bias_add ``:867-874``, plain
     store ``:875-879``.
     """
@@ -342,9 +363,10 @@ def _epilogue(acc, m, n, bm, bn, *, epilogue, residual, bias, rope_cos,
     to_out = (lambda x: x.astype(np.float32)) if output_dtype == "float32" else bf16_round
     if epilogue is None:
         return to_out(_assemble(acc, m, n, bm, bn))
-    if epilogue == "swiglu":
-        top = silu(acc[0]) * acc[1]
-        bottom = silu(acc[2]) * acc[3]
+    if epilogue in ("swiglu", "geglu"):
+        gate = silu if epilogue == "swiglu" else gelu_tanh
+        top = gate(acc[0]) * acc[1]
+        bottom = gate(acc[2]) * acc[3]
         # Output tile (bm, bn/2): rows [0,hm) from the top pair, [hm,bm) bottom.
         out = np.empty((m // bm, 2, hm, n // bn, hn), dtype=np.float32)
         out[:, 0] = top.reshape(m // bm, hm, n // bn, hn)

@@ -30,6 +30,7 @@ SMX_EPI = {
     "residual_add": 2,
     "bias_add": 3,
     "qk_norm_rope": 4,
+    "geglu": 5,
 }
 
 SMX_A_ROWMAJOR = 0
@@ -38,6 +39,8 @@ SMX_B_KCONTIG = 1
 SMX_B_PACKED = 2
 SMX_SIDE_LHS = 0
 SMX_SIDE_RHS = 1
+SMX_SIDE_LHS_T = 2
+SMX_FLAG_OUT_F32 = 1
 SMX_AUX_BIAS_F32 = 1
 SMX_AUX_SCALE_F32 = 2
 

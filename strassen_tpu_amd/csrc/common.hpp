@@ -102,7 +102,7 @@ __device__ __forceinline__ void strassen_b_ops(const u32x4 (&q)[4], u32x4 (&ops)
 struct Params {
   const uint16_t* a;
   const uint16_t* b;  // B^T [N, K] (plain) or the pre-summed operands [N/2*7, K/2]
-  uint16_t* c;
+  void* c;           // bf16, or float32 when out_f32
   const uint16_t* residual;
   const void* bias;
   const uint16_t* rope_cos;
@@ -116,6 +116,7 @@ struct Params {
   float eps;
   int32_t tiles_m, tiles_n;  // product-space workgroup grid
   int32_t group_m;           // tile rows per rasterization group
+  int32_t out_f32;           // store float32 instead of bf16
 };
 
 // Workgroup id -> product-space tile. Workgroups are dispatched round-robin
@@ -160,6 +161,34 @@ __device__ __forceinline__ TileOrigin tile_origin(const Params& p, int64_t prow0
 
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 
+// GELU, tanh approximation (jax.nn.gelu(approximate=True), the GeGLU gate of
+// strassen_pallas.py:143-153): 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).
+__device__ __forceinline__ float gelu_tanh_f32(float x) {
+  const float k = 0.7978845608028654f;  // sqrt(2/pi)
+  return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
+}
+
+template <int kEpi>
+__device__ __forceinline__ float gate_f32(float x) {
+  if constexpr (kEpi == SMX_EPI_GEGLU)
+    return gelu_tanh_f32(x);
+  else
+    return silu_f32(x);
+}
+
+// Output rows: a per-wave base plus 32-bit element offsets, stored as bf16
+// or (out_f32) float32. The element type is uniform per launch.
+struct OutRow {
+  char* base;
+  int f32;
+  __device__ __forceinline__ void put(int off, float v) const {
+    if (f32)
+      reinterpret_cast<float*>(base)[off] = v;
+    else
+      reinterpret_cast<uint16_t*>(base)[off] = f32_to_bf16(v);
+  }
+};
+
 __device__ __forceinline__ float load_vec(const void* v, int is_f32, int64_t i) {
   return is_f32 ? reinterpret_cast<const float*>(v)[i] : bf16_to_f32(reinterpret_cast<const uint16_t*>(v)[i]);
 }
@@ -172,7 +201,7 @@ __device__ __forceinline__ float half_wave_sum(float x) {
 }
 
 // Combines the accumulator sets into the four quadrants, applies the
-// epilogue and stores bf16. acc has kNacc sets (7 Strassen products P1..P7,
+// epilogue and stores bf16 (or float32). acc has kNacc sets (7 Strassen products P1..P7,
 // or the 4 quadrants for the cubic) of kMB x kNB 32x32 blocks; the wave's
 // block (i, j) sits at product-space rows row0 + 32 i and columns
 // col0 + 32 j, relative to the tile origin o.
@@ -195,7 +224,10 @@ __device__ __forceinline__ void epilogue(const Params& p, const TileOrigin& o, i
   const int64_t cc_base = o.tc + col0;
   const int64_t col_base = o.tj * p.bn + cc_base;
   const int64_t ocol_base = o.tj * hn + cc_base;  // SwiGLU output column
-  uint16_t* const cw = p.c + row_base * p.ldc + (kEpi == SMX_EPI_SWIGLU ? ocol_base : col_base);
+  constexpr bool kGated = kEpi == SMX_EPI_SWIGLU || kEpi == SMX_EPI_GEGLU;
+  const OutRow cw{reinterpret_cast<char*>(p.c) +
+                      (row_base * p.ldc + (kGated ? ocol_base : col_base)) * (p.out_f32 ? 4 : 2),
+                  p.out_f32};
   const uint16_t* const rw = kEpi == SMX_EPI_RESIDUAL_ADD ? p.residual + row_base * p.ldr + col_base : nullptr;
   const int hm_c = hm * ldc, hm_r = hm * ldr;
 #pragma unroll
@@ -226,11 +258,11 @@ __device__ __forceinline__ void epilogue(const Params& p, const TileOrigin& o, i
           q2 = acc[2][i][j][r];
           q3 = acc[3][i][j][r];
         }
-        if constexpr (kEpi == SMX_EPI_SWIGLU) {
+        if constexpr (kGated) {
           // Quadrants 0/2 are gate, 1/3 up; output [M, N/2].
           const int off = ri * ldc + cj;
-          cw[off] = f32_to_bf16(silu_f32(q0) * q1);
-          cw[off + hm_c] = f32_to_bf16(silu_f32(q2) * q3);
+          cw.put(off, gate_f32<kEpi>(q0) * q1);
+          cw.put(off + hm_c, gate_f32<kEpi>(q2) * q3);
         } else if constexpr (kEpi == SMX_EPI_QK_NORM_ROPE) {
           // Normalisation needs whole head segments: keep the quadrant
           // values and finish below.
@@ -252,10 +284,10 @@ __device__ __forceinline__ void epilogue(const Params& p, const TileOrigin& o, i
             q2 += bl;
             q3 += br;
           }
-          cw[off] = f32_to_bf16(q0);
-          cw[off + hn] = f32_to_bf16(q1);
-          cw[off + hm_c] = f32_to_bf16(q2);
-          cw[off + hm_c + hn] = f32_to_bf16(q3);
+          cw.put(off, q0);
+          cw.put(off + hn, q1);
+          cw.put(off + hm_c, q2);
+          cw.put(off + hm_c + hn, q3);
         }
       }
       // One 32x32 block at a time keeps the epilogue's live set small.
@@ -301,8 +333,8 @@ __device__ __forceinline__ void epilogue(const Params& p, const TileOrigin& o, i
               const float na = acc[sa][i][j][r] * recip * ga;
               const float nbv = acc[sb][i][j][r] * recip * gb;
               const int off = ri * ldc + cj + half * hm_c;
-              cw[off] = f32_to_bf16(na * cs - nbv * sn);
-              cw[off + hn] = f32_to_bf16(nbv * cs + na * sn);
+              cw.put(off, na * cs - nbv * sn);
+              cw.put(off + hn, nbv * cs + na * sn);
             }
           }
         }

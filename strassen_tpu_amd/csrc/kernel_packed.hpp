@@ -304,7 +304,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
   epilogue<kAlgo, 2, 2, kEpi>(p, o, wm * 64, wn * 64, acc);
 }
 
-// Packs one operand. kSide 0: A [m, k] row-major, product row R = (tile i,
+// Packs one operand. kSide 0: A [m, k] row-major (kSide 2: the same A stored
+// transposed as [k, m]), product row R = (tile i,
 // row r < bm/2) -> physical rows i*bm + r (top) and + bm/2 (bottom).
 // kSide 1: B^T [n, k] row-major, product column C = (tile j, c < bn/2) ->
 // rows j*bn + c (left) and + bn/2 (right) of B^T. Product depth k' = (panel
@@ -329,8 +330,20 @@ __global__ __launch_bounds__(256) void pack_operand(const uint16_t* __restrict__
   const int64_t sg = gwave - rblock * sgroups;
   const int hr = tile_rows / 2, hk = bk / 2;
   const int64_t r = rblock * 32 + (lane & 31);
-  const uint16_t* const first = src + ((r / hr) * tile_rows + r % hr) * ld;
+  const int64_t row_first = (r / hr) * tile_rows + r % hr, row_second = row_first + hr;
+  const uint16_t* const first = src + row_first * ld;
   const uint16_t* const second = first + (int64_t)hr * ld;
+  // kSide 2: A stored transposed, [k, rows] with row stride ld; element
+  // (row, col) of A is src[col * ld + row]. Eight consecutive k of one row
+  // are gathered from eight source rows (lanes cover consecutive rows, so
+  // each load instruction reads 64 contiguous bytes of one source row).
+  auto gather = [&](int64_t row, int64_t col0) {
+    u32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      v[e] = (uint32_t)src[(col0 + 2 * e) * ld + row] | ((uint32_t)src[(col0 + 2 * e + 1) * ld + row] << 16);
+    return v;
+  };
   const int half = lane >> 5;
   uint8_t* const dst_tile = out + frag_offset(rblock / 4, 0, nstages, 0, nops, (int)(rblock % 4)) + lane * 16;
 #pragma unroll
@@ -340,7 +353,12 @@ __global__ __launch_bounds__(256) void pack_operand(const uint16_t* __restrict__
     const int64_t kp = st * TK + half * 8;
     const int64_t lo = (kp / hk) * bk + kp % hk, hi = lo + hk;
     u32x4 q[4];
-    if constexpr (kSide == 0) {
+    if constexpr (kSide == 2) {
+      q[0] = gather(row_first, lo);
+      q[1] = gather(row_first, hi);
+      q[2] = gather(row_second, lo);
+      q[3] = gather(row_second, hi);
+    } else if constexpr (kSide == 0) {
       q[0] = *reinterpret_cast<const u32x4*>(first + lo);
       q[1] = *reinterpret_cast<const u32x4*>(first + hi);
       q[2] = *reinterpret_cast<const u32x4*>(second + lo);
@@ -354,7 +372,7 @@ __global__ __launch_bounds__(256) void pack_operand(const uint16_t* __restrict__
     uint8_t* const dst = dst_tile + st * (int64_t)(nops * kBlocks * kFrag);
     if constexpr (kAlgo == 7) {
       u32x4 ops[7];
-      if constexpr (kSide == 0)
+      if constexpr (kSide != 1)
         strassen_a_ops(q, ops);
       else
         strassen_b_ops(q, ops);

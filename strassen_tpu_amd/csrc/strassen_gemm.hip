@@ -106,6 +106,7 @@ int dispatch_v1(const Params& p, int epilogue, hipStream_t s) {
   switch (epilogue) {
     case SMX_EPI_NONE: return launch_v1<v1::General<kAlgo>, SMX_EPI_NONE>(p, s);
     case SMX_EPI_SWIGLU: return launch_v1<v1::General<kAlgo>, SMX_EPI_SWIGLU>(p, s);
+    case SMX_EPI_GEGLU: return launch_v1<v1::General<kAlgo>, SMX_EPI_GEGLU>(p, s);
     case SMX_EPI_RESIDUAL_ADD: return launch_v1<v1::General<kAlgo>, SMX_EPI_RESIDUAL_ADD>(p, s);
     case SMX_EPI_BIAS_ADD: return launch_v1<v1::General<kAlgo>, SMX_EPI_BIAS_ADD>(p, s);
     case SMX_EPI_QK_NORM_ROPE: return launch_v1<v1::ForQK<kAlgo>, SMX_EPI_QK_NORM_ROPE>(p, s);
@@ -118,6 +119,7 @@ int dispatch_packed(const Params& p, int epilogue, hipStream_t s) {
   switch (epilogue) {
     case SMX_EPI_NONE: return launch_packed<kAlgo, SMX_EPI_NONE>(p, s);
     case SMX_EPI_SWIGLU: return launch_packed<kAlgo, SMX_EPI_SWIGLU>(p, s);
+    case SMX_EPI_GEGLU: return launch_packed<kAlgo, SMX_EPI_GEGLU>(p, s);
     case SMX_EPI_RESIDUAL_ADD: return launch_packed<kAlgo, SMX_EPI_RESIDUAL_ADD>(p, s);
     case SMX_EPI_BIAS_ADD: return launch_packed<kAlgo, SMX_EPI_BIAS_ADD>(p, s);
     case SMX_EPI_QK_NORM_ROPE: return launch_packed<kAlgo, SMX_EPI_QK_NORM_ROPE>(p, s);
@@ -190,7 +192,8 @@ int smx_pack_operand(int32_t algo, int32_t side, int64_t rows, int64_t k, const 
                      int32_t tile_rows, int32_t bk, void* out, void* stream) {
   g_error[0] = 0;
   if (algo != SMX_ALGO_STRASSEN && algo != SMX_ALGO_CUBIC) return fail(SMX_ERR_INVALID, "algo must be 7 or 8");
-  if (side != SMX_SIDE_LHS && side != SMX_SIDE_RHS) return fail(SMX_ERR_INVALID, "side must be LHS (0) or RHS (1)");
+  if (side != SMX_SIDE_LHS && side != SMX_SIDE_RHS && side != SMX_SIDE_LHS_T)
+    return fail(SMX_ERR_INVALID, "side must be LHS (0), RHS (1) or LHS_T (2)");
   if (rows <= 0 || k <= 0 || tile_rows <= 0 || bk <= 0 || rows % tile_rows || k % bk)
     return fail(SMX_ERR_INVALID, "packing needs rows %% tile_rows == 0 and K %% bk == 0");
   if (tile_rows % (2 * packed::TM) || bk % (2 * packed::kKGranule))
@@ -198,15 +201,20 @@ int smx_pack_operand(int32_t algo, int32_t side, int64_t rows, int64_t k, const 
                 side == SMX_SIDE_LHS ? "bm" : "bn", 2 * packed::TM, 2 * packed::kKGranule, tile_rows, bk);
   if (!src || !out) return fail(SMX_ERR_INVALID, "null pointer");
   if (!aligned16(src) || !aligned16(out)) return fail(SMX_ERR_INVALID, "pointers must be 16-byte aligned");
-  if (ld < k || ld % 8) return fail(SMX_ERR_INVALID, "ld must be >= K and a multiple of 8");
+  if (side == SMX_SIDE_LHS_T ? ld < rows : (ld < k || ld % 8))
+    return fail(SMX_ERR_INVALID, side == SMX_SIDE_LHS_T ? "ld must be >= rows for a transposed A"
+                                                        : "ld must be >= K and a multiple of 8");
   const uint16_t* s16 = (const uint16_t*)src;
   uint8_t* o8 = (uint8_t*)out;
   hipStream_t st = (hipStream_t)stream;
-  if (algo == SMX_ALGO_STRASSEN)
-    return side == SMX_SIDE_LHS ? launch_pack<7, 0>(s16, ld, rows, k, tile_rows, bk, o8, st)
-                                : launch_pack<7, 1>(s16, ld, rows, k, tile_rows, bk, o8, st);
-  return side == SMX_SIDE_LHS ? launch_pack<8, 0>(s16, ld, rows, k, tile_rows, bk, o8, st)
-                              : launch_pack<8, 1>(s16, ld, rows, k, tile_rows, bk, o8, st);
+  if (algo == SMX_ALGO_STRASSEN) {
+    if (side == SMX_SIDE_LHS) return launch_pack<7, 0>(s16, ld, rows, k, tile_rows, bk, o8, st);
+    if (side == SMX_SIDE_RHS) return launch_pack<7, 1>(s16, ld, rows, k, tile_rows, bk, o8, st);
+    return launch_pack<7, 2>(s16, ld, rows, k, tile_rows, bk, o8, st);
+  }
+  if (side == SMX_SIDE_LHS) return launch_pack<8, 0>(s16, ld, rows, k, tile_rows, bk, o8, st);
+  if (side == SMX_SIDE_RHS) return launch_pack<8, 1>(s16, ld, rows, k, tile_rows, bk, o8, st);
+  return launch_pack<8, 2>(s16, ld, rows, k, tile_rows, bk, o8, st);
 }
 
 int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, const void* residual, const void* bias,
@@ -223,7 +231,7 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
   const bool packed_path = d->b_layout == SMX_B_PACKED;
   if (packed_path != (d->a_layout == SMX_A_PACKED))
     return fail(SMX_ERR_UNSUPPORTED, "A and B must both be packed (smx_pack_operand) or both unpacked");
-  if (d->flags) return fail(SMX_ERR_INVALID, "flags must be 0, got 0x%x", d->flags);
+  if (d->flags & ~SMX_FLAG_OUT_F32) return fail(SMX_ERR_INVALID, "unknown flags 0x%x", d->flags);
   if (d->m <= 0 || d->n <= 0 || d->k <= 0)
     return fail(SMX_ERR_INVALID, "empty problem m=%lld n=%lld k=%lld", (long long)d->m, (long long)d->n,
                 (long long)d->k);
@@ -240,7 +248,7 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
   if (!aligned16(a) || !aligned16(b)) return fail(SMX_ERR_INVALID, "A and B must be 16-byte aligned");
   if (!packed_path && (d->lda < d->k || d->ldb < d->k || d->lda % 8 || d->ldb % 8))
     return fail(SMX_ERR_INVALID, "lda and ldb must be >= K and multiples of 8 elements");
-  const int64_t out_cols = d->epilogue == SMX_EPI_SWIGLU ? d->n / 2 : d->n;
+  const int64_t out_cols = (d->epilogue == SMX_EPI_SWIGLU || d->epilogue == SMX_EPI_GEGLU) ? d->n / 2 : d->n;
   if (d->ldc < out_cols) return fail(SMX_ERR_INVALID, "ldc must be >= output width");
   // The epilogue addresses a tile half with 32-bit element offsets.
   const int64_t widest = d->ldc > d->ldr ? d->ldc : d->ldr;
@@ -250,7 +258,8 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
   Params p{};
   p.a = (const uint16_t*)a;
   p.b = (const uint16_t*)b;
-  p.c = (uint16_t*)c;
+  p.c = c;
+  p.out_f32 = (d->flags & SMX_FLAG_OUT_F32) ? 1 : 0;
   p.m = d->m;
   p.n = d->n;
   p.k = d->k;
@@ -268,6 +277,7 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
   switch (d->epilogue) {
     case SMX_EPI_NONE:
     case SMX_EPI_SWIGLU:
+    case SMX_EPI_GEGLU:
       break;
     case SMX_EPI_RESIDUAL_ADD:
       if (!residual) return fail(SMX_ERR_INVALID, "residual_add epilogue requires residual");

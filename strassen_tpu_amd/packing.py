@@ -73,12 +73,13 @@ def packed_bytes(algo, rows, k):
 
 
 def pack_operand(x, *, algo, side, tile_rows, bk):
-    """Pack ``x`` (bf16 on the HIP device): ``a [M, K]`` for ``side="lhs"``
-    or a weight ``b [K, N]`` for ``side="rhs"`` (any strides; a K-contiguous
-    view of ``[N, K]`` storage is read in place). Runs asynchronously on
-    torch's current stream."""
-    if side not in ("lhs", "rhs"):
-        raise ValueError("side must be 'lhs' or 'rhs'")
+    """Pack ``x`` (bf16 on the HIP device): ``a [M, K]`` for ``side="lhs"``,
+    the same ``a`` stored transposed as ``[K, M]`` for ``side="lhs_t"``, or a
+    weight ``b [K, N]`` for ``side="rhs"`` (any strides; a K-contiguous view
+    of ``[N, K]`` storage is read in place). Runs asynchronously on torch's
+    current stream."""
+    if side not in ("lhs", "rhs", "lhs_t"):
+        raise ValueError("side must be 'lhs', 'lhs_t' or 'rhs'")
     if algo not in _ALGOS:
         raise ValueError(f"algo must be {_lib.SMX_ALGO_STRASSEN} or {_lib.SMX_ALGO_CUBIC}")
     if x.dim() != 2:
@@ -87,20 +88,27 @@ def pack_operand(x, *, algo, side, tile_rows, bk):
         raise ValueError("pack_operand expects bf16")
     if x.device.type != "cuda":
         raise ValueError("pack_operand runs on the HIP device")
-    src = x if side == "lhs" else x.t()  # rows x K, K contiguous
-    rows, k = src.shape
+    if side == "lhs_t":
+        src = x  # [K, rows], rows contiguous
+        k, rows = src.shape
+        if src.stride(1) != 1 or src.data_ptr() % 16:
+            src = src.contiguous()
+    else:
+        src = x if side == "lhs" else x.t()  # rows x K, K contiguous
+        rows, k = src.shape
+        if src.stride(1) != 1 or src.stride(0) % 8 or src.data_ptr() % 16:
+            src = src.contiguous()
     if rows % tile_rows or k % bk:
         raise ValueError(f"operand [{rows}, {k}] (rows x K) does not tile by ({tile_rows}, {bk})")
-    if src.stride(1) != 1 or src.stride(0) % 8 or src.data_ptr() % 16:
-        src = src.contiguous()
     nbytes = packed_bytes(algo, rows, k)
     data = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=x.device)
-    side_id = _lib.SMX_SIDE_LHS if side == "lhs" else _lib.SMX_SIDE_RHS
+    side_id = {"lhs": _lib.SMX_SIDE_LHS, "rhs": _lib.SMX_SIDE_RHS, "lhs_t": _lib.SMX_SIDE_LHS_T}[side]
     stream = torch.cuda.current_stream(x.device).cuda_stream
     rc = _lib.load().smx_pack_operand(algo, side_id, rows, k, _lib.ptr(src), src.stride(0), tile_rows, bk,
                                       _lib.ptr(data), stream)
     _lib.check(rc)
-    return PackedOperand(data, algo=algo, side=side, rows=rows, k=k, tile_rows=tile_rows, bk=bk)
+    return PackedOperand(data, algo=algo, side="rhs" if side == "rhs" else "lhs", rows=rows, k=k,
+                         tile_rows=tile_rows, bk=bk)
 
 
 def strassen_weight_layout(b, bn, bk):

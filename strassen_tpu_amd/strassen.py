@@ -11,9 +11,8 @@ Differences a caller can observe, all raised as exceptions (never silent):
 
 * Research formula knobs that the tuned dispatcher never selects
   (``formula_variant != "classical"``, ``block_permutation``,
-  ``classical_panels``, ``panel_schedule``) and the ``geglu`` /
-  ``norm_residual_add`` epilogues, FP32 inputs and FP32 output raise
-  ``NotImplementedError``.
+  ``classical_panels``, ``panel_schedule``), the ``norm_residual_add``
+  epilogue and FP32 inputs raise ``NotImplementedError``.
 * TPU-only knobs (``dot_precision``, ``allow_input_fusion`` after its
   validation, ``vmem_limit_bytes``) are accepted and have no effect;
   ``interpret=True`` raises ``NotImplementedError`` (there is no CPU path).
@@ -37,7 +36,7 @@ from .layouts import is_k_contiguous
 from .packing import PackedOperand, pack_operand
 
 __all__ = [
-    "strassen_matmul", "cubic_matmul", "native_matmul", "check_tiling",
+    "strassen_matmul", "strassen_matmul_lhs_transposed", "cubic_matmul", "native_matmul", "check_tiling",
     "TUNED_BM", "TUNED_BN", "TUNED_BK", "VMEM_PROFILE", "PROFILE_INFO",
 ]
 
@@ -199,7 +198,7 @@ def _validate(a, b, *, bm, bn, bk, block_permutation, formula_variant,
 
 
 def _unsupported(formula_variant, block_permutation, classical_panels, panel_schedule,
-                 epilogue, dtype, out_dtype, interpret):
+                 epilogue, dtype, interpret):
     if interpret:
         raise NotImplementedError("interpret=True: the gfx950 kernel has no CPU interpreter path")
     if formula_variant != "classical":
@@ -208,12 +207,10 @@ def _unsupported(formula_variant, block_permutation, classical_panels, panel_sch
         raise NotImplementedError("block_permutation is not implemented on gfx950")
     if classical_panels or panel_schedule is not None:
         raise NotImplementedError("exact-panel policies are not implemented on gfx950")
-    if epilogue in ("geglu", "norm_residual_add"):
+    if epilogue == "norm_residual_add":
         raise NotImplementedError(f"epilogue {epilogue!r} is not implemented on gfx950")
     if dtype != torch.bfloat16:
         raise NotImplementedError("FP32 inputs are not implemented on gfx950 (bf16 MFMA path)")
-    if out_dtype != torch.bfloat16:
-        raise NotImplementedError("FP32 output is not implemented on gfx950")
 
 
 def _require_device(*tensors):
@@ -234,7 +231,7 @@ def _check_packed(x, algo, side, tile_rows, bk):
 
 def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
          rope_cos=None, rope_sin=None, rope_scale=None, rope_head_dim=128,
-         rope_eps=1e-6):
+         rope_eps=1e-6, out_dtype=torch.bfloat16):
     lib = _lib.load()
     m, k = a.shape
     n = b.shape[1]
@@ -261,8 +258,8 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
             b = b.t().contiguous().t()
         bt = b.t()  # [N, K], rows contiguous
         a_ptr, b_ptr, lda, ldb = a, bt, a.stride(0), bt.stride(0)
-    out_cols = n // 2 if epilogue == "swiglu" else n
-    c = torch.empty((m, out_cols), dtype=torch.bfloat16, device=a.device)
+    out_cols = n // 2 if epilogue in ("swiglu", "geglu") else n
+    c = torch.empty((m, out_cols), dtype=out_dtype, device=a.device)
     desc = _lib.SmxGemmDesc()
     desc.m, desc.n, desc.k = m, n, k
     desc.lda, desc.ldb, desc.ldc = lda, ldb, c.stride(0)
@@ -271,6 +268,7 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
     desc.epilogue = _lib.SMX_EPI[epilogue]
     desc.a_layout = _lib.SMX_A_PACKED if packed else _lib.SMX_A_ROWMAJOR
     desc.b_layout = b_layout
+    desc.flags = _lib.SMX_FLAG_OUT_F32 if out_dtype == torch.float32 else 0
     desc.rope_head_dim = rope_head_dim
     desc.rope_eps = rope_eps
     aux = 0
@@ -360,17 +358,63 @@ def strassen_matmul(
         product_aware_swiglu=product_aware_swiglu,
         product_aware_residual=product_aware_residual)
     _unsupported(formula_variant, block_permutation, classical_panels, panel_schedule,
-                 epilogue, a.dtype, out_dtype, interpret)
+                 epilogue, a.dtype, interpret)
     return _run(_lib.SMX_ALGO_STRASSEN, a, b, bm=bm, bn=bn, bk=bk, epilogue=epilogue,
                 residual=residual, bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
-                rope_scale=rope_scale, rope_head_dim=rope_head_dim, rope_eps=rope_eps)
+                rope_scale=rope_scale, rope_head_dim=rope_head_dim, rope_eps=rope_eps,
+                out_dtype=out_dtype)
+
+
+def strassen_matmul_lhs_transposed(a, b, *, bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_BK, dot_precision=None,
+                                   interleave_products=False, output_dtype=None, allow_input_fusion=None,
+                                   interpret=False, vmem_limit_bytes=None):
+    """``a.T @ b`` with ``a`` kept in its producer layout ``[K, M]``
+    (``strassen_pallas.py:1224-1312``), for weight-gradient products.
+
+    The packing pass reads ``a`` transposed tile by tile (no ``[M, K]`` copy is
+    materialised) while forming the A operand sums; ``b`` is a ``[K, N]``
+    tensor (packed on each call) or a ``strassen_weight_layout`` weight.
+    Arguments, checks and messages follow ``:1250-1267``; FP32 inputs and
+    ``interpret=True`` raise ``NotImplementedError``.
+    """
+    if a.dim() != 2 or b.dim() != 2:
+        raise ValueError("strassen_matmul_lhs_transposed expects rank-2 inputs")
+    k, m = a.shape
+    k2, n = b.shape
+    if k != k2:
+        raise ValueError(f"contracting dimensions disagree: {k} vs {k2}")
+    if a.dtype != b.dtype:
+        raise ValueError(f"input dtypes disagree: {a.dtype} vs {b.dtype}")
+    if a.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("inputs must be BF16 or FP32")
+    for name, dimension, block in (("M", m, bm), ("N", n, bn), ("K", k, bk)):
+        if dimension % block:
+            raise ValueError(f"{name}={dimension} is not divisible by {block}")
+    check_tiling(bm, bn, bk)
+    if allow_input_fusion is not None:
+        allow_input_fusion = tuple(allow_input_fusion)
+        if len(allow_input_fusion) != 2:
+            raise ValueError("allow_input_fusion must contain two booleans")
+    out_dtype = a.dtype if output_dtype is None else output_dtype
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("output_dtype must be BF16 or FP32")
+    if interpret:
+        raise NotImplementedError("interpret=True: the gfx950 kernel has no CPU interpreter path")
+    if a.dtype != torch.bfloat16:
+        raise NotImplementedError("FP32 inputs are not implemented on gfx950 (bf16 MFMA path)")
+    _check_device_tiling(_lib.SMX_ALGO_STRASSEN, None, bm, bn, bk, _lib.SMX_B_PACKED)
+    _require_device(a, b.data if isinstance(b, PackedOperand) else b)
+    packed_a = pack_operand(a, algo=_lib.SMX_ALGO_STRASSEN, side="lhs_t", tile_rows=bm, bk=bk)
+    if not isinstance(b, PackedOperand):
+        b = pack_operand(b, algo=_lib.SMX_ALGO_STRASSEN, side="rhs", tile_rows=bn, bk=bk)
+    return _run(_lib.SMX_ALGO_STRASSEN, packed_a, b, bm=bm, bn=bn, bk=bk, out_dtype=out_dtype)
 
 
 def cubic_matmul(a, b, *, variant="blocked", bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_BK,
                  dot_precision=None, allow_input_fusion=None, interpret=False,
                  vmem_limit_bytes=None, epilogue=None, residual=None, bias=None,
                  rope_cos=None, rope_sin=None, rope_scale=None, rope_head_dim=128,
-                 rope_eps=1e-6):
+                 rope_eps=1e-6, output_dtype=None):
     """Matched cubic control (``experiments/qwen3/benchmark_cubic_control.py:116-177``).
 
     Eight half-size products per K panel into four FP32 quadrant
@@ -405,9 +449,13 @@ def cubic_matmul(a, b, *, variant="blocked", bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_
         raise NotImplementedError("interpret=True: the gfx950 kernel has no CPU interpreter path")
     if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
         raise NotImplementedError("the gfx950 cubic control takes bf16 inputs")
+    out_dtype = torch.bfloat16 if output_dtype is None else output_dtype
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("output_dtype must be BF16 or FP32")
     return _run(_lib.SMX_ALGO_CUBIC, a, b, bm=bm, bn=bn, bk=bk, epilogue=epilogue,
                 residual=residual, bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
-                rope_scale=rope_scale, rope_head_dim=rope_head_dim, rope_eps=rope_eps)
+                rope_scale=rope_scale, rope_head_dim=rope_head_dim, rope_eps=rope_eps,
+                out_dtype=out_dtype)
 
 
 def native_matmul(a, b):

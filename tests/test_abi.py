@@ -142,7 +142,8 @@ def test_packed_bytes():
 @pytest.mark.parametrize("args,code", [
     ((7, 0, 0, 512, 512, 256, 512), _lib.SMX_ERR_INVALID),        # rows = 0
     ((7, 0, 512, 512, 512, 256, 500), _lib.SMX_ERR_INVALID),      # k % bk
-    ((7, 2, 512, 512, 512, 256, 512), _lib.SMX_ERR_INVALID),      # side
+    ((7, 3, 512, 512, 512, 256, 512), _lib.SMX_ERR_INVALID),      # side
+    ((7, 2, 512, 512, 256, 256, 512), _lib.SMX_ERR_INVALID),      # transposed A: ld < rows
     ((6, 0, 512, 512, 512, 256, 512), _lib.SMX_ERR_INVALID),      # algo
     ((7, 0, 512, 512, 512, 128, 512), _lib.SMX_ERR_UNSUPPORTED),  # tile_rows % 256
     ((8, 1, 512, 512, 512, 256, 48), _lib.SMX_ERR_INVALID),       # k % bk

@@ -290,6 +290,65 @@ def test_swiglu_epilogue():
                                             interleave_products=True, product_aware_swiglu=True), k=1024)
 
 
+def test_geglu_epilogue():
+    _, a, b = _gaussian(330, 512, 1024, 2048)
+    bm, bn, bk = 256, 512, 512
+    laid = o.swiglu_weight_layout(b, bn)
+    laid_dev = smx.swiglu_weight_layout(dev_weight(b), bn)
+    for arm in ARMS:
+        got = host(run_arm(arm, a, laid_dev, bm=bm, bn=bn, bk=bk, epilogue="geglu"))
+        assert got.shape == (512, 1024)
+        assert_ulp_close(got, oracle_arm(arm, a, laid, bm=bm, bn=bn, bk=bk, epilogue="geglu"), k=1024)
+
+
+def test_fp32_output():
+    """output_dtype=float32: the unrounded FP32 quadrant values (the
+    reference's output-as-accumulator path, strassen_pallas.py:1048-1057; the
+    reference allows it only without a fused epilogue)."""
+    _, a, b = _gaussian(331, 512, 1024, 1024)
+    kw = dict(bm=256, bn=512, bk=512)
+    for arm in ARMS:
+        got_t = run_arm(arm, a, b, output_dtype=torch.float32, **kw)
+        assert got_t.dtype == torch.float32
+        got = host(got_t)
+        want = oracle_arm(arm, a, b, output_dtype="float32", **kw)
+        # FP32 summation order differs: a few FP32 ulps plus the near-zero floor.
+        tol = 4 * np.abs(want) * 2.0 ** -23 + fp32_floor(want, 1024)
+        assert np.all(np.abs(got - want) <= tol), arm
+        # rounding it gives the kernel's bf16 result (same FP32 values)
+        bf = host(run_arm(arm, a, b, **kw))
+        assert np.array_equal(bf, o.bf16_round(got)), arm
+    with pytest.raises(ValueError, match="BF16 output tile"):
+        smx.strassen_matmul(dev(a), dev_weight(b), epilogue="residual_add", residual=dev(a[:, :1024]),
+                            output_dtype=torch.float32, **kw)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_lhs_transposed(out_dtype):
+    """a stored [K, M]: the transposed pack reads it in place; the product
+    equals the oracle's Strassen of a.T (strassen_pallas.py:1224-1312)."""
+    rng = np.random.default_rng(332)
+    k, m, n = 1024, 512, 768
+    a_t = o.bf16_round(rng.standard_normal((k, m)).astype(np.float32))
+    b = o.bf16_round(rng.standard_normal((k, n)).astype(np.float32) * np.float32(0.02))
+    packed = smx.pack_operand(dev(a_t), algo=7, side="lhs_t", tile_rows=256, bk=512)
+    assert np.array_equal(host(packed.data), o.packed_operand(a_t.T, 7, "lhs", 256, 512))
+    got = smx.strassen_matmul_lhs_transposed(dev(a_t), dev(b), bm=256, bn=256, bk=512, output_dtype=out_dtype)
+    assert got.dtype == out_dtype and tuple(got.shape) == (m, n)
+    want = o.strassen_matmul_lhs_transposed(a_t, b, bm=256, bn=256, bk=512,
+                                            output_dtype="float32" if out_dtype == torch.float32 else "bfloat16")
+    if out_dtype == torch.bfloat16:
+        assert_ulp_close(host(got), want, k=k)
+    else:
+        tol = 4 * np.abs(want) * 2.0 ** -23 + fp32_floor(want, k)
+        assert np.all(np.abs(host(got) - want) <= tol)
+    # integer data: exactly a.T @ b
+    ai = rng.integers(-2, 3, (k, m)).astype(np.float32)
+    bi = rng.integers(-2, 3, (k, n)).astype(np.float32)
+    got = host(smx.strassen_matmul_lhs_transposed(dev(ai), dev(bi), bm=256, bn=256, bk=512))
+    assert np.array_equal(got, o.bf16_round(ai.T @ bi))
+
+
 def test_residual_add_epilogue():
     rng, a, b = _gaussian(319, 512, 2048, 1024)
     r = o.bf16_round(rng.standard_normal((512, 1024)).astype(np.float32))

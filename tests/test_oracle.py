@@ -216,6 +216,49 @@ def test_swiglu_closed_form_with_layout():
         np.testing.assert_allclose(got, expected, rtol=2 ** -7, atol=1e-6)
 
 
+def test_gelu_tanh_against_torch_and_closed_form():
+    """The GeGLU gate equals torch's gelu(approximate='tanh') (a separate
+    implementation) and the erf GELU within the tanh approximation's error."""
+    import math
+
+    import torch
+
+    x = np.linspace(-8, 8, 4001, dtype=np.float32)
+    got = o.gelu_tanh(x)
+    want = torch.nn.functional.gelu(torch.from_numpy(x), approximate="tanh").numpy()
+    np.testing.assert_allclose(got, want, rtol=2e-6, atol=2e-6)
+    exact = np.array([0.5 * v * (1 + math.erf(v / math.sqrt(2))) for v in x.astype(np.float64)])
+    assert np.max(np.abs(got - exact)) < 1e-3
+    assert o.gelu_tanh(np.float32(0.0)) == 0.0
+
+
+def test_geglu_closed_form_with_layout():
+    """gelu_tanh(gate) * up of the un-laid-out projection equals the fused
+    GeGLU epilogue on the laid-out weight (Strassen and cubic)."""
+    rng, a, b = _int_problem(319, 32, 512, 1024)
+    laid = o.swiglu_weight_layout(b, 256)
+    exact = (a @ b).astype(np.float64)
+    gate, up = np.split(exact, 2, axis=1)
+    expected = 0.5 * gate * (1 + np.tanh(np.sqrt(2 / np.pi) * (gate + 0.044715 * gate ** 3))) * up
+    for got in (o.strassen_matmul(a, laid, bm=16, bn=256, bk=256, epilogue="geglu"),
+                o.cubic_blocked_matmul(a, laid, bm=16, bn=256, bk=256, epilogue="geglu")):
+        assert got.shape == (32, 512)
+        # float32 1 + tanh(x) cancels for very negative gates (as in the
+        # reference's float32 gelu): a small absolute allowance there.
+        np.testing.assert_allclose(got, expected, rtol=2 ** -7, atol=1e-5)
+
+
+def test_fp32_output_is_the_unrounded_accumulator():
+    """output_dtype float32 returns the FP32 quadrant values: on integer data
+    exactly A @ B (no bf16 rounding), and the bf16 output is its rounding."""
+    rng, a, b = _int_problem(320, 64, 512, 256)
+    f32 = o.strassen_matmul(a, b, bm=32, bn=256, bk=256, output_dtype="float32")
+    assert f32.dtype == np.float32 and np.array_equal(f32, a @ b)
+    big = (a @ b) * 1000.5  # values no longer representable in bf16
+    assert not np.array_equal(o.bf16_round(big), big)
+    assert np.array_equal(o.strassen_matmul(a, b, bm=32, bn=256, bk=256), o.bf16_round(f32))
+
+
 def test_product_aware_residual_bitwise_identical_to_interleaved():
     """strassen_pallas.py:640-643: same FP32 order, bitwise identical."""
     rng = np.random.default_rng(7)

@@ -60,8 +60,7 @@ def test_reference_argument_errors(kwargs, args, exc, match):
     {"block_permutation": 3},
     {"classical_panels": (0,)},
     {"panel_schedule": [0]},
-    {"epilogue": "geglu"},
-    {"output_dtype": torch.float32},
+    {"epilogue": "norm_residual_add", "norm_scale": t(256), "residual": t(256, 256)},
     {"interpret": True},
 ])
 def test_unported_options_raise_not_implemented(kwargs):
@@ -208,3 +207,23 @@ def test_torch_relayouts_match_oracle():
     flat = torch.randn(2 * 4 * 1024).reshape(8, 1024)
     assert np.array_equal(smx.rope_layout_to_heads(flat, 8, 256, 2, 4).numpy(),
                           o.rope_layout_to_heads(flat.numpy(), 8, 256, 2, 4))
+
+
+@pytest.mark.parametrize("args,kwargs,exc,match", [
+    ((t(4), t(4, 4)), {}, ValueError, "expects rank-2 inputs"),
+    ((t(512, 256), t(256, 256)), {}, ValueError, "contracting dimensions disagree: 512 vs 256"),
+    ((t(512, 256), t(512, 256, dtype=torch.float32)), {}, ValueError, "input dtypes disagree"),
+    ((t(512, 256, dtype=torch.float16), t(512, 256, dtype=torch.float16)), {}, ValueError, "BF16 or FP32"),
+    ((t(512, 256), t(512, 256)), {"bm": 96}, ValueError, "M=256 is not divisible by 96"),
+    ((t(512, 256), t(512, 256)), {"allow_input_fusion": (True,)}, ValueError, "two booleans"),
+    ((t(512, 256), t(512, 256)), {"output_dtype": torch.float16}, ValueError, "BF16 or FP32"),
+    ((t(512, 256, dtype=torch.float32), t(512, 256, dtype=torch.float32)), {}, NotImplementedError, "FP32"),
+    ((t(512, 256), t(512, 256)), {"interpret": True}, NotImplementedError, "interpret"),
+    ((t(512, 256), t(512, 256)), {}, ValueError, "HIP device"),
+])
+def test_lhs_transposed_surface(args, kwargs, exc, match):
+    """strassen_matmul_lhs_transposed's checks (strassen_pallas.py:1250-1267)."""
+    kw = dict(bm=256, bn=256, bk=512)
+    kw.update(kwargs)
+    with pytest.raises(exc, match=match):
+        smx.strassen_matmul_lhs_transposed(*args, **kw)
