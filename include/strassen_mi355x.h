@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define SMX_VERSION 3
+#define SMX_VERSION 4
 
 /* Status codes. */
 #define SMX_OK 0
@@ -48,6 +48,11 @@ extern "C" {
 /* Algorithms. */
 #define SMX_ALGO_STRASSEN 7 /* one-level classical Strassen, 7 products */
 #define SMX_ALGO_CUBIC 8    /* matched blocked cubic, 8 products */
+
+/* Strassen formula variants (strassen_pallas.py formula_variant). */
+#define SMX_FORMULA_CLASSICAL 0 /* P1..P7, :324-379 */
+#define SMX_FORMULA_DUAL 1      /* Q1..Q7, :461-517 */
+#define SMX_FORMULA_POWERS 2    /* R1..R7 into a decoded output basis, :381-459 / :744-760; no fused epilogue */
 
 /* Epilogues (strassen_pallas.py:739-879). */
 #define SMX_EPI_NONE 0
@@ -90,6 +95,8 @@ typedef struct smx_gemm_desc {
   float rope_eps;        /* qk_norm_rope epsilon */
   int32_t aux_f32;       /* SMX_AUX_* bits */
   int32_t flags;         /* SMX_FLAG_* bits */
+  int32_t formula;       /* SMX_FORMULA_* (Strassen; packed operands built with the same formula) */
+  int32_t block_permutation; /* 0..7: bit 0 swaps row halves, bit 1 K halves, bit 2 column halves (:205-226) */
 } smx_gemm_desc;
 
 /*
@@ -124,16 +131,18 @@ int smx_packed_bytes(int32_t algo, int64_t rows, int64_t k, int64_t* bytes);
  * transposed, bf16 [k, rows = m] with row stride ld >= m; SMX_SIDE_RHS: src
  * is B^T bf16 [rows = n, k] and tile_rows = bn. Strassen (algo 7) stores the seven operand sums of
  * P1..P7 (A0+A3, A2+A3, A0, A3, A0+A1, A2-A0, A1-A3; B0+B3, B0, B1-B3,
- * B2-B0, B3, B0+B1, B2+B3), each rounded once to bf16; the cubic (algo 8)
- * stores the four quadrants. out (smx_packed_bytes bytes, 16-byte aligned)
+ * B2-B0, B3, B0+B1, B2+B3), each rounded once to bf16, or those of the dual /
+ * powers formula, after the block permutation's quadrant swaps (A uses bits 0
+ * and 1, B bits 1 and 2); the cubic (algo 8, formula 0, permutation 0) stores
+ * the four quadrants. out (smx_packed_bytes bytes, 16-byte aligned)
  * is laid out [rows/256][k/32][nops][4][64][8] bf16: fragment (tile of 128
  * product rows, stage of 16 product k, operand, 32-row block), lane l holding
  * row l%32, depth 8*(l/32)..+8. Needs rows % tile_rows == 0, k % bk == 0,
  * tile_rows % 256 == 0, bk % 64 == 0, ld >= k, ld % 8 == 0 (LHS_T: ld >= m). Asynchronous on
  * stream.
  */
-int smx_pack_operand(int32_t algo, int32_t side, int64_t rows, int64_t k, const void* src, int64_t ld,
-                     int32_t tile_rows, int32_t bk, void* out, void* stream);
+int smx_pack_operand(int32_t algo, int32_t formula, int32_t block_permutation, int32_t side, int64_t rows, int64_t k,
+                     const void* src, int64_t ld, int32_t tile_rows, int32_t bk, void* out, void* stream);
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* smx_last_error(void);

@@ -21,6 +21,8 @@ __all__ = [
     "rope_scale_layout", "rope_layout_to_heads", "rope_values", "rms_norm",
     "apply_rope", "strassen_products", "strassen_a_operands", "strassen_b_operands",
     "operand_planes", "packed_operand", "unpack_operand", "PACK_TILE", "PACK_STAGE",
+    "dual_a_operands", "dual_b_operands", "powers_a_operands", "powers_b_operands", "powers_decode",
+    "permuted_quadrants", "formula_operands", "DUAL_UPDATES", "POWERS_BASIS_UPDATES",
     "PRODUCT_UPDATES",
 ]
 
@@ -122,6 +124,108 @@ def strassen_b_operands(b_q):
     return (r(b0 + b3), b0, r(b1 - b3), r(b2 - b0), b3, r(b0 + b1), r(b2 + b3))
 
 
+# Dual formula (``strassen_pallas.py:461-517``): operands and quadrant updates.
+DUAL_UPDATES = {
+    1: ((0, +1), (3, +1)),
+    2: ((1, +1), (3, -1)),
+    3: ((2, +1), (3, +1)),
+    4: ((0, +1), (1, +1)),
+    5: ((0, -1), (2, +1)),
+    6: ((3, +1),),
+    7: ((0, +1),),
+}
+DUAL_INTERLEAVED_ORDER = (5, 6, 4, 3, 7, 2, 1)       # ``:539-547``
+
+# Power-of-two formula (``:381-459``): updates of the sparse output basis
+# z0..z3, decoded once after the last K panel (``:744-760``).
+POWERS_BASIS_UPDATES = {
+    1: ((3, +1),),
+    2: ((2, +1),),
+    3: ((0, +1), (3, -1)),
+    4: ((2, -1), (3, +1)),
+    5: ((0, +1),),
+    6: ((1, +1),),
+    7: ((1, +1), (3, +1)),
+}
+POWERS_INTERLEAVED_ORDER = (3, 2, 6, 5, 4, 7, 1)     # ``:520-528``
+
+
+def dual_a_operands(a_q):
+    """A operands of the dual formula Q1..Q7 (``:461-517``): A0+A3, A0,
+    A2-A3, A1-A0, A3, A0+A2, A1+A3."""
+    a0, a1, a2, a3 = a_q
+    r = bf16_round
+    return (r(a0 + a3), a0, r(a2 - a3), r(a1 - a0), a3, r(a0 + a2), r(a1 + a3))
+
+
+def dual_b_operands(b_q):
+    """B operands of Q1..Q7: B0+B3, B1+B3, B0, B3, B0+B2, B1-B0, B2-B3."""
+    b0, b1, b2, b3 = b_q
+    r = bf16_round
+    return (r(b0 + b3), r(b1 + b3), b0, b3, r(b0 + b2), r(b1 - b0), r(b2 - b3))
+
+
+def powers_a_operands(a_q):
+    """A operands of R1..R7 (``:398-459``). Every jnp bf16 operation rounds
+    its result to bf16 (the HLO semantics of the traced expressions);
+    scaling by 1/2 and 1/4 is exact, so each two-term sum rounds once and
+    each balanced four-term expression rounds its two halves and their sum."""
+    a0, a1, a2, a3 = a_q
+    r = bf16_round
+    h, q = np.float32(0.5), np.float32(0.25)
+    return (r(a2 - a1),
+            r(r(a0 - a2 * h) + r(a1 * h - a3 * q)),
+            r(a2 - a3 * h),
+            r(a1 - a3 * h),
+            r(a2 + a3 * h),
+            r(r(a0 - a1 * h) + r(a2 * h - a3 * q)),
+            r(a1 + a3 * h))
+
+
+def powers_b_operands(b_q):
+    """B operands of R1..R7 (``:398-459``), rounded as ``powers_a_operands``."""
+    b0, b1, b2, b3 = b_q
+    r = bf16_round
+    h, q = np.float32(0.5), np.float32(0.25)
+    return (r(b0 - b3),
+            r(b0 + b1 * h),
+            r(b1 * h - b3),
+            r(r(b0 * h - b2) + r(b1 * q - b3 * h)),
+            r(b1 * h + b3),
+            r(b0 - b1 * h),
+            r(r(b0 * h + b2) - r(b1 * q + b3 * h)))
+
+
+def powers_decode(z):
+    """Quadrants from the basis (``:744-760``): C3 = z0, C2 = z3 + z0/2,
+    C0 = (z1 + z2)/2 + z0/4, C1 = (z2 - z1) + z3 + z0/2."""
+    z0, z1, z2, z3 = z
+    h, q = np.float32(0.5), np.float32(0.25)
+    return [((z1 + z2) * h + z0 * q).astype(np.float32),
+            (((z2 - z1) + z3) + z0 * h).astype(np.float32),
+            (z3 + z0 * h).astype(np.float32),
+            z0.astype(np.float32)]
+
+
+def permuted_quadrants(quads, swap_rows, swap_cols):
+    """``transformed_index`` (``:209-226``): quadrant (row, col) reads the
+    original quadrant (row ^ swap_rows, col ^ swap_cols)."""
+    return tuple(quads[2 * (row ^ swap_rows) + (col ^ swap_cols)] for row in range(2) for col in range(2))
+
+
+def formula_operands(formula, a_q, b_q):
+    """(A operand, B operand) of products 1..7 of ``formula``."""
+    if formula == "classical":
+        return strassen_products(a_q, b_q)
+    if formula == "dual":
+        sa, tb = dual_a_operands(a_q), dual_b_operands(b_q)
+    elif formula == "powers":
+        sa, tb = powers_a_operands(a_q), powers_b_operands(b_q)
+    else:
+        raise ValueError(f"unknown formula {formula!r}")
+    return {p: (sa[p - 1], tb[p - 1]) for p in range(1, 8)}
+
+
 def strassen_products(a_q, b_q):
     """The seven classical operand pairs {p: (S_p, T_p)}."""
     sa = strassen_a_operands(a_q)
@@ -189,7 +293,7 @@ PACK_TILE = 128  # product rows per packed tile (the kernel's workgroup tile)
 PACK_STAGE = 16  # product depth per packed stage (one MFMA k step)
 
 
-def operand_planes(x, algo, side, tile_rows, bk):
+def operand_planes(x, algo, side, tile_rows, bk, formula="classical", block_permutation=0):
     """The GEMM operands of every tile as (nops, R, K/2) product-space planes.
 
     ``side="lhs"``: x is A [M, K], R = M/2 product rows (row tile, local row).
@@ -199,26 +303,29 @@ def operand_planes(x, algo, side, tile_rows, bk):
     ``strassen_b_operands``; the cubic (algo 8) the four quadrants.
     """
     x = np.asarray(x, dtype=np.float32)
+    sm, sk, sn = block_permutation & 1, (block_permutation >> 1) & 1, (block_permutation >> 2) & 1
+    a_ops = {"classical": strassen_a_operands, "dual": dual_a_operands, "powers": powers_a_operands}[formula]
+    b_ops = {"classical": strassen_b_operands, "dual": dual_b_operands, "powers": powers_b_operands}[formula]
     if side == "lhs":
         steps = x.shape[1] // bk
         quads = [np.concatenate(q, axis=1)
                  for q in zip(*(_split_a(x, tile_rows, bk, s) for s in range(steps)))]
-        ops = strassen_a_operands(quads) if algo == 7 else quads
+        ops = a_ops(permuted_quadrants(quads, sm, sk)) if algo == 7 else quads
     elif side == "rhs":
         steps = x.shape[0] // bk
         quads = [np.concatenate(q, axis=0).T
                  for q in zip(*(_split_b(x, tile_rows, bk, s) for s in range(steps)))]
-        ops = strassen_b_operands(quads) if algo == 7 else quads
+        ops = b_ops(permuted_quadrants(quads, sk, sn)) if algo == 7 else quads
     else:
         raise ValueError("side must be 'lhs' or 'rhs'")
     return np.stack(ops)
 
 
-def packed_operand(x, algo, side, tile_rows, bk):
+def packed_operand(x, algo, side, tile_rows, bk, formula="classical", block_permutation=0):
     """``smx_pack_operand``'s output as a flat float32 array of bf16 values:
     ``[R/128][K/32][nops][4][64][8]``, lane l of a fragment holding product
     row l%32 of its 32-row block and depth 8*(l//32)..+8 of its stage."""
-    planes = operand_planes(x, algo, side, tile_rows, bk)
+    planes = operand_planes(x, algo, side, tile_rows, bk, formula, block_permutation)
     nops, rows, depth = planes.shape
     v = planes.reshape(nops, rows // PACK_TILE, 4, 32, depth // PACK_STAGE, 2, 8)
     # (op, tile, block, row32, stage, half, e) -> (tile, stage, op, block, half, row32, e)
@@ -250,12 +357,19 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
                     epilogue=None, residual=None, bias=None, rope_cos=None,
                     rope_sin=None, rope_scale=None, rope_head_dim=128,
                     rope_eps=1e-6, product_aware_swiglu=False,
-                    product_aware_residual=False, output_dtype="bfloat16"):
+                    product_aware_residual=False, output_dtype="bfloat16",
+                    formula_variant="classical", block_permutation=0):
     """``a @ b`` with one tile-local classical Strassen level.
 
     Restates ``_classical_strassen_kernel`` (``strassen_pallas.py:156-879``)
-    for ``formula_variant="classical"``, ``block_permutation=0`` and no exact
-    panels, under the plumbing of ``strassen_matmul`` (``:882-1221``):
+    without exact panels, under the plumbing of ``strassen_matmul``
+    (``:882-1221``):
+
+    * ``formula_variant`` "classical" (``:324-379``), "dual" (``:461-517``)
+      or "powers" (``:381-459``, sparse output basis decoded after the last
+      panel, ``:744-760``; no fused epilogues);
+    * ``block_permutation`` bits swap the row / K / column halves of the
+      operand and output quadrants (``:205-226``);
 
     * grid ``(M/bm, N/bn, K/bk)``; per K panel the seven half-size products
       update four FP32 quadrant accumulators in the reference's order
@@ -279,7 +393,23 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
         raise ValueError("product_aware_swiglu is only valid with epilogue='swiglu' or 'geglu'")
     if product_aware_residual and epilogue != "residual_add":
         raise ValueError("product_aware_residual is only valid with epilogue='residual_add'")
-    order = INTERLEAVED_ORDER if interleave_products else PLAIN_ORDER
+    if formula_variant not in ("classical", "dual", "powers"):
+        raise ValueError(f"unknown formula_variant {formula_variant!r}")
+    if not 0 <= block_permutation < 8:
+        raise ValueError("block_permutation must be 0..7")
+    if (product_aware_swiglu or product_aware_residual) and (formula_variant != "classical" or block_permutation):
+        raise ValueError("product-aware schedules require unpermuted classical Strassen")
+    if formula_variant == "powers" and epilogue is not None:
+        raise ValueError("fused epilogues require a quadrant-basis formula")
+    swap_m, swap_k, swap_n = block_permutation & 1, (block_permutation >> 1) & 1, (block_permutation >> 2) & 1
+    output_index = [2 * ((q >> 1) ^ swap_m) + ((q & 1) ^ swap_n) for q in range(4)]
+    updates = {"classical": PRODUCT_UPDATES, "dual": DUAL_UPDATES, "powers": POWERS_BASIS_UPDATES}[formula_variant]
+    interleaved = {"classical": INTERLEAVED_ORDER, "dual": DUAL_INTERLEAVED_ORDER,
+                   "powers": POWERS_INTERLEAVED_ORDER}[formula_variant]
+    order = interleaved if interleave_products else PLAIN_ORDER
+    # classical / dual accumulate physical quadrants (``update``, :241-266);
+    # powers accumulates the unpermuted basis (``update_basis``, :268-273)
+    basis = formula_variant == "powers"
 
     acc = [np.zeros((m // 2, n // 2), dtype=np.float32) for _ in range(4)]
 
@@ -287,15 +417,17 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
         for p in sequence:
             s, t = products[p]
             value = np.matmul(s, t, dtype=np.float32)
-            for q, sign in PRODUCT_UPDATES[p]:
+            for q, sign in updates[p]:
+                idx = q if basis else output_index[q]
                 if sign > 0:
-                    acc[q] += value
+                    acc[idx] += value
                 else:
-                    acc[q] -= value
+                    acc[idx] -= value
 
     for step in range(nk):
-        products = strassen_products(_split_a(a, bm, bk, step),
-                                     _split_b(b, bn, bk, step))
+        a_q = permuted_quadrants(_split_a(a, bm, bk, step), swap_m, swap_k)
+        b_q = permuted_quadrants(_split_b(b, bn, bk, step), swap_k, swap_n)
+        products = formula_operands(formula_variant, a_q, b_q)
         last = step == nk - 1
         if last and product_aware_swiglu:
             run(products, PA_SWIGLU_TOP)
@@ -304,6 +436,11 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
             run(products, PA_RESIDUAL_FINAL)
         else:
             run(products, order)
+    if basis:
+        decoded = powers_decode(acc)
+        acc = [None] * 4
+        for q in range(4):
+            acc[output_index[q]] = decoded[q]
     return _epilogue(acc, m, n, bm, bn, epilogue=epilogue, residual=residual,
                      bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
                      rope_scale=rope_scale, rope_head_dim=rope_head_dim,

@@ -95,6 +95,107 @@ __device__ __forceinline__ void strassen_b_ops(const u32x4 (&q)[4], u32x4 (&ops)
   ops[6] = sum8<false>(b2, b3);
 }
 
+// bf16 round trip of a float (round to nearest even).
+__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+// Elementwise map of four unpacked quadrants to one packed bf16 operand; f
+// returns the float value that is rounded once to bf16.
+template <class F>
+__device__ __forceinline__ u32x4 map8(const F8& x0, const F8& x1, const F8& x2, const F8& x3, F f) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    r[i] = pack_bf16(f(x0.v[2 * i], x1.v[2 * i], x2.v[2 * i], x3.v[2 * i]),
+                     f(x0.v[2 * i + 1], x1.v[2 * i + 1], x2.v[2 * i + 1], x3.v[2 * i + 1]));
+  return r;
+}
+
+// Formula variants of strassen_pallas.py (formula_variant): 0 classical
+// (:324-379), 1 dual (:461-517), 2 powers (:381-459).
+constexpr int kFormulaClassical = 0, kFormulaDual = 1, kFormulaPowers = 2;
+
+// Operands of products 1..7 of a formula from the four (permuted) quadrants,
+// A side (kSide 0) or B side (kSide 1). Each jnp bf16 operation of the
+// reference rounds to bf16; scaling by 1/2 and 1/4 is exact, so two-term
+// sums round once and the powers formula's balanced four-term expressions
+// round both halves and their sum.
+template <int kSide>
+__device__ __forceinline__ void formula_ops(int formula, const u32x4 (&q)[4], u32x4 (&ops)[7]) {
+  if (formula == kFormulaClassical) {
+    if constexpr (kSide == 0)
+      strassen_a_ops(q, ops);
+    else
+      strassen_b_ops(q, ops);
+    return;
+  }
+  const F8 x0 = unpack8(q[0]), x1 = unpack8(q[1]), x2 = unpack8(q[2]), x3 = unpack8(q[3]);
+  if (formula == kFormulaDual) {
+    if constexpr (kSide == 0) {  // A0+A3, A0, A2-A3, A1-A0, A3, A0+A2, A1+A3
+      ops[0] = sum8<false>(x0, x3);
+      ops[1] = q[0];
+      ops[2] = sum8<true>(x2, x3);
+      ops[3] = sum8<true>(x1, x0);
+      ops[4] = q[3];
+      ops[5] = sum8<false>(x0, x2);
+      ops[6] = sum8<false>(x1, x3);
+    } else {  // B0+B3, B1+B3, B0, B3, B0+B2, B1-B0, B2-B3
+      ops[0] = sum8<false>(x0, x3);
+      ops[1] = sum8<false>(x1, x3);
+      ops[2] = q[0];
+      ops[3] = q[3];
+      ops[4] = sum8<false>(x0, x2);
+      ops[5] = sum8<true>(x1, x0);
+      ops[6] = sum8<true>(x2, x3);
+    }
+    return;
+  }
+  // Powers (Dumas--Pernet--Sedoglavic).
+  if constexpr (kSide == 0) {
+    ops[0] = map8(x0, x1, x2, x3, [](float a0, float a1, float a2, float a3) { return a2 - a1; });
+    ops[1] = map8(x0, x1, x2, x3, [](float a0, float a1, float a2, float a3) {
+      return round_bf16(a0 - a2 * 0.5f) + round_bf16(a1 * 0.5f - a3 * 0.25f);
+    });
+    ops[2] = map8(x0, x1, x2, x3, [](float a0, float a1, float a2, float a3) { return a2 - a3 * 0.5f; });
+    ops[3] = map8(x0, x1, x2, x3, [](float a0, float a1, float a2, float a3) { return a1 - a3 * 0.5f; });
+    ops[4] = map8(x0, x1, x2, x3, [](float a0, float a1, float a2, float a3) { return a2 + a3 * 0.5f; });
+    ops[5] = map8(x0, x1, x2, x3, [](float a0, float a1, float a2, float a3) {
+      return round_bf16(a0 - a1 * 0.5f) + round_bf16(a2 * 0.5f - a3 * 0.25f);
+    });
+    ops[6] = map8(x0, x1, x2, x3, [](float a0, float a1, float a2, float a3) { return a1 + a3 * 0.5f; });
+  } else {
+    ops[0] = map8(x0, x1, x2, x3, [](float b0, float b1, float b2, float b3) { return b0 - b3; });
+    ops[1] = map8(x0, x1, x2, x3, [](float b0, float b1, float b2, float b3) { return b0 + b1 * 0.5f; });
+    ops[2] = map8(x0, x1, x2, x3, [](float b0, float b1, float b2, float b3) { return b1 * 0.5f - b3; });
+    ops[3] = map8(x0, x1, x2, x3, [](float b0, float b1, float b2, float b3) {
+      return round_bf16(b0 * 0.5f - b2) + round_bf16(b1 * 0.25f - b3 * 0.5f);
+    });
+    ops[4] = map8(x0, x1, x2, x3, [](float b0, float b1, float b2, float b3) { return b1 * 0.5f + b3; });
+    ops[5] = map8(x0, x1, x2, x3, [](float b0, float b1, float b2, float b3) { return b0 - b1 * 0.5f; });
+    ops[6] = map8(x0, x1, x2, x3, [](float b0, float b1, float b2, float b3) {
+      return round_bf16(b0 * 0.5f + b2) - round_bf16(b1 * 0.25f + b3 * 0.5f);
+    });
+  }
+}
+
+// Block permutation (strassen_pallas.py:205-226): quadrant (row, col) takes
+// the original quadrant (row ^ swap_rows, col ^ swap_cols).
+__device__ __forceinline__ void permute_quadrants(u32x4 (&q)[4], int swap_rows, int swap_cols) {
+  if (swap_rows) {
+    const u32x4 t0 = q[0], t1 = q[1];
+    q[0] = q[2];
+    q[1] = q[3];
+    q[2] = t0;
+    q[3] = t1;
+  }
+  if (swap_cols) {
+    const u32x4 t0 = q[0], t2 = q[2];
+    q[0] = q[1];
+    q[2] = q[3];
+    q[1] = t0;
+    q[3] = t2;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Parameters and tile mapping
 // ---------------------------------------------------------------------------
@@ -117,6 +218,8 @@ struct Params {
   int32_t tiles_m, tiles_n;  // product-space workgroup grid
   int32_t group_m;           // tile rows per rasterization group
   int32_t out_f32;           // store float32 instead of bf16
+  int32_t formula;           // kFormula* (Strassen family)
+  int32_t perm;              // block permutation bits: 1 rows, 2 K, 4 columns
 };
 
 // Workgroup id -> product-space tile. Workgroups are dispatched round-robin
@@ -248,10 +351,42 @@ __device__ __forceinline__ void epilogue(const Params& p, const TileOrigin& o, i
           const float p1 = acc[0][i][j][r], p2 = acc[1][i][j][r], p3 = acc[2][i][j][r];
           const float p4 = acc[3][i][j][r], p5 = acc[4][i][j][r], p6 = acc[5][i][j][r];
           const float p7 = acc[6][i][j][r];
-          q0 = ((p4 - p5) + p7) + p1;
-          q1 = p5 + p3;
-          q2 = p4 + p2;
-          q3 = ((p6 - p2) + p3) + p1;
+          if (p.formula == kFormulaClassical) {
+            // C0 = P1+P4-P5+P7, C1 = P3+P5, C2 = P2+P4, C3 = P1-P2+P3+P6
+            q0 = ((p4 - p5) + p7) + p1;
+            q1 = p5 + p3;
+            q2 = p4 + p2;
+            q3 = ((p6 - p2) + p3) + p1;
+          } else if (p.formula == kFormulaDual) {
+            // C0 = Q1+Q4-Q5+Q7, C1 = Q2+Q4, C2 = Q3+Q5, C3 = Q1-Q2+Q3+Q6
+            q0 = ((p4 - p5) + p7) + p1;
+            q1 = p4 + p2;
+            q2 = p5 + p3;
+            q3 = ((p6 + p3) - p2) + p1;
+          } else {
+            // Basis z0 = R3+R5, z1 = R6+R7, z2 = R2-R4, z3 = R1-R3+R4+R7,
+            // decoded as in strassen_pallas.py:744-760.
+            const float z0 = p3 + p5, z1 = p6 + p7, z2 = p2 - p4, z3 = ((p4 - p3) + p7) + p1;
+            q3 = z0;
+            q2 = z3 + z0 * 0.5f;
+            q0 = (z1 + z2) * 0.5f + z0 * 0.25f;
+            q1 = ((z2 - z1) + z3) + z0 * 0.5f;
+          }
+          // Logical quadrant (row, col) lands on physical (row ^ swap_m, col ^ swap_n).
+          if (p.perm & 1) {
+            const float t0 = q0, t1 = q1;
+            q0 = q2;
+            q1 = q3;
+            q2 = t0;
+            q3 = t1;
+          }
+          if (p.perm & 4) {
+            const float t0 = q0, t2 = q2;
+            q0 = q1;
+            q2 = q3;
+            q1 = t0;
+            q3 = t2;
+          }
         } else {
           q0 = acc[0][i][j][r];
           q1 = acc[1][i][j][r];

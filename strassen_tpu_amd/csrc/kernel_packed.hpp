@@ -318,8 +318,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
 // a wave are whole 1 KB fragments.
 template <int kAlgo, int kSide>
 __global__ __launch_bounds__(256) void pack_operand(const uint16_t* __restrict__ src, int64_t ld, int64_t rows,
-                                                    int64_t k, int32_t tile_rows, int32_t bk,
-                                                    uint8_t* __restrict__ out) {
+                                                    int64_t k, int32_t tile_rows, int32_t bk, int32_t formula,
+                                                    int32_t perm, uint8_t* __restrict__ out) {
   constexpr int nops = nops_of(kAlgo);
   const int lane = threadIdx.x & 63;
   const int64_t gwave = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
@@ -372,10 +372,13 @@ __global__ __launch_bounds__(256) void pack_operand(const uint16_t* __restrict__
     uint8_t* const dst = dst_tile + st * (int64_t)(nops * kBlocks * kFrag);
     if constexpr (kAlgo == 7) {
       u32x4 ops[7];
-      if constexpr (kSide != 1)
-        strassen_a_ops(q, ops);
-      else
-        strassen_b_ops(q, ops);
+      if constexpr (kSide != 1) {
+        permute_quadrants(q, perm & 1, (perm >> 1) & 1);  // A: (rows, K halves)
+        formula_ops<0>(formula, q, ops);
+      } else {
+        permute_quadrants(q, (perm >> 1) & 1, (perm >> 2) & 1);  // B: (K halves, columns)
+        formula_ops<1>(formula, q, ops);
+      }
 #pragma unroll
       for (int op = 0; op < 7; ++op) *reinterpret_cast<u32x4*>(dst + op * kBlocks * kFrag) = ops[op];
     } else {

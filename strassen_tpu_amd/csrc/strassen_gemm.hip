@@ -141,15 +141,25 @@ void tile_of_path(bool packed_path, int32_t* tm, int32_t* tn, int32_t* tk) {
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
+// Formula / block-permutation arguments shared by smx_gemm and smx_pack_operand.
+int check_variant(int32_t algo, int32_t formula, int32_t perm) {
+  if (formula < SMX_FORMULA_CLASSICAL || formula > SMX_FORMULA_POWERS)
+    return fail(SMX_ERR_INVALID, "formula must be classical (0), dual (1) or powers (2), got %d", formula);
+  if (perm < 0 || perm > 7) return fail(SMX_ERR_INVALID, "block_permutation must be 0..7, got %d", perm);
+  if (algo == SMX_ALGO_CUBIC && (formula || perm))
+    return fail(SMX_ERR_INVALID, "the cubic control has no formula variant or block permutation");
+  return SMX_OK;
+}
+
 template <int kAlgo, int kSide>
-int launch_pack(const uint16_t* src, int64_t ld, int64_t rows, int64_t k, int32_t tile_rows, int32_t bk, uint8_t* out,
-                hipStream_t stream) {
+int launch_pack(const uint16_t* src, int64_t ld, int64_t rows, int64_t k, int32_t tile_rows, int32_t bk,
+                int32_t formula, int32_t perm, uint8_t* out, hipStream_t stream) {
   const int64_t nstages = k / (2 * packed::TK);
   const int64_t waves = (rows / 64) * ((nstages + packed::kPackStages - 1) / packed::kPackStages);
   const int64_t blocks = (waves + 3) / 4;
   if (blocks >= ((int64_t)1 << 31)) return fail(SMX_ERR_UNSUPPORTED, "operand too large to pack");
   hipLaunchKernelGGL((packed::pack_operand<kAlgo, kSide>), dim3((unsigned)blocks), dim3(256), 0, stream, src, ld, rows,
-                     k, tile_rows, bk, out);
+                     k, tile_rows, bk, formula, perm, out);
   return check_launch();
 }
 
@@ -188,10 +198,11 @@ int smx_packed_bytes(int32_t algo, int64_t rows, int64_t k, int64_t* bytes) {
   return SMX_OK;
 }
 
-int smx_pack_operand(int32_t algo, int32_t side, int64_t rows, int64_t k, const void* src, int64_t ld,
-                     int32_t tile_rows, int32_t bk, void* out, void* stream) {
+int smx_pack_operand(int32_t algo, int32_t formula, int32_t block_permutation, int32_t side, int64_t rows, int64_t k,
+                     const void* src, int64_t ld, int32_t tile_rows, int32_t bk, void* out, void* stream) {
   g_error[0] = 0;
   if (algo != SMX_ALGO_STRASSEN && algo != SMX_ALGO_CUBIC) return fail(SMX_ERR_INVALID, "algo must be 7 or 8");
+  if (int rc = check_variant(algo, formula, block_permutation)) return rc;
   if (side != SMX_SIDE_LHS && side != SMX_SIDE_RHS && side != SMX_SIDE_LHS_T)
     return fail(SMX_ERR_INVALID, "side must be LHS (0), RHS (1) or LHS_T (2)");
   if (rows <= 0 || k <= 0 || tile_rows <= 0 || bk <= 0 || rows % tile_rows || k % bk)
@@ -208,13 +219,13 @@ int smx_pack_operand(int32_t algo, int32_t side, int64_t rows, int64_t k, const 
   uint8_t* o8 = (uint8_t*)out;
   hipStream_t st = (hipStream_t)stream;
   if (algo == SMX_ALGO_STRASSEN) {
-    if (side == SMX_SIDE_LHS) return launch_pack<7, 0>(s16, ld, rows, k, tile_rows, bk, o8, st);
-    if (side == SMX_SIDE_RHS) return launch_pack<7, 1>(s16, ld, rows, k, tile_rows, bk, o8, st);
-    return launch_pack<7, 2>(s16, ld, rows, k, tile_rows, bk, o8, st);
+    if (side == SMX_SIDE_LHS) return launch_pack<7, 0>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, o8, st);
+    if (side == SMX_SIDE_RHS) return launch_pack<7, 1>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, o8, st);
+    return launch_pack<7, 2>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, o8, st);
   }
-  if (side == SMX_SIDE_LHS) return launch_pack<8, 0>(s16, ld, rows, k, tile_rows, bk, o8, st);
-  if (side == SMX_SIDE_RHS) return launch_pack<8, 1>(s16, ld, rows, k, tile_rows, bk, o8, st);
-  return launch_pack<8, 2>(s16, ld, rows, k, tile_rows, bk, o8, st);
+  if (side == SMX_SIDE_LHS) return launch_pack<8, 0>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, o8, st);
+  if (side == SMX_SIDE_RHS) return launch_pack<8, 1>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, o8, st);
+  return launch_pack<8, 2>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, o8, st);
 }
 
 int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, const void* residual, const void* bias,
@@ -232,6 +243,11 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
   if (packed_path != (d->a_layout == SMX_A_PACKED))
     return fail(SMX_ERR_UNSUPPORTED, "A and B must both be packed (smx_pack_operand) or both unpacked");
   if (d->flags & ~SMX_FLAG_OUT_F32) return fail(SMX_ERR_INVALID, "unknown flags 0x%x", d->flags);
+  if (int rc = check_variant(d->algo, d->formula, d->block_permutation)) return rc;
+  if ((d->formula || d->block_permutation) && !packed_path)
+    return fail(SMX_ERR_UNSUPPORTED, "formula variants and block permutations run on packed operands");
+  if (d->formula == SMX_FORMULA_POWERS && d->epilogue != SMX_EPI_NONE)
+    return fail(SMX_ERR_INVALID, "fused epilogues require a quadrant-basis formula");
   if (d->m <= 0 || d->n <= 0 || d->k <= 0)
     return fail(SMX_ERR_INVALID, "empty problem m=%lld n=%lld k=%lld", (long long)d->m, (long long)d->n,
                 (long long)d->k);
@@ -260,6 +276,8 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
   p.b = (const uint16_t*)b;
   p.c = c;
   p.out_f32 = (d->flags & SMX_FLAG_OUT_F32) ? 1 : 0;
+  p.formula = d->formula;
+  p.perm = d->block_permutation;
   p.m = d->m;
   p.n = d->n;
   p.k = d->k;

@@ -40,10 +40,11 @@ class PackedOperand:
     the same tile.
     """
 
-    def __init__(self, data, *, algo, side, rows, k, tile_rows, bk):
+    def __init__(self, data, *, algo, side, rows, k, tile_rows, bk, formula="classical", block_permutation=0):
         self.data = data
         self.algo, self.side = int(algo), side
         self.rows, self.k, self.tile_rows, self.bk = int(rows), int(k), int(tile_rows), int(bk)
+        self.formula, self.block_permutation = formula, int(block_permutation)
 
     # The parts of the tensor interface the callers' argument checks use.
     @property
@@ -62,8 +63,10 @@ class PackedOperand:
         return 2
 
     def __repr__(self):
+        variant = "" if self.algo != _lib.SMX_ALGO_STRASSEN else \
+            f", formula={self.formula}, block_permutation={self.block_permutation}"
         return (f"PackedOperand({_ALGOS[self.algo]}, {self.side}, shape={tuple(self.shape)}, "
-                f"tile_rows={self.tile_rows}, bk={self.bk}, device={self.device})")
+                f"tile_rows={self.tile_rows}, bk={self.bk}{variant}, device={self.device})")
 
 
 def packed_bytes(algo, rows, k):
@@ -72,12 +75,16 @@ def packed_bytes(algo, rows, k):
     return out.value
 
 
-def pack_operand(x, *, algo, side, tile_rows, bk):
+def pack_operand(x, *, algo, side, tile_rows, bk, formula="classical", block_permutation=0):
     """Pack ``x`` (bf16 on the HIP device): ``a [M, K]`` for ``side="lhs"``,
     the same ``a`` stored transposed as ``[K, M]`` for ``side="lhs_t"``, or a
     weight ``b [K, N]`` for ``side="rhs"`` (any strides; a K-contiguous view
     of ``[N, K]`` storage is read in place). Runs asynchronously on torch's
-    current stream."""
+    current stream. Strassen operands carry the operand sums of
+    ``formula`` ("classical", "dual" or "powers") after the quadrant swaps of
+    ``block_permutation``; both operands of a GEMM must be packed alike."""
+    if formula not in _lib.SMX_FORMULA:
+        raise ValueError("formula_variant must be 'classical', 'dual', or 'powers'")
     if side not in ("lhs", "rhs", "lhs_t"):
         raise ValueError("side must be 'lhs', 'lhs_t' or 'rhs'")
     if algo not in _ALGOS:
@@ -104,17 +111,19 @@ def pack_operand(x, *, algo, side, tile_rows, bk):
     data = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=x.device)
     side_id = {"lhs": _lib.SMX_SIDE_LHS, "rhs": _lib.SMX_SIDE_RHS, "lhs_t": _lib.SMX_SIDE_LHS_T}[side]
     stream = torch.cuda.current_stream(x.device).cuda_stream
-    rc = _lib.load().smx_pack_operand(algo, side_id, rows, k, _lib.ptr(src), src.stride(0), tile_rows, bk,
-                                      _lib.ptr(data), stream)
+    rc = _lib.load().smx_pack_operand(algo, _lib.SMX_FORMULA[formula], block_permutation, side_id, rows, k,
+                                      _lib.ptr(src), src.stride(0), tile_rows, bk, _lib.ptr(data), stream)
     _lib.check(rc)
     return PackedOperand(data, algo=algo, side="rhs" if side == "rhs" else "lhs", rows=rows, k=k,
-                         tile_rows=tile_rows, bk=bk)
+                         tile_rows=tile_rows, bk=bk, formula=formula, block_permutation=block_permutation)
 
 
-def strassen_weight_layout(b, bn, bk):
+def strassen_weight_layout(b, bn, bk, *, formula_variant="classical", block_permutation=0):
     """Pre-sum and pack a bf16 ``[K, N]`` weight for ``strassen_matmul``
-    with the tile ``(bn, bk)``."""
-    return pack_operand(b, algo=_lib.SMX_ALGO_STRASSEN, side="rhs", tile_rows=bn, bk=bk)
+    with the tile ``(bn, bk)`` (and the formula / block permutation the
+    calls will use)."""
+    return pack_operand(b, algo=_lib.SMX_ALGO_STRASSEN, side="rhs", tile_rows=bn, bk=bk,
+                        formula=formula_variant, block_permutation=block_permutation)
 
 
 def cubic_weight_layout(b, bn, bk):
@@ -123,7 +132,8 @@ def cubic_weight_layout(b, bn, bk):
     return pack_operand(b, algo=_lib.SMX_ALGO_CUBIC, side="rhs", tile_rows=bn, bk=bk)
 
 
-def pack_activation(a, algo, bm, bk):
+def pack_activation(a, algo, bm, bk, *, formula_variant="classical", block_permutation=0):
     """Pack an activation ``a [M, K]`` once for several GEMMs that share it
     (e.g. the q, k and v projections)."""
-    return pack_operand(a, algo=algo, side="lhs", tile_rows=bm, bk=bk)
+    return pack_operand(a, algo=algo, side="lhs", tile_rows=bm, bk=bk, formula=formula_variant,
+                        block_permutation=block_permutation)

@@ -9,10 +9,11 @@ torch's current stream.
 
 Differences a caller can observe, all raised as exceptions (never silent):
 
-* Research formula knobs that the tuned dispatcher never selects
-  (``formula_variant != "classical"``, ``block_permutation``,
-  ``classical_panels``, ``panel_schedule``), the ``norm_residual_add``
-  epilogue and FP32 inputs raise ``NotImplementedError``.
+* The exact-panel policies (``classical_panels``, ``panel_schedule``), the
+  ``norm_residual_add`` epilogue and FP32 inputs raise ``NotImplementedError``.
+* ``formula_variant`` "dual" / "powers" and ``block_permutation`` run on
+  packed operands: a plain weight is packed for the call (pack it once with
+  ``strassen_weight_layout(..., formula_variant=, block_permutation=)``).
 * TPU-only knobs (``dot_precision``, ``allow_input_fusion`` after its
   validation, ``vmem_limit_bytes``) are accepted and have no effect;
   ``interpret=True`` raises ``NotImplementedError`` (there is no CPU path).
@@ -197,14 +198,9 @@ def _validate(a, b, *, bm, bn, bk, block_permutation, formula_variant,
     return m, k, n, classical_panels, out
 
 
-def _unsupported(formula_variant, block_permutation, classical_panels, panel_schedule,
-                 epilogue, dtype, interpret):
+def _unsupported(classical_panels, panel_schedule, epilogue, dtype, interpret):
     if interpret:
         raise NotImplementedError("interpret=True: the gfx950 kernel has no CPU interpreter path")
-    if formula_variant != "classical":
-        raise NotImplementedError(f"formula_variant={formula_variant!r} is not implemented on gfx950")
-    if block_permutation:
-        raise NotImplementedError("block_permutation is not implemented on gfx950")
     if classical_panels or panel_schedule is not None:
         raise NotImplementedError("exact-panel policies are not implemented on gfx950")
     if epilogue == "norm_residual_add":
@@ -220,36 +216,46 @@ def _require_device(*tensors):
                              f"(got a tensor on {t.device})")
 
 
-def _check_packed(x, algo, side, tile_rows, bk):
+def _check_packed(x, algo, side, tile_rows, bk, formula="classical", block_permutation=0):
     name = "a" if side == "lhs" else "b"
     if x.algo != algo or x.side != side:
         raise ValueError(f"{name} was packed as {x!r}, not as the {side} of this algorithm")
     if (x.tile_rows, x.bk) != (tile_rows, bk):
         raise ValueError(f"{name} was packed for the tile ({x.tile_rows}, bk={x.bk}), "
                          f"called with ({tile_rows}, bk={bk})")
+    if (x.formula, x.block_permutation) != (formula, block_permutation):
+        raise ValueError(f"{name} was packed for formula_variant={x.formula!r}, "
+                         f"block_permutation={x.block_permutation}; called with "
+                         f"formula_variant={formula!r}, block_permutation={block_permutation}")
 
 
 def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
          rope_cos=None, rope_sin=None, rope_scale=None, rope_head_dim=128,
-         rope_eps=1e-6, out_dtype=torch.bfloat16):
+         rope_eps=1e-6, out_dtype=torch.bfloat16, formula="classical", block_permutation=0):
     lib = _lib.load()
     m, k = a.shape
     n = b.shape[1]
-    packed = isinstance(b, PackedOperand)
+    variant = dict(formula=formula, block_permutation=block_permutation)
+    # Formula variants and block permutations run on packed operands; a
+    # plain weight is packed for the call.
+    packed = isinstance(b, PackedOperand) or formula != "classical" or block_permutation != 0
     if isinstance(a, PackedOperand) and not packed:
         raise ValueError("a packed activation needs a packed weight (strassen_weight_layout / "
                          "cubic_weight_layout)")
     b_layout = _lib.SMX_B_PACKED if packed else _lib.SMX_B_KCONTIG
-    if packed:
-        _check_packed(b, algo, "rhs", bn, bk)
-        if isinstance(a, PackedOperand):
-            _check_packed(a, algo, "lhs", bm, bk)
+    if isinstance(b, PackedOperand):
+        _check_packed(b, algo, "rhs", bn, bk, **variant)
+    if isinstance(a, PackedOperand):
+        _check_packed(a, algo, "lhs", bm, bk, **variant)
     _check_device_tiling(algo, epilogue, bm, bn, bk, b_layout)
-    _require_device(a.data if isinstance(a, PackedOperand) else a, b.data if packed else b,
+    _require_device(a.data if isinstance(a, PackedOperand) else a,
+                    b.data if isinstance(b, PackedOperand) else b,
                     residual, bias, rope_cos, rope_sin, rope_scale)
     if packed:
+        if not isinstance(b, PackedOperand):
+            b = pack_operand(b, algo=algo, side="rhs", tile_rows=bn, bk=bk, **variant)
         if not isinstance(a, PackedOperand):
-            a = pack_operand(a, algo=algo, side="lhs", tile_rows=bm, bk=bk)
+            a = pack_operand(a, algo=algo, side="lhs", tile_rows=bm, bk=bk, **variant)
         a_ptr, b_ptr, lda, ldb = a.data, b.data, k, k
     else:
         if a.stride(1) != 1 or a.stride(0) % 8 or a.data_ptr() % 16:
@@ -269,6 +275,8 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
     desc.a_layout = _lib.SMX_A_PACKED if packed else _lib.SMX_A_ROWMAJOR
     desc.b_layout = b_layout
     desc.flags = _lib.SMX_FLAG_OUT_F32 if out_dtype == torch.float32 else 0
+    desc.formula = _lib.SMX_FORMULA[formula]
+    desc.block_permutation = block_permutation
     desc.rope_head_dim = rope_head_dim
     desc.rope_eps = rope_eps
     aux = 0
@@ -357,12 +365,11 @@ def strassen_matmul(
         output_dtype=output_dtype, allow_input_fusion=allow_input_fusion,
         product_aware_swiglu=product_aware_swiglu,
         product_aware_residual=product_aware_residual)
-    _unsupported(formula_variant, block_permutation, classical_panels, panel_schedule,
-                 epilogue, a.dtype, interpret)
+    _unsupported(classical_panels, panel_schedule, epilogue, a.dtype, interpret)
     return _run(_lib.SMX_ALGO_STRASSEN, a, b, bm=bm, bn=bn, bk=bk, epilogue=epilogue,
                 residual=residual, bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
                 rope_scale=rope_scale, rope_head_dim=rope_head_dim, rope_eps=rope_eps,
-                out_dtype=out_dtype)
+                out_dtype=out_dtype, formula=formula_variant, block_permutation=block_permutation)
 
 
 def strassen_matmul_lhs_transposed(a, b, *, bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_BK, dot_precision=None,

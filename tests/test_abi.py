@@ -38,10 +38,13 @@ def test_version_and_macros_match_header():
     assert _lib.load().smx_version() == version
     for name in ("SMX_OK", "SMX_ERR_INVALID", "SMX_ERR_UNSUPPORTED", "SMX_ERR_LAUNCH",
                  "SMX_ALGO_STRASSEN", "SMX_ALGO_CUBIC", "SMX_A_ROWMAJOR", "SMX_A_PACKED",
-                 "SMX_B_KCONTIG", "SMX_B_PACKED", "SMX_SIDE_LHS", "SMX_SIDE_RHS",
+                 "SMX_B_KCONTIG", "SMX_B_PACKED", "SMX_SIDE_LHS", "SMX_SIDE_RHS", "SMX_SIDE_LHS_T",
+                 "SMX_FLAG_OUT_F32",
                  "SMX_AUX_BIAS_F32", "SMX_AUX_SCALE_F32"):
         value = int(re.search(rf"#define {name} (\d+)", header).group(1))
         assert getattr(_lib, name) == value, name
+    for name, code in _lib.SMX_FORMULA.items():
+        assert int(re.search(rf"#define SMX_FORMULA_{name.upper()} (\d+)", header).group(1)) == code
     for epi, code in _lib.SMX_EPI.items():
         if epi is not None:
             macro = "SMX_EPI_" + epi.upper()
@@ -93,6 +96,10 @@ def _desc(**kw):
     ("lda", 100, _lib.SMX_ERR_INVALID),
     ("epilogue", 9, _lib.SMX_ERR_INVALID),
     ("flags", 4, _lib.SMX_ERR_INVALID),
+    ("formula", 3, _lib.SMX_ERR_INVALID),
+    ("block_permutation", 8, _lib.SMX_ERR_INVALID),
+    ("formula", 1, _lib.SMX_ERR_UNSUPPORTED),            # variants need packed operands
+    ("block_permutation", 2, _lib.SMX_ERR_UNSUPPORTED),
 ])
 def test_invalid_descriptors_are_rejected_before_any_launch(field, value, code):
     lib = _lib.load()
@@ -156,8 +163,26 @@ def test_pack_operand_rejects_bad_arguments(args, code):
     lib = _lib.load()
     buf = (ctypes.c_uint8 * 16)()
     p = ctypes.cast(buf, ctypes.c_void_p)
-    assert lib.smx_pack_operand(algo, side, rows, k, p, ld, tile_rows, bk, p, None) == code
+    assert lib.smx_pack_operand(algo, 0, 0, side, rows, k, p, ld, tile_rows, bk, p, None) == code
     assert _lib.last_error()
+
+
+@pytest.mark.parametrize("algo,formula,perm", [(7, 3, 0), (7, -1, 0), (7, 0, 8), (8, 1, 0), (8, 0, 2)])
+def test_pack_operand_rejects_bad_variants(algo, formula, perm):
+    lib = _lib.load()
+    buf = (ctypes.c_uint8 * 16)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    assert lib.smx_pack_operand(algo, formula, perm, 0, 512, 512, p, 512, 256, 512, p, None) == _lib.SMX_ERR_INVALID
+
+
+def test_powers_refuses_fused_epilogues():
+    lib = _lib.load()
+    buf = (ctypes.c_uint8 * 16)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    d = _desc(a_layout=_lib.SMX_A_PACKED, b_layout=_lib.SMX_B_PACKED, formula=2,
+              epilogue=_lib.SMX_EPI["residual_add"])
+    assert lib.smx_gemm(d, p, p, p, p, None, None, None, None, None) == _lib.SMX_ERR_INVALID
+    assert "quadrant-basis" in _lib.last_error()
 
 
 def test_inline_asm_kernel_check():

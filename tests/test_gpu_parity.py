@@ -349,6 +349,56 @@ def test_lhs_transposed(out_dtype):
     assert np.array_equal(got, o.bf16_round(ai.T @ bi))
 
 
+VARIANTS = [("classical", 5), ("dual", 0), ("dual", 3), ("powers", 0), ("powers", 6)]
+
+
+@pytest.mark.parametrize("formula,perm", VARIANTS)
+def test_formula_variant_pack_matches_oracle(formula, perm):
+    rng = np.random.default_rng(410)
+    a = o.bf16_round(rng.standard_normal((512, 1024)).astype(np.float32))
+    b = o.bf16_round(rng.standard_normal((1024, 512)).astype(np.float32))
+    pa = smx.pack_operand(dev(a), algo=7, side="lhs", tile_rows=256, bk=512, formula=formula, block_permutation=perm)
+    assert np.array_equal(host(pa.data), o.packed_operand(a, 7, "lhs", 256, 512, formula, perm))
+    pb = smx.pack_operand(dev_weight(b), algo=7, side="rhs", tile_rows=256, bk=512, formula=formula,
+                          block_permutation=perm)
+    assert np.array_equal(host(pb.data), o.packed_operand(b, 7, "rhs", 256, 512, formula, perm))
+
+
+@pytest.mark.parametrize("formula", ["classical", "dual", "powers"])
+def test_formula_variant_integer_kat(formula):
+    rng = np.random.default_rng(411)
+    a = rng.integers(-2, 3, (512, 1024)).astype(np.float32)
+    b = rng.integers(-2, 3, (1024, 512)).astype(np.float32)
+    for perm in range(8):
+        say(f"  {formula} perm={perm}")
+        got = host(smx.strassen_matmul(dev(a), dev_weight(b), bm=256, bn=256, bk=512, formula_variant=formula,
+                                       block_permutation=perm))
+        assert np.array_equal(got, o.bf16_round(a @ b)), perm
+
+
+@pytest.mark.parametrize("formula,perm", VARIANTS)
+def test_formula_variant_random_matches_oracle(formula, perm):
+    _, a, b = _gaussian(412, 512, 2048, 512)
+    kw = dict(bm=256, bn=256, bk=512, formula_variant=formula, block_permutation=perm)
+    w = smx.strassen_weight_layout(dev_weight(b), 256, 512, formula_variant=formula, block_permutation=perm)
+    got = host(smx.strassen_matmul(dev(a), w, **kw))
+    want = o.strassen_matmul(a, b, **kw)
+    assert_ulp_close(got, want, k=2048)
+    ref = o.high_precision_reference(a, b).astype(np.float64)
+    assert rel_l2(got, ref) <= 1e-2 and rel_l2(got, ref) <= 1.5 * rel_l2(want, ref)
+
+
+def test_dual_permuted_with_fused_epilogues():
+    rng, a, b = _gaussian(413, 512, 1024, 2048)
+    laid = o.swiglu_weight_layout(b, 512)
+    kw = dict(bm=256, bn=512, bk=512, formula_variant="dual", block_permutation=6)
+    got = host(smx.strassen_matmul(dev(a), dev_weight(laid), epilogue="swiglu", **kw))
+    assert_ulp_close(got, o.strassen_matmul(a, laid, epilogue="swiglu", **kw), k=1024)
+    r = o.bf16_round(rng.standard_normal((512, 2048)).astype(np.float32))
+    got = host(smx.strassen_matmul(dev(a), dev_weight(b), epilogue="residual_add", residual=dev(r), **kw))
+    assert_ulp_close(got, o.strassen_matmul(a, b, epilogue="residual_add", residual=r, **kw), k=1024)
+
+
 def test_residual_add_epilogue():
     rng, a, b = _gaussian(319, 512, 2048, 1024)
     r = o.bf16_round(rng.standard_normal((512, 1024)).astype(np.float32))

@@ -354,3 +354,73 @@ def test_rope_tables_and_scale_layout():
     gamma = np.arange(16, dtype=np.float32)
     s = o.rope_scale_layout(gamma, 64, 16)
     assert np.array_equal(s, np.concatenate([np.tile(gamma[:8], 4), np.tile(gamma[8:], 4)]))
+
+
+# ---------------------------------------------------------------------------
+# Formula variants and block permutation (strassen_pallas.py:205-226, 381-517)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("formula", ["classical", "dual", "powers"])
+def test_formula_variants_integer_known_answer(formula):
+    """Small-integer operands keep every variant's operand expressions
+    (multiples of 1/4) exact in bf16, so each formula, under every block
+    permutation and both product orders, must equal A @ B bit-exactly; a
+    wrong sign, operand or basis decode fails this."""
+    rng, a, b = _int_problem(400, 64, 512, 256, lo=-2, hi=3)
+    for perm in range(8):
+        for interleave in (False, True):
+            got = o.strassen_matmul(a, b, bm=32, bn=128, bk=256, formula_variant=formula,
+                                    block_permutation=perm, interleave_products=interleave,
+                                    output_dtype="float32")
+            assert np.array_equal(got, a @ b), (formula, perm, interleave)
+
+
+def _swap_tile_halves(x, tile_r, tile_c, swap_r, swap_c):
+    """Physically swap the row halves / column halves of every tile."""
+    r, c = x.shape
+    v = x.reshape(r // tile_r, 2, tile_r // 2, c // tile_c, 2, tile_c // 2)
+    if swap_r:
+        v = v[:, ::-1]
+    if swap_c:
+        v = v[:, :, :, :, ::-1]
+    return np.ascontiguousarray(v).reshape(r, c)
+
+
+@pytest.mark.parametrize("formula", ["classical", "dual"])
+def test_block_permutation_is_a_quadrant_relabelling(formula):
+    """A permuted run equals the unpermuted formula applied to inputs whose
+    tile halves were physically swapped, with the output halves swapped back
+    (an independent route to the index map of :209-226), bit for bit on
+    random bf16 data where roundings differ between permutations."""
+    rng = np.random.default_rng(401)
+    a = o.bf16_round(rng.standard_normal((64, 512)).astype(np.float32))
+    b = o.bf16_round(rng.standard_normal((512, 256)).astype(np.float32))
+    bm, bn, bk = 32, 128, 256
+    base = o.strassen_matmul(a, b, bm=bm, bn=bn, bk=bk, formula_variant=formula)
+    distinct = 0
+    for perm in range(8):
+        sm, sk, sn = perm & 1, (perm >> 1) & 1, (perm >> 2) & 1
+        got = o.strassen_matmul(a, b, bm=bm, bn=bn, bk=bk, formula_variant=formula, block_permutation=perm)
+        a2 = _swap_tile_halves(a, bm, bk, sm, sk)
+        b2 = _swap_tile_halves(b, bk, bn, sk, sn)
+        want = _swap_tile_halves(o.strassen_matmul(a2, b2, bm=bm, bn=bn, bk=bk, formula_variant=formula),
+                                 bm, bn, sm, sn)
+        assert np.array_equal(got, want), perm
+        distinct += not np.array_equal(got, base)
+    assert distinct >= 6  # permutations change the roundings
+
+
+def test_formula_variants_error_band_and_rules():
+    """Dual and powers stay in the classical error band on random data (no
+    published figures exist for them); powers refuses fused epilogues."""
+    a, b = o.host_uniform_inputs((256, 2048, 256), 20260833)
+    a, b = o.bf16_round(a), o.bf16_round(b)
+    ref = o.high_precision_reference(a, b).astype(np.float64)
+    errs = {f: o.device_error(o.strassen_matmul(a, b, bm=128, bn=128, bk=512, formula_variant=f), ref)["l2_relative"]
+            for f in ("classical", "dual", "powers")}
+    cubic = o.device_error(o.cubic_blocked_matmul(a, b, bm=128, bn=128, bk=512), ref)["l2_relative"]
+    for f, e in errs.items():
+        assert cubic < e < 3 * errs["classical"], (f, errs, cubic)
+    with pytest.raises(ValueError, match="quadrant-basis"):
+        o.strassen_matmul(a, b, bm=128, bn=128, bk=512, formula_variant="powers", epilogue="bias_add",
+                          bias=np.zeros(256, np.float32))

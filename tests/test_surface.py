@@ -55,9 +55,6 @@ def test_reference_argument_errors(kwargs, args, exc, match):
 
 
 @pytest.mark.parametrize("kwargs", [
-    {"formula_variant": "dual"},
-    {"formula_variant": "powers"},
-    {"block_permutation": 3},
     {"classical_panels": (0,)},
     {"panel_schedule": [0]},
     {"epilogue": "norm_residual_add", "norm_scale": t(256), "residual": t(256, 256)},
@@ -227,3 +224,14 @@ def test_lhs_transposed_surface(args, kwargs, exc, match):
     kw.update(kwargs)
     with pytest.raises(exc, match=match):
         smx.strassen_matmul_lhs_transposed(*args, **kw)
+
+
+def test_packed_weight_variant_must_match_the_call():
+    w = smx.PackedOperand(t(1), algo=7, side="rhs", rows=512, k=512, tile_rows=512, bk=512, formula="dual")
+    with pytest.raises(ValueError, match="formula_variant='dual'"):
+        smx.strassen_matmul(t(256, 512), w, bm=256, bn=512, bk=512)
+    w = smx.PackedOperand(t(1), algo=7, side="rhs", rows=512, k=512, tile_rows=512, bk=512, block_permutation=5)
+    with pytest.raises(ValueError, match="block_permutation=5"):
+        smx.strassen_matmul(t(256, 512), w, bm=256, bn=512, bk=512, block_permutation=4)
+    with pytest.raises(ValueError, match="formula_variant must be"):
+        smx.pack_operand(t(512, 512), algo=7, side="rhs", tile_rows=512, bk=512, formula="winograd")
