@@ -14,6 +14,8 @@
  *             <- benchmark_cubic_control.cubic_matmul(a, b, variant="blocked",
  *                bm, bn, bk) (experiments/qwen3/benchmark_cubic_control.py:116-177)
  *                with algo = SMX_ALGO_CUBIC (the matched 8-product control).
+ *   smx_norm_residual_add <- the norm_residual_add epilogue (strassen_pallas.py:836-866),
+ *                run as a second pass over an FP32 smx_gemm result.
  *   smx_last_error / status codes <- the ValueError/RuntimeError raised by
  *                strassen_matmul's argument checks (strassen_pallas.py:927-1047).
  *   smx_tile_requirements <- check_tiling (strassen_pallas.py:127-140): the
@@ -143,6 +145,17 @@ int smx_packed_bytes(int32_t algo, int64_t rows, int64_t k, int64_t* bytes);
  */
 int smx_pack_operand(int32_t algo, int32_t formula, int32_t block_permutation, int32_t side, int64_t rows, int64_t k,
                      const void* src, int64_t ld, int32_t tile_rows, int32_t bk, void* out, void* stream);
+
+/*
+ * Second pass of the norm_residual_add epilogue (strassen_pallas.py:836-866),
+ * whose norm spans a whole output row: from the FP32 product x [m, n] (an
+ * smx_gemm with SMX_FLAG_OUT_F32 and no epilogue) writes
+ * out = bf16(x * rsqrt(mean_row(x^2) + eps) * scale[col] + residual), with
+ * residual and out bf16 [m, n] and scale [n] bf16 or float32 (scale_f32).
+ * Asynchronous on stream.
+ */
+int smx_norm_residual_add(int64_t m, int64_t n, const float* x, int64_t ldx, const void* residual, int64_t ldr,
+                          const void* scale, int32_t scale_f32, float eps, void* out, int64_t ldo, void* stream);
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* smx_last_error(void);

@@ -358,7 +358,8 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
                     rope_sin=None, rope_scale=None, rope_head_dim=128,
                     rope_eps=1e-6, product_aware_swiglu=False,
                     product_aware_residual=False, output_dtype="bfloat16",
-                    formula_variant="classical", block_permutation=0):
+                    formula_variant="classical", block_permutation=0, norm_scale=None,
+                    norm_eps=1e-6):
     """``a @ b`` with one tile-local classical Strassen level.
 
     Restates ``_classical_strassen_kernel`` (``strassen_pallas.py:156-879``)
@@ -444,7 +445,8 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
     return _epilogue(acc, m, n, bm, bn, epilogue=epilogue, residual=residual,
                      bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
                      rope_scale=rope_scale, rope_head_dim=rope_head_dim,
-                     rope_eps=rope_eps, output_dtype=output_dtype)
+                     rope_eps=rope_eps, output_dtype=output_dtype, norm_scale=norm_scale,
+                     norm_eps=norm_eps)
 
 
 def strassen_matmul_lhs_transposed(a_t, b, *, bm, bn, bk, interleave_products=False,
@@ -460,7 +462,7 @@ def strassen_matmul_lhs_transposed(a_t, b, *, bm, bn, bk, interleave_products=Fa
 def cubic_blocked_matmul(a, b, *, bm, bn, bk, epilogue=None, residual=None,
                          bias=None, rope_cos=None, rope_sin=None,
                          rope_scale=None, rope_head_dim=128, rope_eps=1e-6,
-                         output_dtype="bfloat16"):
+                         output_dtype="bfloat16", norm_scale=None, norm_eps=1e-6):
     """The matched cubic control: eight half-size products per K panel.
 
     ``_cubic_blocked_kernel`` (``experiments/qwen3/benchmark_cubic_control.py
@@ -484,11 +486,13 @@ def cubic_blocked_matmul(a, b, *, bm, bn, bk, epilogue=None, residual=None,
     return _epilogue(acc, m, n, bm, bn, epilogue=epilogue, residual=residual,
                      bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
                      rope_scale=rope_scale, rope_head_dim=rope_head_dim,
-                     rope_eps=rope_eps, output_dtype=output_dtype)
+                     rope_eps=rope_eps, output_dtype=output_dtype, norm_scale=norm_scale,
+                     norm_eps=norm_eps)
 
 
 def _epilogue(acc, m, n, bm, bn, *, epilogue, residual, bias, rope_cos,
-              rope_sin, rope_scale, rope_head_dim, rope_eps, output_dtype):
+              rope_sin, rope_scale, rope_head_dim, rope_eps, output_dtype,
+              norm_scale=None, norm_eps=1e-6):
     """Epilogues on the FP32 accumulators, then one bf16 rounding.
 
     ``strassen_pallas.py:739-879``: swiglu / geglu ``:762-777`` with the gate
@@ -519,6 +523,16 @@ def _epilogue(acc, m, n, bm, bn, *, epilogue, residual, bias, rope_cos,
     if epilogue == "qk_norm_rope":
         return to_out(_qk_norm_rope(acc, m, n, bm, bn, rope_cos, rope_sin,
                                     rope_scale, rope_head_dim, rope_eps))
+    if epilogue == "norm_residual_add":
+        # ``:836-866`` (bn == n): per row, recip = rsqrt((sum(left^2) +
+        # sum(right^2)) / n + eps); out = half * recip * scale + residual.
+        full = _assemble(acc, m, n, bm, bn)
+        left, right = full[:, :n // 2], full[:, n // 2:]
+        squares = (np.sum(left * left, axis=1, keepdims=True, dtype=np.float32)
+                   + np.sum(right * right, axis=1, keepdims=True, dtype=np.float32))
+        recip = (np.float32(1.0) / np.sqrt(squares * np.float32(1.0 / n) + np.float32(norm_eps))).astype(np.float32)
+        scale = np.asarray(norm_scale, np.float32)
+        return to_out(full * recip * scale + np.asarray(residual, np.float32))
     raise ValueError(f"unknown epilogue {epilogue!r}")
 
 

@@ -46,8 +46,8 @@ SMX_FORMULA = {"classical": 0, "dual": 1, "powers": 2}
 SMX_AUX_BIAS_F32 = 1
 SMX_AUX_SCALE_F32 = 2
 
-EXPORTS = ("smx_gemm", "smx_tile_requirements", "smx_packed_bytes", "smx_pack_operand", "smx_last_error",
-           "smx_version")
+EXPORTS = ("smx_gemm", "smx_tile_requirements", "smx_packed_bytes", "smx_pack_operand", "smx_norm_residual_add",
+           "smx_last_error", "smx_version")
 
 
 class SmxGemmDesc(ctypes.Structure):
@@ -91,6 +91,9 @@ def load():
     lib.smx_packed_bytes.restype = ctypes.c_int
     lib.smx_pack_operand.argtypes = [i32, i32, i32, i32, i64, i64, vp, i64, i32, i32, vp, vp]
     lib.smx_pack_operand.restype = ctypes.c_int
+    f32 = ctypes.c_float
+    lib.smx_norm_residual_add.argtypes = [i64, i64, vp, i64, vp, i64, vp, i32, f32, vp, i64, vp]
+    lib.smx_norm_residual_add.restype = ctypes.c_int
     lib.smx_last_error.argtypes = []
     lib.smx_last_error.restype = ctypes.c_char_p
     lib.smx_version.argtypes = []

@@ -163,6 +163,32 @@ int launch_pack(const uint16_t* src, int64_t ld, int64_t rows, int64_t k, int32_
   return check_launch();
 }
 
+// norm_residual_add's second pass (strassen_pallas.py:836-866): one
+// workgroup per output row of the FP32 product x [m, n]:
+// out = bf16(x * rsqrt(mean(x^2) + eps) * scale + residual). The row's sum of
+// squares is accumulated in FP32 per thread, then across the workgroup.
+__global__ __launch_bounds__(256) void norm_residual_rows(const float* __restrict__ x, int64_t ldx,
+                                                          const uint16_t* __restrict__ residual, int64_t ldr,
+                                                          const void* __restrict__ scale, int32_t scale_f32,
+                                                          float eps, int64_t n, uint16_t* __restrict__ out,
+                                                          int64_t ldo) {
+  __shared__ float partial[4];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * ldx;
+  float ss = 0.f;
+  for (int64_t c = threadIdx.x; c < n; c += blockDim.x) ss += xr[c] * xr[c];
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) ss += __shfl_xor(ss, s, 64);
+  if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float total = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+  const float recip = 1.0f / sqrtf(total / (float)n + eps);
+  const uint16_t* rr = residual + row * ldr;
+  uint16_t* orow = out + row * ldo;
+  for (int64_t c = threadIdx.x; c < n; c += blockDim.x)
+    orow[c] = f32_to_bf16(xr[c] * recip * load_vec(scale, scale_f32, c) + bf16_to_f32(rr[c]));
+}
+
 }  // namespace
 }  // namespace smx
 
@@ -325,6 +351,18 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
     return d->algo == SMX_ALGO_STRASSEN ? dispatch_packed<7>(p, d->epilogue, s)
                                         : dispatch_packed<8>(p, d->epilogue, s);
   return d->algo == SMX_ALGO_STRASSEN ? dispatch_v1<7>(p, d->epilogue, s) : dispatch_v1<8>(p, d->epilogue, s);
+}
+
+int smx_norm_residual_add(int64_t m, int64_t n, const float* x, int64_t ldx, const void* residual, int64_t ldr,
+                          const void* scale, int32_t scale_f32, float eps, void* out, int64_t ldo, void* stream) {
+  g_error[0] = 0;
+  if (m <= 0 || n <= 0) return fail(SMX_ERR_INVALID, "empty problem m=%lld n=%lld", (long long)m, (long long)n);
+  if (!x || !residual || !scale || !out) return fail(SMX_ERR_INVALID, "null pointer");
+  if (ldx < n || ldr < n || ldo < n) return fail(SMX_ERR_INVALID, "row strides must be >= n");
+  if (m >= ((int64_t)1 << 31)) return fail(SMX_ERR_UNSUPPORTED, "too many rows");
+  hipLaunchKernelGGL(norm_residual_rows, dim3((unsigned)m), dim3(256), 0, (hipStream_t)stream, x, ldx,
+                     (const uint16_t*)residual, ldr, scale, scale_f32 ? 1 : 0, eps, n, (uint16_t*)out, ldo);
+  return check_launch();
 }
 
 }  // extern "C"

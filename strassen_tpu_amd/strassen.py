@@ -9,8 +9,10 @@ torch's current stream.
 
 Differences a caller can observe, all raised as exceptions (never silent):
 
-* The exact-panel policies (``classical_panels``, ``panel_schedule``), the
-  ``norm_residual_add`` epilogue and FP32 inputs raise ``NotImplementedError``.
+* The exact-panel policies (``classical_panels``, ``panel_schedule``) and FP32
+  inputs raise ``NotImplementedError``.
+* ``norm_residual_add`` runs as the GEMM with an FP32 result followed by a
+  row-norm pass (one bf16 rounding, as in the reference).
 * ``formula_variant`` "dual" / "powers" and ``block_permutation`` run on
   packed operands: a plain weight is packed for the call (pack it once with
   ``strassen_weight_layout(..., formula_variant=, block_permutation=)``).
@@ -136,6 +138,10 @@ def _validate(a, b, *, bm, bn, bk, block_permutation, formula_variant,
             raise ValueError(
                 "norm_residual_add normalises over the whole output row, so "
                 f"the tile must span it: bn={bn} must equal n={n}")
+        if tuple(residual.shape) != (m, n):
+            raise ValueError(f"residual shape {tuple(residual.shape)} != output {(m, n)}")
+        if tuple(norm_scale.shape) != (n,):
+            raise ValueError(f"norm_scale shape {tuple(norm_scale.shape)} != output width {(n,)}")
     if epilogue == "qk_norm_rope":
         if rope_cos is None or rope_sin is None or rope_scale is None:
             raise ValueError(
@@ -198,13 +204,11 @@ def _validate(a, b, *, bm, bn, bk, block_permutation, formula_variant,
     return m, k, n, classical_panels, out
 
 
-def _unsupported(classical_panels, panel_schedule, epilogue, dtype, interpret):
+def _unsupported(classical_panels, panel_schedule, dtype, interpret):
     if interpret:
         raise NotImplementedError("interpret=True: the gfx950 kernel has no CPU interpreter path")
     if classical_panels or panel_schedule is not None:
         raise NotImplementedError("exact-panel policies are not implemented on gfx950")
-    if epilogue == "norm_residual_add":
-        raise NotImplementedError(f"epilogue {epilogue!r} is not implemented on gfx950")
     if dtype != torch.bfloat16:
         raise NotImplementedError("FP32 inputs are not implemented on gfx950 (bf16 MFMA path)")
 
@@ -229,9 +233,36 @@ def _check_packed(x, algo, side, tile_rows, bk, formula="classical", block_permu
                          f"formula_variant={formula!r}, block_permutation={block_permutation}")
 
 
+def _norm_residual_add(algo, a, b, *, residual, norm_scale, norm_eps, **kw):
+    """``norm_residual_add`` (``strassen_pallas.py:836-866``) in two passes:
+    the GEMM stores its FP32 result, then ``smx_norm_residual_add`` applies
+    the row RMSNorm, the scale and the residual with one bf16 rounding (the
+    row's sum of squares spans every column tile of the output)."""
+    product = _run(algo, a, b, out_dtype=torch.float32, **kw)
+    m, n = product.shape
+    _require_device(residual, norm_scale)
+    residual = residual.to(torch.bfloat16)
+    if residual.stride(1) != 1:
+        residual = residual.contiguous()
+    scale = norm_scale.contiguous()
+    if scale.dtype not in (torch.bfloat16, torch.float32):
+        scale = scale.to(torch.float32)
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=product.device)
+    stream = torch.cuda.current_stream(product.device).cuda_stream
+    rc = _lib.load().smx_norm_residual_add(m, n, _lib.ptr(product), product.stride(0), _lib.ptr(residual),
+                                           residual.stride(0), _lib.ptr(scale), int(scale.dtype == torch.float32),
+                                           float(norm_eps), _lib.ptr(out), out.stride(0), stream)
+    _lib.check(rc)
+    return out
+
+
 def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
          rope_cos=None, rope_sin=None, rope_scale=None, rope_head_dim=128,
-         rope_eps=1e-6, out_dtype=torch.bfloat16, formula="classical", block_permutation=0):
+         rope_eps=1e-6, out_dtype=torch.bfloat16, formula="classical", block_permutation=0,
+         norm_scale=None, norm_eps=1e-6):
+    if epilogue == "norm_residual_add":
+        return _norm_residual_add(algo, a, b, residual=residual, norm_scale=norm_scale, norm_eps=norm_eps,
+                                  bm=bm, bn=bn, bk=bk, formula=formula, block_permutation=block_permutation)
     lib = _lib.load()
     m, k = a.shape
     n = b.shape[1]
@@ -365,11 +396,12 @@ def strassen_matmul(
         output_dtype=output_dtype, allow_input_fusion=allow_input_fusion,
         product_aware_swiglu=product_aware_swiglu,
         product_aware_residual=product_aware_residual)
-    _unsupported(classical_panels, panel_schedule, epilogue, a.dtype, interpret)
+    _unsupported(classical_panels, panel_schedule, a.dtype, interpret)
     return _run(_lib.SMX_ALGO_STRASSEN, a, b, bm=bm, bn=bn, bk=bk, epilogue=epilogue,
                 residual=residual, bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
                 rope_scale=rope_scale, rope_head_dim=rope_head_dim, rope_eps=rope_eps,
-                out_dtype=out_dtype, formula=formula_variant, block_permutation=block_permutation)
+                out_dtype=out_dtype, formula=formula_variant, block_permutation=block_permutation,
+                norm_scale=norm_scale, norm_eps=norm_eps)
 
 
 def strassen_matmul_lhs_transposed(a, b, *, bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_BK, dot_precision=None,
@@ -421,7 +453,7 @@ def cubic_matmul(a, b, *, variant="blocked", bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_
                  dot_precision=None, allow_input_fusion=None, interpret=False,
                  vmem_limit_bytes=None, epilogue=None, residual=None, bias=None,
                  rope_cos=None, rope_sin=None, rope_scale=None, rope_head_dim=128,
-                 rope_eps=1e-6, output_dtype=None):
+                 rope_eps=1e-6, output_dtype=None, norm_scale=None, norm_eps=1e-6):
     """Matched cubic control (``experiments/qwen3/benchmark_cubic_control.py:116-177``).
 
     Eight half-size products per K panel into four FP32 quadrant
@@ -459,10 +491,12 @@ def cubic_matmul(a, b, *, variant="blocked", bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_
     out_dtype = torch.bfloat16 if output_dtype is None else output_dtype
     if out_dtype not in (torch.bfloat16, torch.float32):
         raise ValueError("output_dtype must be BF16 or FP32")
+    if epilogue == "norm_residual_add" and (residual is None or norm_scale is None):
+        raise ValueError("norm_residual_add requires residual= and norm_scale=")
     return _run(_lib.SMX_ALGO_CUBIC, a, b, bm=bm, bn=bn, bk=bk, epilogue=epilogue,
                 residual=residual, bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
                 rope_scale=rope_scale, rope_head_dim=rope_head_dim, rope_eps=rope_eps,
-                out_dtype=out_dtype)
+                out_dtype=out_dtype, norm_scale=norm_scale, norm_eps=norm_eps)
 
 
 def native_matmul(a, b):

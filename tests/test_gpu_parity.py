@@ -399,6 +399,23 @@ def test_dual_permuted_with_fused_epilogues():
     assert_ulp_close(got, o.strassen_matmul(a, b, epilogue="residual_add", residual=r, **kw), k=1024)
 
 
+@pytest.mark.parametrize("scale_dtype", [torch.bfloat16, torch.float32])
+def test_norm_residual_add_epilogue(scale_dtype):
+    """Row RMSNorm over the whole output row, scale, residual (two passes on
+    gfx950: FP32 GEMM result, then the row kernel)."""
+    rng, a, b = _gaussian(421, 512, 2048, 1024)
+    r = o.bf16_round(rng.standard_normal((512, 1024)).astype(np.float32))
+    g = (1 + 0.1 * rng.standard_normal(1024)).astype(np.float32)
+    if scale_dtype == torch.bfloat16:
+        g = o.bf16_round(g)
+    g_dev = torch.from_numpy(g).to(DEV).to(scale_dtype)
+    kw = dict(bm=256, bn=1024, bk=512, epilogue="norm_residual_add")
+    for arm in ARMS:
+        got = host(run_arm(arm, a, b, residual=dev(r), norm_scale=g_dev, **kw))
+        want = oracle_arm(arm, a, b, residual=r, norm_scale=g, **kw)
+        assert_ulp_close(got, want, k=2048)
+
+
 def test_residual_add_epilogue():
     rng, a, b = _gaussian(319, 512, 2048, 1024)
     r = o.bf16_round(rng.standard_normal((512, 1024)).astype(np.float32))

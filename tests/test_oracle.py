@@ -424,3 +424,19 @@ def test_formula_variants_error_band_and_rules():
     with pytest.raises(ValueError, match="quadrant-basis"):
         o.strassen_matmul(a, b, bm=128, bn=128, bk=512, formula_variant="powers", epilogue="bias_add",
                           bias=np.zeros(256, np.float32))
+
+
+def test_norm_residual_add_closed_form():
+    """norm_residual_add (strassen_pallas.py:836-866): rms_norm over the whole
+    row of the exact product, times the scale, plus the residual; one bf16
+    rounding. Strassen and cubic against a float64 evaluation."""
+    rng, a, b = _int_problem(420, 32, 512, 256)
+    r = o.bf16_round(rng.standard_normal((32, 256)).astype(np.float32))
+    g = o.bf16_round((1 + 0.1 * rng.standard_normal(256)).astype(np.float32))
+    exact = (a @ b).astype(np.float64)
+    expected = exact / np.sqrt(np.mean(exact ** 2, axis=1, keepdims=True) + 1e-6) * g + r
+    for got in (o.strassen_matmul(a, b, bm=16, bn=256, bk=256, epilogue="norm_residual_add", residual=r,
+                                  norm_scale=g),
+                o.cubic_blocked_matmul(a, b, bm=16, bn=256, bk=256, epilogue="norm_residual_add", residual=r,
+                                       norm_scale=g)):
+        np.testing.assert_allclose(got, expected, rtol=2 ** -7, atol=2 ** -7)

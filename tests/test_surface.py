@@ -57,7 +57,6 @@ def test_reference_argument_errors(kwargs, args, exc, match):
 @pytest.mark.parametrize("kwargs", [
     {"classical_panels": (0,)},
     {"panel_schedule": [0]},
-    {"epilogue": "norm_residual_add", "norm_scale": t(256), "residual": t(256, 256)},
     {"interpret": True},
 ])
 def test_unported_options_raise_not_implemented(kwargs):
@@ -235,3 +234,17 @@ def test_packed_weight_variant_must_match_the_call():
         smx.strassen_matmul(t(256, 512), w, bm=256, bn=512, bk=512, block_permutation=4)
     with pytest.raises(ValueError, match="formula_variant must be"):
         smx.pack_operand(t(512, 512), algo=7, side="rhs", tile_rows=512, bk=512, formula="winograd")
+
+
+def test_norm_residual_add_surface_checks():
+    """strassen_pallas.py:972-985."""
+    a, b = t(256, 512), t(512, 256)
+    kw = dict(bm=256, bn=256, bk=512, epilogue="norm_residual_add")
+    with pytest.raises(ValueError, match="requires residual= and norm_scale="):
+        smx.strassen_matmul(a, b, residual=t(256, 256), **kw)
+    with pytest.raises(ValueError, match="residual shape"):
+        smx.strassen_matmul(a, b, residual=t(128, 256), norm_scale=t(256), **kw)
+    with pytest.raises(ValueError, match="norm_scale shape"):
+        smx.strassen_matmul(a, b, residual=t(256, 256), norm_scale=t(128), **kw)
+    with pytest.raises(ValueError, match="HIP device"):
+        smx.strassen_matmul(a, b, residual=t(256, 256), norm_scale=t(256), **kw)
