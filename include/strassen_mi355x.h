@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define SMX_VERSION 4
+#define SMX_VERSION 5
 
 /* Status codes. */
 #define SMX_OK 0
@@ -99,6 +99,13 @@ typedef struct smx_gemm_desc {
   int32_t flags;         /* SMX_FLAG_* bits */
   int32_t formula;       /* SMX_FORMULA_* (Strassen; packed operands built with the same formula) */
   int32_t block_permutation; /* 0..7: bit 0 swaps row halves, bit 1 K halves, bit 2 column halves (:205-226) */
+  /* Cubic only: NULL, or an FP32 [m, n] partial product (row stride ldp >=
+   * n) added to the quadrants before the epilogue. An exact-panel schedule
+   * (classical_panels / panel_schedule, :575-586, :713-735) is the Strassen
+   * GEMM over the ordinary K panels with an FP32 result, then the cubic GEMM
+   * over the exact panels with that result as its partial. */
+  const float* partial;
+  int64_t ldp;
 } smx_gemm_desc;
 
 /*
@@ -136,15 +143,20 @@ int smx_packed_bytes(int32_t algo, int64_t rows, int64_t k, int64_t* bytes);
  * B2-B0, B3, B0+B1, B2+B3), each rounded once to bf16, or those of the dual /
  * powers formula, after the block permutation's quadrant swaps (A uses bits 0
  * and 1, B bits 1 and 2); the cubic (algo 8, formula 0, permutation 0) stores
- * the four quadrants. out (smx_packed_bytes bytes, 16-byte aligned)
+ * the four quadrants. panels: NULL, or device int32 [k / bk] naming the
+ * source K panel (of bk columns) that each packed panel reads, from a
+ * source src_k wide (entries are clamped to 0 .. src_k/bk - 1); this packs
+ * the ordinary or the exact panels of an exact-panel schedule. out
+ * (smx_packed_bytes bytes, 16-byte aligned)
  * is laid out [rows/256][k/32][nops][4][64][8] bf16: fragment (tile of 128
  * product rows, stage of 16 product k, operand, 32-row block), lane l holding
  * row l%32, depth 8*(l/32)..+8. Needs rows % tile_rows == 0, k % bk == 0,
- * tile_rows % 256 == 0, bk % 64 == 0, ld >= k, ld % 8 == 0 (LHS_T: ld >= m). Asynchronous on
+ * tile_rows % 256 == 0, bk % 64 == 0, ld >= src_k, ld % 8 == 0 (LHS_T: ld >= m). Asynchronous on
  * stream.
  */
 int smx_pack_operand(int32_t algo, int32_t formula, int32_t block_permutation, int32_t side, int64_t rows, int64_t k,
-                     const void* src, int64_t ld, int32_t tile_rows, int32_t bk, void* out, void* stream);
+                     const void* src, int64_t ld, int32_t tile_rows, int32_t bk, const int32_t* panels,
+                     int64_t src_k, void* out, void* stream);
 
 /*
  * Second pass of the norm_residual_add epilogue (strassen_pallas.py:836-866),

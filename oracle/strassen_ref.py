@@ -226,6 +226,12 @@ def formula_operands(formula, a_q, b_q):
     return {p: (sa[p - 1], tb[p - 1]) for p in range(1, 8)}
 
 
+# The eight half-size cubic products (A quadrant, B quadrant, C quadrant) in
+# the matched control's order (benchmark_cubic_control.py:96-106), which is
+# also the exact-panel order (strassen_pallas.py:575-586).
+CUBIC_PAIRS = ((0, 0, 0), (0, 1, 1), (2, 0, 2), (2, 1, 3), (1, 2, 0), (1, 3, 1), (3, 2, 2), (3, 3, 3))
+
+
 def strassen_products(a_q, b_q):
     """The seven classical operand pairs {p: (S_p, T_p)}."""
     sa = strassen_a_operands(a_q)
@@ -359,19 +365,20 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
                     rope_eps=1e-6, product_aware_swiglu=False,
                     product_aware_residual=False, output_dtype="bfloat16",
                     formula_variant="classical", block_permutation=0, norm_scale=None,
-                    norm_eps=1e-6):
+                    norm_eps=1e-6, classical_panels=(), panel_schedule=None):
     """``a @ b`` with one tile-local classical Strassen level.
 
     Restates ``_classical_strassen_kernel`` (``strassen_pallas.py:156-879``)
-    without exact panels, under the plumbing of ``strassen_matmul``
-    (``:882-1221``):
+    under the plumbing of ``strassen_matmul`` (``:882-1221``):
 
     * ``formula_variant`` "classical" (``:324-379``), "dual" (``:461-517``)
       or "powers" (``:381-459``, sparse output basis decoded after the last
       panel, ``:744-760``; no fused epilogues);
     * ``block_permutation`` bits swap the row / K / column halves of the
       operand and output quadrants (``:205-226``);
-
+    * ``classical_panels`` / ``panel_schedule`` (nonzero entries) mark K
+      panels that run the exact eight-product cubic update of the quadrant
+      accumulators instead (``run_exact_panel``, ``:575-586``, ``:713-735``);
     * grid ``(M/bm, N/bn, K/bk)``; per K panel the seven half-size products
       update four FP32 quadrant accumulators in the reference's order
       (plain ``:566-573`` or interleaved ``:556-565``; product-aware final
@@ -411,6 +418,11 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
     # classical / dual accumulate physical quadrants (``update``, :241-266);
     # powers accumulates the unpermuted basis (``update_basis``, :268-273)
     basis = formula_variant == "powers"
+    exact = set(int(p) for p in classical_panels)
+    if panel_schedule is not None:
+        exact |= {i for i, v in enumerate(np.asarray(panel_schedule).tolist()) if v}
+    if exact and basis:
+        raise ValueError("exact panels require a quadrant-basis formula")
 
     acc = [np.zeros((m // 2, n // 2), dtype=np.float32) for _ in range(4)]
 
@@ -428,6 +440,10 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
     for step in range(nk):
         a_q = permuted_quadrants(_split_a(a, bm, bk, step), swap_m, swap_k)
         b_q = permuted_quadrants(_split_b(b, bn, bk, step), swap_k, swap_n)
+        if step in exact:
+            for ia, ib, q in CUBIC_PAIRS:
+                acc[output_index[q]] += np.matmul(a_q[ia], b_q[ib], dtype=np.float32)
+            continue
         products = formula_operands(formula_variant, a_q, b_q)
         last = step == nk - 1
         if last and product_aware_swiglu:
@@ -476,12 +492,10 @@ def cubic_blocked_matmul(a, b, *, bm, bn, bk, epilogue=None, residual=None,
     b = np.asarray(b, dtype=np.float32)
     m, k, n = _check_common(a, b, bm, bn, bk)
     acc = [np.zeros((m // 2, n // 2), dtype=np.float32) for _ in range(4)]
-    pairs = ((0, 0, 0), (0, 1, 1), (2, 0, 2), (2, 1, 3),
-             (1, 2, 0), (1, 3, 1), (3, 2, 2), (3, 3, 3))
     for step in range(k // bk):
         aq = _split_a(a, bm, bk, step)
         bq = _split_b(b, bn, bk, step)
-        for ia, ib, q in pairs:
+        for ia, ib, q in CUBIC_PAIRS:
             acc[q] += np.matmul(aq[ia], bq[ib], dtype=np.float32)
     return _epilogue(acc, m, n, bm, bn, epilogue=epilogue, residual=residual,
                      bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,

@@ -42,7 +42,6 @@ SMX_SIDE_RHS = 1
 SMX_SIDE_LHS_T = 2
 SMX_FLAG_OUT_F32 = 1
 SMX_FORMULA = {"classical": 0, "dual": 1, "powers": 2}
-SMX_FORMULA = {"classical": 0, "dual": 1, "powers": 2}
 SMX_AUX_BIAS_F32 = 1
 SMX_AUX_SCALE_F32 = 2
 
@@ -62,6 +61,7 @@ class SmxGemmDesc(ctypes.Structure):
         ("rope_eps", ctypes.c_float), ("aux_f32", ctypes.c_int32),
         ("flags", ctypes.c_int32),
         ("formula", ctypes.c_int32), ("block_permutation", ctypes.c_int32),
+        ("partial", ctypes.c_void_p), ("ldp", ctypes.c_int64),
     ]
 
 
@@ -89,7 +89,7 @@ def load():
     i64, i32 = ctypes.c_int64, ctypes.c_int32
     lib.smx_packed_bytes.argtypes = [i32, i64, i64, ctypes.POINTER(i64)]
     lib.smx_packed_bytes.restype = ctypes.c_int
-    lib.smx_pack_operand.argtypes = [i32, i32, i32, i32, i64, i64, vp, i64, i32, i32, vp, vp]
+    lib.smx_pack_operand.argtypes = [i32, i32, i32, i32, i64, i64, vp, i64, i32, i32, vp, i64, vp, vp]
     lib.smx_pack_operand.restype = ctypes.c_int
     f32 = ctypes.c_float
     lib.smx_norm_residual_add.argtypes = [i64, i64, vp, i64, vp, i64, vp, i32, f32, vp, i64, vp]

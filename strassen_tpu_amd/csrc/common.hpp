@@ -220,6 +220,8 @@ struct Params {
   int32_t out_f32;           // store float32 instead of bf16
   int32_t formula;           // kFormula* (Strassen family)
   int32_t perm;              // block permutation bits: 1 rows, 2 K, 4 columns
+  const float* partial;      // cubic: FP32 [M, N] added before the epilogue, or null
+  int64_t ldp;
 };
 
 // Workgroup id -> product-space tile. Workgroups are dispatched round-robin
@@ -333,6 +335,11 @@ __device__ __forceinline__ void epilogue(const Params& p, const TileOrigin& o, i
                   p.out_f32};
   const uint16_t* const rw = kEpi == SMX_EPI_RESIDUAL_ADD ? p.residual + row_base * p.ldr + col_base : nullptr;
   const int hm_c = hm * ldc, hm_r = hm * ldr;
+  // Cubic only: an FP32 partial product of the same output (the Strassen
+  // panels of an exact-panel schedule) joins the quadrants before the
+  // epilogue.
+  const float* const pw = kAlgo == 8 && p.partial ? p.partial + row_base * p.ldp + col_base : nullptr;
+  const int ldp = (int)p.ldp, hm_p = hm * ldp;
 #pragma unroll
   for (int i = 0; i < kMB; ++i) {
 #pragma unroll
@@ -392,6 +399,13 @@ __device__ __forceinline__ void epilogue(const Params& p, const TileOrigin& o, i
           q1 = acc[1][i][j][r];
           q2 = acc[2][i][j][r];
           q3 = acc[3][i][j][r];
+          if (pw) {
+            const int poff = ri * ldp + cj;
+            q0 += pw[poff];
+            q1 += pw[poff + hn];
+            q2 += pw[poff + hm_p];
+            q3 += pw[poff + hm_p + hn];
+          }
         }
         if constexpr (kGated) {
           // Quadrants 0/2 are gate, 1/3 up; output [M, N/2].

@@ -312,14 +312,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
 // s, kk < bk/2) -> columns s*bk + kk and + bk/2. Quadrants: A0 = (top, k
 // left), A1 = (top, k right), A2 = (bottom, k left), A3 = (bottom, k right);
 // B0 = (k top, left), B1 = (k top, right), B2 = (k bottom, left),
-// B3 = (k bottom, right) (strassen_pallas.py:188-204). One wave packs one
+// B3 = (k bottom, right) (strassen_pallas.py:188-204). With a panel map,
+// packed K panel s reads source panel panels[s] (the Strassen or the exact
+// panels of an exact-panel schedule); without one, panel s. One wave packs one
 // 32-row product block over kPackStages stages: each lane loads 16 bytes of
 // each quadrant per stage and stores nops 16-byte chunks, so the stores of
 // a wave are whole 1 KB fragments.
 template <int kAlgo, int kSide>
 __global__ __launch_bounds__(256) void pack_operand(const uint16_t* __restrict__ src, int64_t ld, int64_t rows,
                                                     int64_t k, int32_t tile_rows, int32_t bk, int32_t formula,
-                                                    int32_t perm, uint8_t* __restrict__ out) {
+                                                    int32_t perm, const int32_t* __restrict__ panels,
+                                                    int32_t src_panels, uint8_t* __restrict__ out) {
   constexpr int nops = nops_of(kAlgo);
   const int lane = threadIdx.x & 63;
   const int64_t gwave = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
@@ -351,7 +354,10 @@ __global__ __launch_bounds__(256) void pack_operand(const uint16_t* __restrict__
     const int64_t st = sg * kPackStages + j;
     if (st >= nstages) break;
     const int64_t kp = st * TK + half * 8;
-    const int64_t lo = (kp / hk) * bk + kp % hk, hi = lo + hk;
+    const int64_t panel = kp / hk;
+    // Map entries are clamped to the source, so a bad map cannot read out of bounds.
+    const int64_t src = panels ? min(max(panels[panel], 0), src_panels - 1) : panel;
+    const int64_t lo = src * bk + kp % hk, hi = lo + hk;
     u32x4 q[4];
     if constexpr (kSide == 2) {
       q[0] = gather(row_first, lo);

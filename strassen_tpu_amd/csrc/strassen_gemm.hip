@@ -153,13 +153,14 @@ int check_variant(int32_t algo, int32_t formula, int32_t perm) {
 
 template <int kAlgo, int kSide>
 int launch_pack(const uint16_t* src, int64_t ld, int64_t rows, int64_t k, int32_t tile_rows, int32_t bk,
-                int32_t formula, int32_t perm, uint8_t* out, hipStream_t stream) {
+                int32_t formula, int32_t perm, const int32_t* panels, int32_t src_panels, uint8_t* out,
+                hipStream_t stream) {
   const int64_t nstages = k / (2 * packed::TK);
   const int64_t waves = (rows / 64) * ((nstages + packed::kPackStages - 1) / packed::kPackStages);
   const int64_t blocks = (waves + 3) / 4;
   if (blocks >= ((int64_t)1 << 31)) return fail(SMX_ERR_UNSUPPORTED, "operand too large to pack");
   hipLaunchKernelGGL((packed::pack_operand<kAlgo, kSide>), dim3((unsigned)blocks), dim3(256), 0, stream, src, ld, rows,
-                     k, tile_rows, bk, formula, perm, out);
+                     k, tile_rows, bk, formula, perm, panels, src_panels, out);
   return check_launch();
 }
 
@@ -225,7 +226,8 @@ int smx_packed_bytes(int32_t algo, int64_t rows, int64_t k, int64_t* bytes) {
 }
 
 int smx_pack_operand(int32_t algo, int32_t formula, int32_t block_permutation, int32_t side, int64_t rows, int64_t k,
-                     const void* src, int64_t ld, int32_t tile_rows, int32_t bk, void* out, void* stream) {
+                     const void* src, int64_t ld, int32_t tile_rows, int32_t bk, const int32_t* panels,
+                     int64_t src_k, void* out, void* stream) {
   g_error[0] = 0;
   if (algo != SMX_ALGO_STRASSEN && algo != SMX_ALGO_CUBIC) return fail(SMX_ERR_INVALID, "algo must be 7 or 8");
   if (int rc = check_variant(algo, formula, block_permutation)) return rc;
@@ -238,20 +240,24 @@ int smx_pack_operand(int32_t algo, int32_t formula, int32_t block_permutation, i
                 side == SMX_SIDE_LHS ? "bm" : "bn", 2 * packed::TM, 2 * packed::kKGranule, tile_rows, bk);
   if (!src || !out) return fail(SMX_ERR_INVALID, "null pointer");
   if (!aligned16(src) || !aligned16(out)) return fail(SMX_ERR_INVALID, "pointers must be 16-byte aligned");
-  if (side == SMX_SIDE_LHS_T ? ld < rows : (ld < k || ld % 8))
+  if (!panels) src_k = k;
+  if (src_k <= 0 || src_k % bk || src_k / bk >= ((int64_t)1 << 31))
+    return fail(SMX_ERR_INVALID, "the source K (%lld) must be a positive multiple of bk", (long long)src_k);
+  if (side == SMX_SIDE_LHS_T ? ld < rows : (ld < src_k || ld % 8))
     return fail(SMX_ERR_INVALID, side == SMX_SIDE_LHS_T ? "ld must be >= rows for a transposed A"
                                                         : "ld must be >= K and a multiple of 8");
   const uint16_t* s16 = (const uint16_t*)src;
   uint8_t* o8 = (uint8_t*)out;
   hipStream_t st = (hipStream_t)stream;
+  const int32_t sp = (int32_t)(src_k / bk);
   if (algo == SMX_ALGO_STRASSEN) {
-    if (side == SMX_SIDE_LHS) return launch_pack<7, 0>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, o8, st);
-    if (side == SMX_SIDE_RHS) return launch_pack<7, 1>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, o8, st);
-    return launch_pack<7, 2>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, o8, st);
+    if (side == SMX_SIDE_LHS) return launch_pack<7, 0>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
+    if (side == SMX_SIDE_RHS) return launch_pack<7, 1>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
+    return launch_pack<7, 2>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
   }
-  if (side == SMX_SIDE_LHS) return launch_pack<8, 0>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, o8, st);
-  if (side == SMX_SIDE_RHS) return launch_pack<8, 1>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, o8, st);
-  return launch_pack<8, 2>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, o8, st);
+  if (side == SMX_SIDE_LHS) return launch_pack<8, 0>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
+  if (side == SMX_SIDE_RHS) return launch_pack<8, 1>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
+  return launch_pack<8, 2>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
 }
 
 int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, const void* residual, const void* bias,
@@ -274,6 +280,10 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
     return fail(SMX_ERR_UNSUPPORTED, "formula variants and block permutations run on packed operands");
   if (d->formula == SMX_FORMULA_POWERS && d->epilogue != SMX_EPI_NONE)
     return fail(SMX_ERR_INVALID, "fused epilogues require a quadrant-basis formula");
+  if (d->partial && d->algo != SMX_ALGO_CUBIC)
+    return fail(SMX_ERR_INVALID, "an FP32 partial is added by the cubic algorithm only");
+  if (d->partial && (d->ldp < d->n || ((uintptr_t)d->partial & 3)))
+    return fail(SMX_ERR_INVALID, "partial needs ldp >= N and 4-byte alignment");
   if (d->m <= 0 || d->n <= 0 || d->k <= 0)
     return fail(SMX_ERR_INVALID, "empty problem m=%lld n=%lld k=%lld", (long long)d->m, (long long)d->n,
                 (long long)d->k);
@@ -293,7 +303,8 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
   const int64_t out_cols = (d->epilogue == SMX_EPI_SWIGLU || d->epilogue == SMX_EPI_GEGLU) ? d->n / 2 : d->n;
   if (d->ldc < out_cols) return fail(SMX_ERR_INVALID, "ldc must be >= output width");
   // The epilogue addresses a tile half with 32-bit element offsets.
-  const int64_t widest = d->ldc > d->ldr ? d->ldc : d->ldr;
+  int64_t widest = d->ldc > d->ldr ? d->ldc : d->ldr;
+  if (d->partial && d->ldp > widest) widest = d->ldp;
   if ((int64_t)(hm + 128) * widest >= ((int64_t)1 << 31))
     return fail(SMX_ERR_UNSUPPORTED, "bm/2 * row stride must stay below 2^31 elements (bm=%d, stride=%lld)", d->bm,
                 (long long)widest);
@@ -304,6 +315,8 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
   p.out_f32 = (d->flags & SMX_FLAG_OUT_F32) ? 1 : 0;
   p.formula = d->formula;
   p.perm = d->block_permutation;
+  p.partial = d->partial;
+  p.ldp = d->partial ? d->ldp : 0;
   p.m = d->m;
   p.n = d->n;
   p.k = d->k;

@@ -15,6 +15,12 @@ Storage (``smx_pack_operand``): for ``R`` product rows (``M/2`` of A,
 bf16, i.e. 1 KB MFMA operand fragments in lane order; ``nops`` is 7
 (Strassen) or 4 (cubic), so a packed operand holds ``nops/4`` times the
 elements of the original.
+
+Exact K panels (``classical_panels`` / ``panel_schedule``) split an operand
+into a ``SplitOperand``: its ordinary panels packed for Strassen and its
+exact panels packed as cubic quadrants. The GEMM runs Strassen over the
+ordinary panels into an FP32 partial and the cubic kernel over the exact
+panels, which adds the partial before the epilogue.
 """
 
 from __future__ import annotations
@@ -25,10 +31,68 @@ import torch
 
 from . import _lib
 
-__all__ = ["PackedOperand", "pack_operand", "strassen_weight_layout", "cubic_weight_layout",
-           "pack_activation"]
+__all__ = ["PackedOperand", "SplitOperand", "ExactSchedule", "exact_schedule", "pack_operand",
+           "strassen_weight_layout", "cubic_weight_layout", "pack_activation"]
 
 _ALGOS = {_lib.SMX_ALGO_STRASSEN: "strassen", _lib.SMX_ALGO_CUBIC: "cubic"}
+
+
+class ExactSchedule:
+    """The exact K panels of a call (``classical_panels`` / ``panel_schedule``):
+    ``exact`` and ``ordinary`` are the sorted panel indices of each kind out
+    of ``nk``."""
+
+    def __init__(self, nk, exact):
+        self.nk = int(nk)
+        self.exact = tuple(sorted(int(p) for p in exact))
+        exact_set = set(self.exact)
+        self.ordinary = tuple(p for p in range(self.nk) if p not in exact_set)
+
+    def panel_map(self, kind, device):
+        """int32 device tensor of the ``kind`` ("exact" / "ordinary") panel
+        indices, uploaded once per (device, schedule)."""
+        key = (str(device), self.nk, self.exact, kind)
+        tensor = _PANEL_MAPS.get(key)
+        if tensor is None:
+            tensor = _PANEL_MAPS[key] = torch.tensor(getattr(self, kind), dtype=torch.int32).to(device)
+        return tensor
+
+    def __eq__(self, other):
+        return isinstance(other, ExactSchedule) and (self.nk, self.exact) == (other.nk, other.exact)
+
+    def __hash__(self):
+        return hash((self.nk, self.exact))
+
+    def __repr__(self):
+        return f"ExactSchedule(exact={self.exact}, nk={self.nk})"
+
+
+_PANEL_MAPS = {}
+
+
+def exact_schedule(nk, *, classical_panels=(), panel_schedule=None):
+    """Resolve the reference's two exact-panel forms (static
+    ``classical_panels``, ``strassen_pallas.py:1030-1045``; prefetched
+    ``panel_schedule``, ``:1079-1090``) into an ``ExactSchedule``, or None
+    when no panel is exact. The split into the two GEMMs is sized on the
+    host, so a schedule held on the device is read back (one
+    synchronisation)."""
+    if panel_schedule is not None:
+        if isinstance(panel_schedule, ExactSchedule):
+            schedule = panel_schedule
+        else:
+            flags = torch.as_tensor(panel_schedule)
+            if tuple(flags.shape) != (nk,):
+                raise ValueError(f"panel_schedule must have shape ({nk},), got {tuple(flags.shape)}")
+            # jnp.asarray(..., dtype=int32): fractions truncate toward zero.
+            flags = flags.to(torch.int32)
+            schedule = ExactSchedule(nk, torch.nonzero(flags).flatten().tolist())
+    else:
+        panels = tuple(sorted({int(p) for p in classical_panels}))
+        if panels and (panels[0] < 0 or panels[-1] >= nk):
+            raise ValueError(f"classical_panels {panels} outside 0..{nk - 1}")
+        schedule = ExactSchedule(nk, panels)
+    return schedule if schedule.exact else None
 
 
 class PackedOperand:
@@ -45,6 +109,8 @@ class PackedOperand:
         self.algo, self.side = int(algo), side
         self.rows, self.k, self.tile_rows, self.bk = int(rows), int(k), int(tile_rows), int(bk)
         self.formula, self.block_permutation = formula, int(block_permutation)
+
+    schedule = None  # packed for every K panel (no exact panels)
 
     # The parts of the tensor interface the callers' argument checks use.
     @property
@@ -69,20 +135,56 @@ class PackedOperand:
                 f"tile_rows={self.tile_rows}, bk={self.bk}{variant}, device={self.device})")
 
 
+class SplitOperand(PackedOperand):
+    """A Strassen operand packed for an exact-panel schedule: ``ordinary``
+    holds its ordinary K panels packed for Strassen (None if every panel is
+    exact), ``exact`` its exact panels packed as cubic quadrants."""
+
+    def __init__(self, ordinary, exact, *, side, rows, k, tile_rows, bk, formula, block_permutation, schedule):
+        super().__init__(exact.data, algo=_lib.SMX_ALGO_STRASSEN, side=side, rows=rows, k=k, tile_rows=tile_rows,
+                         bk=bk, formula=formula, block_permutation=block_permutation)
+        self.ordinary, self.exact, self.schedule = ordinary, exact, schedule
+
+    def __repr__(self):
+        return (f"SplitOperand({self.side}, shape={tuple(self.shape)}, tile_rows={self.tile_rows}, bk={self.bk}, "
+                f"formula={self.formula}, block_permutation={self.block_permutation}, "
+                f"exact_panels={self.schedule.exact}, device={self.device})")
+
+
 def packed_bytes(algo, rows, k):
     out = ctypes.c_int64()
     _lib.check(_lib.load().smx_packed_bytes(algo, rows, k, ctypes.byref(out)))
     return out.value
 
 
-def pack_operand(x, *, algo, side, tile_rows, bk, formula="classical", block_permutation=0):
+def _pack(src, *, algo, side, rows, k, tile_rows, bk, formula, block_permutation, panels=None):
+    """One smx_pack_operand call over ``src`` (rows x K source, or K x rows
+    for lhs_t); ``panels`` (a device int32 map) selects the K panels to
+    pack, in order."""
+    packed_k = k if panels is None else panels.numel() * bk
+    nbytes = packed_bytes(algo, rows, packed_k)
+    data = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=src.device)
+    side_id = {"lhs": _lib.SMX_SIDE_LHS, "rhs": _lib.SMX_SIDE_RHS, "lhs_t": _lib.SMX_SIDE_LHS_T}[side]
+    stream = torch.cuda.current_stream(src.device).cuda_stream
+    rc = _lib.load().smx_pack_operand(algo, _lib.SMX_FORMULA[formula], block_permutation, side_id, rows, packed_k,
+                                      _lib.ptr(src), src.stride(0), tile_rows, bk, _lib.ptr(panels), k,
+                                      _lib.ptr(data), stream)
+    _lib.check(rc)
+    return PackedOperand(data, algo=algo, side="rhs" if side == "rhs" else "lhs", rows=rows, k=packed_k,
+                         tile_rows=tile_rows, bk=bk, formula=formula, block_permutation=block_permutation)
+
+
+def pack_operand(x, *, algo, side, tile_rows, bk, formula="classical", block_permutation=0, classical_panels=(),
+                 panel_schedule=None):
     """Pack ``x`` (bf16 on the HIP device): ``a [M, K]`` for ``side="lhs"``,
     the same ``a`` stored transposed as ``[K, M]`` for ``side="lhs_t"``, or a
     weight ``b [K, N]`` for ``side="rhs"`` (any strides; a K-contiguous view
     of ``[N, K]`` storage is read in place). Runs asynchronously on torch's
     current stream. Strassen operands carry the operand sums of
     ``formula`` ("classical", "dual" or "powers") after the quadrant swaps of
-    ``block_permutation``; both operands of a GEMM must be packed alike."""
+    ``block_permutation``; both operands of a GEMM must be packed alike. With
+    exact panels (``classical_panels`` or ``panel_schedule``) a Strassen
+    operand becomes a ``SplitOperand``."""
     if formula not in _lib.SMX_FORMULA:
         raise ValueError("formula_variant must be 'classical', 'dual', or 'powers'")
     if side not in ("lhs", "rhs", "lhs_t"):
@@ -107,23 +209,33 @@ def pack_operand(x, *, algo, side, tile_rows, bk, formula="classical", block_per
             src = src.contiguous()
     if rows % tile_rows or k % bk:
         raise ValueError(f"operand [{rows}, {k}] (rows x K) does not tile by ({tile_rows}, {bk})")
-    nbytes = packed_bytes(algo, rows, k)
-    data = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=x.device)
-    side_id = {"lhs": _lib.SMX_SIDE_LHS, "rhs": _lib.SMX_SIDE_RHS, "lhs_t": _lib.SMX_SIDE_LHS_T}[side]
-    stream = torch.cuda.current_stream(x.device).cuda_stream
-    rc = _lib.load().smx_pack_operand(algo, _lib.SMX_FORMULA[formula], block_permutation, side_id, rows, k,
-                                      _lib.ptr(src), src.stride(0), tile_rows, bk, _lib.ptr(data), stream)
-    _lib.check(rc)
-    return PackedOperand(data, algo=algo, side="rhs" if side == "rhs" else "lhs", rows=rows, k=k,
-                         tile_rows=tile_rows, bk=bk, formula=formula, block_permutation=block_permutation)
+    common = dict(side=side, rows=rows, k=k, tile_rows=tile_rows, bk=bk)
+    schedule = exact_schedule(k // bk, classical_panels=classical_panels, panel_schedule=panel_schedule)
+    if schedule is None:
+        return _pack(src, algo=algo, formula=formula, block_permutation=block_permutation, **common)
+    if algo != _lib.SMX_ALGO_STRASSEN:
+        raise ValueError("exact panels apply to the Strassen algorithm only")
+    if formula == "powers":
+        raise ValueError("exact panels require a quadrant-basis formula")
+    ordinary = None
+    if schedule.ordinary:
+        ordinary = _pack(src, algo=algo, formula=formula, block_permutation=block_permutation,
+                         panels=schedule.panel_map("ordinary", x.device), **common)
+    exact = _pack(src, algo=_lib.SMX_ALGO_CUBIC, formula="classical", block_permutation=0,
+                  panels=schedule.panel_map("exact", x.device), **common)
+    common["side"] = "rhs" if side == "rhs" else "lhs"
+    return SplitOperand(ordinary, exact, formula=formula, block_permutation=block_permutation, schedule=schedule,
+                        **common)
 
 
-def strassen_weight_layout(b, bn, bk, *, formula_variant="classical", block_permutation=0):
+def strassen_weight_layout(b, bn, bk, *, formula_variant="classical", block_permutation=0, classical_panels=(),
+                           panel_schedule=None):
     """Pre-sum and pack a bf16 ``[K, N]`` weight for ``strassen_matmul``
-    with the tile ``(bn, bk)`` (and the formula / block permutation the
-    calls will use)."""
+    with the tile ``(bn, bk)`` (and the formula, block permutation and exact
+    panels the calls will use)."""
     return pack_operand(b, algo=_lib.SMX_ALGO_STRASSEN, side="rhs", tile_rows=bn, bk=bk,
-                        formula=formula_variant, block_permutation=block_permutation)
+                        formula=formula_variant, block_permutation=block_permutation,
+                        classical_panels=classical_panels, panel_schedule=panel_schedule)
 
 
 def cubic_weight_layout(b, bn, bk):
@@ -132,8 +244,10 @@ def cubic_weight_layout(b, bn, bk):
     return pack_operand(b, algo=_lib.SMX_ALGO_CUBIC, side="rhs", tile_rows=bn, bk=bk)
 
 
-def pack_activation(a, algo, bm, bk, *, formula_variant="classical", block_permutation=0):
+def pack_activation(a, algo, bm, bk, *, formula_variant="classical", block_permutation=0, classical_panels=(),
+                    panel_schedule=None):
     """Pack an activation ``a [M, K]`` once for several GEMMs that share it
     (e.g. the q, k and v projections)."""
     return pack_operand(a, algo=algo, side="lhs", tile_rows=bm, bk=bk, formula=formula_variant,
-                        block_permutation=block_permutation)
+                        block_permutation=block_permutation, classical_panels=classical_panels,
+                        panel_schedule=panel_schedule)

@@ -9,8 +9,15 @@ torch's current stream.
 
 Differences a caller can observe, all raised as exceptions (never silent):
 
-* The exact-panel policies (``classical_panels``, ``panel_schedule``) and FP32
-  inputs raise ``NotImplementedError``.
+* FP32 inputs raise ``NotImplementedError``.
+* The exact-panel policies (``classical_panels``, ``panel_schedule``) run as
+  two GEMMs: Strassen over the ordinary K panels into an FP32 partial, then
+  the matched cubic over the exact panels, which adds the partial before
+  the epilogue. Operands are ``SplitOperand`` s packed with the call's
+  schedule (a plain weight is split for the call); a schedule held on the
+  device is read back once per call. ``panel_schedule`` with the powers
+  formula raises ``ValueError`` (the reference would add raw quadrant
+  products into its encoded basis).
 * ``norm_residual_add`` runs as the GEMM with an FP32 result followed by a
   row-norm pass (one bf16 rounding, as in the reference).
 * ``formula_variant`` "dual" / "powers" and ``block_permutation`` run on
@@ -32,11 +39,12 @@ from __future__ import annotations
 
 import os
 
+import numpy as np
 import torch
 
 from . import _lib
 from .layouts import is_k_contiguous
-from .packing import PackedOperand, pack_operand
+from .packing import PackedOperand, SplitOperand, exact_schedule, pack_operand
 
 __all__ = [
     "strassen_matmul", "strassen_matmul_lhs_transposed", "cubic_matmul", "native_matmul", "check_tiling",
@@ -201,14 +209,35 @@ def _validate(a, b, *, bm, bn, bk, block_permutation, formula_variant,
         raise ValueError("output_dtype must be BF16 or FP32")
     if residual is not None and epilogue == "residual_add" and tuple(residual.shape) != (m, n):
         raise ValueError(f"residual shape {tuple(residual.shape)} != output shape {(m, n)}")
+    nk = k // bk
+    if panel_schedule is not None:
+        # strassen_pallas.py:1079-1090
+        if epilogue is not None:
+            raise ValueError("panel_schedule does not support fused epilogues")
+        shape = tuple(panel_schedule.shape) if hasattr(panel_schedule, "shape") else np.shape(panel_schedule)
+        if shape != (nk,):
+            raise ValueError(f"panel_schedule must have shape ({nk},), got {shape}")
+        if formula_variant == "powers":
+            raise ValueError("panel_schedule requires a quadrant-basis formula")
+    # The kernel's product-aware checks (strassen_pallas.py:299-322).
+    if product_aware_swiglu and (formula_variant != "classical" or block_permutation != 0
+                                 or (nk - 1) in classical_panels or panel_schedule is not None):
+        raise ValueError(
+            "product-aware SwiGLU requires unpermuted classical Strassen "
+            "with quadrant accumulators; exact panels are allowed except on "
+            "the final K panel, whose product order the schedule owns")
+    if product_aware_residual and (formula_variant != "classical" or block_permutation != 0
+                                   or (nk - 1) in classical_panels or panel_schedule is not None):
+        raise ValueError(
+            "product-aware residual requires unpermuted classical Strassen "
+            "with quadrant accumulators and the residual_add epilogue; exact "
+            "panels are allowed except on the final K panel")
     return m, k, n, classical_panels, out
 
 
-def _unsupported(classical_panels, panel_schedule, dtype, interpret):
+def _unsupported(dtype, interpret):
     if interpret:
         raise NotImplementedError("interpret=True: the gfx950 kernel has no CPU interpreter path")
-    if classical_panels or panel_schedule is not None:
-        raise NotImplementedError("exact-panel policies are not implemented on gfx950")
     if dtype != torch.bfloat16:
         raise NotImplementedError("FP32 inputs are not implemented on gfx950 (bf16 MFMA path)")
 
@@ -231,6 +260,9 @@ def _check_packed(x, algo, side, tile_rows, bk, formula="classical", block_permu
         raise ValueError(f"{name} was packed for formula_variant={x.formula!r}, "
                          f"block_permutation={x.block_permutation}; called with "
                          f"formula_variant={formula!r}, block_permutation={block_permutation}")
+    if x.schedule is not None:
+        raise ValueError(f"{name} was packed for the exact panels {x.schedule.exact}; called without exact "
+                         "panels")
 
 
 def _norm_residual_add(algo, a, b, *, residual, norm_scale, norm_eps, **kw):
@@ -259,10 +291,16 @@ def _norm_residual_add(algo, a, b, *, residual, norm_scale, norm_eps, **kw):
 def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
          rope_cos=None, rope_sin=None, rope_scale=None, rope_head_dim=128,
          rope_eps=1e-6, out_dtype=torch.bfloat16, formula="classical", block_permutation=0,
-         norm_scale=None, norm_eps=1e-6):
+         norm_scale=None, norm_eps=1e-6, schedule=None, partial=None):
     if epilogue == "norm_residual_add":
         return _norm_residual_add(algo, a, b, residual=residual, norm_scale=norm_scale, norm_eps=norm_eps,
-                                  bm=bm, bn=bn, bk=bk, formula=formula, block_permutation=block_permutation)
+                                  bm=bm, bn=bn, bk=bk, formula=formula, block_permutation=block_permutation,
+                                  schedule=schedule)
+    if schedule is not None:
+        return _run_split(a, b, bm=bm, bn=bn, bk=bk, schedule=schedule, formula=formula,
+                          block_permutation=block_permutation, epilogue=epilogue, residual=residual, bias=bias,
+                          rope_cos=rope_cos, rope_sin=rope_sin, rope_scale=rope_scale,
+                          rope_head_dim=rope_head_dim, rope_eps=rope_eps, out_dtype=out_dtype)
     lib = _lib.load()
     m, k = a.shape
     n = b.shape[1]
@@ -308,6 +346,8 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
     desc.flags = _lib.SMX_FLAG_OUT_F32 if out_dtype == torch.float32 else 0
     desc.formula = _lib.SMX_FORMULA[formula]
     desc.block_permutation = block_permutation
+    if partial is not None:
+        desc.partial, desc.ldp = partial.data_ptr(), partial.stride(0)
     desc.rope_head_dim = rope_head_dim
     desc.rope_eps = rope_eps
     aux = 0
@@ -339,6 +379,46 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
                       _lib.ptr(rope_scale), stream)
     _lib.check(rc)
     return c
+
+
+def _run_split(a, b, *, bm, bn, bk, schedule, formula, block_permutation, out_dtype, **epilogue_args):
+    """An exact-panel schedule (``strassen_pallas.py:575-586``, ``:713-735``):
+    Strassen over the ordinary K panels with an FP32 result, then the
+    matched cubic over the exact panels (the eight products of
+    ``run_exact_panel`` on raw quadrants), which adds that result to its
+    quadrants before the epilogue. Products are summed in FP32 either way;
+    only the order of the FP32 additions differs from the reference's
+    panel-by-panel accumulation."""
+    variant = dict(formula=formula, block_permutation=block_permutation)
+    for x, name, side, tile_rows in ((a, "a", "lhs", bm), (b, "b", "rhs", bn)):
+        if not isinstance(x, PackedOperand):
+            continue
+        if not isinstance(x, SplitOperand):
+            raise ValueError(f"{name} was packed without exact panels; called with exact panels {schedule.exact} "
+                             "(pack it with the call's classical_panels / panel_schedule)")
+        if x.side != side or (x.tile_rows, x.bk) != (tile_rows, bk):
+            raise ValueError(f"{name} was packed as {x!r}, not as the {side} of this call's tile")
+        if x.schedule != schedule:
+            raise ValueError(f"{name} was packed for the exact panels {x.schedule.exact}; called with "
+                             f"{schedule.exact}")
+        if (x.formula, x.block_permutation) != (formula, block_permutation):
+            raise ValueError(f"{name} was packed for formula_variant={x.formula!r}, "
+                             f"block_permutation={x.block_permutation}; called with "
+                             f"formula_variant={formula!r}, block_permutation={block_permutation}")
+    _check_device_tiling(_lib.SMX_ALGO_STRASSEN, epilogue_args.get("epilogue"), bm, bn, bk, _lib.SMX_B_PACKED)
+    _require_device(a.data if isinstance(a, PackedOperand) else a, b.data if isinstance(b, PackedOperand) else b)
+    if not isinstance(a, SplitOperand):
+        a = pack_operand(a, algo=_lib.SMX_ALGO_STRASSEN, side="lhs", tile_rows=bm, bk=bk, panel_schedule=schedule,
+                         **variant)
+    if not isinstance(b, SplitOperand):
+        b = pack_operand(b, algo=_lib.SMX_ALGO_STRASSEN, side="rhs", tile_rows=bn, bk=bk, panel_schedule=schedule,
+                         **variant)
+    partial = None
+    if a.ordinary is not None:
+        partial = _run(_lib.SMX_ALGO_STRASSEN, a.ordinary, b.ordinary, bm=bm, bn=bn, bk=bk,
+                       out_dtype=torch.float32, **variant)
+    return _run(_lib.SMX_ALGO_CUBIC, a.exact, b.exact, bm=bm, bn=bn, bk=bk, out_dtype=out_dtype, partial=partial,
+                **epilogue_args)
 
 
 def strassen_matmul(
@@ -396,12 +476,13 @@ def strassen_matmul(
         output_dtype=output_dtype, allow_input_fusion=allow_input_fusion,
         product_aware_swiglu=product_aware_swiglu,
         product_aware_residual=product_aware_residual)
-    _unsupported(classical_panels, panel_schedule, a.dtype, interpret)
+    _unsupported(a.dtype, interpret)
+    schedule = exact_schedule(k // bk, classical_panels=classical_panels, panel_schedule=panel_schedule)
     return _run(_lib.SMX_ALGO_STRASSEN, a, b, bm=bm, bn=bn, bk=bk, epilogue=epilogue,
                 residual=residual, bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
                 rope_scale=rope_scale, rope_head_dim=rope_head_dim, rope_eps=rope_eps,
                 out_dtype=out_dtype, formula=formula_variant, block_permutation=block_permutation,
-                norm_scale=norm_scale, norm_eps=norm_eps)
+                norm_scale=norm_scale, norm_eps=norm_eps, schedule=schedule)
 
 
 def strassen_matmul_lhs_transposed(a, b, *, bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_BK, dot_precision=None,

@@ -60,9 +60,14 @@ def test_descriptor_layout_matches_header_order():
         line = line.strip().rstrip(";")
         if not line:
             continue
+        if line.startswith("const "):
+            line = line[len("const "):]
         ctype, names = line.split(None, 1)
+        if ctype.endswith("*") or names.startswith("*"):  # a device pointer
+            ctype, names = "pointer", names.lstrip("*")
         fields += [(n.strip(), ctype) for n in names.split(",")]
-    kinds = {"int64_t": ctypes.c_int64, "int32_t": ctypes.c_int32, "float": ctypes.c_float}
+    kinds = {"int64_t": ctypes.c_int64, "int32_t": ctypes.c_int32, "float": ctypes.c_float,
+             "pointer": ctypes.c_void_p}
     assert [(n, kinds[t]) for n, t in fields] == list(_lib.SmxGemmDesc._fields_)
 
 
@@ -163,8 +168,22 @@ def test_pack_operand_rejects_bad_arguments(args, code):
     lib = _lib.load()
     buf = (ctypes.c_uint8 * 16)()
     p = ctypes.cast(buf, ctypes.c_void_p)
-    assert lib.smx_pack_operand(algo, 0, 0, side, rows, k, p, ld, tile_rows, bk, p, None) == code
+    assert lib.smx_pack_operand(algo, 0, 0, side, rows, k, p, ld, tile_rows, bk, None, 0, p, None) == code
     assert _lib.last_error()
+
+
+@pytest.mark.parametrize("src_k,ld,code", [
+    (0, 1024, _lib.SMX_ERR_INVALID),      # empty source
+    (1000, 1024, _lib.SMX_ERR_INVALID),   # source K not a multiple of bk
+    (1024, 512, _lib.SMX_ERR_INVALID),    # ld below the source K
+])
+def test_pack_operand_panel_map_arguments(src_k, ld, code):
+    """With a panel map, the source is src_k wide and k is the packed K."""
+    lib = _lib.load()
+    buf = (ctypes.c_uint8 * 16)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    assert lib.smx_pack_operand(7, 0, 0, 0, 512, 512, p, ld, 256, 512, p, src_k, p, None) == code
+    assert "source K" in _lib.last_error() or "ld must be" in _lib.last_error()
 
 
 @pytest.mark.parametrize("algo,formula,perm", [(7, 3, 0), (7, -1, 0), (7, 0, 8), (8, 1, 0), (8, 0, 2)])
@@ -172,7 +191,8 @@ def test_pack_operand_rejects_bad_variants(algo, formula, perm):
     lib = _lib.load()
     buf = (ctypes.c_uint8 * 16)()
     p = ctypes.cast(buf, ctypes.c_void_p)
-    assert lib.smx_pack_operand(algo, formula, perm, 0, 512, 512, p, 512, 256, 512, p, None) == _lib.SMX_ERR_INVALID
+    assert lib.smx_pack_operand(algo, formula, perm, 0, 512, 512, p, 512, 256, 512, None, 0, p, None) == \
+        _lib.SMX_ERR_INVALID
 
 
 def test_powers_refuses_fused_epilogues():
@@ -183,6 +203,24 @@ def test_powers_refuses_fused_epilogues():
               epilogue=_lib.SMX_EPI["residual_add"])
     assert lib.smx_gemm(d, p, p, p, p, None, None, None, None, None) == _lib.SMX_ERR_INVALID
     assert "quadrant-basis" in _lib.last_error()
+
+
+@pytest.mark.parametrize("fields,match", [
+    ({"algo": _lib.SMX_ALGO_STRASSEN}, "cubic algorithm only"),
+    ({"algo": _lib.SMX_ALGO_CUBIC, "ldp": 100}, "ldp >= N"),
+])
+def test_partial_product_arguments(fields, match):
+    """The FP32 partial (the Strassen half of an exact-panel schedule) is
+    added by the cubic kernel only, with a full row stride."""
+    lib = _lib.load()
+    buf = (ctypes.c_uint8 * 16)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    d = _desc(a_layout=_lib.SMX_A_PACKED, b_layout=_lib.SMX_B_PACKED, **fields)
+    d.partial = ctypes.cast(buf, ctypes.c_void_p).value
+    if "ldp" not in fields:
+        d.ldp = d.n
+    assert lib.smx_gemm(d, p, p, p, None, None, None, None, None, None) == _lib.SMX_ERR_INVALID
+    assert match in _lib.last_error()
 
 
 def test_inline_asm_kernel_check():

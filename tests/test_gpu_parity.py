@@ -399,6 +399,116 @@ def test_dual_permuted_with_fused_epilogues():
     assert_ulp_close(got, o.strassen_matmul(a, b, epilogue="residual_add", residual=r, **kw), k=1024)
 
 
+# ---------------------------------------------------------------------------
+# Exact panels (classical_panels / panel_schedule): Strassen over the ordinary
+# K panels into an FP32 partial, the cubic over the exact panels adding it.
+# ---------------------------------------------------------------------------
+
+EXACT_CASES = [((1,), "classical", 0), ((0, 3), "dual", 5), ((0, 1, 2, 3), "classical", 7),
+               ((3,), "classical", 2)]
+
+
+def _gather_panels(x, panels, bk, axis):
+    cols = np.concatenate([np.arange(p * bk, (p + 1) * bk) for p in panels])
+    return np.take(x, cols, axis=axis)
+
+
+def test_pack_panel_map_matches_oracle():
+    """A split operand's two parts are the oracle's packing of the gathered
+    ordinary panels (Strassen sums) and exact panels (cubic quadrants)."""
+    rng = np.random.default_rng(430)
+    a = o.bf16_round(rng.standard_normal((512, 2048)).astype(np.float32))
+    b = o.bf16_round(rng.standard_normal((2048, 512)).astype(np.float32))
+    for formula, perm in (("classical", 0), ("dual", 3)):
+        pa = smx.pack_activation(dev(a), 7, 256, 512, formula_variant=formula, block_permutation=perm,
+                                 classical_panels=(2, 0))
+        assert pa.schedule.exact == (0, 2) and pa.schedule.ordinary == (1, 3)
+        assert np.array_equal(host(pa.ordinary.data), o.packed_operand(_gather_panels(a, (1, 3), 512, 1), 7,
+                                                                       "lhs", 256, 512, formula, perm))
+        assert np.array_equal(host(pa.exact.data), o.packed_operand(_gather_panels(a, (0, 2), 512, 1), 8,
+                                                                    "lhs", 256, 512))
+        pb = smx.strassen_weight_layout(dev_weight(b), 256, 512, formula_variant=formula, block_permutation=perm,
+                                        panel_schedule=torch.tensor([1, 0, 1, 0], device=DEV))
+        assert np.array_equal(host(pb.ordinary.data), o.packed_operand(_gather_panels(b, (1, 3), 512, 0), 7,
+                                                                       "rhs", 256, 512, formula, perm))
+        assert np.array_equal(host(pb.exact.data), o.packed_operand(_gather_panels(b, (0, 2), 512, 0), 8,
+                                                                    "rhs", 256, 512))
+    every = smx.pack_activation(dev(a), 7, 256, 512, classical_panels=range(4))
+    assert every.ordinary is None
+    assert np.array_equal(host(every.exact.data), o.packed_operand(a, 8, "lhs", 256, 512))
+
+
+@pytest.mark.parametrize("panels,formula,perm", EXACT_CASES)
+def test_exact_panels_integer_kat(panels, formula, perm):
+    rng = np.random.default_rng(431)
+    a = rng.integers(-2, 3, (512, 2048)).astype(np.float32)
+    b = rng.integers(-2, 3, (2048, 512)).astype(np.float32)
+    want = o.bf16_round(a @ b)
+    kw = dict(bm=256, bn=256, bk=512, formula_variant=formula, block_permutation=perm)
+    got = smx.strassen_matmul(dev(a), dev_weight(b), classical_panels=panels, **kw)
+    assert np.array_equal(host(got), want)
+    flags = torch.zeros(4, dtype=torch.int32, device=DEV)
+    flags[list(panels)] = 1
+    got = smx.strassen_matmul(dev(a), dev_weight(b), panel_schedule=flags, **kw)
+    assert np.array_equal(host(got), want)
+    w = smx.strassen_weight_layout(dev_weight(b), 256, 512, formula_variant=formula, block_permutation=perm,
+                                   classical_panels=panels)
+    got = smx.strassen_matmul(dev(a), w, classical_panels=panels, **kw)
+    assert np.array_equal(host(got), want)
+
+
+@pytest.mark.parametrize("panels,formula,perm", EXACT_CASES)
+def test_exact_panels_random_matches_oracle(panels, formula, perm):
+    _, a, b = _gaussian(432, 512, 2048, 512)
+    kw = dict(bm=256, bn=256, bk=512, formula_variant=formula, block_permutation=perm, classical_panels=panels)
+    got = host(smx.strassen_matmul(dev(a), dev_weight(b), **kw))
+    want = o.strassen_matmul(a, b, **kw)
+    assert_ulp_close(got, want, k=2048)
+    ref = o.high_precision_reference(a, b).astype(np.float64)
+    assert rel_l2(got, ref) <= 1e-2 and rel_l2(got, ref) <= 1.5 * rel_l2(want, ref)
+    # FP32 output: the unrounded sum, to FP32 summation order
+    got32 = host(smx.strassen_matmul(dev(a), dev_weight(b), output_dtype=torch.float32, **kw))
+    want32 = o.strassen_matmul(a, b, output_dtype="float32", **kw)
+    assert np.all(np.abs(got32 - want32) <= 4 * np.abs(want32) * 2.0 ** -23 + fp32_floor(want32, 2048))
+
+
+def test_exact_panels_with_fused_epilogues():
+    rng, a, b = _gaussian(433, 512, 2048, 1024)
+    panels = (1, 2)
+    laid = o.swiglu_weight_layout(b, 512)
+    kw = dict(bm=256, bn=512, bk=512, classical_panels=panels)
+    got = host(smx.strassen_matmul(dev(a), dev_weight(laid), epilogue="swiglu", **kw))
+    assert_ulp_close(got, o.strassen_matmul(a, laid, epilogue="swiglu", **kw), k=2048)
+    got = host(smx.strassen_matmul(dev(a), dev_weight(laid), epilogue="geglu", **kw))
+    assert_ulp_close(got, o.strassen_matmul(a, laid, epilogue="geglu", **kw), k=2048)
+    r = o.bf16_round(rng.standard_normal((512, 1024)).astype(np.float32))
+    got = host(smx.strassen_matmul(dev(a), dev_weight(b), epilogue="residual_add", residual=dev(r), **kw))
+    assert_ulp_close(got, o.strassen_matmul(a, b, epilogue="residual_add", residual=r, **kw), k=2048)
+    bias = o.bf16_round(rng.standard_normal(1024).astype(np.float32))
+    got = host(smx.strassen_matmul(dev(a), dev_weight(b), epilogue="bias_add", bias=dev(bias), **kw))
+    assert_ulp_close(got, o.strassen_matmul(a, b, epilogue="bias_add", bias=bias, **kw), k=2048)
+    g = o.bf16_round((1 + 0.1 * rng.standard_normal(1024)).astype(np.float32))
+    kw_norm = dict(kw, bn=1024, epilogue="norm_residual_add")
+    got = host(smx.strassen_matmul(dev(a), dev_weight(b), residual=dev(r), norm_scale=dev(g), **kw_norm))
+    assert_ulp_close(got, o.strassen_matmul(a, b, residual=r, norm_scale=g, **kw_norm), k=2048)
+
+
+def test_split_weight_reuse_and_mismatch():
+    """A weight split once serves repeated calls with its schedule and is
+    refused for another schedule or none."""
+    _, a, b = _gaussian(434, 256, 2048, 512)
+    w = smx.strassen_weight_layout(dev_weight(b), 256, 512, classical_panels=(0,))
+    kw = dict(bm=256, bn=256, bk=512)
+    first = smx.strassen_matmul(dev(a), w, classical_panels=(0,), **kw)
+    second = smx.strassen_matmul(dev(a), w, panel_schedule=[1, 0, 0, 0], **kw)
+    assert torch.equal(first, second)
+    assert_ulp_close(host(first), o.strassen_matmul(a, b, classical_panels=(0,), **kw), k=2048)
+    with pytest.raises(ValueError, match="packed for the exact panels"):
+        smx.strassen_matmul(dev(a), w, classical_panels=(1,), **kw)
+    with pytest.raises(ValueError, match="called without exact panels"):
+        smx.strassen_matmul(dev(a), w, **kw)
+
+
 @pytest.mark.parametrize("scale_dtype", [torch.bfloat16, torch.float32])
 def test_norm_residual_add_epilogue(scale_dtype):
     """Row RMSNorm over the whole output row, scale, residual (two passes on

@@ -440,3 +440,55 @@ def test_norm_residual_add_closed_form():
                 o.cubic_blocked_matmul(a, b, bm=16, bn=256, bk=256, epilogue="norm_residual_add", residual=r,
                                        norm_scale=g)):
         np.testing.assert_allclose(got, expected, rtol=2 ** -7, atol=2 ** -7)
+
+
+# Exact panels (classical_panels / panel_schedule, strassen_pallas.py:575-586,
+# :713-735): the marked K panels run the eight cubic products on raw quadrants.
+
+@pytest.mark.parametrize("formula", ["classical", "dual"])
+@pytest.mark.parametrize("perm", [0, 5, 7])
+def test_exact_panels_integer_known_answer(formula, perm):
+    """Small integers keep every sum exact, so any schedule returns a @ b;
+    an exact product sent to the wrong quadrant or dropped fails here."""
+    _, a, b = _int_problem(11, 64, 1024, 256, lo=-2, hi=3)
+    for panels in ((0,), (1, 3), (0, 1, 2, 3)):
+        got = o.strassen_matmul(a, b, bm=32, bn=128, bk=256, formula_variant=formula, block_permutation=perm,
+                                classical_panels=panels, output_dtype="float32")
+        np.testing.assert_array_equal(got, a @ b)
+
+
+def test_all_exact_panels_are_the_cubic_control():
+    """Every panel exact: the same eight products per panel into the same
+    quadrant accumulators in the same order as the matched cubic."""
+    rng = np.random.default_rng(12)
+    a = o.bf16_round(rng.standard_normal((64, 1024)).astype(np.float32))
+    b = o.bf16_round(rng.standard_normal((1024, 256)).astype(np.float32))
+    got = o.strassen_matmul(a, b, bm=32, bn=128, bk=256, classical_panels=range(4), output_dtype="float32")
+    want = o.cubic_blocked_matmul(a, b, bm=32, bn=128, bk=256, output_dtype="float32")
+    np.testing.assert_array_equal(got, want)
+
+
+def test_exact_panel_uses_raw_quadrants_of_its_own_panel():
+    """Only panel 2 of K is nonzero. Marking panel 2 exact gives the cubic
+    product of that panel bit for bit (no pre-added, rounded sums); marking
+    another panel leaves the Strassen rounding of panel 2 in place."""
+    rng = np.random.default_rng(13)
+    a = np.zeros((64, 1024), np.float32)
+    b = np.zeros((1024, 256), np.float32)
+    a[:, 512:768] = o.bf16_round(rng.standard_normal((64, 256)).astype(np.float32))
+    b[512:768] = o.bf16_round(rng.standard_normal((256, 256)).astype(np.float32))
+    cubic = o.cubic_blocked_matmul(a, b, bm=32, bn=128, bk=256, output_dtype="float32")
+    exact = o.strassen_matmul(a, b, bm=32, bn=128, bk=256, classical_panels=(2,), output_dtype="float32")
+    np.testing.assert_array_equal(exact, cubic)
+    other = o.strassen_matmul(a, b, bm=32, bn=128, bk=256, classical_panels=(1,), output_dtype="float32")
+    plain = o.strassen_matmul(a, b, bm=32, bn=128, bk=256, output_dtype="float32")
+    np.testing.assert_array_equal(other, plain)
+    assert not np.array_equal(plain, cubic)
+
+
+def test_panel_schedule_is_the_prefetched_form_of_classical_panels():
+    a, b = (o.bf16_round(np.random.default_rng(14).standard_normal(s).astype(np.float32))
+            for s in ((64, 1024), (1024, 256)))
+    static = o.strassen_matmul(a, b, bm=32, bn=128, bk=256, classical_panels=(0, 3))
+    prefetched = o.strassen_matmul(a, b, bm=32, bn=128, bk=256, panel_schedule=np.array([1, 0, 0, 7], np.int32))
+    np.testing.assert_array_equal(static, prefetched)

@@ -54,9 +54,64 @@ def test_reference_argument_errors(kwargs, args, exc, match):
         smx.strassen_matmul(a, b, **base)
 
 
+@pytest.mark.parametrize("kwargs,match", [
+    # strassen_pallas.py:1079-1090
+    ({"panel_schedule": [1], "epilogue": "bias_add", "bias": t(256)}, "does not support fused epilogues"),
+    ({"panel_schedule": [1, 0]}, "must have shape \\(1,\\), got \\(2,\\)"),
+    ({"panel_schedule": torch.zeros(1, 1, dtype=torch.int32)}, "must have shape \\(1,\\), got \\(1, 1\\)"),
+    ({"panel_schedule": [1], "formula_variant": "powers"}, "quadrant-basis formula"),
+    ({"classical_panels": (0,), "formula_variant": "powers"}, "quadrant-basis formula"),
+    # the kernel's product-aware checks (:299-322): not on the final K panel
+    ({"classical_panels": (0,), "epilogue": "swiglu", "product_aware_swiglu": True}, "product-aware SwiGLU"),
+    ({"epilogue": "swiglu", "product_aware_swiglu": True, "block_permutation": 1}, "product-aware SwiGLU"),
+    ({"classical_panels": (0,), "epilogue": "residual_add", "residual": t(256, 256),
+      "product_aware_residual": True}, "product-aware residual"),
+])
+def test_exact_panel_argument_errors(kwargs, match):
+    a, b = t(256, 512), t(512, 256)
+    with pytest.raises(ValueError, match=match):
+        smx.strassen_matmul(a, b, bm=256, bn=256, bk=512, **kwargs)
+
+
+def test_exact_schedule_resolution():
+    from strassen_tpu_amd.packing import exact_schedule
+
+    assert exact_schedule(4) is None
+    assert exact_schedule(4, panel_schedule=[0, 0, 0, 0]) is None
+    s = exact_schedule(4, classical_panels=(3, 1, 1))
+    assert (s.exact, s.ordinary, s.nk) == ((1, 3), (0, 2), 4)
+    assert exact_schedule(4, panel_schedule=[0, 2, 0, -1]) == s
+    # int32 conversion truncates toward zero, like jnp.asarray(..., int32)
+    assert exact_schedule(4, panel_schedule=[0.5, 1.0, 0.0, 0.9]).exact == (1,)
+    with pytest.raises(ValueError, match="outside 0..3"):
+        exact_schedule(4, classical_panels=(4,))
+
+
+def test_split_operand_checks():
+    from strassen_tpu_amd.packing import SplitOperand, exact_schedule
+
+    def part(algo, k):
+        return smx.PackedOperand(t(1), algo=algo, side="rhs", rows=512, k=k, tile_rows=512, bk=512)
+
+    sched = exact_schedule(2, classical_panels=(1,))
+    w = SplitOperand(part(7, 512), part(8, 512), side="rhs", rows=512, k=1024, tile_rows=512, bk=512,
+                     formula="classical", block_permutation=0, schedule=sched)
+    assert w.shape == (1024, 512) and "exact_panels=(1,)" in repr(w)
+    a = t(256, 1024)
+    with pytest.raises(ValueError, match="packed for the exact panels \\(1,\\); called without"):
+        smx.strassen_matmul(a, w, bm=256, bn=512, bk=512)
+    with pytest.raises(ValueError, match="packed for the exact panels \\(1,\\); called with \\(0,\\)"):
+        smx.strassen_matmul(a, w, bm=256, bn=512, bk=512, classical_panels=(0,))
+    with pytest.raises(ValueError, match="packed for formula_variant"):
+        smx.strassen_matmul(a, w, bm=256, bn=512, bk=512, classical_panels=(1,), formula_variant="dual")
+    plain = smx.PackedOperand(t(1), algo=7, side="rhs", rows=512, k=1024, tile_rows=512, bk=512)
+    with pytest.raises(ValueError, match="packed without exact panels"):
+        smx.strassen_matmul(a, plain, bm=256, bn=512, bk=512, classical_panels=(1,))
+    with pytest.raises(ValueError, match="HIP device"):
+        smx.strassen_matmul(a, w, bm=256, bn=512, bk=512, classical_panels=(1,))
+
+
 @pytest.mark.parametrize("kwargs", [
-    {"classical_panels": (0,)},
-    {"panel_schedule": [0]},
     {"interpret": True},
 ])
 def test_unported_options_raise_not_implemented(kwargs):
