@@ -12,11 +12,13 @@ from .layouts import (  # noqa: F401
 )
 from .strassen import (  # noqa: F401
     PROFILE_INFO, TUNED_BK, TUNED_BM, TUNED_BN, VMEM_PROFILE, check_tiling,
-    cubic_matmul, native_matmul, strassen_matmul, strassen_matmul_lhs_transposed,
+    cubic_matmul, native_matmul, plain_weight_kernel, strassen_matmul, strassen_matmul_lhs_transposed,
 )
 
 from .packing import (  # noqa: F401
-    PackedOperand, cubic_weight_layout, pack_activation, pack_operand, strassen_weight_layout,
+    ExactSchedule, PackedOperand, SplitOperand, cubic_weight_layout, pack_activation, pack_operand,
+    strassen_weight_layout,
 )
+from .tuning import tuned_matmul  # noqa: F401
 
-__version__ = "0.3.0"
+__version__ = "0.4.0"

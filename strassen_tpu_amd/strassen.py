@@ -37,6 +37,7 @@ Differences a caller can observe, all raised as exceptions (never silent):
 
 from __future__ import annotations
 
+import contextlib
 import os
 
 import numpy as np
@@ -48,7 +49,7 @@ from .packing import PackedOperand, SplitOperand, exact_schedule, pack_operand
 
 __all__ = [
     "strassen_matmul", "strassen_matmul_lhs_transposed", "cubic_matmul", "native_matmul", "check_tiling",
-    "TUNED_BM", "TUNED_BN", "TUNED_BK", "VMEM_PROFILE", "PROFILE_INFO",
+    "TUNED_BM", "TUNED_BN", "TUNED_BK", "VMEM_PROFILE", "PROFILE_INFO", "plain_weight_kernel",
 ]
 
 LANE = 128
@@ -91,6 +92,33 @@ def _check_device_tiling(algo, epilogue, bm, bn, bk, b_layout):
     ]
     if errors:
         raise ValueError("tile breaks the gfx950 kernel tiling:\n  " + "\n  ".join(errors))
+
+
+# Kernel for a plain (unpacked) weight: "pack" packs both operands for the
+# call and runs the packed kernel whenever the tile suits it (the packing
+# passes are bandwidth-bound and far cheaper than the compact kernel's
+# in-register operand sums); "compact" always runs the compact kernel.
+# SMX_PLAIN_WEIGHTS sets the default; plain_weight_kernel() switches it.
+PLAIN_WEIGHTS = os.environ.get("SMX_PLAIN_WEIGHTS", "pack")
+
+
+@contextlib.contextmanager
+def plain_weight_kernel(kind):
+    """Run plain-weight calls inside the block on ``kind`` ("pack" or
+    "compact"). Process-wide; not for concurrent use."""
+    global PLAIN_WEIGHTS
+    if kind not in ("pack", "compact"):
+        raise ValueError("plain-weight kernel must be 'pack' or 'compact'")
+    previous, PLAIN_WEIGHTS = PLAIN_WEIGHTS, kind
+    try:
+        yield
+    finally:
+        PLAIN_WEIGHTS = previous
+
+
+def _fits_packed(algo, epilogue, bm, bn, bk):
+    tm, tn, tk = _lib.tile_requirements(algo, epilogue, _lib.SMX_B_PACKED)
+    return bm % (2 * tm) == 0 and bn % (2 * tn) == 0 and bk % (2 * tk) == 0
 
 
 def _is_dtype(x, dtype):
@@ -306,8 +334,11 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
     n = b.shape[1]
     variant = dict(formula=formula, block_permutation=block_permutation)
     # Formula variants and block permutations run on packed operands; a
-    # plain weight is packed for the call.
+    # plain weight is packed for the call, as is any plain weight whose tile
+    # suits the packed kernel unless the compact kernel is selected.
     packed = isinstance(b, PackedOperand) or formula != "classical" or block_permutation != 0
+    if not packed and PLAIN_WEIGHTS == "pack" and _fits_packed(algo, epilogue, bm, bn, bk):
+        packed = True
     if isinstance(a, PackedOperand) and not packed:
         raise ValueError("a packed activation needs a packed weight (strassen_weight_layout / "
                          "cubic_weight_layout)")

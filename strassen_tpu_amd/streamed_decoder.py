@@ -1,9 +1,10 @@
 """Streamed Qwen3-32B decoder: every layer on the three arms, one layer resident.
 
 Restates the scope of the reference's streamed harness
-(``experiments/qwen3/benchmark_qwen3_32b_streamed_inference.py:452-560``) with
-random-init weights: there is no network to stream a checkpoint, so each
-layer's weights are generated on the device instead of transferred. Timing
+(``experiments/qwen3/benchmark_qwen3_32b_streamed_inference.py:452-560``).
+There is no network to stream a checkpoint: each layer's weights are either
+generated on the device (random init) or read from a local safetensors
+checkpoint (``--checkpoint DIR``, ``checkpoint.LocalSafetensors``). Timing
 is "summed resident layer compute", not end-to-end latency; layer
 generation, relayout / packing, embeddings and the final logits are excluded
 (``docs/COLAB_RUNBOOK.md:121-127``).
@@ -42,6 +43,7 @@ import numpy as np
 import torch
 
 from . import qwen3_block as qb
+from .checkpoint import TENSOR_PREFIX, LocalSafetensors, dims_from_config, load_block_weights
 
 __all__ = ["ARMS", "device_error", "logit_chunk_metrics", "run"]
 
@@ -105,14 +107,20 @@ def _time_forward(x, block):
 
 
 def run(num_layers, *, dims=qb.QWEN3_32B, batch=8, seq=1024, vocab=151936, warmups=1, runs=3, seed=0,
-        tile=(1024, 1024, 512), device="cuda:0", emit=None):
-    """Stream ``num_layers`` random-init layers through the three arms;
-    returns the summary record (and passes every record to ``emit``)."""
+        tile=(1024, 1024, 512), device="cuda:0", emit=None, checkpoint=None):
+    """Stream ``num_layers`` layers through the three arms; returns the
+    summary record (and passes every record to ``emit``). Weights are
+    random-init, or read layer by layer from ``checkpoint`` (a
+    ``LocalSafetensors`` whose layers match ``dims``); token ids are random
+    either way."""
     emit = emit or (lambda record: None)
     dev = torch.device(device)
     gen = torch.Generator(device=dev).manual_seed(seed)
     token_ids = torch.randint(0, vocab, (batch, seq), device=dev, generator=gen)
-    embeddings = (torch.randn(vocab, dims.hidden, device=dev, generator=gen)).to(torch.bfloat16)
+    if checkpoint is not None:
+        embeddings = checkpoint.tensor(f"{TENSOR_PREFIX}.embed_tokens.weight", device=dev)
+    else:
+        embeddings = (torch.randn(vocab, dims.hidden, device=dev, generator=gen)).to(torch.bfloat16)
     initial = embeddings[token_ids.reshape(-1)]
     del embeddings
     hidden = {arm: initial.clone() for arm in ARMS}
@@ -120,13 +128,17 @@ def run(num_layers, *, dims=qb.QWEN3_32B, batch=8, seq=1024, vocab=151936, warmu
     emit({"kind": "metadata", "layers": num_layers, "dims": dataclasses.asdict(dims), "batch": batch, "seq": seq,
           "vocab": vocab, "tile": list(tile), "arms": list(ARMS), "warmups_per_layer": warmups, "runs_per_layer": runs,
           "performance_scope": "aggregate resident layer compute; layer generation and relayout excluded",
-          "data": "random-init bf16 weights, random token ids"})
+          "data": ("local checkpoint bf16 weights" if checkpoint is not None else "random-init bf16 weights")
+          + ", random token ids"})
 
     per_layer = {arm: [] for arm in ARMS}
     all_finite = True
     for index in range(num_layers):
         started = time.perf_counter()
-        weights = qb.BlockWeights.random_init(dims, dev, seed=seed * 1000 + index + 1)
+        if checkpoint is not None:
+            weights = load_block_weights(checkpoint, index, device=dev)
+        else:
+            weights = qb.BlockWeights.random_init(dims, dev, seed=seed * 1000 + index + 1)
         blocks = {arm: qb.PreparedBlock(weights, dims, arm, batch=batch, seq=seq, tile=tile) for arm in ARMS}
         torch.cuda.synchronize()
         prepare_s = time.perf_counter() - started
@@ -171,8 +183,14 @@ def run(num_layers, *, dims=qb.QWEN3_32B, batch=8, seq=1024, vocab=151936, warmu
     }
 
     # Final norm and LM head (excluded from timing), chunked like the reference.
-    final_norm = (1.0 + 0.1 * torch.randn(dims.hidden, device=dev, generator=gen)).to(torch.bfloat16)
-    lm_head = (torch.randn(vocab, dims.hidden, device=dev, generator=gen) * 0.02).to(torch.bfloat16).t()
+    if checkpoint is not None:
+        final_norm = checkpoint.tensor(f"{TENSOR_PREFIX}.norm.weight", device=dev)
+        head_name = "lm_head.weight" if "lm_head.weight" in checkpoint.shard_of else \
+            f"{TENSOR_PREFIX}.embed_tokens.weight"  # tied embeddings
+        lm_head = checkpoint.tensor(head_name, device=dev).t()
+    else:
+        final_norm = (1.0 + 0.1 * torch.randn(dims.hidden, device=dev, generator=gen)).to(torch.bfloat16)
+        lm_head = (torch.randn(vocab, dims.hidden, device=dev, generator=gen) * 0.02).to(torch.bfloat16).t()
     rows = {arm: qb.rms_norm(h, final_norm, dims.eps).view(batch, seq, dims.hidden)[:, :-1]
             .reshape(-1, dims.hidden) for arm, h in hidden.items()}
     targets = token_ids[:, 1:].reshape(-1)
@@ -219,6 +237,8 @@ def main(argv=None):
     ap.add_argument("--runs", type=int, default=3)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--out", default=None, help="also write the records to this JSONL file")
+    ap.add_argument("--checkpoint", default=None,
+                    help="local Hugging Face checkpoint directory (config.json + safetensors) instead of random init")
     args = ap.parse_args(argv)
     sink = open(args.out, "w") if args.out else None
 
@@ -229,8 +249,13 @@ def main(argv=None):
             sink.write(line + "\n")
             sink.flush()
 
+    extra = {}
+    if args.checkpoint:
+        dims, layers, vocab = dims_from_config(args.checkpoint)
+        extra = dict(dims=dims, vocab=vocab, checkpoint=LocalSafetensors(args.checkpoint))
+        args.layers = min(args.layers, layers)
     summary = run(args.layers, batch=args.batch, seq=args.seq, warmups=args.warmups, runs=args.runs,
-                  seed=args.seed, emit=emit)
+                  seed=args.seed, emit=emit, **extra)
     return 0 if summary["all_finite"] else 1
 
 

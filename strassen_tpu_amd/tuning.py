@@ -1,0 +1,308 @@
+"""Tile screening and the measured dispatcher (``tuned_matmul``).
+
+Restates two pieces of the reference for gfx950:
+
+* ``tuned_matmul`` (``strassen_pallas.py:1428-1461``): dispatch a bf16 GEMM
+  to Strassen only for shapes where Strassen measurably beat the native GEMM
+  on this hardware, otherwise to ``native_matmul`` (hipBLASLt). The set of
+  winning shapes is data: the reference hard-codes its TPU wins
+  (``:49-72``); here the table is produced by ``measure_dispatch`` on an
+  MI355X and shipped as ``tuned_shapes.json`` (override with the
+  ``SMX_TUNED_TABLE`` environment variable).
+* the fixed-budget tile screen of
+  ``experiments/qwen3/benchmark_qwen3_scaling_tile_tune.py:103-133``, with the
+  same rules: enumerate ``(bm, bn, bk)`` candidates that divide the geometry,
+  satisfy the kernels' tile rule and admit the paired gate|up layout; give
+  every surviving candidate exactly ``warmups`` + ``runs`` timed calls per
+  arm; record failures in-band; the winner per arm is the lowest mean, ties
+  to the earlier candidate, with no re-timing. On gfx950 the tile rule is
+  the packed kernel's (``bm % 256``, ``bn % 256``, ``bk % 64``); there is no
+  VMEM budget to screen against, because the kernel's LDS footprint is fixed
+  by its 128 x 128 product-space workgroup tile, not by ``(bm, bn, bk)``.
+
+Timing is per call with HIP events on torch's current stream (the stream
+the kernels launch on), so one sample is one whole call: activation packing,
+GEMM and fused epilogue.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+
+import torch
+
+from . import _lib
+from .layouts import swiglu_weight_layout
+from .packing import cubic_weight_layout, strassen_weight_layout
+from .strassen import cubic_matmul, native_matmul, strassen_matmul
+
+__all__ = ["TILE_RULE", "enumerate_candidates", "time_calls", "screen_tiles", "measure_dispatch",
+           "load_table", "tuned_matmul", "DEFAULT_TABLE"]
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+DEFAULT_TABLE = os.path.join(HERE, "tuned_shapes.json")
+
+# The packed kernel's tile rule (smx_tile_requirements): bm, bn multiples of
+# 2 x 128 product rows / columns, bk of 2 x 32 product depth.
+TILE_RULE = (256, 256, 64)
+BM_CANDIDATES = (512, 1024, 2048)
+BN_CANDIDATES = (512, 1024, 2048, 2560)
+BK_CANDIDATES = (256, 512, 1024)
+
+
+def enumerate_candidates(m, k, n, *, paired_width=None, bm_candidates=BM_CANDIDATES, bn_candidates=BN_CANDIDATES,
+                         bk_candidates=BK_CANDIDATES):
+    """(kept, filtered) tile candidates for a ``[m, k] @ [k, n]`` GEMM, in
+    enumeration order. ``paired_width``: the gate (= up) width of a SwiGLU
+    weight, which must hold whole ``bn/2`` blocks
+    (``benchmark_qwen3_scaling_tile_tune.py:103-133``)."""
+    kept, filtered = [], []
+    for bm in bm_candidates:
+        for bn in bn_candidates:
+            for bk in bk_candidates:
+                reasons = []
+                if m % bm:
+                    reasons.append(f"M {m} % bm")
+                if n % bn:
+                    reasons.append(f"N {n} % bn")
+                elif paired_width is not None and paired_width % (bn // 2):
+                    reasons.append(f"gate width {paired_width} % (bn//2)")
+                if k % bk:
+                    reasons.append(f"K {k} % bk")
+                if bm % TILE_RULE[0] or bn % TILE_RULE[1] or bk % TILE_RULE[2]:
+                    reasons.append("gfx950 tile rule")
+                entry = {"tile": [bm, bn, bk]}
+                if reasons:
+                    entry["filtered_because"] = reasons
+                    filtered.append(entry)
+                else:
+                    kept.append(entry)
+    return kept, filtered
+
+
+def time_calls(function, warmups, runs):
+    """``warmups`` untimed calls, then ``runs`` calls timed one by one with
+    HIP events; returns milliseconds per call."""
+    for _ in range(warmups):
+        function()
+    torch.cuda.synchronize()
+    events = []
+    for _ in range(runs):
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        function()
+        stop.record()
+        events.append((start, stop))
+    torch.cuda.synchronize()
+    return [start.elapsed_time(stop) for start, stop in events]
+
+
+def _device_name(device):
+    props = torch.cuda.get_device_properties(device)
+    return f"{props.name} ({props.gcnArchName.split(':')[0]})"
+
+
+def _inputs(m, k, n, seed, device):
+    """Activations ~N(0, 1), weight ~N(0, 0.02) stored [n, k] and viewed
+    ``[k, n]`` (the layout of an nn.Linear weight), bf16."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    x = torch.randn(m, k, device=device, generator=g).to(torch.bfloat16)
+    w = (torch.randn(n, k, device=device, generator=g) * 0.02).to(torch.bfloat16).t()
+    return x, w
+
+
+def _activate(full):
+    gate, up = full.chunk(2, dim=-1)
+    return (torch.nn.functional.silu(gate.float()) * up.float()).to(torch.bfloat16)
+
+
+def screen_tiles(m, k, n, *, swiglu=True, seed=20260907, warmups=2, runs=5, device="cuda", emit=None, **axes):
+    """Fixed-budget tile screen for one GEMM geometry; returns the winners.
+
+    Arms: ``strassen`` (packed weight, fused SwiGLU when ``swiglu``) and
+    ``cubic`` (the matched cubic, same form); the hipBLASLt GEMM (plus the
+    activation) is timed once for context and takes no part in the choice.
+    Weights are laid out and packed outside the timed calls, as the
+    reference relayouts them offline."""
+    emit = emit or (lambda record: None)
+    device = torch.device(device)
+    kept, filtered = enumerate_candidates(m, k, n, paired_width=n // 2 if swiglu else None, **axes)
+    emit({"kind": "metadata", "shape": [m, k, n], "swiglu": swiglu, "device": _device_name(device),
+          "candidates": kept, "filtered": filtered, "budget": {"warmups": warmups, "runs": runs,
+                                                               "arms": ["strassen", "cubic"]},
+          "seed": seed,
+          "rule": "identical enumeration and budget per candidate; winner per arm is the lowest mean; failures "
+                  "recorded in-band skip only that candidate/arm; no re-timing",
+          "scope": "tile screening only; not a registered comparison"})
+    if not kept:
+        emit({"kind": "verdict", "passes": False, "reason": "no feasible tile candidate"})
+        return {}
+    x, w = _inputs(m, k, n, seed, device)
+    if swiglu:
+        context = time_calls(lambda: _activate(native_matmul(x, w)), warmups, runs)
+    else:
+        context = time_calls(lambda: native_matmul(x, w), warmups, runs)
+    emit({"kind": "tune", "arm": "hipblaslt", "tile": None, "mean_ms": statistics.fmean(context),
+          "samples_ms": context, "note": "context only; not part of the tile decision"})
+    epilogue = "swiglu" if swiglu else None
+    results = {"strassen": [], "cubic": []}
+    laid_cache = {}
+    for entry in kept:
+        bm, bn, bk = entry["tile"]
+        if bn not in laid_cache:
+            laid_cache.clear()
+            laid_cache[bn] = swiglu_weight_layout(w, bn) if swiglu else w
+        laid = laid_cache[bn]
+        for arm in ("strassen", "cubic"):
+            try:
+                pack = strassen_weight_layout if arm == "strassen" else cubic_weight_layout
+                packed = pack(laid, bn, bk)
+                gemm = strassen_matmul if arm == "strassen" else cubic_matmul
+                values = time_calls(lambda: gemm(x, packed, bm=bm, bn=bn, bk=bk, epilogue=epilogue), warmups, runs)
+            except (ValueError, RuntimeError) as error:
+                emit({"kind": "tune_failure", "arm": arm, "tile": [bm, bn, bk], "error_type": type(error).__name__,
+                      "error": str(error).splitlines()[-1][:2000]})
+            else:
+                mean = statistics.fmean(values)
+                results[arm].append(([bm, bn, bk], mean))
+                emit({"kind": "tune", "arm": arm, "tile": [bm, bn, bk], "mean_ms": mean, "samples_ms": values})
+            finally:
+                packed = None
+    chosen = {}
+    for arm, rows in results.items():
+        if rows:
+            tile, mean = min(rows, key=lambda row: row[1])  # min keeps the earliest of equal means
+            chosen[arm] = {"tile": tile, "mean_ms": mean}
+    emit({"kind": "chosen", "shape": [m, k, n], "winners": chosen,
+          "hipblaslt_context_mean_ms": statistics.fmean(context)})
+    emit({"kind": "verdict", "passes": "strassen" in chosen and "cubic" in chosen,
+          "scope": "tile screening; winners feed the harnesses"})
+    return chosen
+
+
+def measure_dispatch(shapes, *, tile=(1024, 1024, 512), margin=0.02, seed=0, warmups=2, runs=10, device="cuda",
+                     emit=None):
+    """Same-run comparison of ``strassen_matmul`` (plain weight, as
+    ``tuned_matmul`` calls it) against ``native_matmul`` per ``(m, k, n)``,
+    with calls interleaved per sample. A shape enters the table only when
+    Strassen's mean is lower than native's by more than ``margin``. Returns
+    the table ``{"shapes": {"m,k,n": {"tile": [...], ...}}, ...}``."""
+    emit = emit or (lambda record: None)
+    device = torch.device(device)
+    bm, bn, bk = tile
+    table = {"device": _device_name(device), "tile": list(tile), "margin": margin,
+             "rule": "strassen mean below native mean by more than margin, same run, interleaved samples",
+             "shapes": {}}
+    for m, k, n in shapes:
+        if m % bm or n % bn or k % bk:
+            emit({"kind": "dispatch_skip", "shape": [m, k, n], "reason": f"does not tile by {tuple(tile)}"})
+            continue
+        x, w = _inputs(m, k, n, seed, device)
+        for _ in range(warmups):
+            native_matmul(x, w)
+            strassen_matmul(x, w, bm=bm, bn=bn, bk=bk)
+        samples = {"native": [], "strassen": []}
+        for r in range(runs):
+            order = ("native", "strassen") if r % 2 == 0 else ("strassen", "native")
+            for arm in order:
+                call = (lambda: native_matmul(x, w)) if arm == "native" else \
+                    (lambda: strassen_matmul(x, w, bm=bm, bn=bn, bk=bk))
+                samples[arm] += time_calls(call, 0, 1)
+        means = {arm: statistics.fmean(v) for arm, v in samples.items()}
+        wins = means["strassen"] < (1.0 - margin) * means["native"]
+        record = {"kind": "dispatch", "shape": [m, k, n], "mean_ms": means, "samples_ms": samples,
+                  "strassen_wins": wins, "flops": 2 * m * k * n}
+        emit(record)
+        if wins:
+            table["shapes"][f"{m},{k},{n}"] = {"tile": list(tile), "strassen_ms": means["strassen"],
+                                               "native_ms": means["native"]}
+        del x, w
+    return table
+
+
+_TABLE = None
+
+
+def load_table(path=None):
+    """The dispatch table (``measure_dispatch`` output) from ``path``,
+    ``$SMX_TUNED_TABLE`` or the shipped ``tuned_shapes.json``."""
+    global _TABLE
+    path = path or os.environ.get("SMX_TUNED_TABLE") or DEFAULT_TABLE
+    if _TABLE is None or _TABLE[0] != path:
+        with open(path) as f:
+            _TABLE = (path, json.load(f))
+    return _TABLE[1]
+
+
+def tuned_matmul(a, b, *, interpret=False):
+    """Dispatch measured bf16 shapes to Strassen, everything else to the
+    native GEMM (``strassen_pallas.py:1428-1461``). A shape goes to Strassen
+    only if it is in the measured table, both operands are 2-D bf16 with
+    matching K, and the table's tile divides it."""
+    if a.dim() != 2 or b.dim() != 2:
+        return native_matmul(a, b)
+    m, k = a.shape
+    k2, n = b.shape
+    entry = load_table()["shapes"].get(f"{m},{k},{n}")
+    use_strassen = (entry is not None and k == k2 and a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16
+                    and m % entry["tile"][0] == 0 and n % entry["tile"][1] == 0 and k % entry["tile"][2] == 0)
+    if not use_strassen:
+        return native_matmul(a, b)
+    bm, bn, bk = entry["tile"]
+    return strassen_matmul(a, b, bm=bm, bn=bn, bk=bk, interpret=interpret)
+
+
+# Shapes timed for the shipped table: the reference's square crossover and
+# projection shapes (strassen_pallas.py:49-72) and the Qwen3-32B GEMM sites
+# at 8192 tokens.
+DISPATCH_SHAPES = (
+    (4096, 4096, 4096), (8192, 8192, 8192), (16384, 16384, 16384),
+    (8192, 4096, 8192), (8192, 4096, 12288), (8192, 4096, 28672), (8192, 14336, 4096),
+    (8192, 5120, 8192), (8192, 5120, 1024), (8192, 8192, 5120), (8192, 5120, 25600), (8192, 5120, 51200),
+    (8192, 25600, 5120),
+)
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description="gfx950 tile screen and dispatch-table measurement")
+    sub = ap.add_subparsers(dest="command", required=True)
+    screen = sub.add_parser("screen", help="fixed-budget tile screen of one GEMM geometry")
+    screen.add_argument("--shape", default="8192,5120,51200", help="m,k,n (default: Qwen3-32B gate|up)")
+    screen.add_argument("--no-swiglu", action="store_true")
+    screen.add_argument("--warmups", type=int, default=2)
+    screen.add_argument("--runs", type=int, default=5)
+    dispatch = sub.add_parser("dispatch", help="measure Strassen against the native GEMM per shape")
+    dispatch.add_argument("--runs", type=int, default=10)
+    dispatch.add_argument("--table", default=None, help="write the dispatch table here")
+    for p in (screen, dispatch):
+        p.add_argument("--out", default=None, help="also append the JSON records to this file")
+    args = ap.parse_args(argv)
+    sink = open(args.out, "a") if args.out else None
+
+    def emit(record):
+        line = json.dumps(record, sort_keys=True)
+        print(line, flush=True)
+        if sink:
+            sink.write(line + "\n")
+            sink.flush()
+
+    _lib.load()
+    if args.command == "screen":
+        m, k, n = (int(v) for v in args.shape.split(","))
+        screen_tiles(m, k, n, swiglu=not args.no_swiglu, warmups=args.warmups, runs=args.runs, emit=emit)
+    else:
+        table = measure_dispatch(DISPATCH_SHAPES, runs=args.runs, emit=emit)
+        emit({"kind": "table", **table})
+        if args.table:
+            with open(args.table, "w") as f:
+                json.dump(table, f, indent=1, sort_keys=True)
+                f.write("\n")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -28,3 +28,48 @@ def test_streamed_decoder_small():
     logits = summary["logit_metrics"]
     assert logits["strassen"]["positions"] == 2 * 255
     assert logits["strassen"]["mean_kl_nats"] < 0.05
+
+
+def test_streamed_decoder_from_local_checkpoint(tmp_path):
+    """Two layers read from a toy safetensors checkpoint written here (the
+    naming of a Hugging Face Qwen3 checkpoint) run through the same path."""
+    import json
+
+    import torch
+    from safetensors.torch import save_file
+
+    from strassen_tpu_amd.checkpoint import LocalSafetensors, dims_from_config
+
+    hidden, ffn, heads, kv, hd, vocab = 1024, 2048, 8, 2, 128, 4096
+    g = torch.Generator().manual_seed(3)
+
+    def w(out, inp):
+        return (torch.randn(out, inp, generator=g) * 0.02).to(torch.bfloat16)
+
+    def scale(n):
+        return (1 + 0.1 * torch.randn(n, generator=g)).to(torch.bfloat16)
+
+    tensors = {"model.embed_tokens.weight": torch.randn(vocab, hidden, generator=g).to(torch.bfloat16),
+               "model.norm.weight": scale(hidden)}
+    for layer in range(2):
+        p = f"model.layers.{layer}."
+        tensors.update({
+            p + "input_layernorm.weight": scale(hidden), p + "post_attention_layernorm.weight": scale(hidden),
+            p + "self_attn.q_proj.weight": w(heads * hd, hidden), p + "self_attn.k_proj.weight": w(kv * hd, hidden),
+            p + "self_attn.v_proj.weight": w(kv * hd, hidden), p + "self_attn.o_proj.weight": w(hidden, heads * hd),
+            p + "self_attn.q_norm.weight": scale(hd), p + "self_attn.k_norm.weight": scale(hd),
+            p + "mlp.gate_proj.weight": w(ffn, hidden), p + "mlp.up_proj.weight": w(ffn, hidden),
+            p + "mlp.down_proj.weight": w(hidden, ffn)})
+    save_file(tensors, str(tmp_path / "model.safetensors"))
+    (tmp_path / "config.json").write_text(json.dumps({
+        "hidden_size": hidden, "intermediate_size": ffn, "num_attention_heads": heads, "num_key_value_heads": kv,
+        "head_dim": hd, "num_hidden_layers": 2, "vocab_size": vocab}))
+    dims, layers, vocab = dims_from_config(str(tmp_path))
+    records = []
+    summary = sd.run(layers, dims=dims, batch=2, seq=256, vocab=vocab, warmups=1, runs=2, tile=(256, 256, 256),
+                     emit=records.append, checkpoint=LocalSafetensors(str(tmp_path)))
+    assert summary["all_finite"]
+    assert records[0]["data"].startswith("local checkpoint")
+    for r in (r for r in records if r["kind"] == "layer"):
+        for arm in ("cubic", "strassen"):
+            assert r["errors_vs_hipblaslt"][arm]["l2_relative"] < 5e-2, (r["layer"], arm)

@@ -89,9 +89,11 @@ def rel_l2(got, ref):
 
 
 # The four kernels behind the surface: Strassen and the cubic control with a
-# plain weight (the compact kernel: operand sums / quadrants read from
+# plain weight on the compact kernel (operand sums / quadrants read from
 # row-major A and B^T), and both with packed operands (the packed kernel:
-# weight packed offline, activation packed per call).
+# weight packed offline, activation packed per call). A plain weight whose
+# tile suits the packed kernel is otherwise packed per call; the plain arms
+# select the compact kernel explicitly.
 ARMS = ("strassen_plain", "strassen_packed", "cubic_plain", "cubic_packed")
 
 
@@ -101,6 +103,13 @@ def run_arm(arm, a, b, *, bm, bn, bk, **kw):
     say(f"  arm {arm} tile=({bm},{bn},{bk}) epilogue={kw.get('epilogue')}")
     a_dev = a if torch.is_tensor(a) else dev(a)
     b_dev = b if torch.is_tensor(b) else dev_weight(b)
+    if arm.endswith("plain"):
+        with smx.plain_weight_kernel("compact"):
+            return _run_arm(arm, a_dev, b_dev, bm=bm, bn=bn, bk=bk, **kw)
+    return _run_arm(arm, a_dev, b_dev, bm=bm, bn=bn, bk=bk, **kw)
+
+
+def _run_arm(arm, a_dev, b_dev, *, bm, bn, bk, **kw):
     if arm == "strassen_plain":
         return smx.strassen_matmul(a_dev, b_dev, bm=bm, bn=bn, bk=bk, **kw)
     if arm == "strassen_packed":

@@ -1,0 +1,53 @@
+"""The tile screen and the measured dispatcher on the GPU, at a small
+geometry: the screen times every kept candidate for both arms and picks a
+kept tile; tuned_matmul sends a tabled shape to Strassen (bit-identical to a
+direct call) and anything else to the native GEMM."""
+
+import json
+
+import pytest
+import torch
+
+import strassen_tpu_amd as smx
+from strassen_tpu_amd import tuning
+
+pytestmark = pytest.mark.gpu
+
+
+def test_small_tile_screen():
+    records = []
+    chosen = tuning.screen_tiles(1024, 1024, 2048, swiglu=True, warmups=1, runs=2, emit=records.append,
+                                 bm_candidates=(512, 1024), bn_candidates=(512, 1024), bk_candidates=(256, 512))
+    kept = [tuple(e["tile"]) for e in records[0]["candidates"]]
+    assert len(kept) == 8
+    tunes = [r for r in records if r["kind"] == "tune" and r["arm"] != "hipblaslt"]
+    assert len(tunes) == 2 * len(kept) and all(len(r["samples_ms"]) == 2 for r in tunes)
+    for arm in ("strassen", "cubic"):
+        assert tuple(chosen[arm]["tile"]) in kept
+        best = min((r for r in tunes if r["arm"] == arm), key=lambda r: r["mean_ms"])
+        assert chosen[arm]["mean_ms"] == best["mean_ms"]
+    assert records[-1] == {"kind": "verdict", "passes": True, "scope": "tile screening; winners feed the harnesses"}
+
+
+def test_tuned_matmul_dispatch(tmp_path, monkeypatch):
+    path = tmp_path / "table.json"
+    path.write_text(json.dumps({"shapes": {"512,1024,512": {"tile": [256, 256, 512], "strassen_ms": 1.0,
+                                                           "native_ms": 2.0}}}))
+    monkeypatch.setenv("SMX_TUNED_TABLE", str(path))
+    g = torch.Generator(device="cuda").manual_seed(1)
+    a = torch.randn(512, 1024, device="cuda", generator=g).to(torch.bfloat16)
+    b = (torch.randn(512, 1024, device="cuda", generator=g) * 0.02).to(torch.bfloat16).t()
+    got = tuning.tuned_matmul(a, b)
+    assert torch.equal(got, smx.strassen_matmul(a, b, bm=256, bn=256, bk=512))
+    c = (torch.randn(1024, 1024, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    assert torch.equal(tuning.tuned_matmul(a, c), smx.native_matmul(a, c))
+
+
+def test_dispatch_measurement_records():
+    records = []
+    table = tuning.measure_dispatch([(512, 1024, 1024), (500, 1024, 1024)], tile=(256, 256, 512), runs=2,
+                                    emit=records.append)
+    assert records[0]["kind"] == "dispatch" and len(records[0]["samples_ms"]["native"]) == 2
+    assert records[1]["kind"] == "dispatch_skip"
+    for key, entry in table["shapes"].items():
+        assert entry["strassen_ms"] < entry["native_ms"]

@@ -162,9 +162,14 @@ def test_packed_weight_surface():
         smx.strassen_matmul(a, w, bm=256, bn=512, bk=512)
     with pytest.raises(ValueError, match="packed as"):
         smx.strassen_matmul(a, packed_weight(algo=8), bm=256, bn=512, bk=512)
-    with pytest.raises(ValueError, match="needs a packed weight"):
-        pa = smx.PackedOperand(t(1), algo=7, side="lhs", rows=256, k=512, tile_rows=256, bk=512)
+    pa = smx.PackedOperand(t(1), algo=7, side="lhs", rows=256, k=512, tile_rows=256, bk=512)
+    with pytest.raises(ValueError, match="needs a packed weight"), smx.plain_weight_kernel("compact"):
         smx.strassen_matmul(pa, t(512, 512), bm=256, bn=512, bk=512)
+    # by default a plain weight with a packed-kernel tile is packed for the call
+    with pytest.raises(ValueError, match="HIP device"):
+        smx.strassen_matmul(pa, t(512, 512), bm=256, bn=512, bk=512)
+    with pytest.raises(ValueError, match="must be 'pack' or 'compact'"), smx.plain_weight_kernel("fast"):
+        pass
     with pytest.raises(ValueError, match="HIP device"):
         smx.strassen_weight_layout(t(512, 256), 256, 512)
     with pytest.raises(ValueError, match="bf16"):
