@@ -68,17 +68,26 @@ def verify_inline_asm_kernels(asm_text):
         if not _ASM_MFMA.search(body):
             continue
         checked += 1
-        drain = body.find(_DRAIN)
-        first_mfma = body.find("v_mfma")
-        if drain < 0:
+        if _DRAIN not in body:
             raise RuntimeError(f"{name}: inline-asm MFMAs without the drain sequence")
-        # Between the first MFMA and the drain nothing may read, copy or
-        # spill registers (before the first MFMA no accumulator holds an
-        # MFMA result yet).
-        bad = _FORBIDDEN.search(body[first_mfma:drain])
-        if bad:
-            raise RuntimeError(f"{name}: '{bad.group(1)}' before the MFMA drain "
-                               "(accumulators spilled or copied); refusing to build")
+        # A kernel may hold several MFMA loops (one per wave role), each
+        # ending in its own drain. In every stretch between drains, nothing
+        # may read, copy or spill registers from the stretch's first MFMA to
+        # the drain that ends it (before an MFMA no accumulator holds an MFMA
+        # result yet); MFMAs after the last drain are refused.
+        start = 0
+        while True:
+            first_mfma = body.find("v_mfma", start)
+            if first_mfma < 0:
+                break
+            drain = body.find(_DRAIN, first_mfma)
+            if drain < 0:
+                raise RuntimeError(f"{name}: an MFMA after the last drain sequence")
+            bad = _FORBIDDEN.search(body[first_mfma:drain])
+            if bad:
+                raise RuntimeError(f"{name}: '{bad.group(1)}' before the MFMA drain "
+                                   "(accumulators spilled or copied); refusing to build")
+            start = drain + len(_DRAIN)
     if not checked:
         raise RuntimeError("no inline-asm MFMA kernels found in the device assembly")
     return checked

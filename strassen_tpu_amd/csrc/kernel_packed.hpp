@@ -223,10 +223,39 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
     auto body = [&](const Stage& cur) {
       // Slot of stage s+1, and of stage s+kSlots-1 (the one read at s-1).
       const int slot1 = slot == kSlots - 1 ? 0 : slot + 1, refill = slot == 0 ? kSlots - 1 : slot - 1;
-      dma(a_src, s + kSlots - 1, a_region + refill * L::kStage);
-      dma(b_src, s + kSlots - 1, b_region + refill * L::kStage);
+      // The stage's DMA fragments (A then B) go out two at a time between
+      // the first half's MFMA groups rather than as one burst ahead of them;
+      // all are issued before the mid-stage barrier, so its vmcnt
+      // accounting is unchanged.
+      const int stage = min(s + kSlots - 1, nstages - 1);
+      const uint8_t* const a_from = a_src + (int64_t)stage * L::kStage + lane_off;
+      const uint8_t* const b_from = b_src + (int64_t)stage * L::kStage + lane_off;
+      uint8_t* const a_to = a_region + refill * L::kStage + wave_u * kFrag;
+      uint8_t* const b_to = b_region + refill * L::kStage + wave_u * kFrag;
+      auto dma_pair = [&](int g) {
+#pragma unroll
+        for (int q = 2 * g; q < 2 * g + 2; ++q) {
+          const bool is_a = q < L::kDmaPerWave;
+          const int x = is_a ? q : q - L::kDmaPerWave;
+          __builtin_amdgcn_global_load_lds((is_a ? a_from : b_from) + x * 4 * kFrag,
+                                           (__attribute__((address_space(3))) void*)((is_a ? a_to : b_to) +
+                                                                                      4 * x * kFrag),
+                                           16, 0, 0);
+        }
+      };
       __builtin_amdgcn_sched_barrier(0);
-      half(cur.h0t, cur.h0b);
+      {
+        const Frags& t = cur.h0t;
+        const Frags& b = cur.h0b;
+        mfma4(Frags{t.a0, t.a1, t.b0, t.b1}, 0);
+        dma_pair(0);
+        mfma4(Frags{t.a0, t.a1, b.b0, b.b1}, 1);
+        dma_pair(1);
+        mfma4(Frags{b.a0, b.a1, t.b0, t.b1}, 2);
+        dma_pair(2);
+        mfma4(Frags{b.a0, b.a1, b.b0, b.b1}, 3);
+        dma_pair(3);
+      }
       __builtin_amdgcn_sched_barrier(0);
       stage_barrier<L::kPending>();
       const Stage next = load_stage(slot1);  // past the last stage: re-reads it, unused

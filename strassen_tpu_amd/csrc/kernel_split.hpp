@@ -1,0 +1,283 @@
+// Product-split Strassen kernel: the packed kernel's operands, DMA ring and
+// stage pipeline, with the seven products divided among the waves instead
+// of the output.
+//
+// The 128x128 product-space workgroup tile holds 7 products x 4 block rows
+// = 28 strips of 32x128 (one product, one 32-row block row, all four
+// 32-column blocks). Wave w owns strips 7w .. 7w+6 in (product, row) order,
+// so it accumulates 28 32x32 blocks (448 registers, as in gemm_packed) but
+// reads each A fragment once and each product's four B fragments once per
+// stage: 7 + 4 x (products touched) fragments for 28 MFMAs, against 28 for
+// 28 when every wave owns a 64x64 region of all seven products. Per stage
+// the workgroup reads 68 KB of LDS instead of 112 KB (0.61 KB per MFMA
+// instead of 1.0), while the DMA writes are unchanged.
+//
+// After the last stage the waves exchange accumulator blocks through LDS so
+// that wave (wm, wn) holds all seven products of its 64x64 region, the
+// layout gemm_packed ends with; the shared epilogue then combines and
+// stores them.
+#pragma once
+
+#include "kernel_packed.hpp"
+
+namespace smx {
+namespace split {
+
+using packed::kBlocks;
+using packed::kFrag;
+using packed::TK;
+
+// Strip plan of wave kWave.
+template <int kWave>
+struct Plan {
+  static constexpr int kFirst = 7 * kWave;
+  __device__ static constexpr int product(int j) { return (kFirst + j) / 4; }
+  __device__ static constexpr int row(int j) { return (kFirst + j) % 4; }
+  // Whether strip j starts a product (its B fragments must be read).
+  __device__ static constexpr bool opens(int j) { return j == 0 || product(j) != product(j - 1); }
+};
+
+// Accumulators of strips 0-3 live in AGPRs, strips 4-6 in VGPRs.
+__device__ __forceinline__ void drain(f32x16 (&acc)[7][4]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+  for (int j = 0; j < 7; ++j)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (j < 4)
+        asm volatile("" : "+a"(acc[j][c]));
+      else
+        asm volatile("" : "+v"(acc[j][c]));
+    }
+}
+
+struct StripFrags {
+  bf16x8 a;
+  bf16x8 b[4];
+};
+
+// One wave's main loop, accumulator exchange and epilogue. The stage ring
+// holds kNA A stages and kNB B stages (gemm_packed<7>: 2 and 3); each wave
+// moves fragments wave + 4x of every stage.
+template <int kWave, int kEpi, int kNA, int kNB>
+__device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, int nstages, int lane,
+                                         const uint8_t* a_src, const uint8_t* b_src, uint8_t* lds) {
+  using L = packed::Lay<7>;
+  using P = Plan<kWave>;
+  // The operand with the shorter prefetch distance is issued first each
+  // stage, so the barrier's vmcnt can leave the other one in flight.
+  // VMEM operations issued after the last one stage s+1 needs: with equal
+  // depths N, the 2(N-2) later stage prefetches; otherwise everything after
+  // the shorter operand's stage s+1 prefetch.
+  constexpr int kMin = kNA < kNB ? kNA : kNB;
+  constexpr int kPending = (kNA == kNB ? 2 * (kNA - 2) : 2 * kMin - 3) * L::kDmaPerWave;
+  static_assert(kMin >= 2 && (kNA + kNB) * L::kStage <= 160 * 1024, "ring depth / LDS budget");
+  uint8_t* const a_region = lds;
+  uint8_t* const b_region = lds + kNA * L::kStage;
+  const uint32_t lane_off = lane * 16;
+  const int lo = lane * 16;
+  auto load_a = [&](const uint8_t* sa, int j) {
+    return packed::ld_frag(sa + (P::product(j) * kBlocks + P::row(j)) * kFrag + lo);
+  };
+  auto load_b = [&](const uint8_t* sb, int j, bf16x8 (&b)[4]) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) b[c] = packed::ld_frag(sb + (P::product(j) * kBlocks + c) * kFrag + lo);
+  };
+
+  f32x16 acc[7][4];
+#pragma unroll
+  for (int j = 0; j < 7; ++j)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][c][r] = 0.0f;
+  auto mfma_strip = [&](int j, const bf16x8& a, const bf16x8 (&b)[4]) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (j < 4)
+        packed::mfma_agpr(acc[j][c], a, b[c]);
+      else
+        packed::mfma_vgpr(acc[j][c], a, b[c]);
+    }
+  };
+
+  // Stage s: prefetch stages s+kNA-1 (A) and s+kNB-1 (B) spread over strips
+  // 0-5, with the next strip's fragments read under the current strip's
+  // MFMAs; barrier; the next stage's strip-0 fragments read under strip 6's
+  // MFMAs. The barrier sees every read of stage s complete and every wave's
+  // DMA of stage s+1 landed (vmcnt leaves only the newer prefetches in
+  // flight).
+  int s = 0, a_slot = 0, b_slot = 0;
+  bf16x8 a_cur = load_a(a_region, 0);
+  bf16x8 b_cur[4];
+  load_b(b_region, 0, b_cur);
+  do {
+    // Slots of stage s + kN - 1 (the one read at stage s - 1) and s + 1.
+    const int a_fill = a_slot == 0 ? kNA - 1 : a_slot - 1, a_slot1 = a_slot == kNA - 1 ? 0 : a_slot + 1;
+    const int b_fill = b_slot == 0 ? kNB - 1 : b_slot - 1, b_slot1 = b_slot == kNB - 1 ? 0 : b_slot + 1;
+    // The stage's 14 DMA fragments (7 of each operand, the operand with the
+    // shorter prefetch distance first) are issued two or three at a time
+    // after each of strips 0-5, so the vector memory queue never holds a
+    // whole stage in front of the MFMAs; all are issued before the barrier,
+    // whose vmcnt accounting is unchanged.
+    constexpr bool kAFirst = kNA <= kNB;
+    const uint8_t* const a_from = a_src + (int64_t)min(s + kNA - 1, nstages - 1) * L::kStage + lane_off;
+    const uint8_t* const b_from = b_src + (int64_t)min(s + kNB - 1, nstages - 1) * L::kStage + lane_off;
+    uint8_t* const a_to = a_region + a_fill * L::kStage + kWave * kFrag;
+    uint8_t* const b_to = b_region + b_fill * L::kStage + kWave * kFrag;
+    auto dma_op = [&](int q) {
+      const bool is_a = kAFirst ? q < L::kDmaPerWave : q >= L::kDmaPerWave;
+      const int x = q < L::kDmaPerWave ? q : q - L::kDmaPerWave;
+      __builtin_amdgcn_global_load_lds((is_a ? a_from : b_from) + x * 4 * kFrag,
+                                       (__attribute__((address_space(3))) void*)((is_a ? a_to : b_to) + 4 * x * kFrag),
+                                       16, 0, 0);
+    };
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t* const sa = a_region + a_slot * L::kStage;
+    const uint8_t* const sb = b_region + b_slot * L::kStage;
+#pragma unroll
+    for (int j = 0; j < 6; ++j) {
+      const bf16x8 a_next = load_a(sa, j + 1);
+      if (P::opens(j + 1)) {
+        bf16x8 b_next_frags[4];
+        load_b(sb, j + 1, b_next_frags);
+        mfma_strip(j, a_cur, b_cur);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) b_cur[c] = b_next_frags[c];
+      } else {
+        mfma_strip(j, a_cur, b_cur);
+      }
+#pragma unroll
+      for (int q = (2 * L::kDmaPerWave * j) / 6; q < (2 * L::kDmaPerWave * (j + 1)) / 6; ++q) dma_op(q);
+      __builtin_amdgcn_sched_barrier(0);
+      a_cur = a_next;
+    }
+    packed::stage_barrier<kPending>();
+    // Stage s+1's strip 0 (past the last stage: a re-loaded copy, unused).
+    const uint8_t* const na = a_region + a_slot1 * L::kStage;
+    const uint8_t* const nb = b_region + b_slot1 * L::kStage;
+    const bf16x8 a_first = load_a(na, 0);
+    bf16x8 b_first[4];
+    load_b(nb, 0, b_first);
+    mfma_strip(6, a_cur, b_cur);
+    __builtin_amdgcn_sched_barrier(0);
+    a_cur = a_first;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) b_cur[c] = b_first[c];
+    b_slot = b_slot1;
+    a_slot = a_slot1;
+  } while (++s < nstages);
+  drain(acc);
+
+  // Every wave's DMAs (including the unread prefetches past the last stage)
+  // have landed and every wave is past its last LDS read of the ring before
+  // the exchange reuses it.
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  // Exchange, four rounds: in round t = 2i + jj every wave receives the
+  // blocks (i, jj) of its 64x64 region for all seven products, i.e. strip
+  // rows r with r % 2 == i and columns c with c % 2 == jj. Slot (dest wave,
+  // product) is one 32x32 FP32 block stored as [4 register groups][64
+  // lanes][4 floats]: source and destination share the MFMA accumulator
+  // lane layout, so a block moves register for register.
+  constexpr int kBlockBytes = 64 * 16 * 4;
+  const int wm = kWave >> 1, wn = kWave & 1;
+  f32x16 dst[7][2][2];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int i = t >> 1, jj = t & 1;
+#pragma unroll
+    for (int j = 0; j < 7; ++j) {
+      const int r = P::row(j);
+      if (r % 2 != i) continue;
+#pragma unroll
+      for (int c = jj; c < 4; c += 2) {
+        const int dest = 2 * (r / 2) + c / 2;
+        uint8_t* const slot = lds + (dest * 7 + P::product(j)) * kBlockBytes + lane * 16;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          f32x4 v = {acc[j][c][4 * g], acc[j][c][4 * g + 1], acc[j][c][4 * g + 2], acc[j][c][4 * g + 3]};
+          *reinterpret_cast<f32x4*>(slot + g * 1024) = v;
+        }
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+    for (int q = 0; q < 7; ++q) {
+      const uint8_t* const slot = lds + (kWave * 7 + q) * kBlockBytes + lane * 16;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(slot + g * 1024);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[q][i][jj][4 * g + e] = v[e];
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  }
+  epilogue<7, 2, 2, kEpi>(p, o, wm * 64, wn * 64, dst);
+}
+
+template <int kEpi, int kNA = 2, int kNB = 3>
+__global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
+  using L = packed::Lay<7>;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  int tile_m, tile_n;
+  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tile_m, tile_n);
+  const TileOrigin o = tile_origin(p, (int64_t)tile_m * packed::TM, (int64_t)tile_n * packed::TN);
+  const int nstages = (int)(p.k / (2 * TK));
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint8_t* const a_src =
+      reinterpret_cast<const uint8_t*>(p.a) + (int64_t)tile_m * nstages * L::kStage + wave * kFrag;
+  const uint8_t* const b_src =
+      reinterpret_cast<const uint8_t*>(p.b) + (int64_t)tile_n * nstages * L::kStage + wave * kFrag;
+
+  // Prologue: A stages 0 .. kNA-2 and B stages 0 .. kNB-2, issued in the
+  // loop's order (shorter distance first) so the barrier's vmcnt matches.
+  const uint32_t lane_off = lane * 16;
+  auto dma = [&](const uint8_t* src, int stage, uint8_t* slot) {
+    const uint8_t* from = src + (int64_t)min(stage, nstages - 1) * L::kStage + lane_off;
+#pragma unroll
+    for (int x = 0; x < L::kDmaPerWave; ++x)
+      __builtin_amdgcn_global_load_lds(from + x * 4 * kFrag,
+                                       (__attribute__((address_space(3))) void*)(slot + (wave + 4 * x) * kFrag), 16,
+                                       0, 0);
+  };
+  uint8_t* const b_region = lds + kNA * L::kStage;
+#pragma unroll
+  for (int st = 0; st + 1 < (kNA > kNB ? kNA : kNB); ++st) {
+    if constexpr (kNA <= kNB) {
+      if (st + 1 < kNA) dma(a_src, st, lds + st * L::kStage);
+      if (st + 1 < kNB) dma(b_src, st, b_region + st * L::kStage);
+    } else {
+      if (st + 1 < kNB) dma(b_src, st, b_region + st * L::kStage);
+      if (st + 1 < kNA) dma(a_src, st, lds + st * L::kStage);
+    }
+  }
+  // Stage 0 of both operands has landed once only the later prologue
+  // stages remain in flight.
+  constexpr int kPrologue = (kNA > kNB ? kNA - kNB : kNB - kNA) * L::kDmaPerWave +
+                            ((kNA < kNB ? kNA : kNB) - 2) * 2 * L::kDmaPerWave;
+  packed::stage_barrier<kPrologue>();
+
+  // One code path per wave (its strip plan is a compile-time constant); no
+  // accumulator is live across the branches.
+  switch (wave) {
+    case 0:
+      run_wave<0, kEpi, kNA, kNB>(p, o, nstages, lane, a_src, b_src, lds);
+      break;
+    case 1:
+      run_wave<1, kEpi, kNA, kNB>(p, o, nstages, lane, a_src, b_src, lds);
+      break;
+    case 2:
+      run_wave<2, kEpi, kNA, kNB>(p, o, nstages, lane, a_src, b_src, lds);
+      break;
+    default:
+      run_wave<3, kEpi, kNA, kNB>(p, o, nstages, lane, a_src, b_src, lds);
+      break;
+  }
+}
+
+}  // namespace split
+}  // namespace smx

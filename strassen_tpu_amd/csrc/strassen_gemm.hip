@@ -39,6 +39,7 @@
 #include "common.hpp"
 #include "kernel_v1.hpp"
 #include "kernel_packed.hpp"
+#include "kernel_split.hpp"
 
 namespace smx {
 namespace {
@@ -63,6 +64,17 @@ int set_lds(K kern, int bytes) {
 
 // Tile rows per rasterization group; SMX_GROUP_M overrides the default for
 // tuning sweeps.
+// Strassen packed kernel: the product-split kernel by default;
+// SMX_STRASSEN_KERNEL=region selects the per-region kernel (gemm_packed)
+// for comparison.
+bool split_kernel_setting() {
+  static const bool value = [] {
+    const char* env = getenv("SMX_STRASSEN_KERNEL");
+    return !(env && strcmp(env, "region") == 0);
+  }();
+  return value;
+}
+
 int group_m_setting() {
   static const int value = [] {
     const char* env = getenv("SMX_GROUP_M");
@@ -95,6 +107,12 @@ int launch_packed(Params p, hipStream_t stream) {
   p.tiles_n = (int)((p.n / 2) / packed::TN);
   p.group_m = group_m_setting();
   auto kern = packed::gemm_packed<kAlgo, kEpi>;
+  if constexpr (kAlgo == 7)
+    if (split_kernel_setting()) kern = split::gemm_split<kEpi>;
+  if constexpr (kAlgo == 7 && kEpi == SMX_EPI_SWIGLU) {
+    const char* ring = getenv("SMX_SPLIT_RING");
+    if (ring && strcmp(ring, "32") == 0) kern = split::gemm_split<kEpi, 3, 2>;
+  }
   constexpr int lds = packed::Lay<kAlgo>::kLds;
   if (int rc = set_lds(kern, lds)) return rc;
   hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n), dim3(kThreads), lds, stream, p);
