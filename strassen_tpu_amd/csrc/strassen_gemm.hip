@@ -22,12 +22,19 @@
 //   C0 = P1 + P4 - P5 + P7, C1 = P3 + P5, C2 = P2 + P4, C3 = P1 - P2 + P3 + P6.
 //
 // Kernels:
+//   split (kernel_split.hpp): the Strassen kernel for packed operands. The
+//      packed kernel's operands, LDS ring and DMA, with each wave owning
+//      seven (product, 32-row strip) pairs of the 128x128 product-space tile
+//      instead of a 64x64 region of all seven products; the accumulators are
+//      regrouped by region through LDS before the shared epilogue.
 //   packed (kernel_packed.hpp): 128x128 product-space tiles, 64x64 waves,
 //      both operands pre-packed (smx_pack_operand: the Strassen operand sums
 //      or the cubic quadrants, in MFMA fragment order) and streamed into an
-//      LDS ring by DMA. The default for both algorithms.
+//      LDS ring by DMA. The cubic's kernel; for Strassen it is the per-region
+//      design that SMX_STRASSEN_KERNEL=region selects for comparison.
 //   v1 (kernel_v1.hpp): 128x64 tiles, row-major A and B^T, both operand sums
-//      formed in registers; serves unpacked calls.
+//      formed in registers; serves unpacked calls whose tile the packed
+//      kernels cannot take, or all of them under SMX_PLAIN_WEIGHTS=compact.
 
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
@@ -109,10 +116,6 @@ int launch_packed(Params p, hipStream_t stream) {
   auto kern = packed::gemm_packed<kAlgo, kEpi>;
   if constexpr (kAlgo == 7)
     if (split_kernel_setting()) kern = split::gemm_split<kEpi>;
-  if constexpr (kAlgo == 7 && kEpi == SMX_EPI_SWIGLU) {
-    const char* ring = getenv("SMX_SPLIT_RING");
-    if (ring && strcmp(ring, "32") == 0) kern = split::gemm_split<kEpi, 3, 2>;
-  }
   constexpr int lds = packed::Lay<kAlgo>::kLds;
   if (int rc = set_lds(kern, lds)) return rc;
   hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n), dim3(kThreads), lds, stream, p);
