@@ -403,17 +403,18 @@ def main():
     _, ev = time_steps(torch, lambda: smx.pack_activation(d["y"], 7, bm, bk), args.steps, 2)
     pack_ms = statistics.mean(ev)
     traffic, traffic_note = None, None
-    measured = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemm_packed_gate_up_traffic.json")
+    measured = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gate_up_swiglu_qwen3_32b_traffic.json")
     if os.path.exists(measured):
         rec = json.load(open(measured))["strassen"]
         traffic = round(rec["traffic_bytes"])
         traffic_note = (f"HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE passes scaled by a copy-kernel "
-                        f"calibration (profiles/gemm_packed_strassen_swiglu_qwen3_32b_gate_up.md); algorithmic "
+                        f"calibration (profiles/gemm_split_strassen_swiglu_qwen3_32b_gate_up.md); algorithmic "
                         f"{rec['algorithmic_bytes']} B")
     roofline = {
         "bound": "mfma", "achieved": round(gu_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
         "frac": round(gu_tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic, "traffic_note": traffic_note,
-        "kernel": "smx::packed::gemm_packed<7, SMX_EPI_SWIGLU> (gate|up, M=8192 K=5120 N=51200, packed operands)",
+        "kernel": "smx::split::gemm_split<SMX_EPI_SWIGLU> (product-split Strassen; gate|up, M=8192 K=5120 N=51200, "
+                  "packed operands)",
         "mfma_executed_frac": round(gu_tflops * 7 / 8 / PEAK_BF16_TFLOPS, 4),
         "avg_launch_ms": round(gu_ms, 4),
         "cubic_same_site_ms": round(gu_cubic_ms, 4),

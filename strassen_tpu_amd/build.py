@@ -54,6 +54,7 @@ def compile_command(output=LIBRARY, extra=()):
 _FUNCTION = re.compile(r"^(_Z\w+):", re.M)
 _ASM_MFMA = re.compile(r";;#ASMSTART\s*\n\s*v_mfma")
 _DRAIN = "s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+_CALL = re.compile(r"^\s*s_swappc_b64.*$", re.M)
 _FORBIDDEN = re.compile(r"^\s*(scratch_\w+|buffer_store\w*|v_accvgpr_read\w*|v_accvgpr_mov\w*)\b", re.M)
 
 
@@ -68,6 +69,10 @@ def verify_inline_asm_kernels(asm_text):
         if not _ASM_MFMA.search(body):
             continue
         checked += 1
+        call = _CALL.search(body)
+        if call:
+            raise RuntimeError(f"{name}: calls a device function ({call.group(0).strip()}); the kernel's helpers "
+                               "must inline, or their results turn divergent; refusing to build")
         if _DRAIN not in body:
             raise RuntimeError(f"{name}: inline-asm MFMAs without the drain sequence")
         # A kernel may hold several MFMA loops (one per wave role), each

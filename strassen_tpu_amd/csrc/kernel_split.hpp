@@ -27,14 +27,16 @@ using packed::kBlocks;
 using packed::kFrag;
 using packed::TK;
 
-// Strip plan of wave kWave.
+// Strip plan of wave kWave. Forced inline: a call would return its value in
+// a VGPR, which the compiler must treat as divergent, and the strip schedule
+// would turn into exec-masked branches inside the main loop.
 template <int kWave>
 struct Plan {
   static constexpr int kFirst = 7 * kWave;
-  __device__ static constexpr int product(int j) { return (kFirst + j) / 4; }
-  __device__ static constexpr int row(int j) { return (kFirst + j) % 4; }
+  __device__ __forceinline__ static constexpr int product(int j) { return (kFirst + j) / 4; }
+  __device__ __forceinline__ static constexpr int row(int j) { return (kFirst + j) % 4; }
   // Whether strip j starts a product (its B fragments must be read).
-  __device__ static constexpr bool opens(int j) { return j == 0 || product(j) != product(j - 1); }
+  __device__ __forceinline__ static constexpr bool opens(int j) { return j == 0 || product(j) != product(j - 1); }
 };
 
 // Accumulators of strips 0-3 live in AGPRs, strips 4-6 in VGPRs.
