@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define SMX_VERSION 5
+#define SMX_VERSION 6
 
 /* Status codes. */
 #define SMX_OK 0
@@ -83,6 +83,16 @@ extern "C" {
 /* aux_f32 bits: element type of the small auxiliary vectors. */
 #define SMX_AUX_BIAS_F32 1  /* bias is float32 (else bf16) */
 #define SMX_AUX_SCALE_F32 2 /* rope_scale is float32 (else bf16) */
+#define SMX_AUX_RESIDUAL_F32 4 /* residual is float32 (else bf16) */
+
+/* Source element type for smx_pack_operand. */
+#define SMX_DTYPE_BF16 0
+#define SMX_DTYPE_F32 1 /* FP32 inputs: operand sums formed in float, each operand rounded once to bf16 */
+
+/* smx_norm_residual_add dtype bits (else bf16). */
+#define SMX_NRA_SCALE_F32 1
+#define SMX_NRA_RESIDUAL_F32 2
+#define SMX_NRA_OUT_F32 4
 
 typedef struct smx_gemm_desc {
   int64_t m, n, k;       /* C[m, n] = A[m, k] @ B[k, n] */
@@ -114,8 +124,8 @@ typedef struct smx_gemm_desc {
  * the operand sums in registers; or both packed by smx_pack_operand for the
  * same algo and (bm, bk) / (bn, bk), served by the packed kernel (lda / ldb
  * ignored). C: bf16 [m, n] (or [m, n/2] for SwiGLU / GeGLU), float32 with
- * SMX_FLAG_OUT_F32. residual: bf16 [m, n]
- * (ldr). bias: [n] bf16 or f32. rope_cos / rope_sin: bf16 [m, bn/2] tables
+ * SMX_FLAG_OUT_F32. residual: [m, n] (ldr), bf16 or float32
+ * (SMX_AUX_RESIDUAL_F32). bias: [n] bf16 or f32. rope_cos / rope_sin: bf16 [m, bn/2] tables
  * indexed by output row (rope_layout_tables). rope_scale: [bn] bf16 or f32
  * (rope_scale_layout). Unused pointers may be NULL.
  * Returns SMX_OK or an SMX_ERR_* code; smx_last_error() describes it.
@@ -135,10 +145,13 @@ int smx_tile_requirements(int32_t algo, int32_t epilogue, int32_t b_layout, int3
 int smx_packed_bytes(int32_t algo, int64_t rows, int64_t k, int64_t* bytes);
 
 /*
- * Packs one operand for the packed kernel. side SMX_SIDE_LHS: src is A bf16
+ * Packs one operand for the packed kernel. side SMX_SIDE_LHS: src is A
  * [rows = m, k] and tile_rows = bm; SMX_SIDE_LHS_T: src is the same A stored
- * transposed, bf16 [k, rows = m] with row stride ld >= m; SMX_SIDE_RHS: src
- * is B^T bf16 [rows = n, k] and tile_rows = bn. Strassen (algo 7) stores the seven operand sums of
+ * transposed, [k, rows = m] with row stride ld >= m; SMX_SIDE_RHS: src is
+ * B^T [rows = n, k] and tile_rows = bn. src_dtype: SMX_DTYPE_BF16, or
+ * SMX_DTYPE_F32 for FP32 inputs (operand sums formed in float, every operand
+ * rounded once to bf16: the one-pass bf16 product of the reference's FP32
+ * path at DEFAULT precision). Strassen (algo 7) stores the seven operand sums of
  * P1..P7 (A0+A3, A2+A3, A0, A3, A0+A1, A2-A0, A1-A3; B0+B3, B0, B1-B3,
  * B2-B0, B3, B0+B1, B2+B3), each rounded once to bf16, or those of the dual /
  * powers formula, after the block permutation's quadrant swaps (A uses bits 0
@@ -151,23 +164,25 @@ int smx_packed_bytes(int32_t algo, int64_t rows, int64_t k, int64_t* bytes);
  * is laid out [rows/256][k/32][nops][4][64][8] bf16: fragment (tile of 128
  * product rows, stage of 16 product k, operand, 32-row block), lane l holding
  * row l%32, depth 8*(l/32)..+8. Needs rows % tile_rows == 0, k % bk == 0,
- * tile_rows % 256 == 0, bk % 64 == 0, ld >= src_k, ld % 8 == 0 (LHS_T: ld >= m). Asynchronous on
+ * tile_rows % 256 == 0, bk % 64 == 0, ld >= src_k, rows 16-byte aligned (ld % 8 for bf16, % 4 for
+ * float32; LHS_T: ld >= m). Asynchronous on
  * stream.
  */
 int smx_pack_operand(int32_t algo, int32_t formula, int32_t block_permutation, int32_t side, int64_t rows, int64_t k,
-                     const void* src, int64_t ld, int32_t tile_rows, int32_t bk, const int32_t* panels,
-                     int64_t src_k, void* out, void* stream);
+                     const void* src, int32_t src_dtype, int64_t ld, int32_t tile_rows, int32_t bk,
+                     const int32_t* panels, int64_t src_k, void* out, void* stream);
 
 /*
  * Second pass of the norm_residual_add epilogue (strassen_pallas.py:836-866),
  * whose norm spans a whole output row: from the FP32 product x [m, n] (an
  * smx_gemm with SMX_FLAG_OUT_F32 and no epilogue) writes
- * out = bf16(x * rsqrt(mean_row(x^2) + eps) * scale[col] + residual), with
- * residual and out bf16 [m, n] and scale [n] bf16 or float32 (scale_f32).
+ * out = x * rsqrt(mean_row(x^2) + eps) * scale[col] + residual, with
+ * residual and out [m, n] and scale [n]; each bf16 or float32 by the dtypes
+ * bits (SMX_NRA_*).
  * Asynchronous on stream.
  */
 int smx_norm_residual_add(int64_t m, int64_t n, const float* x, int64_t ldx, const void* residual, int64_t ldr,
-                          const void* scale, int32_t scale_f32, float eps, void* out, int64_t ldo, void* stream);
+                          const void* scale, int32_t dtypes, float eps, void* out, int64_t ldo, void* stream);
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* smx_last_error(void);

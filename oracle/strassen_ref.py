@@ -102,7 +102,11 @@ PA_SWIGLU_BOTTOM = (6, 2)                           # ``:633-634``
 PA_RESIDUAL_FINAL = (4, 6, 5, 2, 7, 3, 1)           # ``:679-687``
 
 
-def strassen_a_operands(a_q):
+def _identity(x):
+    return x
+
+
+def strassen_a_operands(a_q, r=bf16_round):
     """The A operands of P1..P7 (``strassen_pallas.py:324-379``): A0+A3,
     A2+A3, A0, A3, A0+A1, A2-A0, A1-A3, every sum rounded once to bf16.
 
@@ -111,16 +115,18 @@ def strassen_a_operands(a_q):
     float32 holds that sum exactly or within half a float32 ulp, and float32
     precision (24 bits) >= 2*8+2, so rounding the float32 sum to bf16 is the
     correctly rounded bf16 sum.
+
+    ``r`` rounds each jnp operation's result: ``bf16_round`` for bf16 inputs
+    (compute dtype bf16), the identity for FP32 inputs (compute dtype f32,
+    the finished operand is rounded by the product, ``operand_round``).
     """
     a0, a1, a2, a3 = a_q
-    r = bf16_round
     return (r(a0 + a3), r(a2 + a3), a0, a3, r(a0 + a1), r(a2 - a0), r(a1 - a3))
 
 
-def strassen_b_operands(b_q):
+def strassen_b_operands(b_q, r=bf16_round):
     """The B operands of P1..P7: B0+B3, B0, B1-B3, B2-B0, B3, B0+B1, B2+B3."""
     b0, b1, b2, b3 = b_q
-    r = bf16_round
     return (r(b0 + b3), b0, r(b1 - b3), r(b2 - b0), b3, r(b0 + b1), r(b2 + b3))
 
 
@@ -150,28 +156,25 @@ POWERS_BASIS_UPDATES = {
 POWERS_INTERLEAVED_ORDER = (3, 2, 6, 5, 4, 7, 1)     # ``:520-528``
 
 
-def dual_a_operands(a_q):
+def dual_a_operands(a_q, r=bf16_round):
     """A operands of the dual formula Q1..Q7 (``:461-517``): A0+A3, A0,
     A2-A3, A1-A0, A3, A0+A2, A1+A3."""
     a0, a1, a2, a3 = a_q
-    r = bf16_round
     return (r(a0 + a3), a0, r(a2 - a3), r(a1 - a0), a3, r(a0 + a2), r(a1 + a3))
 
 
-def dual_b_operands(b_q):
+def dual_b_operands(b_q, r=bf16_round):
     """B operands of Q1..Q7: B0+B3, B1+B3, B0, B3, B0+B2, B1-B0, B2-B3."""
     b0, b1, b2, b3 = b_q
-    r = bf16_round
     return (r(b0 + b3), r(b1 + b3), b0, b3, r(b0 + b2), r(b1 - b0), r(b2 - b3))
 
 
-def powers_a_operands(a_q):
+def powers_a_operands(a_q, r=bf16_round):
     """A operands of R1..R7 (``:398-459``). Every jnp bf16 operation rounds
     its result to bf16 (the HLO semantics of the traced expressions);
     scaling by 1/2 and 1/4 is exact, so each two-term sum rounds once and
     each balanced four-term expression rounds its two halves and their sum."""
     a0, a1, a2, a3 = a_q
-    r = bf16_round
     h, q = np.float32(0.5), np.float32(0.25)
     return (r(a2 - a1),
             r(r(a0 - a2 * h) + r(a1 * h - a3 * q)),
@@ -182,10 +185,9 @@ def powers_a_operands(a_q):
             r(a1 + a3 * h))
 
 
-def powers_b_operands(b_q):
+def powers_b_operands(b_q, r=bf16_round):
     """B operands of R1..R7 (``:398-459``), rounded as ``powers_a_operands``."""
     b0, b1, b2, b3 = b_q
-    r = bf16_round
     h, q = np.float32(0.5), np.float32(0.25)
     return (r(b0 - b3),
             r(b0 + b1 * h),
@@ -213,17 +215,37 @@ def permuted_quadrants(quads, swap_rows, swap_cols):
     return tuple(quads[2 * (row ^ swap_rows) + (col ^ swap_cols)] for row in range(2) for col in range(2))
 
 
-def formula_operands(formula, a_q, b_q):
-    """(A operand, B operand) of products 1..7 of ``formula``."""
+def operation_round(input_dtype):
+    """Rounding of each jnp operation in the kernel: the compute dtype is the
+    input dtype (``compute_dtype=a.dtype``, ``strassen_pallas.py:1062``)."""
+    if input_dtype == "bfloat16":
+        return bf16_round
+    if input_dtype == "float32":
+        return _identity
+    raise ValueError(f"input_dtype must be 'bfloat16' or 'float32', got {input_dtype!r}")
+
+
+def operand_round(x):
+    """What the product sees of an operand: ``jnp.dot`` at DEFAULT precision
+    multiplies one bf16 pass on the TPU (``:228-232``), so a float32 operand
+    is rounded to bf16 (bf16 operands are unchanged)."""
+    return bf16_round(x)
+
+
+def formula_operands(formula, a_q, b_q, input_dtype="bfloat16"):
+    """(A operand, B operand) of products 1..7 of ``formula``, each operand
+    as the product sees it."""
+    r = operation_round(input_dtype)
     if formula == "classical":
-        return strassen_products(a_q, b_q)
+        products = strassen_products(a_q, b_q, r)
+        return {p: (operand_round(s_), operand_round(t_)) for p, (s_, t_) in products.items()}
     if formula == "dual":
-        sa, tb = dual_a_operands(a_q), dual_b_operands(b_q)
+        sa, tb = dual_a_operands(a_q, r), dual_b_operands(b_q, r)
     elif formula == "powers":
-        sa, tb = powers_a_operands(a_q), powers_b_operands(b_q)
+        sa, tb = powers_a_operands(a_q, r), powers_b_operands(b_q, r)
     else:
         raise ValueError(f"unknown formula {formula!r}")
-    return {p: (sa[p - 1], tb[p - 1]) for p in range(1, 8)}
+    return {p: (operand_round(sa[p - 1]), operand_round(tb[p - 1])) for p in range(1, 8)}
 
 
 # The eight half-size cubic products (A quadrant, B quadrant, C quadrant) in
@@ -232,10 +254,10 @@ def formula_operands(formula, a_q, b_q):
 CUBIC_PAIRS = ((0, 0, 0), (0, 1, 1), (2, 0, 2), (2, 1, 3), (1, 2, 0), (1, 3, 1), (3, 2, 2), (3, 3, 3))
 
 
-def strassen_products(a_q, b_q):
+def strassen_products(a_q, b_q, r=bf16_round):
     """The seven classical operand pairs {p: (S_p, T_p)}."""
-    sa = strassen_a_operands(a_q)
-    tb = strassen_b_operands(b_q)
+    sa = strassen_a_operands(a_q, r)
+    tb = strassen_b_operands(b_q, r)
     return {p: (sa[p - 1], tb[p - 1]) for p in range(1, 8)}
 
 
@@ -299,15 +321,19 @@ PACK_TILE = 128  # product rows per packed tile (the kernel's workgroup tile)
 PACK_STAGE = 16  # product depth per packed stage (one MFMA k step)
 
 
-def operand_planes(x, algo, side, tile_rows, bk, formula="classical", block_permutation=0):
+def operand_planes(x, algo, side, tile_rows, bk, formula="classical", block_permutation=0,
+                   input_dtype="bfloat16"):
     """The GEMM operands of every tile as (nops, R, K/2) product-space planes.
 
     ``side="lhs"``: x is A [M, K], R = M/2 product rows (row tile, local row).
     ``side="rhs"``: x is B [K, N], R = N/2 product columns (column tile,
     local column). Depth k' = (K panel, local k < bk/2). Strassen (algo 7)
     gives the seven operand sums of ``strassen_a_operands`` /
-    ``strassen_b_operands``; the cubic (algo 8) the four quadrants.
+    ``strassen_b_operands``; the cubic (algo 8) the four quadrants. Every
+    operand is as the product sees it (``operand_round``; FP32 inputs form
+    the sums in float32 first).
     """
+    r = operation_round(input_dtype)
     x = np.asarray(x, dtype=np.float32)
     sm, sk, sn = block_permutation & 1, (block_permutation >> 1) & 1, (block_permutation >> 2) & 1
     a_ops = {"classical": strassen_a_operands, "dual": dual_a_operands, "powers": powers_a_operands}[formula]
@@ -316,22 +342,23 @@ def operand_planes(x, algo, side, tile_rows, bk, formula="classical", block_perm
         steps = x.shape[1] // bk
         quads = [np.concatenate(q, axis=1)
                  for q in zip(*(_split_a(x, tile_rows, bk, s) for s in range(steps)))]
-        ops = a_ops(permuted_quadrants(quads, sm, sk)) if algo == 7 else quads
+        ops = a_ops(permuted_quadrants(quads, sm, sk), r) if algo == 7 else quads
     elif side == "rhs":
         steps = x.shape[0] // bk
         quads = [np.concatenate(q, axis=0).T
                  for q in zip(*(_split_b(x, tile_rows, bk, s) for s in range(steps)))]
-        ops = b_ops(permuted_quadrants(quads, sk, sn)) if algo == 7 else quads
+        ops = b_ops(permuted_quadrants(quads, sk, sn), r) if algo == 7 else quads
     else:
         raise ValueError("side must be 'lhs' or 'rhs'")
-    return np.stack(ops)
+    return np.stack([operand_round(o) for o in ops])
 
 
-def packed_operand(x, algo, side, tile_rows, bk, formula="classical", block_permutation=0):
+def packed_operand(x, algo, side, tile_rows, bk, formula="classical", block_permutation=0,
+                   input_dtype="bfloat16"):
     """``smx_pack_operand``'s output as a flat float32 array of bf16 values:
     ``[R/128][K/32][nops][4][64][8]``, lane l of a fragment holding product
     row l%32 of its 32-row block and depth 8*(l//32)..+8 of its stage."""
-    planes = operand_planes(x, algo, side, tile_rows, bk, formula, block_permutation)
+    planes = operand_planes(x, algo, side, tile_rows, bk, formula, block_permutation, input_dtype)
     nops, rows, depth = planes.shape
     v = planes.reshape(nops, rows // PACK_TILE, 4, 32, depth // PACK_STAGE, 2, 8)
     # (op, tile, block, row32, stage, half, e) -> (tile, stage, op, block, half, row32, e)
@@ -365,7 +392,7 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
                     rope_eps=1e-6, product_aware_swiglu=False,
                     product_aware_residual=False, output_dtype="bfloat16",
                     formula_variant="classical", block_permutation=0, norm_scale=None,
-                    norm_eps=1e-6, classical_panels=(), panel_schedule=None):
+                    norm_eps=1e-6, classical_panels=(), panel_schedule=None, input_dtype="bfloat16"):
     """``a @ b`` with one tile-local classical Strassen level.
 
     Restates ``_classical_strassen_kernel`` (``strassen_pallas.py:156-879``)
@@ -389,8 +416,12 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
       (the reference's output-as-accumulator mode ``:1054-1057`` sums the
       same values in the same order).
 
-    Inputs must hold bf16 values (use ``bf16_round`` first). Returns float32
-    arrays holding bf16 values (or raw FP32 for ``output_dtype="float32"``).
+    With ``input_dtype="bfloat16"`` the inputs must hold bf16 values (use
+    ``bf16_round`` first); with ``"float32"`` they are FP32 inputs: the
+    operand sums are formed in float32 and every operand is rounded once to
+    bf16 by the one-pass DEFAULT-precision product (``operand_round``).
+    Returns float32 arrays holding bf16 values (or raw FP32 for
+    ``output_dtype="float32"``).
     """
     a = np.asarray(a, dtype=np.float32)
     b = np.asarray(b, dtype=np.float32)
@@ -442,9 +473,10 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
         b_q = permuted_quadrants(_split_b(b, bn, bk, step), swap_k, swap_n)
         if step in exact:
             for ia, ib, q in CUBIC_PAIRS:
-                acc[output_index[q]] += np.matmul(a_q[ia], b_q[ib], dtype=np.float32)
+                acc[output_index[q]] += np.matmul(operand_round(a_q[ia]), operand_round(b_q[ib]),
+                                                  dtype=np.float32)
             continue
-        products = formula_operands(formula_variant, a_q, b_q)
+        products = formula_operands(formula_variant, a_q, b_q, input_dtype)
         last = step == nk - 1
         if last and product_aware_swiglu:
             run(products, PA_SWIGLU_TOP)
@@ -466,13 +498,14 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
 
 
 def strassen_matmul_lhs_transposed(a_t, b, *, bm, bn, bk, interleave_products=False,
-                                   output_dtype="bfloat16"):
+                                   output_dtype="bfloat16", input_dtype="bfloat16"):
     """``a_t.T @ b`` (``strassen_pallas.py:1224-1312``): the kernel transposes
     each resident ``(bk, bm)`` tile of ``a_t`` and runs the ordinary classical
     Strassen body on it (``:1273-1289``), so the result is ``strassen_matmul``
     of the transposed matrix."""
     return strassen_matmul(np.asarray(a_t, dtype=np.float32).T, b, bm=bm, bn=bn, bk=bk,
-                           interleave_products=interleave_products, output_dtype=output_dtype)
+                           interleave_products=interleave_products, output_dtype=output_dtype,
+                           input_dtype=input_dtype)
 
 
 def cubic_blocked_matmul(a, b, *, bm, bn, bk, epilogue=None, residual=None,
@@ -480,6 +513,10 @@ def cubic_blocked_matmul(a, b, *, bm, bn, bk, epilogue=None, residual=None,
                          rope_scale=None, rope_head_dim=128, rope_eps=1e-6,
                          output_dtype="bfloat16", norm_scale=None, norm_eps=1e-6):
     """The matched cubic control: eight half-size products per K panel.
+
+    FP32 inputs (float32 values that are not bf16) take the same one-pass
+    bf16 product as Strassen: each quadrant is rounded to bf16 at the
+    product (``operand_round``; a no-op on bf16 values).
 
     ``_cubic_blocked_kernel`` (``experiments/qwen3/benchmark_cubic_control.py
     :76-113``): same quadrant split and four FP32 accumulators as Strassen,
@@ -496,7 +533,7 @@ def cubic_blocked_matmul(a, b, *, bm, bn, bk, epilogue=None, residual=None,
         aq = _split_a(a, bm, bk, step)
         bq = _split_b(b, bn, bk, step)
         for ia, ib, q in CUBIC_PAIRS:
-            acc[q] += np.matmul(aq[ia], bq[ib], dtype=np.float32)
+            acc[q] += np.matmul(operand_round(aq[ia]), operand_round(bq[ib]), dtype=np.float32)
     return _epilogue(acc, m, n, bm, bn, epilogue=epilogue, residual=residual,
                      bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
                      rope_scale=rope_scale, rope_head_dim=rope_head_dim,

@@ -44,6 +44,12 @@ SMX_FLAG_OUT_F32 = 1
 SMX_FORMULA = {"classical": 0, "dual": 1, "powers": 2}
 SMX_AUX_BIAS_F32 = 1
 SMX_AUX_SCALE_F32 = 2
+SMX_AUX_RESIDUAL_F32 = 4
+SMX_DTYPE_BF16 = 0
+SMX_DTYPE_F32 = 1
+SMX_NRA_SCALE_F32 = 1
+SMX_NRA_RESIDUAL_F32 = 2
+SMX_NRA_OUT_F32 = 4
 
 EXPORTS = ("smx_gemm", "smx_tile_requirements", "smx_packed_bytes", "smx_pack_operand", "smx_norm_residual_add",
            "smx_last_error", "smx_version")
@@ -89,7 +95,7 @@ def load():
     i64, i32 = ctypes.c_int64, ctypes.c_int32
     lib.smx_packed_bytes.argtypes = [i32, i64, i64, ctypes.POINTER(i64)]
     lib.smx_packed_bytes.restype = ctypes.c_int
-    lib.smx_pack_operand.argtypes = [i32, i32, i32, i32, i64, i64, vp, i64, i32, i32, vp, i64, vp, vp]
+    lib.smx_pack_operand.argtypes = [i32, i32, i32, i32, i64, i64, vp, i32, i64, i32, i32, vp, i64, vp, vp]
     lib.smx_pack_operand.restype = ctypes.c_int
     f32 = ctypes.c_float
     lib.smx_norm_residual_add.argtypes = [i64, i64, vp, i64, vp, i64, vp, i32, f32, vp, i64, vp]

@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/strassen_mi355x.h"
 
 namespace smx {
@@ -115,81 +117,108 @@ __device__ __forceinline__ u32x4 map8(const F8& x0, const F8& x1, const F8& x2, 
 // (:324-379), 1 dual (:461-517), 2 powers (:381-459).
 constexpr int kFormulaClassical = 0, kFormulaDual = 1, kFormulaPowers = 2;
 
-// Operands of products 1..7 of a formula from the four (permuted) quadrants,
-// A side (kSide 0) or B side (kSide 1). Each jnp bf16 operation of the
-// reference rounds to bf16; scaling by 1/2 and 1/4 is exact, so two-term
-// sums round once and the powers formula's balanced four-term expressions
-// round both halves and their sum.
-template <int kSide>
-__device__ __forceinline__ void formula_ops(int formula, const u32x4 (&q)[4], u32x4 (&ops)[7]) {
+// Eight floats rounded to bf16 and packed (round to nearest even).
+__device__ __forceinline__ u32x4 pack8(const F8& x) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = pack_bf16(x.v[2 * i], x.v[2 * i + 1]);
+  return r;
+}
+
+// Operands of products 1..7 of a formula from the four (permuted) quadrants
+// in float, A side (kSide 0) or B side (kSide 1), each rounded once to bf16.
+// kBf16Compute: the reference's compute dtype is bf16 (bf16 inputs), so each
+// jnp bf16 operation rounds: two-term sums round once (as they also do in
+// float), and the powers formula's balanced four-term expressions round
+// both halves and their sum. With FP32 inputs the compute dtype is float and
+// only the finished operand is rounded, by the one-pass bf16 MXU product at
+// DEFAULT precision. Raw quadrants (A0, B3, ...) are rounded to bf16, which
+// leaves bf16 inputs unchanged; scaling by 1/2 and 1/4 is exact.
+template <int kSide, bool kBf16Compute>
+__device__ __forceinline__ void formula_ops_f(int formula, const F8 (&x)[4], u32x4 (&ops)[7]) {
+  const F8 &x0 = x[0], &x1 = x[1], &x2 = x[2], &x3 = x[3];
+  auto rnd = [](float v) { return kBf16Compute ? round_bf16(v) : v; };
   if (formula == kFormulaClassical) {
-    if constexpr (kSide == 0)
-      strassen_a_ops(q, ops);
-    else
-      strassen_b_ops(q, ops);
+    if constexpr (kSide == 0) {  // A0+A3, A2+A3, A0, A3, A0+A1, A2-A0, A1-A3 (:324-379)
+      ops[0] = sum8<false>(x0, x3);
+      ops[1] = sum8<false>(x2, x3);
+      ops[2] = pack8(x0);
+      ops[3] = pack8(x3);
+      ops[4] = sum8<false>(x0, x1);
+      ops[5] = sum8<true>(x2, x0);
+      ops[6] = sum8<true>(x1, x3);
+    } else {  // B0+B3, B0, B1-B3, B2-B0, B3, B0+B1, B2+B3
+      ops[0] = sum8<false>(x0, x3);
+      ops[1] = pack8(x0);
+      ops[2] = sum8<true>(x1, x3);
+      ops[3] = sum8<true>(x2, x0);
+      ops[4] = pack8(x3);
+      ops[5] = sum8<false>(x0, x1);
+      ops[6] = sum8<false>(x2, x3);
+    }
     return;
   }
-  const F8 x0 = unpack8(q[0]), x1 = unpack8(q[1]), x2 = unpack8(q[2]), x3 = unpack8(q[3]);
   if (formula == kFormulaDual) {
-    if constexpr (kSide == 0) {  // A0+A3, A0, A2-A3, A1-A0, A3, A0+A2, A1+A3
+    if constexpr (kSide == 0) {  // A0+A3, A0, A2-A3, A1-A0, A3, A0+A2, A1+A3 (:461-517)
       ops[0] = sum8<false>(x0, x3);
-      ops[1] = q[0];
+      ops[1] = pack8(x0);
       ops[2] = sum8<true>(x2, x3);
       ops[3] = sum8<true>(x1, x0);
-      ops[4] = q[3];
+      ops[4] = pack8(x3);
       ops[5] = sum8<false>(x0, x2);
       ops[6] = sum8<false>(x1, x3);
     } else {  // B0+B3, B1+B3, B0, B3, B0+B2, B1-B0, B2-B3
       ops[0] = sum8<false>(x0, x3);
       ops[1] = sum8<false>(x1, x3);
-      ops[2] = q[0];
-      ops[3] = q[3];
+      ops[2] = pack8(x0);
+      ops[3] = pack8(x3);
       ops[4] = sum8<false>(x0, x2);
       ops[5] = sum8<true>(x1, x0);
       ops[6] = sum8<true>(x2, x3);
     }
     return;
   }
-  // Powers (Dumas--Pernet--Sedoglavic).
+  // Powers (Dumas--Pernet--Sedoglavic, :381-459).
   if constexpr (kSide == 0) {
     ops[0] = map8(x0, x1, x2, x3, [](float a0, float a1, float a2, float a3) { return a2 - a1; });
-    ops[1] = map8(x0, x1, x2, x3, [](float a0, float a1, float a2, float a3) {
-      return round_bf16(a0 - a2 * 0.5f) + round_bf16(a1 * 0.5f - a3 * 0.25f);
+    ops[1] = map8(x0, x1, x2, x3, [&](float a0, float a1, float a2, float a3) {
+      return rnd(a0 - a2 * 0.5f) + rnd(a1 * 0.5f - a3 * 0.25f);
     });
     ops[2] = map8(x0, x1, x2, x3, [](float a0, float a1, float a2, float a3) { return a2 - a3 * 0.5f; });
     ops[3] = map8(x0, x1, x2, x3, [](float a0, float a1, float a2, float a3) { return a1 - a3 * 0.5f; });
     ops[4] = map8(x0, x1, x2, x3, [](float a0, float a1, float a2, float a3) { return a2 + a3 * 0.5f; });
-    ops[5] = map8(x0, x1, x2, x3, [](float a0, float a1, float a2, float a3) {
-      return round_bf16(a0 - a1 * 0.5f) + round_bf16(a2 * 0.5f - a3 * 0.25f);
+    ops[5] = map8(x0, x1, x2, x3, [&](float a0, float a1, float a2, float a3) {
+      return rnd(a0 - a1 * 0.5f) + rnd(a2 * 0.5f - a3 * 0.25f);
     });
     ops[6] = map8(x0, x1, x2, x3, [](float a0, float a1, float a2, float a3) { return a1 + a3 * 0.5f; });
   } else {
     ops[0] = map8(x0, x1, x2, x3, [](float b0, float b1, float b2, float b3) { return b0 - b3; });
     ops[1] = map8(x0, x1, x2, x3, [](float b0, float b1, float b2, float b3) { return b0 + b1 * 0.5f; });
     ops[2] = map8(x0, x1, x2, x3, [](float b0, float b1, float b2, float b3) { return b1 * 0.5f - b3; });
-    ops[3] = map8(x0, x1, x2, x3, [](float b0, float b1, float b2, float b3) {
-      return round_bf16(b0 * 0.5f - b2) + round_bf16(b1 * 0.25f - b3 * 0.5f);
+    ops[3] = map8(x0, x1, x2, x3, [&](float b0, float b1, float b2, float b3) {
+      return rnd(b0 * 0.5f - b2) + rnd(b1 * 0.25f - b3 * 0.5f);
     });
     ops[4] = map8(x0, x1, x2, x3, [](float b0, float b1, float b2, float b3) { return b1 * 0.5f + b3; });
     ops[5] = map8(x0, x1, x2, x3, [](float b0, float b1, float b2, float b3) { return b0 - b1 * 0.5f; });
-    ops[6] = map8(x0, x1, x2, x3, [](float b0, float b1, float b2, float b3) {
-      return round_bf16(b0 * 0.5f + b2) - round_bf16(b1 * 0.25f + b3 * 0.5f);
+    ops[6] = map8(x0, x1, x2, x3, [&](float b0, float b1, float b2, float b3) {
+      return rnd(b0 * 0.5f + b2) - rnd(b1 * 0.25f + b3 * 0.5f);
     });
   }
 }
 
 // Block permutation (strassen_pallas.py:205-226): quadrant (row, col) takes
 // the original quadrant (row ^ swap_rows, col ^ swap_cols).
-__device__ __forceinline__ void permute_quadrants(u32x4 (&q)[4], int swap_rows, int swap_cols) {
+template <class T>
+__device__ __forceinline__ void permute_quadrants(T (&q)[4], int swap_rows, int swap_cols) {
   if (swap_rows) {
-    const u32x4 t0 = q[0], t1 = q[1];
+    const T t0 = q[0], t1 = q[1];
     q[0] = q[2];
     q[1] = q[3];
     q[2] = t0;
     q[3] = t1;
   }
   if (swap_cols) {
-    const u32x4 t0 = q[0], t2 = q[2];
+    const T t0 = q[0], t2 = q[2];
     q[0] = q[1];
     q[2] = q[3];
     q[1] = t0;
@@ -205,15 +234,15 @@ struct Params {
   const uint16_t* a;
   const uint16_t* b;  // B^T [N, K] (plain) or the pre-summed operands [N/2*7, K/2]
   void* c;           // bf16, or float32 when out_f32
-  const uint16_t* residual;
+  const void* residual;      // bf16, or float32 when residual_f32
   const void* bias;
-  const uint16_t* rope_cos;
+  const uint16_t* rope_cos;  // bf16 [M, bn/2]
   const uint16_t* rope_sin;
   const void* rope_scale;
   int64_t m, n, k;
   int64_t lda, ldb, ldc, ldr;
   int32_t bm, bn, bk;
-  int32_t bias_f32, scale_f32;
+  int32_t bias_f32, scale_f32, residual_f32;
   int32_t head_dim;
   float eps;
   int32_t tiles_m, tiles_n;  // product-space workgroup grid
@@ -282,6 +311,17 @@ __device__ __forceinline__ float gate_f32(float x) {
     return silu_f32(x);
 }
 
+// Input rows of an epilogue operand (residual, RoPE tables): a per-wave
+// base plus 32-bit element offsets, bf16 or float32, uniform per launch.
+struct InRow {
+  const char* base;
+  int f32;
+  __device__ __forceinline__ float get(int off) const {
+    return f32 ? reinterpret_cast<const float*>(base)[off]
+               : bf16_to_f32(reinterpret_cast<const uint16_t*>(base)[off]);
+  }
+};
+
 // Output rows: a per-wave base plus 32-bit element offsets, stored as bf16
 // or (out_f32) float32. The element type is uniform per launch.
 struct OutRow {
@@ -319,7 +359,11 @@ __device__ __forceinline__ float half_wave_sum(float x) {
 template <int kAlgo, int kMB, int kNB, int kEpi, int kNacc>
 __device__ __forceinline__ void epilogue(const Params& p, const TileOrigin& o, int row0, int col0,
                                          f32x16 (&acc)[kNacc][kMB][kNB]) {
-  const int lane = threadIdx.x & 63;
+  // The lane index passes through an empty asm here, after the main loop's
+  // drain: every per-lane epilogue address depends on it, so none can be
+  // computed ahead of the loop and held (or spilled) across it.
+  int lane = threadIdx.x & 63;
+  asm volatile("" : "+v"(lane));
   const int hm = p.bm / 2, hn = p.bn / 2;
   const int lcol = lane & 31;
   const int lrow4 = (lane >> 5) * 4;
@@ -334,7 +378,10 @@ __device__ __forceinline__ void epilogue(const Params& p, const TileOrigin& o, i
   const OutRow cw{reinterpret_cast<char*>(p.c) +
                       (row_base * p.ldc + (kGated ? ocol_base : col_base)) * (p.out_f32 ? 4 : 2),
                   p.out_f32};
-  const uint16_t* const rw = kEpi == SMX_EPI_RESIDUAL_ADD ? p.residual + row_base * p.ldr + col_base : nullptr;
+  const InRow rw{kEpi == SMX_EPI_RESIDUAL_ADD ? reinterpret_cast<const char*>(p.residual) +
+                                                  (row_base * p.ldr + col_base) * (p.residual_f32 ? 4 : 2)
+                                            : nullptr,
+                  p.residual_f32};
   const int hm_c = hm * ldc, hm_r = hm * ldr;
   // Cubic only: an FP32 partial product of the same output (the Strassen
   // panels of an exact-panel schedule) joins the quadrants before the
@@ -424,10 +471,10 @@ __device__ __forceinline__ void epilogue(const Params& p, const TileOrigin& o, i
           const int off = ri * ldc + cj;
           if constexpr (kEpi == SMX_EPI_RESIDUAL_ADD) {
             const int roff = ri * ldr + cj;
-            q0 += bf16_to_f32(rw[roff]);
-            q1 += bf16_to_f32(rw[roff + hn]);
-            q2 += bf16_to_f32(rw[roff + hm_r]);
-            q3 += bf16_to_f32(rw[roff + hm_r + hn]);
+            q0 += rw.get(roff);
+            q1 += rw.get(roff + hn);
+            q2 += rw.get(roff + hm_r);
+            q3 += rw.get(roff + hm_r + hn);
           } else if constexpr (kEpi == SMX_EPI_BIAS_ADD) {
             q0 += bl;
             q1 += br;

@@ -347,11 +347,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
 // 32-row product block over kPackStages stages: each lane loads 16 bytes of
 // each quadrant per stage and stores nops 16-byte chunks, so the stores of
 // a wave are whole 1 KB fragments.
-template <int kAlgo, int kSide>
-__global__ __launch_bounds__(256) void pack_operand(const uint16_t* __restrict__ src, int64_t ld, int64_t rows,
+template <int kAlgo, int kSide, bool kF32>
+__global__ __launch_bounds__(256) void pack_operand(const void* __restrict__ src_v, int64_t ld, int64_t rows,
                                                     int64_t k, int32_t tile_rows, int32_t bk, int32_t formula,
                                                     int32_t perm, const int32_t* __restrict__ panels,
                                                     int32_t src_panels, uint8_t* __restrict__ out) {
+  // Source elements: bf16, or float (FP32 inputs: the operand sums are
+  // formed in float and each operand is rounded once to bf16).
+  using Elem = typename std::conditional<kF32, float, uint16_t>::type;
+  const Elem* const src = reinterpret_cast<const Elem*>(src_v);
   constexpr int nops = nops_of(kAlgo);
   const int lane = threadIdx.x & 63;
   const int64_t gwave = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
@@ -363,18 +367,39 @@ __global__ __launch_bounds__(256) void pack_operand(const uint16_t* __restrict__
   const int hr = tile_rows / 2, hk = bk / 2;
   const int64_t r = rblock * 32 + (lane & 31);
   const int64_t row_first = (r / hr) * tile_rows + r % hr, row_second = row_first + hr;
-  const uint16_t* const first = src + row_first * ld;
-  const uint16_t* const second = first + (int64_t)hr * ld;
+  const Elem* const first = src + row_first * ld;
+  const Elem* const second = first + (int64_t)hr * ld;
+  // Eight consecutive elements (columns col0 .. col0+7) of a row-major row.
+  auto load_row = [&](const Elem* row, int64_t col0) {
+    F8 f;
+    if constexpr (kF32) {
+      const f32x4 v0 = *reinterpret_cast<const f32x4*>(row + col0);
+      const f32x4 v1 = *reinterpret_cast<const f32x4*>(row + col0 + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f.v[e] = v0[e];
+        f.v[4 + e] = v1[e];
+      }
+    } else {
+      f = unpack8(*reinterpret_cast<const u32x4*>(row + col0));
+    }
+    return f;
+  };
   // kSide 2: A stored transposed, [k, rows] with row stride ld; element
   // (row, col) of A is src[col * ld + row]. Eight consecutive k of one row
   // are gathered from eight source rows (lanes cover consecutive rows, so
-  // each load instruction reads 64 contiguous bytes of one source row).
+  // each load instruction reads 64 contiguous bytes of one source row, 128
+  // for float).
   auto gather = [&](int64_t row, int64_t col0) {
-    u32x4 v;
+    F8 f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      v[e] = (uint32_t)src[(col0 + 2 * e) * ld + row] | ((uint32_t)src[(col0 + 2 * e + 1) * ld + row] << 16);
-    return v;
+    for (int e = 0; e < 8; ++e) {
+      if constexpr (kF32)
+        f.v[e] = src[(col0 + e) * ld + row];
+      else
+        f.v[e] = bf16_to_f32(src[(col0 + e) * ld + row]);
+    }
+    return f;
   };
   const int half = lane >> 5;
   uint8_t* const dst_tile = out + frag_offset(rblock / 4, 0, nstages, 0, nops, (int)(rblock % 4)) + lane * 16;
@@ -385,40 +410,40 @@ __global__ __launch_bounds__(256) void pack_operand(const uint16_t* __restrict__
     const int64_t kp = st * TK + half * 8;
     const int64_t panel = kp / hk;
     // Map entries are clamped to the source, so a bad map cannot read out of bounds.
-    const int64_t src = panels ? min(max(panels[panel], 0), src_panels - 1) : panel;
-    const int64_t lo = src * bk + kp % hk, hi = lo + hk;
-    u32x4 q[4];
+    const int64_t src_panel = panels ? min(max(panels[panel], 0), src_panels - 1) : panel;
+    const int64_t lo = src_panel * bk + kp % hk, hi = lo + hk;
+    F8 x[4];
     if constexpr (kSide == 2) {
-      q[0] = gather(row_first, lo);
-      q[1] = gather(row_first, hi);
-      q[2] = gather(row_second, lo);
-      q[3] = gather(row_second, hi);
+      x[0] = gather(row_first, lo);
+      x[1] = gather(row_first, hi);
+      x[2] = gather(row_second, lo);
+      x[3] = gather(row_second, hi);
     } else if constexpr (kSide == 0) {
-      q[0] = *reinterpret_cast<const u32x4*>(first + lo);
-      q[1] = *reinterpret_cast<const u32x4*>(first + hi);
-      q[2] = *reinterpret_cast<const u32x4*>(second + lo);
-      q[3] = *reinterpret_cast<const u32x4*>(second + hi);
+      x[0] = load_row(first, lo);
+      x[1] = load_row(first, hi);
+      x[2] = load_row(second, lo);
+      x[3] = load_row(second, hi);
     } else {
-      q[0] = *reinterpret_cast<const u32x4*>(first + lo);
-      q[1] = *reinterpret_cast<const u32x4*>(second + lo);
-      q[2] = *reinterpret_cast<const u32x4*>(first + hi);
-      q[3] = *reinterpret_cast<const u32x4*>(second + hi);
+      x[0] = load_row(first, lo);
+      x[1] = load_row(second, lo);
+      x[2] = load_row(first, hi);
+      x[3] = load_row(second, hi);
     }
     uint8_t* const dst = dst_tile + st * (int64_t)(nops * kBlocks * kFrag);
     if constexpr (kAlgo == 7) {
       u32x4 ops[7];
       if constexpr (kSide != 1) {
-        permute_quadrants(q, perm & 1, (perm >> 1) & 1);  // A: (rows, K halves)
-        formula_ops<0>(formula, q, ops);
+        permute_quadrants(x, perm & 1, (perm >> 1) & 1);  // A: (rows, K halves)
+        formula_ops_f<0, !kF32>(formula, x, ops);
       } else {
-        permute_quadrants(q, (perm >> 1) & 1, (perm >> 2) & 1);  // B: (K halves, columns)
-        formula_ops<1>(formula, q, ops);
+        permute_quadrants(x, (perm >> 1) & 1, (perm >> 2) & 1);  // B: (K halves, columns)
+        formula_ops_f<1, !kF32>(formula, x, ops);
       }
 #pragma unroll
       for (int op = 0; op < 7; ++op) *reinterpret_cast<u32x4*>(dst + op * kBlocks * kFrag) = ops[op];
     } else {
 #pragma unroll
-      for (int op = 0; op < 4; ++op) *reinterpret_cast<u32x4*>(dst + op * kBlocks * kFrag) = q[op];
+      for (int op = 0; op < 4; ++op) *reinterpret_cast<u32x4*>(dst + op * kBlocks * kFrag) = pack8(x[op]);
     }
   }
 }

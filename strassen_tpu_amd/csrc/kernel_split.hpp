@@ -123,14 +123,22 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
     // whole stage in front of the MFMAs; all are issued before the barrier,
     // whose vmcnt accounting is unchanged.
     constexpr bool kAFirst = kNA <= kNB;
-    const uint8_t* const a_from = a_src + (int64_t)min(s + kNA - 1, nstages - 1) * L::kStage + lane_off;
-    const uint8_t* const b_from = b_src + (int64_t)min(s + kNB - 1, nstages - 1) * L::kStage + lane_off;
+    // The lane offset is re-derived opaquely each stage: otherwise the
+    // compiler hoists (operand base + lane offset) out of the loop as two
+    // 64-bit per-lane addresses held across it, where the VGPRs next to the
+    // accumulators cannot afford them; this way the loads take a uniform
+    // base plus a 32-bit lane offset.
+    uint32_t dma_lane = lane_off;
+    asm volatile("" : "+v"(dma_lane));
+    const uint8_t* const a_from = a_src + (int64_t)min(s + kNA - 1, nstages - 1) * L::kStage;
+    const uint8_t* const b_from = b_src + (int64_t)min(s + kNB - 1, nstages - 1) * L::kStage;
     uint8_t* const a_to = a_region + a_fill * L::kStage + kWave * kFrag;
     uint8_t* const b_to = b_region + b_fill * L::kStage + kWave * kFrag;
     auto dma_op = [&](int q) {
       const bool is_a = kAFirst ? q < L::kDmaPerWave : q >= L::kDmaPerWave;
       const int x = q < L::kDmaPerWave ? q : q - L::kDmaPerWave;
-      __builtin_amdgcn_global_load_lds((is_a ? a_from : b_from) + x * 4 * kFrag,
+      // uniform base + fragment offset, then the lane's 32-bit offset
+      __builtin_amdgcn_global_load_lds((is_a ? a_from : b_from) + x * 4 * kFrag + dma_lane,
                                        (__attribute__((address_space(3))) void*)((is_a ? a_to : b_to) + 4 * x * kFrag),
                                        16, 0, 0);
     };
@@ -227,6 +235,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
   const int lane = tid & 63;
   int tile_m, tile_n;
   tile_of(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tile_m, tile_n);
+  // The tile indices are uniform, but the integer divisions that produce
+  // them run on VALU; readfirstlane moves them (and every operand address
+  // derived from them) to SGPRs, which keeps VGPRs for the accumulators.
+  tile_m = __builtin_amdgcn_readfirstlane(tile_m);
+  tile_n = __builtin_amdgcn_readfirstlane(tile_n);
   const TileOrigin o = tile_origin(p, (int64_t)tile_m * packed::TM, (int64_t)tile_n * packed::TN);
   const int nstages = (int)(p.k / (2 * TK));
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);

@@ -173,15 +173,19 @@ int check_variant(int32_t algo, int32_t formula, int32_t perm) {
 }
 
 template <int kAlgo, int kSide>
-int launch_pack(const uint16_t* src, int64_t ld, int64_t rows, int64_t k, int32_t tile_rows, int32_t bk,
+int launch_pack(const void* src, bool src_f32, int64_t ld, int64_t rows, int64_t k, int32_t tile_rows, int32_t bk,
                 int32_t formula, int32_t perm, const int32_t* panels, int32_t src_panels, uint8_t* out,
                 hipStream_t stream) {
   const int64_t nstages = k / (2 * packed::TK);
   const int64_t waves = (rows / 64) * ((nstages + packed::kPackStages - 1) / packed::kPackStages);
   const int64_t blocks = (waves + 3) / 4;
   if (blocks >= ((int64_t)1 << 31)) return fail(SMX_ERR_UNSUPPORTED, "operand too large to pack");
-  hipLaunchKernelGGL((packed::pack_operand<kAlgo, kSide>), dim3((unsigned)blocks), dim3(256), 0, stream, src, ld, rows,
-                     k, tile_rows, bk, formula, perm, panels, src_panels, out);
+  if (src_f32)
+    hipLaunchKernelGGL((packed::pack_operand<kAlgo, kSide, true>), dim3((unsigned)blocks), dim3(256), 0, stream, src,
+                       ld, rows, k, tile_rows, bk, formula, perm, panels, src_panels, out);
+  else
+    hipLaunchKernelGGL((packed::pack_operand<kAlgo, kSide, false>), dim3((unsigned)blocks), dim3(256), 0, stream, src,
+                       ld, rows, k, tile_rows, bk, formula, perm, panels, src_panels, out);
   return check_launch();
 }
 
@@ -190,9 +194,9 @@ int launch_pack(const uint16_t* src, int64_t ld, int64_t rows, int64_t k, int32_
 // out = bf16(x * rsqrt(mean(x^2) + eps) * scale + residual). The row's sum of
 // squares is accumulated in FP32 per thread, then across the workgroup.
 __global__ __launch_bounds__(256) void norm_residual_rows(const float* __restrict__ x, int64_t ldx,
-                                                          const uint16_t* __restrict__ residual, int64_t ldr,
-                                                          const void* __restrict__ scale, int32_t scale_f32,
-                                                          float eps, int64_t n, uint16_t* __restrict__ out,
+                                                          const void* __restrict__ residual, int64_t ldr,
+                                                          const void* __restrict__ scale, int32_t dtypes,
+                                                          float eps, int64_t n, void* __restrict__ out,
                                                           int64_t ldo) {
   __shared__ float partial[4];
   const int64_t row = blockIdx.x;
@@ -205,10 +209,14 @@ __global__ __launch_bounds__(256) void norm_residual_rows(const float* __restric
   __syncthreads();
   const float total = (partial[0] + partial[1]) + (partial[2] + partial[3]);
   const float recip = 1.0f / sqrtf(total / (float)n + eps);
-  const uint16_t* rr = residual + row * ldr;
-  uint16_t* orow = out + row * ldo;
-  for (int64_t c = threadIdx.x; c < n; c += blockDim.x)
-    orow[c] = f32_to_bf16(xr[c] * recip * load_vec(scale, scale_f32, c) + bf16_to_f32(rr[c]));
+  const int scale_f32 = dtypes & SMX_NRA_SCALE_F32, residual_f32 = dtypes & SMX_NRA_RESIDUAL_F32;
+  for (int64_t c = threadIdx.x; c < n; c += blockDim.x) {
+    const float v = xr[c] * recip * load_vec(scale, scale_f32, c) + load_vec(residual, residual_f32, row * ldr + c);
+    if (dtypes & SMX_NRA_OUT_F32)
+      reinterpret_cast<float*>(out)[row * ldo + c] = v;
+    else
+      reinterpret_cast<uint16_t*>(out)[row * ldo + c] = f32_to_bf16(v);
+  }
 }
 
 }  // namespace
@@ -247,8 +255,8 @@ int smx_packed_bytes(int32_t algo, int64_t rows, int64_t k, int64_t* bytes) {
 }
 
 int smx_pack_operand(int32_t algo, int32_t formula, int32_t block_permutation, int32_t side, int64_t rows, int64_t k,
-                     const void* src, int64_t ld, int32_t tile_rows, int32_t bk, const int32_t* panels,
-                     int64_t src_k, void* out, void* stream) {
+                     const void* src, int32_t src_dtype, int64_t ld, int32_t tile_rows, int32_t bk,
+                     const int32_t* panels, int64_t src_k, void* out, void* stream) {
   g_error[0] = 0;
   if (algo != SMX_ALGO_STRASSEN && algo != SMX_ALGO_CUBIC) return fail(SMX_ERR_INVALID, "algo must be 7 or 8");
   if (int rc = check_variant(algo, formula, block_permutation)) return rc;
@@ -261,24 +269,28 @@ int smx_pack_operand(int32_t algo, int32_t formula, int32_t block_permutation, i
                 side == SMX_SIDE_LHS ? "bm" : "bn", 2 * packed::TM, 2 * packed::kKGranule, tile_rows, bk);
   if (!src || !out) return fail(SMX_ERR_INVALID, "null pointer");
   if (!aligned16(src) || !aligned16(out)) return fail(SMX_ERR_INVALID, "pointers must be 16-byte aligned");
+  if (src_dtype != SMX_DTYPE_BF16 && src_dtype != SMX_DTYPE_F32)
+    return fail(SMX_ERR_INVALID, "src_dtype must be SMX_DTYPE_BF16 (0) or SMX_DTYPE_F32 (1), got %d", src_dtype);
+  const bool src_f32 = src_dtype == SMX_DTYPE_F32;
   if (!panels) src_k = k;
   if (src_k <= 0 || src_k % bk || src_k / bk >= ((int64_t)1 << 31))
     return fail(SMX_ERR_INVALID, "the source K (%lld) must be a positive multiple of bk", (long long)src_k);
-  if (side == SMX_SIDE_LHS_T ? ld < rows : (ld < src_k || ld % 8))
+  // Row-major sources are read 16 bytes at a time: rows must stay 16-byte aligned.
+  if (side == SMX_SIDE_LHS_T ? ld < rows : (ld < src_k || ld % (src_f32 ? 4 : 8)))
     return fail(SMX_ERR_INVALID, side == SMX_SIDE_LHS_T ? "ld must be >= rows for a transposed A"
-                                                        : "ld must be >= K and a multiple of 8");
-  const uint16_t* s16 = (const uint16_t*)src;
+                                                        : "ld must be >= K and a multiple of 16 bytes");
+  const void* s16 = src;
   uint8_t* o8 = (uint8_t*)out;
   hipStream_t st = (hipStream_t)stream;
   const int32_t sp = (int32_t)(src_k / bk);
   if (algo == SMX_ALGO_STRASSEN) {
-    if (side == SMX_SIDE_LHS) return launch_pack<7, 0>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
-    if (side == SMX_SIDE_RHS) return launch_pack<7, 1>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
-    return launch_pack<7, 2>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
+    if (side == SMX_SIDE_LHS) return launch_pack<7, 0>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
+    if (side == SMX_SIDE_RHS) return launch_pack<7, 1>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
+    return launch_pack<7, 2>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
   }
-  if (side == SMX_SIDE_LHS) return launch_pack<8, 0>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
-  if (side == SMX_SIDE_RHS) return launch_pack<8, 1>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
-  return launch_pack<8, 2>(s16, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
+  if (side == SMX_SIDE_LHS) return launch_pack<8, 0>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
+  if (side == SMX_SIDE_RHS) return launch_pack<8, 1>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
+  return launch_pack<8, 2>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
 }
 
 int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, const void* residual, const void* bias,
@@ -352,6 +364,7 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
   p.eps = d->rope_eps;
   p.bias_f32 = d->aux_f32 & SMX_AUX_BIAS_F32 ? 1 : 0;
   p.scale_f32 = d->aux_f32 & SMX_AUX_SCALE_F32 ? 1 : 0;
+  p.residual_f32 = d->aux_f32 & SMX_AUX_RESIDUAL_F32 ? 1 : 0;
   switch (d->epilogue) {
     case SMX_EPI_NONE:
     case SMX_EPI_SWIGLU:
@@ -360,7 +373,7 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
     case SMX_EPI_RESIDUAL_ADD:
       if (!residual) return fail(SMX_ERR_INVALID, "residual_add epilogue requires residual");
       if (d->ldr < d->n) return fail(SMX_ERR_INVALID, "ldr must be >= N");
-      p.residual = (const uint16_t*)residual;
+      p.residual = residual;
       break;
     case SMX_EPI_BIAS_ADD:
       if (!bias) return fail(SMX_ERR_INVALID, "bias_add epilogue requires bias");
@@ -388,14 +401,16 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
 }
 
 int smx_norm_residual_add(int64_t m, int64_t n, const float* x, int64_t ldx, const void* residual, int64_t ldr,
-                          const void* scale, int32_t scale_f32, float eps, void* out, int64_t ldo, void* stream) {
+                          const void* scale, int32_t dtypes, float eps, void* out, int64_t ldo, void* stream) {
   g_error[0] = 0;
   if (m <= 0 || n <= 0) return fail(SMX_ERR_INVALID, "empty problem m=%lld n=%lld", (long long)m, (long long)n);
   if (!x || !residual || !scale || !out) return fail(SMX_ERR_INVALID, "null pointer");
   if (ldx < n || ldr < n || ldo < n) return fail(SMX_ERR_INVALID, "row strides must be >= n");
   if (m >= ((int64_t)1 << 31)) return fail(SMX_ERR_UNSUPPORTED, "too many rows");
+  if (dtypes & ~(SMX_NRA_SCALE_F32 | SMX_NRA_RESIDUAL_F32 | SMX_NRA_OUT_F32))
+    return fail(SMX_ERR_INVALID, "unknown dtype bits 0x%x", dtypes);
   hipLaunchKernelGGL(norm_residual_rows, dim3((unsigned)m), dim3(256), 0, (hipStream_t)stream, x, ldx,
-                     (const uint16_t*)residual, ldr, scale, scale_f32 ? 1 : 0, eps, n, (uint16_t*)out, ldo);
+                     residual, ldr, scale, dtypes, eps, n, out, ldo);
   return check_launch();
 }
 

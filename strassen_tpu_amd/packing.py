@@ -104,8 +104,10 @@ class PackedOperand:
     the same tile.
     """
 
-    def __init__(self, data, *, algo, side, rows, k, tile_rows, bk, formula="classical", block_permutation=0):
+    def __init__(self, data, *, algo, side, rows, k, tile_rows, bk, formula="classical", block_permutation=0,
+                 source_dtype=torch.bfloat16):
         self.data = data
+        self.source_dtype = source_dtype  # the packed fragments are bf16 either way
         self.algo, self.side = int(algo), side
         self.rows, self.k, self.tile_rows, self.bk = int(rows), int(k), int(tile_rows), int(bk)
         self.formula, self.block_permutation = formula, int(block_permutation)
@@ -119,7 +121,7 @@ class PackedOperand:
 
     @property
     def dtype(self):
-        return self.data.dtype
+        return self.source_dtype
 
     @property
     def device(self):
@@ -142,7 +144,8 @@ class SplitOperand(PackedOperand):
 
     def __init__(self, ordinary, exact, *, side, rows, k, tile_rows, bk, formula, block_permutation, schedule):
         super().__init__(exact.data, algo=_lib.SMX_ALGO_STRASSEN, side=side, rows=rows, k=k, tile_rows=tile_rows,
-                         bk=bk, formula=formula, block_permutation=block_permutation)
+                         bk=bk, formula=formula, block_permutation=block_permutation,
+                         source_dtype=exact.source_dtype)
         self.ordinary, self.exact, self.schedule = ordinary, exact, schedule
 
     def __repr__(self):
@@ -166,12 +169,14 @@ def _pack(src, *, algo, side, rows, k, tile_rows, bk, formula, block_permutation
     data = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=src.device)
     side_id = {"lhs": _lib.SMX_SIDE_LHS, "rhs": _lib.SMX_SIDE_RHS, "lhs_t": _lib.SMX_SIDE_LHS_T}[side]
     stream = torch.cuda.current_stream(src.device).cuda_stream
+    src_dtype = _lib.SMX_DTYPE_F32 if src.dtype == torch.float32 else _lib.SMX_DTYPE_BF16
     rc = _lib.load().smx_pack_operand(algo, _lib.SMX_FORMULA[formula], block_permutation, side_id, rows, packed_k,
-                                      _lib.ptr(src), src.stride(0), tile_rows, bk, _lib.ptr(panels), k,
+                                      _lib.ptr(src), src_dtype, src.stride(0), tile_rows, bk, _lib.ptr(panels), k,
                                       _lib.ptr(data), stream)
     _lib.check(rc)
     return PackedOperand(data, algo=algo, side="rhs" if side == "rhs" else "lhs", rows=rows, k=packed_k,
-                         tile_rows=tile_rows, bk=bk, formula=formula, block_permutation=block_permutation)
+                         tile_rows=tile_rows, bk=bk, formula=formula, block_permutation=block_permutation,
+                         source_dtype=src.dtype)
 
 
 def pack_operand(x, *, algo, side, tile_rows, bk, formula="classical", block_permutation=0, classical_panels=(),
@@ -193,8 +198,8 @@ def pack_operand(x, *, algo, side, tile_rows, bk, formula="classical", block_per
         raise ValueError(f"algo must be {_lib.SMX_ALGO_STRASSEN} or {_lib.SMX_ALGO_CUBIC}")
     if x.dim() != 2:
         raise ValueError("pack_operand expects a rank-2 matrix")
-    if x.dtype != torch.bfloat16:
-        raise ValueError("pack_operand expects bf16")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("pack_operand expects bf16 or float32")
     if x.device.type != "cuda":
         raise ValueError("pack_operand runs on the HIP device")
     if side == "lhs_t":
@@ -205,7 +210,7 @@ def pack_operand(x, *, algo, side, tile_rows, bk, formula="classical", block_per
     else:
         src = x if side == "lhs" else x.t()  # rows x K, K contiguous
         rows, k = src.shape
-        if src.stride(1) != 1 or src.stride(0) % 8 or src.data_ptr() % 16:
+        if src.stride(1) != 1 or (src.stride(0) * src.element_size()) % 16 or src.data_ptr() % 16:
             src = src.contiguous()
     if rows % tile_rows or k % bk:
         raise ValueError(f"operand [{rows}, {k}] (rows x K) does not tile by ({tile_rows}, {bk})")

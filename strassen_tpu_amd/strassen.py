@@ -3,13 +3,20 @@
 ``strassen_matmul`` keeps the keyword surface, argument meaning and error
 messages of ``strassen_pallas.strassen_matmul`` (``strassen_pallas.py:882-1221``)
 and runs the hand-written HIP kernel in ``csrc/strassen_gemm.hip`` through
-the C ABI of ``include/strassen_mi355x.h``. Tensors are torch bf16 tensors on
-the HIP device; the result is a new bf16 tensor, computed asynchronously on
-torch's current stream.
+the C ABI of ``include/strassen_mi355x.h``. Tensors are torch bf16 or
+float32 tensors on the HIP device; the result is a new tensor of the input
+dtype (or ``output_dtype``), computed asynchronously on torch's current
+stream.
 
 Differences a caller can observe, all raised as exceptions (never silent):
 
-* FP32 inputs raise ``NotImplementedError``.
+* FP32 inputs run the DEFAULT-precision product (the ``jnp.dot`` of
+  ``strassen_pallas.py:228-232`` at its default ``dot_precision``, ``:889``,
+  which makes one bf16 pass on a TPU): the packing pass forms each
+  operand sum in float and rounds it once to bf16, and every product is one
+  bf16 MFMA pass into FP32. ``dot_precision`` HIGH / HIGHEST (multi-pass
+  products) raise ``NotImplementedError``. RoPE tables are read as bf16 (a
+  float32 table is rounded once on the host).
 * The exact-panel policies (``classical_panels``, ``panel_schedule``) run as
   two GEMMs: Strassen over the ordinary K panels into an FP32 partial, then
   the matched cubic over the exact panels, which adds the partial before
@@ -23,8 +30,8 @@ Differences a caller can observe, all raised as exceptions (never silent):
 * ``formula_variant`` "dual" / "powers" and ``block_permutation`` run on
   packed operands: a plain weight is packed for the call (pack it once with
   ``strassen_weight_layout(..., formula_variant=, block_permutation=)``).
-* TPU-only knobs (``dot_precision``, ``allow_input_fusion`` after its
-  validation, ``vmem_limit_bytes``) are accepted and have no effect;
+* TPU-only knobs (``dot_precision`` for bf16 inputs, ``allow_input_fusion``
+  after its validation, ``vmem_limit_bytes``) are accepted and have no effect;
   ``interpret=True`` raises ``NotImplementedError`` (there is no CPU path).
 * The kernel keeps seven persistent FP32 product accumulators and combines
   the quadrants once after the last K panel, so ``interleave_products`` and
@@ -263,11 +270,23 @@ def _validate(a, b, *, bm, bn, bk, block_permutation, formula_variant,
     return m, k, n, classical_panels, out
 
 
-def _unsupported(dtype, interpret):
+def _multi_pass(dot_precision):
+    """Whether ``dot_precision`` asks for more than the one-pass bf16 product
+    (HIGH / HIGHEST, as ``jax.lax.Precision`` members or strings)."""
+    if dot_precision is None:
+        return False
+    name = str(getattr(dot_precision, "name", dot_precision)).upper()
+    return not (name.endswith("DEFAULT") or name in ("BFLOAT16", "FASTEST"))
+
+
+def _unsupported(dtype, interpret, dot_precision=None):
     if interpret:
         raise NotImplementedError("interpret=True: the gfx950 kernel has no CPU interpreter path")
-    if dtype != torch.bfloat16:
-        raise NotImplementedError("FP32 inputs are not implemented on gfx950 (bf16 MFMA path)")
+    # FP32 inputs run as the reference's DEFAULT-precision path: operand sums
+    # in float, one bf16 pass per product. More passes are not built.
+    if dtype == torch.float32 and _multi_pass(dot_precision):
+        raise NotImplementedError("FP32 inputs at dot_precision HIGH/HIGHEST (multi-pass bf16 products) are not "
+                                  "implemented on gfx950; the FP32 path is the one-pass DEFAULT product")
 
 
 def _require_device(*tensors):
@@ -293,24 +312,32 @@ def _check_packed(x, algo, side, tile_rows, bk, formula="classical", block_permu
                          "panels")
 
 
+def _aux_tensor(x):
+    """An epilogue operand as bf16 or float32 (other dtypes become float32,
+    as the reference casts them to float32 in the kernel)."""
+    return x if x.dtype in (torch.bfloat16, torch.float32) else x.to(torch.float32)
+
+
 def _norm_residual_add(algo, a, b, *, residual, norm_scale, norm_eps, **kw):
     """``norm_residual_add`` (``strassen_pallas.py:836-866``) in two passes:
     the GEMM stores its FP32 result, then ``smx_norm_residual_add`` applies
     the row RMSNorm, the scale and the residual with one bf16 rounding (the
     row's sum of squares spans every column tile of the output)."""
+    out_dtype = kw.pop("out_dtype", torch.bfloat16)
     product = _run(algo, a, b, out_dtype=torch.float32, **kw)
     m, n = product.shape
     _require_device(residual, norm_scale)
-    residual = residual.to(torch.bfloat16)
+    residual = _aux_tensor(residual)
     if residual.stride(1) != 1:
         residual = residual.contiguous()
-    scale = norm_scale.contiguous()
-    if scale.dtype not in (torch.bfloat16, torch.float32):
-        scale = scale.to(torch.float32)
-    out = torch.empty((m, n), dtype=torch.bfloat16, device=product.device)
+    scale = _aux_tensor(norm_scale.contiguous())
+    out = torch.empty((m, n), dtype=out_dtype, device=product.device)
+    dtypes = ((_lib.SMX_NRA_SCALE_F32 if scale.dtype == torch.float32 else 0)
+              | (_lib.SMX_NRA_RESIDUAL_F32 if residual.dtype == torch.float32 else 0)
+              | (_lib.SMX_NRA_OUT_F32 if out_dtype == torch.float32 else 0))
     stream = torch.cuda.current_stream(product.device).cuda_stream
     rc = _lib.load().smx_norm_residual_add(m, n, _lib.ptr(product), product.stride(0), _lib.ptr(residual),
-                                           residual.stride(0), _lib.ptr(scale), int(scale.dtype == torch.float32),
+                                           residual.stride(0), _lib.ptr(scale), dtypes,
                                            float(norm_eps), _lib.ptr(out), out.stride(0), stream)
     _lib.check(rc)
     return out
@@ -323,7 +350,7 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
     if epilogue == "norm_residual_add":
         return _norm_residual_add(algo, a, b, residual=residual, norm_scale=norm_scale, norm_eps=norm_eps,
                                   bm=bm, bn=bn, bk=bk, formula=formula, block_permutation=block_permutation,
-                                  schedule=schedule)
+                                  schedule=schedule, out_dtype=out_dtype)
     if schedule is not None:
         return _run_split(a, b, bm=bm, bn=bn, bk=bk, schedule=schedule, formula=formula,
                           block_permutation=block_permutation, epilogue=epilogue, residual=residual, bias=bias,
@@ -339,6 +366,8 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
     packed = isinstance(b, PackedOperand) or formula != "classical" or block_permutation != 0
     if not packed and PLAIN_WEIGHTS == "pack" and _fits_packed(algo, epilogue, bm, bn, bk):
         packed = True
+    if not packed and (a.dtype == torch.float32 or b.dtype == torch.float32):
+        packed = True  # FP32 inputs reach the kernels through the packing pass only
     if isinstance(a, PackedOperand) and not packed:
         raise ValueError("a packed activation needs a packed weight (strassen_weight_layout / "
                          "cubic_weight_layout)")
@@ -383,25 +412,23 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
     desc.rope_eps = rope_eps
     aux = 0
     if residual is not None:
-        residual = residual.to(torch.bfloat16)
+        residual = _aux_tensor(residual)
         if residual.stride(1) != 1:
             residual = residual.contiguous()
+        if residual.dtype == torch.float32:
+            aux |= _lib.SMX_AUX_RESIDUAL_F32
         desc.ldr = residual.stride(0)
     if bias is not None:
-        bias = bias.contiguous()
+        bias = _aux_tensor(bias.contiguous())
         if bias.dtype == torch.float32:
             aux |= _lib.SMX_AUX_BIAS_F32
-        elif bias.dtype != torch.bfloat16:
-            bias = bias.to(torch.float32)
-            aux |= _lib.SMX_AUX_BIAS_F32
     if rope_cos is not None:
+        # The kernels read bf16 tables (rope_values builds them in bf16);
+        # float32 tables are rounded to bf16 here.
         rope_cos = rope_cos.to(torch.bfloat16).contiguous()
         rope_sin = rope_sin.to(torch.bfloat16).contiguous()
-        rope_scale = rope_scale.contiguous()
+        rope_scale = _aux_tensor(rope_scale.contiguous())
         if rope_scale.dtype == torch.float32:
-            aux |= _lib.SMX_AUX_SCALE_F32
-        elif rope_scale.dtype != torch.bfloat16:
-            rope_scale = rope_scale.to(torch.float32)
             aux |= _lib.SMX_AUX_SCALE_F32
     desc.aux_f32 = aux
     stream = torch.cuda.current_stream(a.device).cuda_stream
@@ -507,7 +534,7 @@ def strassen_matmul(
         output_dtype=output_dtype, allow_input_fusion=allow_input_fusion,
         product_aware_swiglu=product_aware_swiglu,
         product_aware_residual=product_aware_residual)
-    _unsupported(a.dtype, interpret)
+    _unsupported(a.dtype, interpret, dot_precision)
     schedule = exact_schedule(k // bk, classical_panels=classical_panels, panel_schedule=panel_schedule)
     return _run(_lib.SMX_ALGO_STRASSEN, a, b, bm=bm, bn=bn, bk=bk, epilogue=epilogue,
                 residual=residual, bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
@@ -525,7 +552,8 @@ def strassen_matmul_lhs_transposed(a, b, *, bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_B
     The packing pass reads ``a`` transposed tile by tile (no ``[M, K]`` copy is
     materialised) while forming the A operand sums; ``b`` is a ``[K, N]``
     tensor (packed on each call) or a ``strassen_weight_layout`` weight.
-    Arguments, checks and messages follow ``:1250-1267``; FP32 inputs and
+    Arguments, checks and messages follow ``:1250-1267``; FP32 inputs run
+    the one-pass DEFAULT product, and ``dot_precision`` HIGH/HIGHEST and
     ``interpret=True`` raise ``NotImplementedError``.
     """
     if a.dim() != 2 or b.dim() != 2:
@@ -549,10 +577,7 @@ def strassen_matmul_lhs_transposed(a, b, *, bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_B
     out_dtype = a.dtype if output_dtype is None else output_dtype
     if out_dtype not in (torch.bfloat16, torch.float32):
         raise ValueError("output_dtype must be BF16 or FP32")
-    if interpret:
-        raise NotImplementedError("interpret=True: the gfx950 kernel has no CPU interpreter path")
-    if a.dtype != torch.bfloat16:
-        raise NotImplementedError("FP32 inputs are not implemented on gfx950 (bf16 MFMA path)")
+    _unsupported(a.dtype, interpret, dot_precision)
     _check_device_tiling(_lib.SMX_ALGO_STRASSEN, None, bm, bn, bk, _lib.SMX_B_PACKED)
     _require_device(a, b.data if isinstance(b, PackedOperand) else b)
     packed_a = pack_operand(a, algo=_lib.SMX_ALGO_STRASSEN, side="lhs_t", tile_rows=bm, bk=bk)
@@ -596,11 +621,12 @@ def cubic_matmul(a, b, *, variant="blocked", bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_
         if dimension % block:
             raise ValueError(f"{name}={dimension} is not divisible by {block}")
     check_tiling(bm, bn, bk)
-    if interpret:
-        raise NotImplementedError("interpret=True: the gfx950 kernel has no CPU interpreter path")
-    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
-        raise NotImplementedError("the gfx950 cubic control takes bf16 inputs")
-    out_dtype = torch.bfloat16 if output_dtype is None else output_dtype
+    if a.dtype != b.dtype:
+        raise ValueError(f"input dtypes disagree: {a.dtype} vs {b.dtype}")
+    if a.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("inputs must be BF16 or FP32")
+    _unsupported(a.dtype, interpret, dot_precision)
+    out_dtype = a.dtype if output_dtype is None else output_dtype
     if out_dtype not in (torch.bfloat16, torch.float32):
         raise ValueError("output_dtype must be BF16 or FP32")
     if epilogue == "norm_residual_add" and (residual is None or norm_scale is None):

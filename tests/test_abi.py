@@ -168,7 +168,8 @@ def test_pack_operand_rejects_bad_arguments(args, code):
     lib = _lib.load()
     buf = (ctypes.c_uint8 * 16)()
     p = ctypes.cast(buf, ctypes.c_void_p)
-    assert lib.smx_pack_operand(algo, 0, 0, side, rows, k, p, ld, tile_rows, bk, None, 0, p, None) == code
+    assert lib.smx_pack_operand(algo, 0, 0, side, rows, k, p, _lib.SMX_DTYPE_BF16, ld, tile_rows, bk, None, 0, p,
+                                None) == code
     assert _lib.last_error()
 
 
@@ -182,7 +183,7 @@ def test_pack_operand_panel_map_arguments(src_k, ld, code):
     lib = _lib.load()
     buf = (ctypes.c_uint8 * 16)()
     p = ctypes.cast(buf, ctypes.c_void_p)
-    assert lib.smx_pack_operand(7, 0, 0, 0, 512, 512, p, ld, 256, 512, p, src_k, p, None) == code
+    assert lib.smx_pack_operand(7, 0, 0, 0, 512, 512, p, _lib.SMX_DTYPE_BF16, ld, 256, 512, p, src_k, p, None) == code
     assert "source K" in _lib.last_error() or "ld must be" in _lib.last_error()
 
 
@@ -191,8 +192,24 @@ def test_pack_operand_rejects_bad_variants(algo, formula, perm):
     lib = _lib.load()
     buf = (ctypes.c_uint8 * 16)()
     p = ctypes.cast(buf, ctypes.c_void_p)
-    assert lib.smx_pack_operand(algo, formula, perm, 0, 512, 512, p, 512, 256, 512, None, 0, p, None) == \
+    assert lib.smx_pack_operand(algo, formula, perm, 0, 512, 512, p, _lib.SMX_DTYPE_BF16, 512, 256, 512, None, 0, p,
+                                None) == \
         _lib.SMX_ERR_INVALID
+
+
+@pytest.mark.parametrize("src_dtype,ld,code", [
+    (2, 512, _lib.SMX_ERR_INVALID),                  # unknown source dtype
+    (-1, 512, _lib.SMX_ERR_INVALID),
+    (_lib.SMX_DTYPE_BF16, 516, _lib.SMX_ERR_INVALID),  # bf16 rows need ld % 8 == 0
+    (_lib.SMX_DTYPE_F32, 515, _lib.SMX_ERR_INVALID),   # f32 rows need ld % 4 == 0
+])
+def test_pack_operand_source_dtype(src_dtype, ld, code):
+    """The source is bf16 or float32; its row stride keeps rows 16-byte aligned."""
+    lib = _lib.load()
+    buf = (ctypes.c_uint8 * 16)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    assert lib.smx_pack_operand(7, 0, 0, 0, 512, 512, p, src_dtype, ld, 256, 512, None, 0, p, None) == code
+    assert _lib.last_error()
 
 
 def test_powers_refuses_fused_epilogues():

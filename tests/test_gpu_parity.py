@@ -584,6 +584,161 @@ def test_qk_norm_rope_epilogue(scale_dtype):
 
 
 # ---------------------------------------------------------------------------
+# FP32 inputs: the one-pass DEFAULT product (operand sums in float, each
+# operand rounded once to bf16, FP32 accumulation)
+# ---------------------------------------------------------------------------
+
+def dev32(x):
+    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(DEV)
+
+
+def dev32_weight(b):
+    """[K, N] float32 as a K-contiguous view of [N, K] device storage."""
+    return dev32(np.asarray(b, np.float32).T).t()
+
+
+def _gaussian32(seed, m, k, n, b_std=0.02):
+    """Float32 inputs whose values are (almost all) not bf16 values."""
+    rng = np.random.default_rng(seed)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32) * np.float32(b_std)
+    assert not np.array_equal(a, o.bf16_round(a))
+    return rng, a, b
+
+
+def assert_f32_close(got, want, k):
+    """FP32 results summed in another order: a few FP32 ulps plus the
+    near-zero floor."""
+    got = np.asarray(got, np.float32)
+    assert got.dtype == np.float32 and np.isfinite(got).all()
+    tol = 4 * np.abs(want) * 2.0 ** -23 + fp32_floor(want, k)
+    bad = np.abs(got - want) > tol
+    assert not bad.any(), f"{int(bad.sum())} elements beyond the FP32 tolerance"
+
+
+FP32_PACK_CASES = [(7, "classical", 0), (7, "classical", 5), (7, "dual", 3), (7, "powers", 6), (8, "classical", 0)]
+
+
+@pytest.mark.parametrize("algo,formula,perm", FP32_PACK_CASES)
+def test_fp32_pack_matches_oracle(algo, formula, perm):
+    """The packing pass on float32 sources: sums in float, one bf16
+    rounding per operand, bit for bit (lhs, transposed lhs and rhs)."""
+    _, a, b = _gaussian32(501, 512, 1024, 512)
+    kw = dict(formula=formula, block_permutation=perm)
+    pa = smx.pack_operand(dev32(a), algo=algo, side="lhs", tile_rows=256, bk=512, **kw)
+    want_a = o.packed_operand(a, algo, "lhs", 256, 512, formula, perm, input_dtype="float32")
+    assert pa.source_dtype == torch.float32
+    assert np.array_equal(host(pa.data), want_a)
+    pt = smx.pack_operand(dev32(a.T), algo=algo, side="lhs_t", tile_rows=256, bk=512, **kw)
+    assert np.array_equal(host(pt.data), want_a)
+    pb = smx.pack_operand(dev32_weight(b), algo=algo, side="rhs", tile_rows=256, bk=512, **kw)
+    assert np.array_equal(host(pb.data), o.packed_operand(b, algo, "rhs", 256, 512, formula, perm,
+                                                          input_dtype="float32"))
+    # a row-major [K, N] weight is transposed by the wrapper, same bits
+    pr = smx.pack_operand(dev32(b), algo=algo, side="rhs", tile_rows=256, bk=512, **kw)
+    assert torch.equal(pr.data, pb.data)
+
+
+def test_fp32_integer_kat():
+    """Integer float32 data is exact under any summation order."""
+    rng = np.random.default_rng(502)
+    a = rng.integers(-2, 3, (512, 1024)).astype(np.float32)
+    b = rng.integers(-2, 3, (1024, 512)).astype(np.float32)
+    kw = dict(bm=256, bn=256, bk=512)
+    for fn in (smx.strassen_matmul, smx.cubic_matmul):
+        got = fn(dev32(a), dev32_weight(b), **kw)
+        assert got.dtype == torch.float32
+        assert np.array_equal(host(got), a @ b)
+
+
+@pytest.mark.parametrize("arm", ARMS)
+def test_fp32_inputs_match_oracle(arm):
+    """FP32 inputs on every arm (the plain arms are packed for the call: FP32
+    reaches the kernels through the packing pass). Default output FP32, and
+    BF16 when asked; error against the float64 product within the gate."""
+    _, a, b = _gaussian32(503, 512, 2048, 768)
+    kw = dict(bm=256, bn=256, bk=512)
+    okw = dict(kw, input_dtype="float32") if arm.startswith("strassen") else dict(kw)
+    got = run_arm(arm, dev32(a), dev32_weight(b), **kw)
+    assert got.dtype == torch.float32
+    want = oracle_arm(arm, a, b, output_dtype="float32", **okw)
+    assert_f32_close(host(got), want, 2048)
+    got16 = run_arm(arm, dev32(a), dev32_weight(b), output_dtype=torch.bfloat16, **kw)
+    assert got16.dtype == torch.bfloat16
+    assert np.array_equal(host(got16), o.bf16_round(host(got)))
+    # the gate: <= 1e-2 and <= 1.5x the reference algorithm's own error. With
+    # FP32 inputs the one-pass product rounds Strassen's operand sums, which
+    # costs about 2x the cubic's error (the cubic rounds single quadrants).
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    assert rel_l2(host(got), ref) <= 1e-2
+    assert rel_l2(host(got), ref) <= 1.5 * rel_l2(want, ref)
+
+
+@pytest.mark.parametrize("formula,perm", VARIANTS)
+def test_fp32_formula_variants(formula, perm):
+    _, a, b = _gaussian32(504, 512, 1024, 512)
+    kw = dict(bm=256, bn=256, bk=512, formula_variant=formula, block_permutation=perm)
+    got = host(smx.strassen_matmul(dev32(a), dev32_weight(b), **kw))
+    assert_f32_close(got, o.strassen_matmul(a, b, output_dtype="float32", input_dtype="float32", **kw), 1024)
+    w = smx.strassen_weight_layout(dev32_weight(b), 256, 512, formula_variant=formula, block_permutation=perm)
+    assert torch.equal(torch.from_numpy(got), smx.strassen_matmul(dev32(a), w, **kw).cpu())
+
+
+def test_fp32_epilogues():
+    """Fused epilogues on FP32 inputs: a BF16 tile when asked (one rounding of
+    the same FP32 values), else an FP32 tile; FP32 residual and bias."""
+    rng, a, b = _gaussian32(505, 512, 1024, 1024)
+    kw = dict(bm=256, bn=512, bk=512)
+    okw = dict(kw, input_dtype="float32")
+    laid = o.swiglu_weight_layout(b, 512)
+    laid_dev = smx.swiglu_weight_layout(dev32_weight(b), 512)
+    r = rng.standard_normal((512, 1024)).astype(np.float32)
+    bias = rng.standard_normal(1024).astype(np.float32)
+    cases = [
+        (dict(epilogue="swiglu"), dict(epilogue="swiglu"), laid_dev, laid),
+        (dict(epilogue="geglu"), dict(epilogue="geglu"), laid_dev, laid),
+        (dict(epilogue="residual_add", residual=dev32(r)), dict(epilogue="residual_add", residual=r),
+         dev32_weight(b), b),
+        (dict(epilogue="bias_add", bias=dev32(bias)), dict(epilogue="bias_add", bias=bias), dev32_weight(b), b),
+    ]
+    for dkw, hkw, w_dev, w in cases:
+        say(f"  {dkw['epilogue']}")
+        got16 = host(smx.strassen_matmul(dev32(a), w_dev, output_dtype=torch.bfloat16, **dkw, **kw))
+        assert_ulp_close(got16, o.strassen_matmul(a, w, **hkw, **okw), k=1024)
+        got = smx.strassen_matmul(dev32(a), w_dev, **dkw, **kw)
+        assert got.dtype == torch.float32
+        want = o.strassen_matmul(a, w, output_dtype="float32", **hkw, **okw)
+        assert rel_l2(host(got), want) <= 1e-6
+    g = (1 + 0.1 * rng.standard_normal(1024)).astype(np.float32)
+    nkw = dict(kw, bn=1024, epilogue="norm_residual_add")
+    got = host(smx.strassen_matmul(dev32(a), dev32_weight(b), residual=dev32(r), norm_scale=dev32(g),
+                                   output_dtype=torch.bfloat16, **nkw))
+    assert_ulp_close(got, o.strassen_matmul(a, b, residual=r, norm_scale=g, input_dtype="float32", **nkw), k=1024)
+
+
+def test_fp32_lhs_transposed():
+    rng = np.random.default_rng(506)
+    k, m, n = 1024, 512, 768
+    a_t = rng.standard_normal((k, m)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32) * np.float32(0.02)
+    got = smx.strassen_matmul_lhs_transposed(dev32(a_t), dev32(b), bm=256, bn=256, bk=512)
+    assert got.dtype == torch.float32 and tuple(got.shape) == (m, n)
+    want = o.strassen_matmul_lhs_transposed(a_t, b, bm=256, bn=256, bk=512, output_dtype="float32",
+                                            input_dtype="float32")
+    assert_f32_close(host(got), want, k)
+
+
+@pytest.mark.parametrize("panels,formula,perm", [((1,), "classical", 0), ((0, 3), "dual", 2)])
+def test_fp32_exact_panels(panels, formula, perm):
+    _, a, b = _gaussian32(507, 512, 2048, 512)
+    kw = dict(bm=256, bn=256, bk=512, formula_variant=formula, block_permutation=perm, classical_panels=panels)
+    got = host(smx.strassen_matmul(dev32(a), dev32_weight(b), **kw))
+    assert_f32_close(got, o.strassen_matmul(a, b, output_dtype="float32", input_dtype="float32", **kw), 2048)
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    assert rel_l2(got, ref) <= 1e-2
+
+
+# ---------------------------------------------------------------------------
 # Full Qwen3-32B shapes (8 x 1024 tokens)
 # ---------------------------------------------------------------------------
 

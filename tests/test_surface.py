@@ -120,10 +120,27 @@ def test_unported_options_raise_not_implemented(kwargs):
         smx.strassen_matmul(a, b, bm=256, bn=256, bk=512, **kwargs)
 
 
-def test_fp32_inputs_not_implemented():
+def test_fp32_inputs_take_the_one_pass_path():
+    """FP32 inputs run the DEFAULT-precision product (one bf16 pass); more
+    passes are not built. CPU tensors still stop at the device check."""
     a, b = t(256, 512, dtype=torch.float32), t(512, 256, dtype=torch.float32)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError, match="HIP device"):
         smx.strassen_matmul(a, b, bm=256, bn=256, bk=512)
+    with pytest.raises(ValueError, match="HIP device"):
+        smx.strassen_matmul(a, b, bm=256, bn=256, bk=512, dot_precision="DEFAULT")
+    for precision in ("HIGHEST", "high"):
+        with pytest.raises(NotImplementedError, match="HIGH/HIGHEST"):
+            smx.strassen_matmul(a, b, bm=256, bn=256, bk=512, dot_precision=precision)
+        with pytest.raises(NotImplementedError, match="HIGH/HIGHEST"):
+            smx.cubic_matmul(a, b, bm=256, bn=256, bk=512, dot_precision=precision)
+        with pytest.raises(NotImplementedError, match="HIGH/HIGHEST"):
+            smx.strassen_matmul_lhs_transposed(t(512, 256, dtype=torch.float32), b, bm=256, bn=256, bk=512,
+                                               dot_precision=precision)
+    # bf16 products are exact in FP32 accumulation: precision is irrelevant there
+    with pytest.raises(ValueError, match="HIP device"):
+        smx.strassen_matmul(t(256, 512), t(512, 256), bm=256, bn=256, bk=512, dot_precision="HIGHEST")
+    with pytest.raises(ValueError, match="input dtypes disagree"):
+        smx.cubic_matmul(a, t(512, 256), bm=256, bn=256, bk=512)
 
 
 def test_gfx950_tile_rule_and_device_check():
@@ -172,8 +189,8 @@ def test_packed_weight_surface():
         pass
     with pytest.raises(ValueError, match="HIP device"):
         smx.strassen_weight_layout(t(512, 256), 256, 512)
-    with pytest.raises(ValueError, match="bf16"):
-        smx.strassen_weight_layout(t(512, 256, dtype=torch.float32), 256, 512)
+    with pytest.raises(ValueError, match="bf16 or float32"):
+        smx.strassen_weight_layout(t(512, 256, dtype=torch.float16), 256, 512)
 
 
 @pytest.mark.parametrize("algo", [7, 8])
@@ -273,7 +290,9 @@ def test_torch_relayouts_match_oracle():
     ((t(512, 256), t(512, 256)), {"bm": 96}, ValueError, "M=256 is not divisible by 96"),
     ((t(512, 256), t(512, 256)), {"allow_input_fusion": (True,)}, ValueError, "two booleans"),
     ((t(512, 256), t(512, 256)), {"output_dtype": torch.float16}, ValueError, "BF16 or FP32"),
-    ((t(512, 256, dtype=torch.float32), t(512, 256, dtype=torch.float32)), {}, NotImplementedError, "FP32"),
+    ((t(512, 256, dtype=torch.float32), t(512, 256, dtype=torch.float32)), {"dot_precision": "HIGHEST"},
+     NotImplementedError, "FP32"),
+    ((t(512, 256, dtype=torch.float32), t(512, 256, dtype=torch.float32)), {}, ValueError, "HIP device"),
     ((t(512, 256), t(512, 256)), {"interpret": True}, NotImplementedError, "interpret"),
     ((t(512, 256), t(512, 256)), {}, ValueError, "HIP device"),
 ])
