@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define SMX_VERSION 6
+#define SMX_VERSION 7
 
 /* Status codes. */
 #define SMX_OK 0
@@ -151,26 +151,36 @@ int smx_packed_bytes(int32_t algo, int64_t rows, int64_t k, int64_t* bytes);
  * B^T [rows = n, k] and tile_rows = bn. src_dtype: SMX_DTYPE_BF16, or
  * SMX_DTYPE_F32 for FP32 inputs (operand sums formed in float, every operand
  * rounded once to bf16: the one-pass bf16 product of the reference's FP32
- * path at DEFAULT precision). Strassen (algo 7) stores the seven operand sums of
+ * path at DEFAULT precision). passes: bf16 passes per product, 1, or for a
+ * float32 source 3 (dot_precision HIGH) or 6 (HIGHEST): each operand v is
+ * split into bf16 parts p0 = bf16(v), p1 = bf16(v - p0), p2 = bf16(v - p0 - p1).
+ * The packed K runs pass-major: with slots = k / (passes * bk) panels per
+ * pass, packed panel j holds pass j / slots of panel slot j % slots; the A
+ * side carries parts (1, 0, 0) or (2, 1, 0, 1, 0, 0) over the passes and the
+ * B side (0, 1, 0) or (0, 1, 2, 0, 1, 0) (smallest products first), so that
+ * one GEMM over the packed K = passes x the source K sums every pass product
+ * in FP32.
+ * Strassen (algo 7) stores the seven operand sums of
  * P1..P7 (A0+A3, A2+A3, A0, A3, A0+A1, A2-A0, A1-A3; B0+B3, B0, B1-B3,
  * B2-B0, B3, B0+B1, B2+B3), each rounded once to bf16, or those of the dual /
  * powers formula, after the block permutation's quadrant swaps (A uses bits 0
  * and 1, B bits 1 and 2); the cubic (algo 8, formula 0, permutation 0) stores
- * the four quadrants. panels: NULL, or device int32 [k / bk] naming the
- * source K panel (of bk columns) that each packed panel reads, from a
+ * the four quadrants. panels: NULL, or device int32 [slots] naming the
+ * source K panel (of bk columns) that each slot reads (in every pass), from a
  * source src_k wide (entries are clamped to 0 .. src_k/bk - 1); this packs
- * the ordinary or the exact panels of an exact-panel schedule. out
+ * the ordinary or the exact panels of an exact-panel schedule (without a map,
+ * src_k = k / passes). out
  * (smx_packed_bytes bytes, 16-byte aligned)
  * is laid out [rows/256][k/32][nops][4][64][8] bf16: fragment (tile of 128
  * product rows, stage of 16 product k, operand, 32-row block), lane l holding
- * row l%32, depth 8*(l/32)..+8. Needs rows % tile_rows == 0, k % bk == 0,
+ * row l%32, depth 8*(l/32)..+8. Needs rows % tile_rows == 0, k % (passes * bk) == 0,
  * tile_rows % 256 == 0, bk % 64 == 0, ld >= src_k, rows 16-byte aligned (ld % 8 for bf16, % 4 for
  * float32; LHS_T: ld >= m). Asynchronous on
  * stream.
  */
 int smx_pack_operand(int32_t algo, int32_t formula, int32_t block_permutation, int32_t side, int64_t rows, int64_t k,
-                     const void* src, int32_t src_dtype, int64_t ld, int32_t tile_rows, int32_t bk,
-                     const int32_t* panels, int64_t src_k, void* out, void* stream);
+                     const void* src, int32_t src_dtype, int32_t passes, int64_t ld, int32_t tile_rows,
+                     int32_t bk, const int32_t* panels, int64_t src_k, void* out, void* stream);
 
 /*
  * Second pass of the norm_residual_add epilogue (strassen_pallas.py:836-866),

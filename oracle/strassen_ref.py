@@ -22,8 +22,8 @@ __all__ = [
     "apply_rope", "strassen_products", "strassen_a_operands", "strassen_b_operands",
     "operand_planes", "packed_operand", "unpack_operand", "PACK_TILE", "PACK_STAGE",
     "dual_a_operands", "dual_b_operands", "powers_a_operands", "powers_b_operands", "powers_decode",
-    "permuted_quadrants", "formula_operands", "DUAL_UPDATES", "POWERS_BASIS_UPDATES",
-    "PRODUCT_UPDATES",
+    "permuted_quadrants", "formula_operands", "operand_values", "DUAL_UPDATES", "POWERS_BASIS_UPDATES",
+    "PRODUCT_UPDATES", "precision_passes", "bf16_part", "pass_product", "PASS_PARTS",
 ]
 
 
@@ -232,20 +232,78 @@ def operand_round(x):
     return bf16_round(x)
 
 
-def formula_operands(formula, a_q, b_q, input_dtype="bfloat16"):
-    """(A operand, B operand) of products 1..7 of ``formula``, each operand
-    as the product sees it."""
+# ``dot_precision`` (``:228-232``, default ``:889``) for FP32 operands: the
+# jax.lax.Precision names and string aliases -> bf16 passes per product.
+# DEFAULT multiplies one bf16 pass; HIGH is XLA's 3-pass bf16 product
+# (bf16_3x) and HIGHEST its 6-pass product (bf16_6x).
+_PRECISION_PASSES = {"DEFAULT": 1, "FASTEST": 1, "BFLOAT16": 1, "HIGH": 3, "BFLOAT16_3X": 3,
+                     "TENSORFLOAT32": 3, "HIGHEST": 6, "FLOAT32": 6}
+
+# Parts (of the A operand, of the B operand) multiplied by each pass: the
+# bf16 expansion v = p0 + p1 + p2 of each operand, and every pass pair whose
+# parts' orders sum to at most 1 (HIGH) or 2 (HIGHEST), smallest products
+# first: p1*p0, p0*p1, p0*p0; p2*p0, p1*p1, p0*p2, p1*p0, p0*p1, p0*p0.
+PASS_PARTS = {1: ((0,), (0,)), 3: ((1, 0, 0), (0, 1, 0)), 6: ((2, 1, 0, 1, 0, 0), (0, 1, 2, 0, 1, 0))}
+
+
+def precision_passes(dot_precision, input_dtype="float32"):
+    """bf16 passes per product: 1 for bf16 inputs (their operands are bf16
+    values, whose low-order parts are zero), else by ``dot_precision``."""
+    if dot_precision is None:
+        passes = 1
+    else:
+        name = str(getattr(dot_precision, "name", dot_precision)).upper().rsplit(".", 1)[-1]
+        if name not in _PRECISION_PASSES:
+            raise ValueError(f"unknown dot_precision {dot_precision!r}")
+        passes = _PRECISION_PASSES[name]
+    return passes if input_dtype == "float32" else 1
+
+
+def bf16_part(x, part):
+    """Part ``part`` of the bf16 expansion of float32 ``x``: p0 = bf16(x),
+    p1 = bf16(x - p0), p2 = bf16(x - p0 - p1), remainders in float32 (they
+    are exact there)."""
+    x = np.asarray(x, dtype=np.float32)
+    p = bf16_round(x)
+    for _ in range(part):
+        x = (x - p).astype(np.float32)
+        p = bf16_round(x)
+    return p
+
+
+def pass_product(s, t, passes=1):
+    """``jnp.dot(s, t, preferred_element_type=float32)`` at ``passes`` bf16
+    passes: the sum over the pass pairs of the bf16-part products, each an
+    exact product summed in FP32. One pass is the DEFAULT product
+    ``bf16(s) @ bf16(t)``."""
+    parts_a, parts_b = PASS_PARTS[passes]
+    value = np.zeros((s.shape[0], t.shape[1]), dtype=np.float32)
+    for i, j in zip(parts_a, parts_b):
+        value += np.matmul(bf16_part(s, i), bf16_part(t, j), dtype=np.float32)
+    return value
+
+
+def operand_values(formula, a_q, b_q, input_dtype="bfloat16"):
+    """{p: (S_p, T_p)} of products 1..7 of ``formula`` in the compute dtype
+    (each jnp operation rounded for bf16 inputs), before the product's own
+    bf16 rounding."""
     r = operation_round(input_dtype)
     if formula == "classical":
-        products = strassen_products(a_q, b_q, r)
-        return {p: (operand_round(s_), operand_round(t_)) for p, (s_, t_) in products.items()}
+        return strassen_products(a_q, b_q, r)
     if formula == "dual":
         sa, tb = dual_a_operands(a_q, r), dual_b_operands(b_q, r)
     elif formula == "powers":
         sa, tb = powers_a_operands(a_q, r), powers_b_operands(b_q, r)
     else:
         raise ValueError(f"unknown formula {formula!r}")
-    return {p: (operand_round(sa[p - 1]), operand_round(tb[p - 1])) for p in range(1, 8)}
+    return {p: (sa[p - 1], tb[p - 1]) for p in range(1, 8)}
+
+
+def formula_operands(formula, a_q, b_q, input_dtype="bfloat16"):
+    """(A operand, B operand) of products 1..7 of ``formula``, each operand
+    as the one-pass product sees it."""
+    return {p: (operand_round(s_), operand_round(t_))
+            for p, (s_, t_) in operand_values(formula, a_q, b_q, input_dtype).items()}
 
 
 # The eight half-size cubic products (A quadrant, B quadrant, C quadrant) in
@@ -322,7 +380,7 @@ PACK_STAGE = 16  # product depth per packed stage (one MFMA k step)
 
 
 def operand_planes(x, algo, side, tile_rows, bk, formula="classical", block_permutation=0,
-                   input_dtype="bfloat16"):
+                   input_dtype="bfloat16", dot_precision=None):
     """The GEMM operands of every tile as (nops, R, K/2) product-space planes.
 
     ``side="lhs"``: x is A [M, K], R = M/2 product rows (row tile, local row).
@@ -331,34 +389,36 @@ def operand_planes(x, algo, side, tile_rows, bk, formula="classical", block_perm
     gives the seven operand sums of ``strassen_a_operands`` /
     ``strassen_b_operands``; the cubic (algo 8) the four quadrants. Every
     operand is as the product sees it (``operand_round``; FP32 inputs form
-    the sums in float32 first).
+    the sums in float32 first). A multi-pass ``dot_precision`` (FP32
+    inputs) lays the passes out pass-major: depth (pass, K panel, local k),
+    the pass taking the operand's bf16 part of ``PASS_PARTS``.
     """
     r = operation_round(input_dtype)
     x = np.asarray(x, dtype=np.float32)
     sm, sk, sn = block_permutation & 1, (block_permutation >> 1) & 1, (block_permutation >> 2) & 1
     a_ops = {"classical": strassen_a_operands, "dual": dual_a_operands, "powers": powers_a_operands}[formula]
     b_ops = {"classical": strassen_b_operands, "dual": dual_b_operands, "powers": powers_b_operands}[formula]
+    passes = precision_passes(dot_precision, input_dtype)
     if side == "lhs":
-        steps = x.shape[1] // bk
-        quads = [np.concatenate(q, axis=1)
-                 for q in zip(*(_split_a(x, tile_rows, bk, s) for s in range(steps)))]
-        ops = a_ops(permuted_quadrants(quads, sm, sk), r) if algo == 7 else quads
+        panels = [_split_a(x, tile_rows, bk, s) for s in range(x.shape[1] // bk)]
+        ops_of = (lambda q: a_ops(permuted_quadrants(q, sm, sk), r)) if algo == 7 else list
+        parts = PASS_PARTS[passes][0]
     elif side == "rhs":
-        steps = x.shape[0] // bk
-        quads = [np.concatenate(q, axis=0).T
-                 for q in zip(*(_split_b(x, tile_rows, bk, s) for s in range(steps)))]
-        ops = b_ops(permuted_quadrants(quads, sk, sn), r) if algo == 7 else quads
+        panels = [[q.T for q in _split_b(x, tile_rows, bk, s)] for s in range(x.shape[0] // bk)]
+        ops_of = (lambda q: b_ops(permuted_quadrants(q, sk, sn), r)) if algo == 7 else list
+        parts = PASS_PARTS[passes][1]
     else:
         raise ValueError("side must be 'lhs' or 'rhs'")
-    return np.stack([operand_round(o) for o in ops])
+    ops = [np.stack(ops_of(quads)) for quads in panels]
+    return np.concatenate([bf16_part(o, part) for part in parts for o in ops], axis=2)
 
 
 def packed_operand(x, algo, side, tile_rows, bk, formula="classical", block_permutation=0,
-                   input_dtype="bfloat16"):
+                   input_dtype="bfloat16", dot_precision=None):
     """``smx_pack_operand``'s output as a flat float32 array of bf16 values:
     ``[R/128][K/32][nops][4][64][8]``, lane l of a fragment holding product
     row l%32 of its 32-row block and depth 8*(l//32)..+8 of its stage."""
-    planes = operand_planes(x, algo, side, tile_rows, bk, formula, block_permutation, input_dtype)
+    planes = operand_planes(x, algo, side, tile_rows, bk, formula, block_permutation, input_dtype, dot_precision)
     nops, rows, depth = planes.shape
     v = planes.reshape(nops, rows // PACK_TILE, 4, 32, depth // PACK_STAGE, 2, 8)
     # (op, tile, block, row32, stage, half, e) -> (tile, stage, op, block, half, row32, e)
@@ -392,7 +452,8 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
                     rope_eps=1e-6, product_aware_swiglu=False,
                     product_aware_residual=False, output_dtype="bfloat16",
                     formula_variant="classical", block_permutation=0, norm_scale=None,
-                    norm_eps=1e-6, classical_panels=(), panel_schedule=None, input_dtype="bfloat16"):
+                    norm_eps=1e-6, classical_panels=(), panel_schedule=None, input_dtype="bfloat16",
+                    dot_precision=None):
     """``a @ b`` with one tile-local classical Strassen level.
 
     Restates ``_classical_strassen_kernel`` (``strassen_pallas.py:156-879``)
@@ -456,11 +517,12 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
         raise ValueError("exact panels require a quadrant-basis formula")
 
     acc = [np.zeros((m // 2, n // 2), dtype=np.float32) for _ in range(4)]
+    passes = precision_passes(dot_precision, input_dtype)
 
     def run(products, sequence):
         for p in sequence:
             s, t = products[p]
-            value = np.matmul(s, t, dtype=np.float32)
+            value = pass_product(s, t, passes)
             for q, sign in updates[p]:
                 idx = q if basis else output_index[q]
                 if sign > 0:
@@ -473,10 +535,9 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
         b_q = permuted_quadrants(_split_b(b, bn, bk, step), swap_k, swap_n)
         if step in exact:
             for ia, ib, q in CUBIC_PAIRS:
-                acc[output_index[q]] += np.matmul(operand_round(a_q[ia]), operand_round(b_q[ib]),
-                                                  dtype=np.float32)
+                acc[output_index[q]] += pass_product(a_q[ia], b_q[ib], passes)
             continue
-        products = formula_operands(formula_variant, a_q, b_q, input_dtype)
+        products = operand_values(formula_variant, a_q, b_q, input_dtype)
         last = step == nk - 1
         if last and product_aware_swiglu:
             run(products, PA_SWIGLU_TOP)
@@ -498,21 +559,25 @@ def strassen_matmul(a, b, *, bm, bn, bk, interleave_products=False,
 
 
 def strassen_matmul_lhs_transposed(a_t, b, *, bm, bn, bk, interleave_products=False,
-                                   output_dtype="bfloat16", input_dtype="bfloat16"):
+                                   output_dtype="bfloat16", input_dtype="bfloat16", dot_precision=None):
     """``a_t.T @ b`` (``strassen_pallas.py:1224-1312``): the kernel transposes
     each resident ``(bk, bm)`` tile of ``a_t`` and runs the ordinary classical
     Strassen body on it (``:1273-1289``), so the result is ``strassen_matmul``
     of the transposed matrix."""
     return strassen_matmul(np.asarray(a_t, dtype=np.float32).T, b, bm=bm, bn=bn, bk=bk,
                            interleave_products=interleave_products, output_dtype=output_dtype,
-                           input_dtype=input_dtype)
+                           input_dtype=input_dtype, dot_precision=dot_precision)
 
 
 def cubic_blocked_matmul(a, b, *, bm, bn, bk, epilogue=None, residual=None,
                          bias=None, rope_cos=None, rope_sin=None,
                          rope_scale=None, rope_head_dim=128, rope_eps=1e-6,
-                         output_dtype="bfloat16", norm_scale=None, norm_eps=1e-6):
+                         output_dtype="bfloat16", norm_scale=None, norm_eps=1e-6, dot_precision=None):
     """The matched cubic control: eight half-size products per K panel.
+
+    ``dot_precision`` HIGH / HIGHEST multiplies the bf16 parts of each
+    quadrant in 3 / 6 passes (``pass_product``); bf16 values have zero
+    low-order parts, so bf16 inputs give the one-pass result.
 
     FP32 inputs (float32 values that are not bf16) take the same one-pass
     bf16 product as Strassen: each quadrant is rounded to bf16 at the
@@ -528,12 +593,13 @@ def cubic_blocked_matmul(a, b, *, bm, bn, bk, epilogue=None, residual=None,
     a = np.asarray(a, dtype=np.float32)
     b = np.asarray(b, dtype=np.float32)
     m, k, n = _check_common(a, b, bm, bn, bk)
+    passes = precision_passes(dot_precision)
     acc = [np.zeros((m // 2, n // 2), dtype=np.float32) for _ in range(4)]
     for step in range(k // bk):
         aq = _split_a(a, bm, bk, step)
         bq = _split_b(b, bn, bk, step)
         for ia, ib, q in CUBIC_PAIRS:
-            acc[q] += np.matmul(operand_round(aq[ia]), operand_round(bq[ib]), dtype=np.float32)
+            acc[q] += pass_product(aq[ia], bq[ib], passes)
     return _epilogue(acc, m, n, bm, bn, epilogue=epilogue, residual=residual,
                      bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
                      rope_scale=rope_scale, rope_head_dim=rope_head_dim,

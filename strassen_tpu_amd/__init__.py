@@ -17,8 +17,8 @@ from .strassen import (  # noqa: F401
 
 from .packing import (  # noqa: F401
     ExactSchedule, PackedOperand, SplitOperand, cubic_weight_layout, pack_activation, pack_operand,
-    strassen_weight_layout,
+    precision_passes, strassen_weight_layout,
 )
 from .tuning import tuned_matmul  # noqa: F401
 
-__version__ = "0.4.0"
+__version__ = "0.5.0"

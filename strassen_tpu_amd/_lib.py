@@ -95,7 +95,7 @@ def load():
     i64, i32 = ctypes.c_int64, ctypes.c_int32
     lib.smx_packed_bytes.argtypes = [i32, i64, i64, ctypes.POINTER(i64)]
     lib.smx_packed_bytes.restype = ctypes.c_int
-    lib.smx_pack_operand.argtypes = [i32, i32, i32, i32, i64, i64, vp, i32, i64, i32, i32, vp, i64, vp, vp]
+    lib.smx_pack_operand.argtypes = [i32, i32, i32, i32, i64, i64, vp, i32, i32, i64, i32, i32, vp, i64, vp, vp]
     lib.smx_pack_operand.restype = ctypes.c_int
     f32 = ctypes.c_float
     lib.smx_norm_residual_add.argtypes = [i64, i64, vp, i64, vp, i64, vp, i32, f32, vp, i64, vp]

@@ -101,15 +101,21 @@ __device__ __forceinline__ void strassen_b_ops(const u32x4 (&q)[4], u32x4 (&ops)
 // bf16 round trip of a float (round to nearest even).
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
-// Elementwise map of four unpacked quadrants to one packed bf16 operand; f
-// returns the float value that is rounded once to bf16.
-template <class F>
-__device__ __forceinline__ u32x4 map8(const F8& x0, const F8& x1, const F8& x2, const F8& x3, F f) {
-  u32x4 r;
+// Elementwise x + y or x - y in float, unrounded.
+template <bool kSub>
+__device__ __forceinline__ F8 add8(const F8& x, const F8& y) {
+  F8 r;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    r[i] = pack_bf16(f(x0.v[2 * i], x1.v[2 * i], x2.v[2 * i], x3.v[2 * i]),
-                     f(x0.v[2 * i + 1], x1.v[2 * i + 1], x2.v[2 * i + 1], x3.v[2 * i + 1]));
+  for (int i = 0; i < 8; ++i) r.v[i] = kSub ? x.v[i] - y.v[i] : x.v[i] + y.v[i];
+  return r;
+}
+
+// Elementwise map of four unpacked quadrants to one float operand.
+template <class F>
+__device__ __forceinline__ F8 map8(const F8& x0, const F8& x1, const F8& x2, const F8& x3, F f) {
+  F8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r.v[i] = f(x0.v[i], x1.v[i], x2.v[i], x3.v[i]);
   return r;
 }
 
@@ -125,56 +131,92 @@ __device__ __forceinline__ u32x4 pack8(const F8& x) {
   return r;
 }
 
+// Part `part` of the bf16 expansion of a float v = p0 + p1 + p2 + r:
+// p0 = bf16(v), p1 = bf16(v - p0), p2 = bf16(v - p0 - p1). Each remainder
+// is exact in float (v and its bf16 rounding share the exponent range), so
+// the parts are those of the exact value.
+__device__ __forceinline__ float bf16_part(float v, int part) {
+  const float p0 = round_bf16(v);
+  if (part == 0) return p0;
+  const float r1 = v - p0;
+  const float p1 = round_bf16(r1);
+  return part == 1 ? p1 : round_bf16(r1 - p1);
+}
+
+__device__ __forceinline__ u32x4 pack8_part(const F8& x, int part) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = pack_bf16(bf16_part(x.v[2 * i], part), bf16_part(x.v[2 * i + 1], part));
+  return r;
+}
+
+// Multi-pass bf16 products of FP32 operands (dot_precision HIGH: 3 passes,
+// HIGHEST: 6). Pass i multiplies part pass_part(A, i) of the A operand by
+// part pass_part(B, i) of the B operand, smallest products first so that
+// the FP32 accumulator takes the leading p0*p0 pass last: p1*p0, p0*p1,
+// p0*p0 (3 passes); p2*p0, p1*p1, p0*p2, p1*p0, p0*p1, p0*p0 (6 passes).
+// The tables hold the part of pass i in bits 4i..4i+3.
+constexpr uint32_t kPassPartsA3 = 0x001, kPassPartsB3 = 0x010;
+constexpr uint32_t kPassPartsA6 = 0x001012, kPassPartsB6 = 0x010210;
+
+__device__ __forceinline__ int pass_part(bool side_b, int passes, int pass) {
+  const uint32_t table = passes == 3 ? (side_b ? kPassPartsB3 : kPassPartsA3)
+                         : passes == 6 ? (side_b ? kPassPartsB6 : kPassPartsA6) : 0u;
+  return (int)((table >> (4 * pass)) & 15u);
+}
+
 // Operands of products 1..7 of a formula from the four (permuted) quadrants
-// in float, A side (kSide 0) or B side (kSide 1), each rounded once to bf16.
+// in float, A side (kSide 0) or B side (kSide 1), before their final bf16
+// rounding (pack8, or pack8_part for a multi-pass product).
 // kBf16Compute: the reference's compute dtype is bf16 (bf16 inputs), so each
 // jnp bf16 operation rounds: two-term sums round once (as they also do in
 // float), and the powers formula's balanced four-term expressions round
 // both halves and their sum. With FP32 inputs the compute dtype is float and
 // only the finished operand is rounded, by the one-pass bf16 MXU product at
-// DEFAULT precision. Raw quadrants (A0, B3, ...) are rounded to bf16, which
-// leaves bf16 inputs unchanged; scaling by 1/2 and 1/4 is exact.
+// DEFAULT precision (or split into bf16 parts by a multi-pass product). Raw
+// quadrants (A0, B3, ...) are rounded the same way, which leaves bf16 inputs
+// unchanged; scaling by 1/2 and 1/4 is exact.
 template <int kSide, bool kBf16Compute>
-__device__ __forceinline__ void formula_ops_f(int formula, const F8 (&x)[4], u32x4 (&ops)[7]) {
+__device__ __forceinline__ void formula_vals(int formula, const F8 (&x)[4], F8 (&ops)[7]) {
   const F8 &x0 = x[0], &x1 = x[1], &x2 = x[2], &x3 = x[3];
   auto rnd = [](float v) { return kBf16Compute ? round_bf16(v) : v; };
   if (formula == kFormulaClassical) {
     if constexpr (kSide == 0) {  // A0+A3, A2+A3, A0, A3, A0+A1, A2-A0, A1-A3 (:324-379)
-      ops[0] = sum8<false>(x0, x3);
-      ops[1] = sum8<false>(x2, x3);
-      ops[2] = pack8(x0);
-      ops[3] = pack8(x3);
-      ops[4] = sum8<false>(x0, x1);
-      ops[5] = sum8<true>(x2, x0);
-      ops[6] = sum8<true>(x1, x3);
+      ops[0] = add8<false>(x0, x3);
+      ops[1] = add8<false>(x2, x3);
+      ops[2] = x0;
+      ops[3] = x3;
+      ops[4] = add8<false>(x0, x1);
+      ops[5] = add8<true>(x2, x0);
+      ops[6] = add8<true>(x1, x3);
     } else {  // B0+B3, B0, B1-B3, B2-B0, B3, B0+B1, B2+B3
-      ops[0] = sum8<false>(x0, x3);
-      ops[1] = pack8(x0);
-      ops[2] = sum8<true>(x1, x3);
-      ops[3] = sum8<true>(x2, x0);
-      ops[4] = pack8(x3);
-      ops[5] = sum8<false>(x0, x1);
-      ops[6] = sum8<false>(x2, x3);
+      ops[0] = add8<false>(x0, x3);
+      ops[1] = x0;
+      ops[2] = add8<true>(x1, x3);
+      ops[3] = add8<true>(x2, x0);
+      ops[4] = x3;
+      ops[5] = add8<false>(x0, x1);
+      ops[6] = add8<false>(x2, x3);
     }
     return;
   }
   if (formula == kFormulaDual) {
     if constexpr (kSide == 0) {  // A0+A3, A0, A2-A3, A1-A0, A3, A0+A2, A1+A3 (:461-517)
-      ops[0] = sum8<false>(x0, x3);
-      ops[1] = pack8(x0);
-      ops[2] = sum8<true>(x2, x3);
-      ops[3] = sum8<true>(x1, x0);
-      ops[4] = pack8(x3);
-      ops[5] = sum8<false>(x0, x2);
-      ops[6] = sum8<false>(x1, x3);
+      ops[0] = add8<false>(x0, x3);
+      ops[1] = x0;
+      ops[2] = add8<true>(x2, x3);
+      ops[3] = add8<true>(x1, x0);
+      ops[4] = x3;
+      ops[5] = add8<false>(x0, x2);
+      ops[6] = add8<false>(x1, x3);
     } else {  // B0+B3, B1+B3, B0, B3, B0+B2, B1-B0, B2-B3
-      ops[0] = sum8<false>(x0, x3);
-      ops[1] = sum8<false>(x1, x3);
-      ops[2] = pack8(x0);
-      ops[3] = pack8(x3);
-      ops[4] = sum8<false>(x0, x2);
-      ops[5] = sum8<true>(x1, x0);
-      ops[6] = sum8<true>(x2, x3);
+      ops[0] = add8<false>(x0, x3);
+      ops[1] = add8<false>(x1, x3);
+      ops[2] = x0;
+      ops[3] = x3;
+      ops[4] = add8<false>(x0, x2);
+      ops[5] = add8<true>(x1, x0);
+      ops[6] = add8<true>(x2, x3);
     }
     return;
   }

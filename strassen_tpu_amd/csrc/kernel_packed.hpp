@@ -351,9 +351,13 @@ template <int kAlgo, int kSide, bool kF32>
 __global__ __launch_bounds__(256) void pack_operand(const void* __restrict__ src_v, int64_t ld, int64_t rows,
                                                     int64_t k, int32_t tile_rows, int32_t bk, int32_t formula,
                                                     int32_t perm, const int32_t* __restrict__ panels,
-                                                    int32_t src_panels, uint8_t* __restrict__ out) {
+                                                    int32_t src_panels, int32_t passes,
+                                                    uint8_t* __restrict__ out) {
   // Source elements: bf16, or float (FP32 inputs: the operand sums are
-  // formed in float and each operand is rounded once to bf16).
+  // formed in float and each operand is rounded once to bf16, or, for a
+  // product of `passes` bf16 passes, split into bf16 parts: the packed K runs
+  // pass-major, packed panel j holding pass j / slots of slot j % slots,
+  // slots = k / (passes * bk)).
   using Elem = typename std::conditional<kF32, float, uint16_t>::type;
   const Elem* const src = reinterpret_cast<const Elem*>(src_v);
   constexpr int nops = nops_of(kAlgo);
@@ -409,8 +413,12 @@ __global__ __launch_bounds__(256) void pack_operand(const void* __restrict__ src
     if (st >= nstages) break;
     const int64_t kp = st * TK + half * 8;
     const int64_t panel = kp / hk;
+    const int64_t slots = k / ((int64_t)passes * bk);
+    const int64_t pass = kF32 ? panel / slots : 0;
+    const int64_t slot = panel - pass * slots;
+    const int part = kF32 ? pass_part(kSide == 1, passes, (int)pass) : 0;
     // Map entries are clamped to the source, so a bad map cannot read out of bounds.
-    const int64_t src_panel = panels ? min(max(panels[panel], 0), src_panels - 1) : panel;
+    const int64_t src_panel = panels ? min(max(panels[slot], 0), src_panels - 1) : slot;
     const int64_t lo = src_panel * bk + kp % hk, hi = lo + hk;
     F8 x[4];
     if constexpr (kSide == 2) {
@@ -430,20 +438,23 @@ __global__ __launch_bounds__(256) void pack_operand(const void* __restrict__ src
       x[3] = load_row(second, hi);
     }
     uint8_t* const dst = dst_tile + st * (int64_t)(nops * kBlocks * kFrag);
+    auto store = [&](int op, const F8& v) {
+      *reinterpret_cast<u32x4*>(dst + op * kBlocks * kFrag) = kF32 ? pack8_part(v, part) : pack8(v);
+    };
     if constexpr (kAlgo == 7) {
-      u32x4 ops[7];
+      F8 ops[7];
       if constexpr (kSide != 1) {
         permute_quadrants(x, perm & 1, (perm >> 1) & 1);  // A: (rows, K halves)
-        formula_ops_f<0, !kF32>(formula, x, ops);
+        formula_vals<0, !kF32>(formula, x, ops);
       } else {
         permute_quadrants(x, (perm >> 1) & 1, (perm >> 2) & 1);  // B: (K halves, columns)
-        formula_ops_f<1, !kF32>(formula, x, ops);
+        formula_vals<1, !kF32>(formula, x, ops);
       }
 #pragma unroll
-      for (int op = 0; op < 7; ++op) *reinterpret_cast<u32x4*>(dst + op * kBlocks * kFrag) = ops[op];
+      for (int op = 0; op < 7; ++op) store(op, ops[op]);
     } else {
 #pragma unroll
-      for (int op = 0; op < 4; ++op) *reinterpret_cast<u32x4*>(dst + op * kBlocks * kFrag) = pack8(x[op]);
+      for (int op = 0; op < 4; ++op) store(op, x[op]);
     }
   }
 }

@@ -174,18 +174,18 @@ int check_variant(int32_t algo, int32_t formula, int32_t perm) {
 
 template <int kAlgo, int kSide>
 int launch_pack(const void* src, bool src_f32, int64_t ld, int64_t rows, int64_t k, int32_t tile_rows, int32_t bk,
-                int32_t formula, int32_t perm, const int32_t* panels, int32_t src_panels, uint8_t* out,
-                hipStream_t stream) {
+                int32_t formula, int32_t perm, const int32_t* panels, int32_t src_panels, int32_t passes,
+                uint8_t* out, hipStream_t stream) {
   const int64_t nstages = k / (2 * packed::TK);
   const int64_t waves = (rows / 64) * ((nstages + packed::kPackStages - 1) / packed::kPackStages);
   const int64_t blocks = (waves + 3) / 4;
   if (blocks >= ((int64_t)1 << 31)) return fail(SMX_ERR_UNSUPPORTED, "operand too large to pack");
   if (src_f32)
     hipLaunchKernelGGL((packed::pack_operand<kAlgo, kSide, true>), dim3((unsigned)blocks), dim3(256), 0, stream, src,
-                       ld, rows, k, tile_rows, bk, formula, perm, panels, src_panels, out);
+                       ld, rows, k, tile_rows, bk, formula, perm, panels, src_panels, passes, out);
   else
     hipLaunchKernelGGL((packed::pack_operand<kAlgo, kSide, false>), dim3((unsigned)blocks), dim3(256), 0, stream, src,
-                       ld, rows, k, tile_rows, bk, formula, perm, panels, src_panels, out);
+                       ld, rows, k, tile_rows, bk, formula, perm, panels, src_panels, 1, out);
   return check_launch();
 }
 
@@ -255,8 +255,8 @@ int smx_packed_bytes(int32_t algo, int64_t rows, int64_t k, int64_t* bytes) {
 }
 
 int smx_pack_operand(int32_t algo, int32_t formula, int32_t block_permutation, int32_t side, int64_t rows, int64_t k,
-                     const void* src, int32_t src_dtype, int64_t ld, int32_t tile_rows, int32_t bk,
-                     const int32_t* panels, int64_t src_k, void* out, void* stream) {
+                     const void* src, int32_t src_dtype, int32_t passes, int64_t ld, int32_t tile_rows,
+                     int32_t bk, const int32_t* panels, int64_t src_k, void* out, void* stream) {
   g_error[0] = 0;
   if (algo != SMX_ALGO_STRASSEN && algo != SMX_ALGO_CUBIC) return fail(SMX_ERR_INVALID, "algo must be 7 or 8");
   if (int rc = check_variant(algo, formula, block_permutation)) return rc;
@@ -272,7 +272,12 @@ int smx_pack_operand(int32_t algo, int32_t formula, int32_t block_permutation, i
   if (src_dtype != SMX_DTYPE_BF16 && src_dtype != SMX_DTYPE_F32)
     return fail(SMX_ERR_INVALID, "src_dtype must be SMX_DTYPE_BF16 (0) or SMX_DTYPE_F32 (1), got %d", src_dtype);
   const bool src_f32 = src_dtype == SMX_DTYPE_F32;
-  if (!panels) src_k = k;
+  if (passes != 1 && passes != 3 && passes != 6)
+    return fail(SMX_ERR_INVALID, "passes must be 1, 3 or 6, got %d", passes);
+  if (passes > 1 && !src_f32) return fail(SMX_ERR_INVALID, "multi-pass products need a float32 source");
+  if (k % ((int64_t)passes * bk))
+    return fail(SMX_ERR_INVALID, "the packed K (%lld) must hold whole passes of bk panels", (long long)k);
+  if (!panels) src_k = k / passes;
   if (src_k <= 0 || src_k % bk || src_k / bk >= ((int64_t)1 << 31))
     return fail(SMX_ERR_INVALID, "the source K (%lld) must be a positive multiple of bk", (long long)src_k);
   // Row-major sources are read 16 bytes at a time: rows must stay 16-byte aligned.
@@ -284,13 +289,13 @@ int smx_pack_operand(int32_t algo, int32_t formula, int32_t block_permutation, i
   hipStream_t st = (hipStream_t)stream;
   const int32_t sp = (int32_t)(src_k / bk);
   if (algo == SMX_ALGO_STRASSEN) {
-    if (side == SMX_SIDE_LHS) return launch_pack<7, 0>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
-    if (side == SMX_SIDE_RHS) return launch_pack<7, 1>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
-    return launch_pack<7, 2>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
+    if (side == SMX_SIDE_LHS) return launch_pack<7, 0>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, passes, o8, st);
+    if (side == SMX_SIDE_RHS) return launch_pack<7, 1>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, passes, o8, st);
+    return launch_pack<7, 2>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, passes, o8, st);
   }
-  if (side == SMX_SIDE_LHS) return launch_pack<8, 0>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
-  if (side == SMX_SIDE_RHS) return launch_pack<8, 1>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
-  return launch_pack<8, 2>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, o8, st);
+  if (side == SMX_SIDE_LHS) return launch_pack<8, 0>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, passes, o8, st);
+  if (side == SMX_SIDE_RHS) return launch_pack<8, 1>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, passes, o8, st);
+  return launch_pack<8, 2>(s16, src_f32, ld, rows, k, tile_rows, bk, formula, block_permutation, panels, sp, passes, o8, st);
 }
 
 int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, const void* residual, const void* bias,

@@ -31,10 +31,41 @@ import torch
 
 from . import _lib
 
-__all__ = ["PackedOperand", "SplitOperand", "ExactSchedule", "exact_schedule", "pack_operand",
+__all__ = ["PackedOperand", "SplitOperand", "ExactSchedule", "exact_schedule", "pack_operand", "precision_passes",
            "strassen_weight_layout", "cubic_weight_layout", "pack_activation"]
 
 _ALGOS = {_lib.SMX_ALGO_STRASSEN: "strassen", _lib.SMX_ALGO_CUBIC: "cubic"}
+
+# jax.lax.Precision names and their string aliases -> bf16 passes per product
+# of FP32 operands (DEFAULT one pass; HIGH the 3-pass and HIGHEST the 6-pass
+# bf16 product).
+_PRECISION_PASSES = {"DEFAULT": 1, "FASTEST": 1, "BFLOAT16": 1,
+                     "HIGH": 3, "BFLOAT16_3X": 3, "TENSORFLOAT32": 3,
+                     "HIGHEST": 6, "FLOAT32": 6}
+
+
+def precision_passes(dot_precision, dtype):
+    """bf16 passes per product for ``dot_precision`` on inputs of ``dtype``:
+    1 for bf16 inputs (their operands have no low-order part: the reference
+    forms bf16 operand sums in bf16, so HIGH / HIGHEST products equal the
+    one-pass product), else 1 / 3 / 6 for DEFAULT / HIGH / HIGHEST. A pair
+    (lhs, rhs) must name one precision."""
+    if isinstance(dot_precision, (tuple, list)):
+        if len(dot_precision) != 2:
+            raise ValueError(f"dot_precision pair expected, got {dot_precision!r}")
+        first, second = (precision_passes(p, torch.float32) for p in dot_precision)
+        if first != second:
+            raise NotImplementedError("dot_precision pairs with two different precisions are not implemented")
+        dot_precision = dot_precision[0]
+    if dot_precision is None:
+        passes = 1
+    else:
+        name = str(getattr(dot_precision, "name", dot_precision)).upper()
+        name = name.rsplit(".", 1)[-1]
+        if name not in _PRECISION_PASSES:
+            raise ValueError(f"unknown dot_precision {dot_precision!r}")
+        passes = _PRECISION_PASSES[name]
+    return passes if dtype == torch.float32 else 1
 
 
 class ExactSchedule:
@@ -105,9 +136,12 @@ class PackedOperand:
     """
 
     def __init__(self, data, *, algo, side, rows, k, tile_rows, bk, formula="classical", block_permutation=0,
-                 source_dtype=torch.bfloat16):
+                 source_dtype=torch.bfloat16, passes=1):
         self.data = data
         self.source_dtype = source_dtype  # the packed fragments are bf16 either way
+        # bf16 passes per product (FP32 sources at HIGH / HIGHEST): the packed
+        # K is passes * k, pass-major
+        self.passes = int(passes)
         self.algo, self.side = int(algo), side
         self.rows, self.k, self.tile_rows, self.bk = int(rows), int(k), int(tile_rows), int(bk)
         self.formula, self.block_permutation = formula, int(block_permutation)
@@ -133,6 +167,8 @@ class PackedOperand:
     def __repr__(self):
         variant = "" if self.algo != _lib.SMX_ALGO_STRASSEN else \
             f", formula={self.formula}, block_permutation={self.block_permutation}"
+        if self.passes > 1:
+            variant += f", passes={self.passes}"
         return (f"PackedOperand({_ALGOS[self.algo]}, {self.side}, shape={tuple(self.shape)}, "
                 f"tile_rows={self.tile_rows}, bk={self.bk}{variant}, device={self.device})")
 
@@ -145,7 +181,7 @@ class SplitOperand(PackedOperand):
     def __init__(self, ordinary, exact, *, side, rows, k, tile_rows, bk, formula, block_permutation, schedule):
         super().__init__(exact.data, algo=_lib.SMX_ALGO_STRASSEN, side=side, rows=rows, k=k, tile_rows=tile_rows,
                          bk=bk, formula=formula, block_permutation=block_permutation,
-                         source_dtype=exact.source_dtype)
+                         source_dtype=exact.source_dtype, passes=exact.passes)
         self.ordinary, self.exact, self.schedule = ordinary, exact, schedule
 
     def __repr__(self):
@@ -160,27 +196,28 @@ def packed_bytes(algo, rows, k):
     return out.value
 
 
-def _pack(src, *, algo, side, rows, k, tile_rows, bk, formula, block_permutation, panels=None):
+def _pack(src, *, algo, side, rows, k, tile_rows, bk, formula, block_permutation, panels=None, passes=1):
     """One smx_pack_operand call over ``src`` (rows x K source, or K x rows
     for lhs_t); ``panels`` (a device int32 map) selects the K panels to
-    pack, in order."""
+    pack, in order; ``passes`` > 1 packs the bf16 parts of a multi-pass
+    product after each panel."""
     packed_k = k if panels is None else panels.numel() * bk
-    nbytes = packed_bytes(algo, rows, packed_k)
+    nbytes = packed_bytes(algo, rows, packed_k * passes)
     data = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=src.device)
     side_id = {"lhs": _lib.SMX_SIDE_LHS, "rhs": _lib.SMX_SIDE_RHS, "lhs_t": _lib.SMX_SIDE_LHS_T}[side]
     stream = torch.cuda.current_stream(src.device).cuda_stream
     src_dtype = _lib.SMX_DTYPE_F32 if src.dtype == torch.float32 else _lib.SMX_DTYPE_BF16
-    rc = _lib.load().smx_pack_operand(algo, _lib.SMX_FORMULA[formula], block_permutation, side_id, rows, packed_k,
-                                      _lib.ptr(src), src_dtype, src.stride(0), tile_rows, bk, _lib.ptr(panels), k,
-                                      _lib.ptr(data), stream)
+    rc = _lib.load().smx_pack_operand(algo, _lib.SMX_FORMULA[formula], block_permutation, side_id, rows,
+                                      packed_k * passes, _lib.ptr(src), src_dtype, passes, src.stride(0), tile_rows,
+                                      bk, _lib.ptr(panels), k, _lib.ptr(data), stream)
     _lib.check(rc)
     return PackedOperand(data, algo=algo, side="rhs" if side == "rhs" else "lhs", rows=rows, k=packed_k,
                          tile_rows=tile_rows, bk=bk, formula=formula, block_permutation=block_permutation,
-                         source_dtype=src.dtype)
+                         source_dtype=src.dtype, passes=passes)
 
 
 def pack_operand(x, *, algo, side, tile_rows, bk, formula="classical", block_permutation=0, classical_panels=(),
-                 panel_schedule=None):
+                 panel_schedule=None, dot_precision=None):
     """Pack ``x`` (bf16 on the HIP device): ``a [M, K]`` for ``side="lhs"``,
     the same ``a`` stored transposed as ``[K, M]`` for ``side="lhs_t"``, or a
     weight ``b [K, N]`` for ``side="rhs"`` (any strides; a K-contiguous view
@@ -189,7 +226,9 @@ def pack_operand(x, *, algo, side, tile_rows, bk, formula="classical", block_per
     ``formula`` ("classical", "dual" or "powers") after the quadrant swaps of
     ``block_permutation``; both operands of a GEMM must be packed alike. With
     exact panels (``classical_panels`` or ``panel_schedule``) a Strassen
-    operand becomes a ``SplitOperand``."""
+    operand becomes a ``SplitOperand``. A float32 ``x`` is packed for the
+    product of ``dot_precision`` (DEFAULT: each operand rounded once to bf16;
+    HIGH / HIGHEST: its bf16 parts for 3 / 6 passes)."""
     if formula not in _lib.SMX_FORMULA:
         raise ValueError("formula_variant must be 'classical', 'dual', or 'powers'")
     if side not in ("lhs", "rhs", "lhs_t"):
@@ -214,10 +253,11 @@ def pack_operand(x, *, algo, side, tile_rows, bk, formula="classical", block_per
             src = src.contiguous()
     if rows % tile_rows or k % bk:
         raise ValueError(f"operand [{rows}, {k}] (rows x K) does not tile by ({tile_rows}, {bk})")
+    passes = precision_passes(dot_precision, x.dtype)
     common = dict(side=side, rows=rows, k=k, tile_rows=tile_rows, bk=bk)
     schedule = exact_schedule(k // bk, classical_panels=classical_panels, panel_schedule=panel_schedule)
     if schedule is None:
-        return _pack(src, algo=algo, formula=formula, block_permutation=block_permutation, **common)
+        return _pack(src, algo=algo, formula=formula, block_permutation=block_permutation, passes=passes, **common)
     if algo != _lib.SMX_ALGO_STRASSEN:
         raise ValueError("exact panels apply to the Strassen algorithm only")
     if formula == "powers":
@@ -225,34 +265,36 @@ def pack_operand(x, *, algo, side, tile_rows, bk, formula="classical", block_per
     ordinary = None
     if schedule.ordinary:
         ordinary = _pack(src, algo=algo, formula=formula, block_permutation=block_permutation,
-                         panels=schedule.panel_map("ordinary", x.device), **common)
+                         panels=schedule.panel_map("ordinary", x.device), passes=passes, **common)
     exact = _pack(src, algo=_lib.SMX_ALGO_CUBIC, formula="classical", block_permutation=0,
-                  panels=schedule.panel_map("exact", x.device), **common)
+                  panels=schedule.panel_map("exact", x.device), passes=passes, **common)
     common["side"] = "rhs" if side == "rhs" else "lhs"
     return SplitOperand(ordinary, exact, formula=formula, block_permutation=block_permutation, schedule=schedule,
                         **common)
 
 
 def strassen_weight_layout(b, bn, bk, *, formula_variant="classical", block_permutation=0, classical_panels=(),
-                           panel_schedule=None):
-    """Pre-sum and pack a bf16 ``[K, N]`` weight for ``strassen_matmul``
-    with the tile ``(bn, bk)`` (and the formula, block permutation and exact
-    panels the calls will use)."""
+                           panel_schedule=None, dot_precision=None):
+    """Pre-sum and pack a bf16 or float32 ``[K, N]`` weight for
+    ``strassen_matmul`` with the tile ``(bn, bk)`` (and the formula, block
+    permutation, exact panels and, for float32, ``dot_precision`` the calls
+    will use)."""
     return pack_operand(b, algo=_lib.SMX_ALGO_STRASSEN, side="rhs", tile_rows=bn, bk=bk,
                         formula=formula_variant, block_permutation=block_permutation,
-                        classical_panels=classical_panels, panel_schedule=panel_schedule)
+                        classical_panels=classical_panels, panel_schedule=panel_schedule,
+                        dot_precision=dot_precision)
 
 
-def cubic_weight_layout(b, bn, bk):
-    """Pack a bf16 ``[K, N]`` weight's quadrants for ``cubic_matmul`` with
-    the tile ``(bn, bk)``."""
-    return pack_operand(b, algo=_lib.SMX_ALGO_CUBIC, side="rhs", tile_rows=bn, bk=bk)
+def cubic_weight_layout(b, bn, bk, *, dot_precision=None):
+    """Pack a bf16 or float32 ``[K, N]`` weight's quadrants for
+    ``cubic_matmul`` with the tile ``(bn, bk)``."""
+    return pack_operand(b, algo=_lib.SMX_ALGO_CUBIC, side="rhs", tile_rows=bn, bk=bk, dot_precision=dot_precision)
 
 
 def pack_activation(a, algo, bm, bk, *, formula_variant="classical", block_permutation=0, classical_panels=(),
-                    panel_schedule=None):
+                    panel_schedule=None, dot_precision=None):
     """Pack an activation ``a [M, K]`` once for several GEMMs that share it
     (e.g. the q, k and v projections)."""
     return pack_operand(a, algo=algo, side="lhs", tile_rows=bm, bk=bk, formula=formula_variant,
                         block_permutation=block_permutation, classical_panels=classical_panels,
-                        panel_schedule=panel_schedule)
+                        panel_schedule=panel_schedule, dot_precision=dot_precision)

@@ -14,9 +14,15 @@ Differences a caller can observe, all raised as exceptions (never silent):
   ``strassen_pallas.py:228-232`` at its default ``dot_precision``, ``:889``,
   which makes one bf16 pass on a TPU): the packing pass forms each
   operand sum in float and rounds it once to bf16, and every product is one
-  bf16 MFMA pass into FP32. ``dot_precision`` HIGH / HIGHEST (multi-pass
-  products) raise ``NotImplementedError``. RoPE tables are read as bf16 (a
-  float32 table is rounded once on the host).
+  bf16 MFMA pass into FP32. ``dot_precision`` HIGH / HIGHEST run the 3- and
+  6-pass bf16 products: the packing pass splits each float operand into
+  bf16 parts (p0 = bf16(v), p1 = bf16(v - p0), p2 = bf16(v - p0 - p1)) and
+  lays the pass pairs out along K pass-major, smallest products first
+  ([p2 p0, p1 p1, p0 p2,] p1 p0, p0 p1, p0 p0), so one GEMM over 3K or 6K
+  sums them in FP32 with the leading pass added last. How XLA orders and
+  rounds these passes on a TPU is not visible here; the pass pairs are those
+  of its published bf16_3x / bf16_6x algorithms. RoPE tables are read as
+  bf16 (a float32 table is rounded once on the host).
 * The exact-panel policies (``classical_panels``, ``panel_schedule``) run as
   two GEMMs: Strassen over the ordinary K panels into an FP32 partial, then
   the matched cubic over the exact panels, which adds the partial before
@@ -30,8 +36,9 @@ Differences a caller can observe, all raised as exceptions (never silent):
 * ``formula_variant`` "dual" / "powers" and ``block_permutation`` run on
   packed operands: a plain weight is packed for the call (pack it once with
   ``strassen_weight_layout(..., formula_variant=, block_permutation=)``).
-* TPU-only knobs (``dot_precision`` for bf16 inputs, ``allow_input_fusion``
-  after its validation, ``vmem_limit_bytes``) are accepted and have no effect;
+* TPU-only knobs (``allow_input_fusion`` after its validation,
+  ``vmem_limit_bytes``) are accepted and have no effect, as is
+  ``dot_precision`` for bf16 inputs (bf16 operands have no low-order part);
   ``interpret=True`` raises ``NotImplementedError`` (there is no CPU path).
 * The kernel keeps seven persistent FP32 product accumulators and combines
   the quadrants once after the last K panel, so ``interleave_products`` and
@@ -52,7 +59,7 @@ import torch
 
 from . import _lib
 from .layouts import is_k_contiguous
-from .packing import PackedOperand, SplitOperand, exact_schedule, pack_operand
+from .packing import PackedOperand, SplitOperand, exact_schedule, pack_operand, precision_passes
 
 __all__ = [
     "strassen_matmul", "strassen_matmul_lhs_transposed", "cubic_matmul", "native_matmul", "check_tiling",
@@ -270,23 +277,10 @@ def _validate(a, b, *, bm, bn, bk, block_permutation, formula_variant,
     return m, k, n, classical_panels, out
 
 
-def _multi_pass(dot_precision):
-    """Whether ``dot_precision`` asks for more than the one-pass bf16 product
-    (HIGH / HIGHEST, as ``jax.lax.Precision`` members or strings)."""
-    if dot_precision is None:
-        return False
-    name = str(getattr(dot_precision, "name", dot_precision)).upper()
-    return not (name.endswith("DEFAULT") or name in ("BFLOAT16", "FASTEST"))
-
-
 def _unsupported(dtype, interpret, dot_precision=None):
     if interpret:
         raise NotImplementedError("interpret=True: the gfx950 kernel has no CPU interpreter path")
-    # FP32 inputs run as the reference's DEFAULT-precision path: operand sums
-    # in float, one bf16 pass per product. More passes are not built.
-    if dtype == torch.float32 and _multi_pass(dot_precision):
-        raise NotImplementedError("FP32 inputs at dot_precision HIGH/HIGHEST (multi-pass bf16 products) are not "
-                                  "implemented on gfx950; the FP32 path is the one-pass DEFAULT product")
+    precision_passes(dot_precision, dtype)  # an unknown precision raises here
 
 
 def _require_device(*tensors):
@@ -296,8 +290,15 @@ def _require_device(*tensors):
                              f"(got a tensor on {t.device})")
 
 
-def _check_packed(x, algo, side, tile_rows, bk, formula="classical", block_permutation=0):
+def _check_passes(x, name, passes):
+    if x.passes != passes:
+        raise ValueError(f"{name} was packed for {x.passes} bf16 pass(es) per product; the call's dot_precision "
+                         f"needs {passes} (pack it with the call's dot_precision)")
+
+
+def _check_packed(x, algo, side, tile_rows, bk, formula="classical", block_permutation=0, passes=1):
     name = "a" if side == "lhs" else "b"
+    _check_passes(x, name, passes)
     if x.algo != algo or x.side != side:
         raise ValueError(f"{name} was packed as {x!r}, not as the {side} of this algorithm")
     if (x.tile_rows, x.bk) != (tile_rows, bk):
@@ -346,19 +347,22 @@ def _norm_residual_add(algo, a, b, *, residual, norm_scale, norm_eps, **kw):
 def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
          rope_cos=None, rope_sin=None, rope_scale=None, rope_head_dim=128,
          rope_eps=1e-6, out_dtype=torch.bfloat16, formula="classical", block_permutation=0,
-         norm_scale=None, norm_eps=1e-6, schedule=None, partial=None):
+         norm_scale=None, norm_eps=1e-6, schedule=None, partial=None, dot_precision=None):
     if epilogue == "norm_residual_add":
         return _norm_residual_add(algo, a, b, residual=residual, norm_scale=norm_scale, norm_eps=norm_eps,
                                   bm=bm, bn=bn, bk=bk, formula=formula, block_permutation=block_permutation,
-                                  schedule=schedule, out_dtype=out_dtype)
+                                  schedule=schedule, out_dtype=out_dtype, dot_precision=dot_precision)
     if schedule is not None:
         return _run_split(a, b, bm=bm, bn=bn, bk=bk, schedule=schedule, formula=formula,
                           block_permutation=block_permutation, epilogue=epilogue, residual=residual, bias=bias,
                           rope_cos=rope_cos, rope_sin=rope_sin, rope_scale=rope_scale,
-                          rope_head_dim=rope_head_dim, rope_eps=rope_eps, out_dtype=out_dtype)
+                          rope_head_dim=rope_head_dim, rope_eps=rope_eps, out_dtype=out_dtype,
+                          dot_precision=dot_precision)
     lib = _lib.load()
     m, k = a.shape
     n = b.shape[1]
+    # bf16 passes per product: the packed operands hold passes * k columns
+    passes = precision_passes(dot_precision, a.dtype)
     variant = dict(formula=formula, block_permutation=block_permutation)
     # Formula variants and block permutations run on packed operands; a
     # plain weight is packed for the call, as is any plain weight whose tile
@@ -373,19 +377,19 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
                          "cubic_weight_layout)")
     b_layout = _lib.SMX_B_PACKED if packed else _lib.SMX_B_KCONTIG
     if isinstance(b, PackedOperand):
-        _check_packed(b, algo, "rhs", bn, bk, **variant)
+        _check_packed(b, algo, "rhs", bn, bk, passes=passes, **variant)
     if isinstance(a, PackedOperand):
-        _check_packed(a, algo, "lhs", bm, bk, **variant)
+        _check_packed(a, algo, "lhs", bm, bk, passes=passes, **variant)
     _check_device_tiling(algo, epilogue, bm, bn, bk, b_layout)
     _require_device(a.data if isinstance(a, PackedOperand) else a,
                     b.data if isinstance(b, PackedOperand) else b,
                     residual, bias, rope_cos, rope_sin, rope_scale)
     if packed:
         if not isinstance(b, PackedOperand):
-            b = pack_operand(b, algo=algo, side="rhs", tile_rows=bn, bk=bk, **variant)
+            b = pack_operand(b, algo=algo, side="rhs", tile_rows=bn, bk=bk, dot_precision=dot_precision, **variant)
         if not isinstance(a, PackedOperand):
-            a = pack_operand(a, algo=algo, side="lhs", tile_rows=bm, bk=bk, **variant)
-        a_ptr, b_ptr, lda, ldb = a.data, b.data, k, k
+            a = pack_operand(a, algo=algo, side="lhs", tile_rows=bm, bk=bk, dot_precision=dot_precision, **variant)
+        a_ptr, b_ptr, lda, ldb = a.data, b.data, k * passes, k * passes
     else:
         if a.stride(1) != 1 or a.stride(0) % 8 or a.data_ptr() % 16:
             a = a.contiguous()
@@ -396,7 +400,7 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
     out_cols = n // 2 if epilogue in ("swiglu", "geglu") else n
     c = torch.empty((m, out_cols), dtype=out_dtype, device=a.device)
     desc = _lib.SmxGemmDesc()
-    desc.m, desc.n, desc.k = m, n, k
+    desc.m, desc.n, desc.k = m, n, k * passes
     desc.lda, desc.ldb, desc.ldc = lda, ldb, c.stride(0)
     desc.bm, desc.bn, desc.bk = bm, bn, bk
     desc.algo = algo
@@ -439,7 +443,8 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
     return c
 
 
-def _run_split(a, b, *, bm, bn, bk, schedule, formula, block_permutation, out_dtype, **epilogue_args):
+def _run_split(a, b, *, bm, bn, bk, schedule, formula, block_permutation, out_dtype, dot_precision=None,
+               **epilogue_args):
     """An exact-panel schedule (``strassen_pallas.py:575-586``, ``:713-735``):
     Strassen over the ordinary K panels with an FP32 result, then the
     matched cubic over the exact panels (the eight products of
@@ -459,6 +464,7 @@ def _run_split(a, b, *, bm, bn, bk, schedule, formula, block_permutation, out_dt
         if x.schedule != schedule:
             raise ValueError(f"{name} was packed for the exact panels {x.schedule.exact}; called with "
                              f"{schedule.exact}")
+        _check_passes(x, name, precision_passes(dot_precision, x.dtype))
         if (x.formula, x.block_permutation) != (formula, block_permutation):
             raise ValueError(f"{name} was packed for formula_variant={x.formula!r}, "
                              f"block_permutation={x.block_permutation}; called with "
@@ -467,16 +473,16 @@ def _run_split(a, b, *, bm, bn, bk, schedule, formula, block_permutation, out_dt
     _require_device(a.data if isinstance(a, PackedOperand) else a, b.data if isinstance(b, PackedOperand) else b)
     if not isinstance(a, SplitOperand):
         a = pack_operand(a, algo=_lib.SMX_ALGO_STRASSEN, side="lhs", tile_rows=bm, bk=bk, panel_schedule=schedule,
-                         **variant)
+                         dot_precision=dot_precision, **variant)
     if not isinstance(b, SplitOperand):
         b = pack_operand(b, algo=_lib.SMX_ALGO_STRASSEN, side="rhs", tile_rows=bn, bk=bk, panel_schedule=schedule,
-                         **variant)
+                         dot_precision=dot_precision, **variant)
     partial = None
     if a.ordinary is not None:
         partial = _run(_lib.SMX_ALGO_STRASSEN, a.ordinary, b.ordinary, bm=bm, bn=bn, bk=bk,
-                       out_dtype=torch.float32, **variant)
+                       out_dtype=torch.float32, dot_precision=dot_precision, **variant)
     return _run(_lib.SMX_ALGO_CUBIC, a.exact, b.exact, bm=bm, bn=bn, bk=bk, out_dtype=out_dtype, partial=partial,
-                **epilogue_args)
+                dot_precision=dot_precision, **epilogue_args)
 
 
 def strassen_matmul(
@@ -540,7 +546,7 @@ def strassen_matmul(
                 residual=residual, bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
                 rope_scale=rope_scale, rope_head_dim=rope_head_dim, rope_eps=rope_eps,
                 out_dtype=out_dtype, formula=formula_variant, block_permutation=block_permutation,
-                norm_scale=norm_scale, norm_eps=norm_eps, schedule=schedule)
+                norm_scale=norm_scale, norm_eps=norm_eps, schedule=schedule, dot_precision=dot_precision)
 
 
 def strassen_matmul_lhs_transposed(a, b, *, bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_BK, dot_precision=None,
@@ -553,8 +559,8 @@ def strassen_matmul_lhs_transposed(a, b, *, bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_B
     materialised) while forming the A operand sums; ``b`` is a ``[K, N]``
     tensor (packed on each call) or a ``strassen_weight_layout`` weight.
     Arguments, checks and messages follow ``:1250-1267``; FP32 inputs run
-    the one-pass DEFAULT product, and ``dot_precision`` HIGH/HIGHEST and
-    ``interpret=True`` raise ``NotImplementedError``.
+    the product of ``dot_precision`` (one pass at DEFAULT, 3 / 6 bf16 passes
+    at HIGH / HIGHEST) and ``interpret=True`` raises ``NotImplementedError``.
     """
     if a.dim() != 2 or b.dim() != 2:
         raise ValueError("strassen_matmul_lhs_transposed expects rank-2 inputs")
@@ -580,10 +586,12 @@ def strassen_matmul_lhs_transposed(a, b, *, bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_B
     _unsupported(a.dtype, interpret, dot_precision)
     _check_device_tiling(_lib.SMX_ALGO_STRASSEN, None, bm, bn, bk, _lib.SMX_B_PACKED)
     _require_device(a, b.data if isinstance(b, PackedOperand) else b)
-    packed_a = pack_operand(a, algo=_lib.SMX_ALGO_STRASSEN, side="lhs_t", tile_rows=bm, bk=bk)
+    packed_a = pack_operand(a, algo=_lib.SMX_ALGO_STRASSEN, side="lhs_t", tile_rows=bm, bk=bk,
+                            dot_precision=dot_precision)
     if not isinstance(b, PackedOperand):
-        b = pack_operand(b, algo=_lib.SMX_ALGO_STRASSEN, side="rhs", tile_rows=bn, bk=bk)
-    return _run(_lib.SMX_ALGO_STRASSEN, packed_a, b, bm=bm, bn=bn, bk=bk, out_dtype=out_dtype)
+        b = pack_operand(b, algo=_lib.SMX_ALGO_STRASSEN, side="rhs", tile_rows=bn, bk=bk, dot_precision=dot_precision)
+    return _run(_lib.SMX_ALGO_STRASSEN, packed_a, b, bm=bm, bn=bn, bk=bk, out_dtype=out_dtype,
+                dot_precision=dot_precision)
 
 
 def cubic_matmul(a, b, *, variant="blocked", bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_BK,
@@ -634,7 +642,7 @@ def cubic_matmul(a, b, *, variant="blocked", bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_
     return _run(_lib.SMX_ALGO_CUBIC, a, b, bm=bm, bn=bn, bk=bk, epilogue=epilogue,
                 residual=residual, bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
                 rope_scale=rope_scale, rope_head_dim=rope_head_dim, rope_eps=rope_eps,
-                out_dtype=out_dtype, norm_scale=norm_scale, norm_eps=norm_eps)
+                out_dtype=out_dtype, norm_scale=norm_scale, norm_eps=norm_eps, dot_precision=dot_precision)
 
 
 def native_matmul(a, b):

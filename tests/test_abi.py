@@ -168,7 +168,7 @@ def test_pack_operand_rejects_bad_arguments(args, code):
     lib = _lib.load()
     buf = (ctypes.c_uint8 * 16)()
     p = ctypes.cast(buf, ctypes.c_void_p)
-    assert lib.smx_pack_operand(algo, 0, 0, side, rows, k, p, _lib.SMX_DTYPE_BF16, ld, tile_rows, bk, None, 0, p,
+    assert lib.smx_pack_operand(algo, 0, 0, side, rows, k, p, _lib.SMX_DTYPE_BF16, 1, ld, tile_rows, bk, None, 0, p,
                                 None) == code
     assert _lib.last_error()
 
@@ -183,7 +183,7 @@ def test_pack_operand_panel_map_arguments(src_k, ld, code):
     lib = _lib.load()
     buf = (ctypes.c_uint8 * 16)()
     p = ctypes.cast(buf, ctypes.c_void_p)
-    assert lib.smx_pack_operand(7, 0, 0, 0, 512, 512, p, _lib.SMX_DTYPE_BF16, ld, 256, 512, p, src_k, p, None) == code
+    assert lib.smx_pack_operand(7, 0, 0, 0, 512, 512, p, _lib.SMX_DTYPE_BF16, 1, ld, 256, 512, p, src_k, p, None) == code
     assert "source K" in _lib.last_error() or "ld must be" in _lib.last_error()
 
 
@@ -192,7 +192,7 @@ def test_pack_operand_rejects_bad_variants(algo, formula, perm):
     lib = _lib.load()
     buf = (ctypes.c_uint8 * 16)()
     p = ctypes.cast(buf, ctypes.c_void_p)
-    assert lib.smx_pack_operand(algo, formula, perm, 0, 512, 512, p, _lib.SMX_DTYPE_BF16, 512, 256, 512, None, 0, p,
+    assert lib.smx_pack_operand(algo, formula, perm, 0, 512, 512, p, _lib.SMX_DTYPE_BF16, 1, 512, 256, 512, None, 0, p,
                                 None) == \
         _lib.SMX_ERR_INVALID
 
@@ -208,8 +208,25 @@ def test_pack_operand_source_dtype(src_dtype, ld, code):
     lib = _lib.load()
     buf = (ctypes.c_uint8 * 16)()
     p = ctypes.cast(buf, ctypes.c_void_p)
-    assert lib.smx_pack_operand(7, 0, 0, 0, 512, 512, p, src_dtype, ld, 256, 512, None, 0, p, None) == code
+    assert lib.smx_pack_operand(7, 0, 0, 0, 512, 512, p, src_dtype, 1, ld, 256, 512, None, 0, p, None) == code
     assert _lib.last_error()
+
+
+@pytest.mark.parametrize("src_dtype,passes,k,code", [
+    (_lib.SMX_DTYPE_F32, 2, 1536, _lib.SMX_ERR_INVALID),   # passes not 1, 3 or 6
+    (_lib.SMX_DTYPE_F32, 0, 1536, _lib.SMX_ERR_INVALID),
+    (_lib.SMX_DTYPE_BF16, 3, 1536, _lib.SMX_ERR_INVALID),  # multi-pass needs a float32 source
+    (_lib.SMX_DTYPE_F32, 3, 1024, _lib.SMX_ERR_INVALID),   # packed K not whole passes of bk panels
+    (_lib.SMX_DTYPE_F32, 6, 1536, _lib.SMX_ERR_INVALID),
+])
+def test_pack_operand_passes(src_dtype, passes, k, code):
+    """Multi-pass packing: 3 or 6 passes of a float32 source; the packed K is
+    passes x the source K."""
+    lib = _lib.load()
+    buf = (ctypes.c_uint8 * 16)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    assert lib.smx_pack_operand(7, 0, 0, 0, 512, k, p, src_dtype, passes, 512, 256, 512, None, 0, p, None) == code
+    assert "pass" in _lib.last_error()
 
 
 def test_powers_refuses_fused_epilogues():

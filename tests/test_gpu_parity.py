@@ -113,13 +113,13 @@ def _run_arm(arm, a_dev, b_dev, *, bm, bn, bk, **kw):
     if arm == "strassen_plain":
         return smx.strassen_matmul(a_dev, b_dev, bm=bm, bn=bn, bk=bk, **kw)
     if arm == "strassen_packed":
-        w = smx.strassen_weight_layout(b_dev, bn, bk)
+        w = smx.strassen_weight_layout(b_dev, bn, bk, dot_precision=kw.get("dot_precision"))
         return smx.strassen_matmul(a_dev, w, bm=bm, bn=bn, bk=bk, **kw)
     kw.pop("interleave_products", None)
     kw.pop("product_aware_swiglu", None)
     kw.pop("product_aware_residual", None)
     if arm == "cubic_packed":
-        b_dev = smx.cubic_weight_layout(b_dev, bn, bk)
+        b_dev = smx.cubic_weight_layout(b_dev, bn, bk, dot_precision=kw.get("dot_precision"))
     return smx.cubic_matmul(a_dev, b_dev, bm=bm, bn=bn, bk=bk, **kw)
 
 
@@ -736,6 +736,82 @@ def test_fp32_exact_panels(panels, formula, perm):
     assert_f32_close(got, o.strassen_matmul(a, b, output_dtype="float32", input_dtype="float32", **kw), 2048)
     ref = a.astype(np.float64) @ b.astype(np.float64)
     assert rel_l2(got, ref) <= 1e-2
+
+
+# ---------------------------------------------------------------------------
+# FP32 inputs at dot_precision HIGH / HIGHEST (3 / 6 bf16 passes per product)
+# ---------------------------------------------------------------------------
+
+PRECISIONS = ("high", "highest")
+# float64-product error bounds per precision on N(0,1) x N(0,0.02) data at
+# K = 2048 (HIGH drops second-order parts, ~1e-5; HIGHEST reaches the FP32
+# accumulation level, ~1e-6)
+PRECISION_BOUND = {"high": 3e-5, "highest": 3e-6}
+
+
+@pytest.mark.parametrize("precision", PRECISIONS)
+@pytest.mark.parametrize("algo,formula,perm", [(7, "classical", 0), (7, "dual", 3), (7, "powers", 6),
+                                               (8, "classical", 0)])
+def test_multi_pass_pack_matches_oracle(precision, algo, formula, perm):
+    """Packed bf16 parts, panel by panel with each panel's passes, bit for
+    bit (lhs, transposed lhs and rhs)."""
+    _, a, b = _gaussian32(511, 512, 1024, 512)
+    kw = dict(formula=formula, block_permutation=perm, dot_precision=precision)
+    okw = dict(input_dtype="float32", dot_precision=precision)
+    pa = smx.pack_operand(dev32(a), algo=algo, side="lhs", tile_rows=256, bk=512, **kw)
+    assert pa.passes == {"high": 3, "highest": 6}[precision] and pa.k == 1024
+    want_a = o.packed_operand(a, algo, "lhs", 256, 512, formula, perm, **okw)
+    assert np.array_equal(host(pa.data), want_a)
+    pt = smx.pack_operand(dev32(a.T), algo=algo, side="lhs_t", tile_rows=256, bk=512, **kw)
+    assert np.array_equal(host(pt.data), want_a)
+    pb = smx.pack_operand(dev32_weight(b), algo=algo, side="rhs", tile_rows=256, bk=512, **kw)
+    assert np.array_equal(host(pb.data), o.packed_operand(b, algo, "rhs", 256, 512, formula, perm, **okw))
+
+
+@pytest.mark.parametrize("precision", PRECISIONS)
+@pytest.mark.parametrize("arm", ARMS)
+def test_multi_pass_matches_oracle(precision, arm):
+    _, a, b = _gaussian32(512, 512, 2048, 512)
+    kw = dict(bm=256, bn=256, bk=512, dot_precision=precision)
+    okw = dict(kw, input_dtype="float32") if arm.startswith("strassen") else dict(kw)
+    got = host(run_arm(arm, dev32(a), dev32_weight(b), **kw))
+    want = oracle_arm(arm, a, b, output_dtype="float32", **okw)
+    passes = {"high": 3, "highest": 6}[precision]
+    assert_f32_close(got, want, passes * 2048)
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    assert rel_l2(got, ref) <= PRECISION_BOUND[precision]
+    assert rel_l2(got, ref) <= 1.5 * rel_l2(want, ref) + 1e-7
+
+
+def test_multi_pass_variants_and_epilogues():
+    """Formula variants, an offline-packed weight, exact panels, the
+    transposed LHS and a fused epilogue at HIGHEST; a weight packed for
+    another precision is refused."""
+    rng, a, b = _gaussian32(513, 512, 2048, 512)
+    kw = dict(bm=256, bn=256, bk=512, dot_precision="highest")
+    okw = dict(kw, input_dtype="float32", output_dtype="float32")
+    for formula, perm in (("dual", 5), ("powers", 2)):
+        vkw = dict(formula_variant=formula, block_permutation=perm)
+        got = host(smx.strassen_matmul(dev32(a), dev32_weight(b), **vkw, **kw))
+        assert_f32_close(got, o.strassen_matmul(a, b, **vkw, **okw), 6 * 2048)
+    w = smx.strassen_weight_layout(dev32_weight(b), 256, 512, dot_precision="highest")
+    got = host(smx.strassen_matmul(dev32(a), w, **kw))
+    assert_f32_close(got, o.strassen_matmul(a, b, **okw), 6 * 2048)
+    with pytest.raises(ValueError, match="bf16 pass"):
+        smx.strassen_matmul(dev32(a), w, bm=256, bn=256, bk=512, dot_precision="high")
+    with pytest.raises(ValueError, match="bf16 pass"):
+        smx.strassen_matmul(dev32(a), w, bm=256, bn=256, bk=512)
+    got = host(smx.strassen_matmul(dev32(a), dev32_weight(b), classical_panels=(1, 2), **kw))
+    assert_f32_close(got, o.strassen_matmul(a, b, classical_panels=(1, 2), **okw), 6 * 2048)
+    got = host(smx.strassen_matmul_lhs_transposed(dev32(a.T), dev32(b), bm=256, bn=256, bk=512,
+                                                  dot_precision="high"))
+    assert_f32_close(got, o.strassen_matmul(a, b, **dict(okw, dot_precision="high")), 3 * 2048)
+    r = rng.standard_normal((512, 512)).astype(np.float32)
+    got = host(smx.strassen_matmul(dev32(a), dev32_weight(b), epilogue="residual_add", residual=dev32(r), **kw))
+    want = o.strassen_matmul(a, b, epilogue="residual_add", residual=r, **okw)
+    assert rel_l2(got, want) <= 1e-6
+    ref = a.astype(np.float64) @ b.astype(np.float64) + r
+    assert rel_l2(got, ref) <= PRECISION_BOUND["highest"]
 
 
 # ---------------------------------------------------------------------------

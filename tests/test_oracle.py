@@ -533,3 +533,111 @@ def test_fp32_inputs_are_a_one_pass_bf16_product():
     # the cubic control on FP32 inputs is the bf16-rounded-input cubic
     np.testing.assert_array_equal(o.cubic_blocked_matmul(a, b, **kw),
                                   o.cubic_blocked_matmul(o.bf16_round(a), o.bf16_round(b), **kw))
+
+
+# ---------------------------------------------------------------------------
+# Multi-pass FP32 products (dot_precision HIGH / HIGHEST)
+# ---------------------------------------------------------------------------
+# XLA's multi-pass bf16 products are not observable here (no TPU, no JAX);
+# the pass pairs are those of the published bf16_3x / bf16_6x algorithms
+# (parity unpinned against a TPU run). These checks pin the expansion, the
+# pairs and the accuracy each precision must reach.
+
+def test_bf16_parts_reconstruct_float32_exactly():
+    """p0 + p1 + p2 == x for normal float32 x (24 bits in three 8-bit parts
+    with signed remainders), and each part is a bf16 value below half an
+    ulp of the previous one."""
+    rng = np.random.default_rng(17)
+    x = (rng.standard_normal(20000) * np.exp2(rng.integers(-60, 60, 20000))).astype(np.float32)
+    p0, p1, p2 = (o.bf16_part(x, i) for i in range(3))
+    for p in (p0, p1, p2):
+        np.testing.assert_array_equal(p, o.bf16_round(p))
+    np.testing.assert_array_equal(p0.astype(np.float64) + p1 + p2, x.astype(np.float64))
+    assert np.all(np.abs(p1) <= np.abs(p0) * 2.0 ** -8) and np.all(np.abs(p2) <= np.abs(p1) * 2.0 ** -8)
+    # two parts do not suffice: the third carries information
+    assert np.mean(p0.astype(np.float64) + p1 != x) > 0.5
+    np.testing.assert_array_equal(o.bf16_part(x, 0), o.bf16_round(x))
+
+
+def test_pass_product_known_answers():
+    """s = 1 + 2^-10 + 2^-20 (parts 1, 2^-10, 2^-20), t = 3 + 2^-9 (parts 3,
+    2^-9, 0): each precision keeps exactly its pass pairs, so a wrong or
+    missing pair changes the sum. Every partial sum is exact in float32."""
+    s = np.array([[1 + 2.0 ** -10 + 2.0 ** -20]], np.float32)
+    t = np.array([[3 + 2.0 ** -9]], np.float32)
+    s_parts, t_parts = (1.0, 2.0 ** -10, 2.0 ** -20), (3.0, 2.0 ** -9, 0.0)
+    for i, (ps, pt) in enumerate(zip(s_parts, t_parts)):
+        assert o.bf16_part(s, i)[0, 0] == ps and o.bf16_part(t, i)[0, 0] == pt
+    want = {1: 3.0,
+            3: 3.0 + 2.0 ** -9 + 3 * 2.0 ** -10,
+            6: 3.0 + 2.0 ** -9 + 3 * 2.0 ** -10 + 2.0 ** -19 + 3 * 2.0 ** -20}
+    for passes, value in want.items():
+        assert o.pass_product(s, t, passes)[0, 0] == np.float32(value), passes
+    # the pairs are not symmetric in the parts: swapping the operands keeps the
+    # value only because each pass set is closed under swapping A and B
+    for passes in (1, 3, 6):
+        assert o.pass_product(t.T, s.T, passes)[0, 0] == o.pass_product(s, t, passes)[0, 0]
+    assert [o.precision_passes(p) for p in (None, "default", "bfloat16", "high", "tensorfloat32", "highest",
+                                            "float32")] == [1, 1, 1, 3, 3, 6, 6]
+    assert o.precision_passes("highest", "bfloat16") == 1
+    with pytest.raises(ValueError, match="unknown dot_precision"):
+        o.precision_passes("fp64")
+
+
+@pytest.mark.parametrize("formula", ["classical", "dual", "powers"])
+def test_multi_pass_accuracy_ladder(formula):
+    """Against the float64 product: DEFAULT is at the bf16 level, HIGH drops
+    only second-order parts (about 2^-16), HIGHEST only third-order ones, so
+    it reaches the FP32 accumulation level. The cubic control climbs the
+    same ladder."""
+    rng = np.random.default_rng(18)
+    a = rng.standard_normal((64, 1024)).astype(np.float32)
+    b = rng.standard_normal((1024, 256)).astype(np.float32)
+    ref64 = a.astype(np.float64) @ b.astype(np.float64)
+    kw = dict(bm=32, bn=128, bk=256, output_dtype="float32", input_dtype="float32", formula_variant=formula)
+    err = {}
+    for precision in ("default", "high", "highest"):
+        got = o.strassen_matmul(a, b, dot_precision=precision, **kw)
+        err[precision] = np.linalg.norm(got - ref64) / np.linalg.norm(ref64)
+        cubic = o.cubic_blocked_matmul(a, b, bm=32, bn=128, bk=256, output_dtype="float32", dot_precision=precision)
+        err["cubic_" + precision] = np.linalg.norm(cubic - ref64) / np.linalg.norm(ref64)
+    # measured: DEFAULT ~4.7e-3, HIGH ~8.7e-6, HIGHEST ~2.1e-7 (the cubic half of each)
+    assert 1e-3 < err["default"] < 1e-2
+    assert 2e-6 < err["high"] < 3e-5
+    assert err["highest"] < 1e-6 and err["highest"] < err["high"] / 10
+    assert err["cubic_highest"] < 1e-6 < err["cubic_high"] < 1e-4 < err["cubic_default"]
+    # bf16 inputs take one pass whatever dot_precision says
+    a16, b16 = o.bf16_round(a), o.bf16_round(b)
+    kw16 = dict(kw, input_dtype="bfloat16")
+    np.testing.assert_array_equal(o.strassen_matmul(a16, b16, dot_precision="highest", **kw16),
+                                  o.strassen_matmul(a16, b16, **kw16))
+
+
+def test_multi_pass_packed_planes():
+    """Packed depth runs (pass, K panel, local k): pass i of every panel
+    holds the operand's bf16 part PASS_PARTS[passes][side][i], HIGH's passes
+    are HIGHEST's last three, and the three distinct parts of a HIGHEST
+    operand sum to the float32 operand sums recomputed from the quadrants."""
+    rng = np.random.default_rng(19)
+    hk, npanels = 256, 2
+    for side, x in (("lhs", rng.standard_normal((256, 1024)).astype(np.float32)),
+                    ("rhs", rng.standard_normal((1024, 256)).astype(np.float32))):
+        one = o.operand_planes(x, 7, side, 256, 512, input_dtype="float32")
+        three = o.operand_planes(x, 7, side, 256, 512, input_dtype="float32", dot_precision="high")
+        six = o.operand_planes(x, 7, side, 256, 512, input_dtype="float32", dot_precision="highest")
+        width = npanels * hk
+        assert three.shape[2] == 3 * width and six.shape[2] == 6 * width
+        np.testing.assert_array_equal(three, six[:, :, 3 * width:])
+        np.testing.assert_array_equal(six[:, :, 5 * width:], one)  # the leading pass comes last
+        if side == "lhs":
+            q = [np.concatenate(c, axis=1) for c in zip(*(ref._split_a(x, 256, 512, s) for s in range(npanels)))]
+            ops = np.stack(o.strassen_a_operands(q, ref._identity))
+        else:
+            q = [np.concatenate(c, axis=0).T for c in zip(*(ref._split_b(x, 256, 512, s) for s in range(npanels)))]
+            ops = np.stack(o.strassen_b_operands(q, ref._identity))
+        parts = o.PASS_PARTS[6][0 if side == "lhs" else 1]
+        for i, part in enumerate(parts):
+            np.testing.assert_array_equal(six[:, :, i * width:(i + 1) * width], o.bf16_part(ops, part))
+        first = {part: i for i, part in reversed(list(enumerate(parts)))}
+        total = sum(six[:, :, first[p] * width:(first[p] + 1) * width].astype(np.float64) for p in range(3))
+        np.testing.assert_array_equal(total, ops.astype(np.float64))

@@ -120,25 +120,41 @@ def test_unported_options_raise_not_implemented(kwargs):
         smx.strassen_matmul(a, b, bm=256, bn=256, bk=512, **kwargs)
 
 
-def test_fp32_inputs_take_the_one_pass_path():
-    """FP32 inputs run the DEFAULT-precision product (one bf16 pass); more
-    passes are not built. CPU tensors still stop at the device check."""
+def test_fp32_inputs_and_dot_precision():
+    """FP32 inputs run the product of dot_precision: one bf16 pass at
+    DEFAULT, 3 at HIGH, 6 at HIGHEST (names and aliases as jax.lax.Precision
+    takes them, the same mapping as the oracle's); bf16 inputs always take
+    one pass. CPU tensors stop at the device check."""
+    import enum
+
+    import oracle as o
     a, b = t(256, 512, dtype=torch.float32), t(512, 256, dtype=torch.float32)
-    with pytest.raises(ValueError, match="HIP device"):
-        smx.strassen_matmul(a, b, bm=256, bn=256, bk=512)
-    with pytest.raises(ValueError, match="HIP device"):
-        smx.strassen_matmul(a, b, bm=256, bn=256, bk=512, dot_precision="DEFAULT")
-    for precision in ("HIGHEST", "high"):
-        with pytest.raises(NotImplementedError, match="HIGH/HIGHEST"):
+
+    class Precision(enum.Enum):  # the shape of jax.lax.Precision members
+        DEFAULT = 0
+        HIGH = 1
+        HIGHEST = 2
+
+    names = [None, "DEFAULT", "default", "fastest", "bfloat16", "high", "HIGH", "bfloat16_3x", "tensorfloat32",
+             "highest", "float32", "Precision.HIGHEST", Precision.DEFAULT, Precision.HIGH, Precision.HIGHEST]
+    for precision in names:
+        passes = smx.precision_passes(precision, torch.float32)
+        assert passes == o.precision_passes(precision, "float32")
+        assert smx.precision_passes(precision, torch.bfloat16) == 1
+        with pytest.raises(ValueError, match="HIP device"):
             smx.strassen_matmul(a, b, bm=256, bn=256, bk=512, dot_precision=precision)
-        with pytest.raises(NotImplementedError, match="HIGH/HIGHEST"):
+        with pytest.raises(ValueError, match="HIP device"):
             smx.cubic_matmul(a, b, bm=256, bn=256, bk=512, dot_precision=precision)
-        with pytest.raises(NotImplementedError, match="HIGH/HIGHEST"):
+        with pytest.raises(ValueError, match="HIP device"):
             smx.strassen_matmul_lhs_transposed(t(512, 256, dtype=torch.float32), b, bm=256, bn=256, bk=512,
                                                dot_precision=precision)
-    # bf16 products are exact in FP32 accumulation: precision is irrelevant there
-    with pytest.raises(ValueError, match="HIP device"):
-        smx.strassen_matmul(t(256, 512), t(512, 256), bm=256, bn=256, bk=512, dot_precision="HIGHEST")
+    assert [smx.precision_passes(p, torch.float32) for p in (Precision.DEFAULT, Precision.HIGH,
+                                                             Precision.HIGHEST)] == [1, 3, 6]
+    assert smx.precision_passes(("high", Precision.HIGH), torch.float32) == 3
+    with pytest.raises(NotImplementedError, match="two different precisions"):
+        smx.precision_passes(("high", "highest"), torch.float32)
+    with pytest.raises(ValueError, match="unknown dot_precision"):
+        smx.strassen_matmul(a, b, bm=256, bn=256, bk=512, dot_precision="fp64")
     with pytest.raises(ValueError, match="input dtypes disagree"):
         smx.cubic_matmul(a, t(512, 256), bm=256, bn=256, bk=512)
 
@@ -291,7 +307,9 @@ def test_torch_relayouts_match_oracle():
     ((t(512, 256), t(512, 256)), {"allow_input_fusion": (True,)}, ValueError, "two booleans"),
     ((t(512, 256), t(512, 256)), {"output_dtype": torch.float16}, ValueError, "BF16 or FP32"),
     ((t(512, 256, dtype=torch.float32), t(512, 256, dtype=torch.float32)), {"dot_precision": "HIGHEST"},
-     NotImplementedError, "FP32"),
+     ValueError, "HIP device"),
+    ((t(512, 256, dtype=torch.float32), t(512, 256, dtype=torch.float32)), {"dot_precision": "fp64"},
+     ValueError, "unknown dot_precision"),
     ((t(512, 256, dtype=torch.float32), t(512, 256, dtype=torch.float32)), {}, ValueError, "HIP device"),
     ((t(512, 256), t(512, 256)), {"interpret": True}, NotImplementedError, "interpret"),
     ((t(512, 256), t(512, 256)), {}, ValueError, "HIP device"),
