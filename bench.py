@@ -289,12 +289,47 @@ def cpu_baseline(seconds):
         if elapsed >= seconds:
             break
     tflops = tiles * 2.0 * bm * bn * HIDDEN / elapsed / 1e12
+    # Beside it, the FP32 cubic product of the same tile (numpy matmul).
+    a32, b32 = a.astype(np.float32), b.astype(np.float32)
+    np.matmul(a32, b32)
+    cubic_tiles, t1 = 0, time.perf_counter()
+    while True:
+        np.matmul(a32, b32)
+        cubic_tiles += 1
+        cubic_elapsed = time.perf_counter() - t1
+        if cubic_elapsed >= min(seconds, 3.0):
+            break
+    cpu_model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu_model = next((line.split(":", 1)[1].strip() for line in f if line.startswith("model name")), None)
+    except OSError:
+        pass
     return {
         "value": tflops, "unit": "TFLOP/s", "cores": int(cores), "kind": "port",
         "sample": f"{tiles} output tiles of 1024x1024 (K=5120) of the gate|up site, "
                   f"numpy oracle Strassen restatement, {elapsed:.1f} s",
         "ms_per_tile": elapsed * 1e3 / tiles,
+        "cubic_fp32_matmul_tflops": cubic_tiles * 2.0 * bm * bn * HIDDEN / cubic_elapsed / 1e12,
+        "cpu_model": cpu_model,
     }
+
+
+def summary(samples):
+    """mean / median / std (ms) of per-step event times."""
+    return {"mean": round(statistics.mean(samples), 4), "median": round(statistics.median(samples), 4),
+            "std": round(statistics.stdev(samples), 4) if len(samples) > 1 else 0.0, "n": len(samples)}
+
+
+def paired_ci95(numerator, denominator):
+    """Mean and 95% t-interval of the per-round ratios numerator_i /
+    denominator_i (rounds paired: both arms timed back to back)."""
+    ratios = [x / y for x, y in zip(numerator, denominator)]
+    n = len(ratios)
+    mean = statistics.mean(ratios)
+    t975 = {2: 12.706, 3: 4.303, 4: 3.182, 5: 2.776, 6: 2.571, 7: 2.447, 8: 2.365}.get(n, 2.0)
+    half = t975 * statistics.stdev(ratios) / n ** 0.5 if n > 1 else float("nan")
+    return {"mean": round(mean, 4), "lo": round(mean - half, 4), "hi": round(mean + half, 4), "rounds": n}
 
 
 def main():
@@ -360,15 +395,17 @@ def main():
     log("timing strassen block")
     wall_s, ev_s = time_steps(torch, run_block(arms["strassen"]), args.steps, args.warmup)
     results = {"strassen": statistics.median(ev_s)}
+    stats = {"strassen": summary(ev_s)}
     for arm in ("cubic", "hipblaslt", "strassen_plain", "cubic_plain"):
         log(f"timing {arm} block")
         _, ev = time_steps(torch, run_block(arms[arm]), args.steps, args.warmup)
         results[arm] = statistics.median(ev)
+        stats[arm] = summary(ev)
     # Interleaved rounds (rotated arm order) to check the comparison is not
-    # an ordering artefact.
+    # an ordering artefact; the paired per-round ratios give the speedup CI.
     names = ["strassen", "cubic", "hipblaslt"]
     rounds = {a: [] for a in names}
-    for r in range(3):
+    for r in range(5):
         order = names[r % 3:] + names[:r % 3]
         for arm in order:
             _, ev = time_steps(torch, run_block(arms[arm]), max(3, args.steps // 4), 1)
@@ -448,9 +485,12 @@ def main():
             "sites": {k: list(v) for k, v in shapes.items()},
         },
         "arms_ms": {k: round(v, 4) for k, v in results.items()},
+        "arms_stats_ms": stats,
         "arms_interleaved_ms": {k: [round(x, 4) for x in v] for k, v in rounds.items()},
         "speedup_vs_cubic": round(results["cubic"] / ms, 4),
         "speedup_vs_hipblaslt": round(results["hipblaslt"] / ms, 4),
+        "speedup_vs_cubic_ci95": paired_ci95(rounds["cubic"], rounds["strassen"]),
+        "speedup_vs_hipblaslt_ci95": paired_ci95(rounds["hipblaslt"], rounds["strassen"]),
         "sites_ms": {arm: {k: round(v, 4) for k, v in s.items()} for arm, s in per_site.items()},
         "sites_tflops": {arm: {k: round(flops(shapes[k]) / (v * 1e-3) / 1e12, 1) for k, v in s.items()}
                          for arm, s in per_site.items()},

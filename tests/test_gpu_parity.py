@@ -864,3 +864,31 @@ def test_qwen3_32b_shapes_sampled_tiles(site):
         assert rel_l2(host(got[rows, cols]), ref_tile) <= 1.5 * rel_l2(want, ref_tile)
         want_c = o.cubic_blocked_matmul(a_h[rows], b_h[:, cols], bm=bm, bn=bn, bk=bk)
         assert_ulp_close(host(cub[rows, cols]), want_c, k=k)
+
+
+def test_output_beyond_2gib():
+    """M = 65536 tokens on the gate|up shape: the 3.4 GB output (and the
+    residual of residual_add) lie past 2^31 bytes, so every store and load
+    offset needs 64 bits. Tiles at the far end are recomputed by the oracle."""
+    m, k, n = 65536, 5120, 25600
+    bm, bn, bk = 1024, 1024, 512
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    a = torch.randn(m, k, device=DEV, generator=gen).to(torch.bfloat16)
+    b = (torch.randn(n, k, device=DEV, generator=gen) * 0.02).to(torch.bfloat16).t()
+    r = torch.randn(m, n, device=DEV, generator=gen).to(torch.bfloat16)
+    assert r.numel() * 2 > 2 ** 31
+    say(f"  m={m} k={k} n={n}")
+    w = smx.strassen_weight_layout(b, bn, bk)
+    got = smx.strassen_matmul(a, w, bm=bm, bn=bn, bk=bk)
+    res = smx.strassen_matmul(a, w, bm=bm, bn=bn, bk=bk, epilogue="residual_add", residual=r)
+    cub = smx.cubic_matmul(a, smx.cubic_weight_layout(b, bn, bk), bm=bm, bn=bn, bk=bk)
+    torch.cuda.synchronize()
+    for i, j in ((m // bm - 1, n // bn - 1), (m // bm - 2, 3), (45, n // bn - 2)):
+        rows, cols = slice(i * bm, (i + 1) * bm), slice(j * bn, (j + 1) * bn)
+        assert (i * bm) * n * 2 >= 2 ** 31
+        a_h, b_h, r_h = host(a[rows]), host(b[:, cols]), host(r[rows, cols])
+        want = o.strassen_matmul(a_h, b_h, bm=bm, bn=bn, bk=bk)
+        assert_ulp_close(host(got[rows, cols]), want, k=k)
+        want_r = o.strassen_matmul(a_h, b_h, bm=bm, bn=bn, bk=bk, epilogue="residual_add", residual=r_h)
+        assert_ulp_close(host(res[rows, cols]), want_r, k=k)
+        assert_ulp_close(host(cub[rows, cols]), o.cubic_blocked_matmul(a_h, b_h, bm=bm, bn=bn, bk=bk), k=k)
