@@ -62,10 +62,17 @@ def verify_inline_asm_kernels(asm_text):
     """Raise if a kernel with inline-asm MFMAs touches accumulators before its
     drain; returns the number of such kernels (at least one is expected)."""
     checked = 0
-    for m in _FUNCTION.finditer(asm_text):
+    labels = list(_FUNCTION.finditer(asm_text))
+    for n, m in enumerate(labels):
         name = m.group(1)
-        end = asm_text.find("s_endpgm", m.end())
-        body = asm_text[m.end():end if end >= 0 else len(asm_text)]
+        # The whole function, up to its end marker or the next function: a
+        # kernel may end some waves (s_endpgm) before another wave's MFMA loop.
+        end = asm_text.find(".Lfunc_end", m.end())
+        if end < 0:
+            end = len(asm_text)
+        if n + 1 < len(labels):
+            end = min(end, labels[n + 1].start())
+        body = asm_text[m.end():end]
         if not _ASM_MFMA.search(body):
             continue
         checked += 1

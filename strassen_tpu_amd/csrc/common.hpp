@@ -336,7 +336,12 @@ __device__ __forceinline__ TileOrigin tile_origin(const Params& p, int64_t prow0
 // Epilogue
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+// SiLU as jax.nn.silu computes it, x * sigmoid(x), with sigmoid(x) =
+// 1 / (1 + 2^(-x log2 e)) on the hardware exp2 and reciprocal (each within
+// about one float ulp, far below the result's bf16 rounding).
+__device__ __forceinline__ float silu_f32(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
 
 // GELU, tanh approximation (jax.nn.gelu(approximate=True), the GeGLU gate of
 // strassen_pallas.py:143-153): 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).
@@ -353,30 +358,6 @@ __device__ __forceinline__ float gate_f32(float x) {
     return silu_f32(x);
 }
 
-// Input rows of an epilogue operand (residual, RoPE tables): a per-wave
-// base plus 32-bit element offsets, bf16 or float32, uniform per launch.
-struct InRow {
-  const char* base;
-  int f32;
-  __device__ __forceinline__ float get(int off) const {
-    return f32 ? reinterpret_cast<const float*>(base)[off]
-               : bf16_to_f32(reinterpret_cast<const uint16_t*>(base)[off]);
-  }
-};
-
-// Output rows: a per-wave base plus 32-bit element offsets, stored as bf16
-// or (out_f32) float32. The element type is uniform per launch.
-struct OutRow {
-  char* base;
-  int f32;
-  __device__ __forceinline__ void put(int off, float v) const {
-    if (f32)
-      reinterpret_cast<float*>(base)[off] = v;
-    else
-      reinterpret_cast<uint16_t*>(base)[off] = f32_to_bf16(v);
-  }
-};
-
 __device__ __forceinline__ float load_vec(const void* v, int is_f32, int64_t i) {
   return is_f32 ? reinterpret_cast<const float*>(v)[i] : bf16_to_f32(reinterpret_cast<const uint16_t*>(v)[i]);
 }
@@ -388,19 +369,147 @@ __device__ __forceinline__ float half_wave_sum(float x) {
   return x;
 }
 
+// One wave's epilogue staging tile in LDS: kRows x kCols floats, row stride
+// kStride bytes. An accumulator register holds rows r (lanes 0-31) and r+4
+// (lanes 32-63) of 32 consecutive columns; the 32-byte row pad puts the two
+// half-waves of a store 32 banks apart. Elements are addressed as a per-lane
+// base plus a compile-time offset, and global memory is read and written in
+// coalesced 16-byte chunks by whole rows.
+template <int kRows_, int kCols_>
+struct StageTile {
+  static constexpr int kRows = kRows_, kCols = kCols_;
+  static constexpr int kStride = kCols * 4 + 32;
+  static constexpr int kBytes = kRows * kStride;
+  // Register r of 32x32 block (i, j), lane part excluded.
+  static constexpr int at(int i, int j, int r) { return (i * 32 + 8 * (r >> 2) + (r & 3)) * kStride + j * 128; }
+  static __device__ __forceinline__ int lane_part(int lane) { return (lane >> 5) * 4 * kStride + (lane & 31) * 4; }
+  static_assert(kRows * kCols % 512 == 0, "whole 16-byte chunks per lane");
+};
+
+// Staging tiles per wave of an epilogue (q/k writes its a and b blocks at
+// once), and the LDS bytes four waves of kRows x kCols tiles need.
+template <int kEpi>
+constexpr int kEpiTiles = kEpi == SMX_EPI_QK_NORM_ROPE ? 2 : 1;
+template <int kEpi, int kRows, int kCols>
+constexpr int kEpiLds = 4 * kEpiTiles<kEpi> * StageTile<kRows, kCols>::kBytes;
+
+// Rows of a global [*, ld] matrix (bf16, or float when f32; 16-byte aligned
+// rows) -> the staging tile as float.
+template <class T>
+__device__ __forceinline__ void tile_load(uint8_t* tile, const char* src, int64_t ld, int f32, int lane) {
+  if (f32) {
+    constexpr int kChunks = T::kCols / 4;
+#pragma unroll
+    for (int t = 0; t < T::kRows * kChunks / 64; ++t) {
+      const int idx = lane + 64 * t, row = idx / kChunks, ch = idx % kChunks;
+      const f32x4 v = *reinterpret_cast<const f32x4*>(src + (row * ld + ch * 4) * 4);
+      *reinterpret_cast<f32x4*>(tile + row * T::kStride + ch * 16) = v;
+    }
+  } else {
+    constexpr int kChunks = T::kCols / 8;
+#pragma unroll
+    for (int t = 0; t < T::kRows * kChunks / 64; ++t) {
+      const int idx = lane + 64 * t, row = idx / kChunks, ch = idx % kChunks;
+      const F8 f = unpack8(*reinterpret_cast<const u32x4*>(src + (row * ld + ch * 8) * 2));
+      const f32x4 v0 = {f.v[0], f.v[1], f.v[2], f.v[3]}, v1 = {f.v[4], f.v[5], f.v[6], f.v[7]};
+      *reinterpret_cast<f32x4*>(tile + row * T::kStride + ch * 32) = v0;
+      *reinterpret_cast<f32x4*>(tile + row * T::kStride + ch * 32 + 16) = v1;
+    }
+  }
+}
+
+// The staging tile -> rows of a global [*, ld] matrix, rounded once to bf16
+// (or stored as float when f32).
+template <class T>
+__device__ __forceinline__ void tile_store(const uint8_t* tile, char* dst, int64_t ld, int f32, int lane) {
+  constexpr int kChunks = T::kCols / 8;  // 8 elements per lane and step
+#pragma unroll
+  for (int t = 0; t < T::kRows * kChunks / 64; ++t) {
+    const int idx = lane + 64 * t, row = idx / kChunks, ch = idx % kChunks;
+    const f32x4 v0 = *reinterpret_cast<const f32x4*>(tile + row * T::kStride + ch * 32);
+    const f32x4 v1 = *reinterpret_cast<const f32x4*>(tile + row * T::kStride + ch * 32 + 16);
+    if (f32) {
+      char* const out = dst + (row * ld + ch * 8) * 4;
+      *reinterpret_cast<f32x4*>(out) = v0;
+      *reinterpret_cast<f32x4*>(out + 16) = v1;
+    } else {
+      F8 f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f.v[e] = v0[e];
+        f.v[4 + e] = v1[e];
+      }
+      *reinterpret_cast<u32x4*>(dst + (row * ld + ch * 8) * 2) = pack8(f);
+    }
+  }
+}
+
+// Quadrant sources of the epilogue: the cubic's quadrants (plus an FP32
+// partial product), or Strassen's seven product sets, combined with the
+// classical formula unpermuted (the hot path) or with the call's formula and
+// permutation.
+constexpr int kQuadCubic = 0, kQuadCubicPartial = 1, kQuadClassical = 2, kQuadGeneric = 3;
+
+template <int kQ>
+using QuadC = std::integral_constant<int, kQ>;
+
+// Physical output quadrant kQ of accumulator element (i, j, r). The
+// accumulators are only read, so no quadrant set is materialised next to
+// the 448 product registers.
+template <int kQuad, int kQ, int kMB, int kNB, int kNacc>
+__device__ __forceinline__ float quadrant_value(const Params& p, const f32x16 (&acc)[kNacc][kMB][kNB], int i, int j,
+                                                int r) {
+  if constexpr (kQuad == kQuadCubic || kQuad == kQuadCubicPartial) {
+    return acc[kQ][i][j][r];
+  } else {
+    const float p1 = acc[0][i][j][r], p2 = acc[1][i][j][r], p3 = acc[2][i][j][r], p4 = acc[3][i][j][r];
+    const float p5 = acc[4][i][j][r], p6 = acc[5][i][j][r], p7 = acc[6][i][j][r];
+    if constexpr (kQuad == kQuadClassical) {
+      // C0 = P1+P4-P5+P7, C1 = P3+P5, C2 = P2+P4, C3 = P1-P2+P3+P6
+      if constexpr (kQ == 0) return ((p4 - p5) + p7) + p1;
+      if constexpr (kQ == 1) return p5 + p3;
+      if constexpr (kQ == 2) return p4 + p2;
+      if constexpr (kQ == 3) return ((p6 - p2) + p3) + p1;
+    } else {
+      // Logical quadrant (row, col) lands on physical (row ^ swap_m, col ^
+      // swap_n): physical kQ holds logical kQ ^ mask.
+      const int logical = kQ ^ ((p.perm & 1) ? 2 : 0) ^ ((p.perm & 4) ? 1 : 0);
+      const bool dual = p.formula == kFormulaDual, powers = p.formula == kFormulaPowers;
+      // classical and dual share C0 = P1+P4-P5+P7; classical C1 = P3+P5,
+      // C2 = P2+P4, C3 = P1-P2+P3+P6; dual C1 = Q2+Q4, C2 = Q3+Q5,
+      // C3 = Q1-Q2+Q3+Q6
+      const float c0 = ((p4 - p5) + p7) + p1, c1 = p5 + p3, c2 = p4 + p2;
+      const float c3 = ((p6 - p2) + p3) + p1, d3 = ((p6 + p3) - p2) + p1;
+      // powers: basis z0 = R3+R5, z1 = R6+R7, z2 = R2-R4, z3 = R1-R3+R4+R7,
+      // decoded as in strassen_pallas.py:744-760
+      const float z0 = p3 + p5, z1 = p6 + p7, z2 = p2 - p4, z3 = ((p4 - p3) + p7) + p1;
+      const float w0 = (z1 + z2) * 0.5f + z0 * 0.25f, w1 = ((z2 - z1) + z3) + z0 * 0.5f, w2 = z3 + z0 * 0.5f;
+      const float q0 = powers ? w0 : c0;
+      const float q1 = powers ? w1 : dual ? c2 : c1;
+      const float q2 = powers ? w2 : dual ? c1 : c2;
+      const float q3 = powers ? z0 : dual ? d3 : c3;
+      return logical == 0 ? q0 : logical == 1 ? q1 : logical == 2 ? q2 : q3;
+    }
+  }
+}
+
 // Combines the accumulator sets into the four quadrants, applies the
-// epilogue and stores bf16 (or float32). acc has kNacc sets (7 Strassen products P1..P7,
-// or the 4 quadrants for the cubic) of kMB x kNB 32x32 blocks; the wave's
-// block (i, j) sits at product-space rows row0 + 32 i and columns
-// col0 + 32 j, relative to the tile origin o.
-// Accumulator lane layout (v_mfma_f32_32x32x16_bf16): column lane%32, row
+// epilogue and stores bf16 (or float32). acc has kNacc sets (7 Strassen
+// products P1..P7, or the 4 quadrants for the cubic) of kMB x kNB 32x32
+// blocks; the wave's block (i, j) sits at product-space rows row0 + 32 i and
+// columns col0 + 32 j, relative to the tile origin o. Accumulator lane
+// layout (v_mfma_f32_32x32x16_bf16): column lane%32, row
 // 8*(r/4) + 4*(lane/32) + r%4 for register r.
-// Addresses are a per-wave 64-bit base plus 32-bit element offsets (the host
-// checks that (bm/2 + 128) * max(ldc, ldr) < 2^31), which keeps the
-// epilogue's register footprint small.
-template <int kAlgo, int kMB, int kNB, int kEpi, int kNacc>
-__device__ __forceinline__ void epilogue(const Params& p, const TileOrigin& o, int row0, int col0,
-                                         f32x16 (&acc)[kNacc][kMB][kNB]) {
+//
+// One output block at a time passes through the wave's staging tile `tile`
+// (StageTile<32 kMB, 32 kNB>::kBytes of LDS, private to the wave): a
+// residual block is loaded into it, each element's result replaces the
+// element in place, and the block is stored. Registers meet LDS at
+// compile-time offsets; global memory sees whole 16-byte row chunks.
+template <int kMB, int kNB, int kEpi, int kNacc, int kQuad>
+__device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin& o, int row0, int col0,
+                                              f32x16 (&acc)[kNacc][kMB][kNB], uint8_t* tile) {
+  using T = StageTile<32 * kMB, 32 * kNB>;
   // The lane index passes through an empty asm here, after the main loop's
   // drain: every per-lane epilogue address depends on it, so none can be
   // computed ahead of the loop and held (or spilled) across it.
@@ -408,155 +517,117 @@ __device__ __forceinline__ void epilogue(const Params& p, const TileOrigin& o, i
   asm volatile("" : "+v"(lane));
   const int hm = p.bm / 2, hn = p.bn / 2;
   const int lcol = lane & 31;
-  const int lrow4 = (lane >> 5) * 4;
-  const int ldc = (int)p.ldc, ldr = (int)p.ldr;
   // Top-left output element of this wave (quadrant 0) and its column inside
   // the tile half.
   const int64_t row_base = o.ti * p.bm + o.tr + row0;
   const int64_t cc_base = o.tc + col0;
   const int64_t col_base = o.tj * p.bn + cc_base;
-  const int64_t ocol_base = o.tj * hn + cc_base;  // SwiGLU output column
-  constexpr bool kGated = kEpi == SMX_EPI_SWIGLU || kEpi == SMX_EPI_GEGLU;
-  const OutRow cw{reinterpret_cast<char*>(p.c) +
-                      (row_base * p.ldc + (kGated ? ocol_base : col_base)) * (p.out_f32 ? 4 : 2),
-                  p.out_f32};
-  const InRow rw{kEpi == SMX_EPI_RESIDUAL_ADD ? reinterpret_cast<const char*>(p.residual) +
-                                                  (row_base * p.ldr + col_base) * (p.residual_f32 ? 4 : 2)
-                                            : nullptr,
-                  p.residual_f32};
-  const int hm_c = hm * ldc, hm_r = hm * ldr;
+  uint8_t* const te = tile + T::lane_part(lane);
+  // LDS operations of one wave complete in order; this keeps the compiler
+  // from moving one lane's tile access across another lane's.
+  auto fence = []() __attribute__((always_inline)) { asm volatile("" ::: "memory"); };
+  auto put = [&](int i, int j, int r, float v) __attribute__((always_inline)) {
+    *reinterpret_cast<float*>(te + T::at(i, j, r)) = v;
+  };
+  auto get = [&](int i, int j, int r) __attribute__((always_inline)) {
+    return *reinterpret_cast<const float*>(te + T::at(i, j, r));
+  };
+  auto value = [&](auto q, int i, int j, int r) __attribute__((always_inline)) {
+    return quadrant_value<kQuad, decltype(q)::value>(p, acc, i, j, r);
+  };
+  // Quadrant q of an [M, N] operand (row stride ld, element size es), for
+  // this wave: rows row_base + (q>>1) hm, columns col_base + (q&1) hn.
+  auto quadrant = [&](const void* base, int64_t ld, int es, int q) __attribute__((always_inline)) {
+    return reinterpret_cast<const char*>(base) + ((row_base + (q >> 1) * hm) * ld + col_base + (q & 1) * hn) * es;
+  };
+  // The tile -> the output block at (row, col).
+  auto emit = [&](int64_t row, int64_t col) __attribute__((always_inline)) {
+    fence();
+    tile_store<T>(tile, reinterpret_cast<char*>(p.c) + (row * p.ldc + col) * (p.out_f32 ? 4 : 2), p.ldc, p.out_f32,
+                  lane);
+    fence();
+  };
+
   // Cubic only: an FP32 partial product of the same output (the Strassen
-  // panels of an exact-panel schedule) joins the quadrants before the
-  // epilogue.
-  const float* const pw = kAlgo == 8 && p.partial ? p.partial + row_base * p.ldp + col_base : nullptr;
-  const int ldp = (int)p.ldp, hm_p = hm * ldp;
+  // panels of an exact-panel schedule) joins the quadrants first.
+  if constexpr (kQuad == kQuadCubicPartial) {
 #pragma unroll
-  for (int i = 0; i < kMB; ++i) {
+    for (int q = 0; q < 4; ++q) {
+      tile_load<T>(tile, quadrant(p.partial, p.ldp, 4, q), p.ldp, 1, lane);
+      fence();
 #pragma unroll
-    for (int j = 0; j < kNB; ++j) {
-      const int cj = j * 32 + lcol;  // column offset inside the wave
-      float bl = 0.f, br = 0.f;
-      if constexpr (kEpi == SMX_EPI_BIAS_ADD) {
-        bl = load_vec(p.bias, p.bias_f32, col_base + cj);
-        br = load_vec(p.bias, p.bias_f32, col_base + cj + hn);
-      }
+      for (int i = 0; i < kMB; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int ri = i * 32 + 8 * (r >> 2) + lrow4 + (r & 3);  // row offset inside the wave
-        float q0, q1, q2, q3;
-        if constexpr (kAlgo == 7) {
-          const float p1 = acc[0][i][j][r], p2 = acc[1][i][j][r], p3 = acc[2][i][j][r];
-          const float p4 = acc[3][i][j][r], p5 = acc[4][i][j][r], p6 = acc[5][i][j][r];
-          const float p7 = acc[6][i][j][r];
-          if (p.formula == kFormulaClassical) {
-            // C0 = P1+P4-P5+P7, C1 = P3+P5, C2 = P2+P4, C3 = P1-P2+P3+P6
-            q0 = ((p4 - p5) + p7) + p1;
-            q1 = p5 + p3;
-            q2 = p4 + p2;
-            q3 = ((p6 - p2) + p3) + p1;
-          } else if (p.formula == kFormulaDual) {
-            // C0 = Q1+Q4-Q5+Q7, C1 = Q2+Q4, C2 = Q3+Q5, C3 = Q1-Q2+Q3+Q6
-            q0 = ((p4 - p5) + p7) + p1;
-            q1 = p4 + p2;
-            q2 = p5 + p3;
-            q3 = ((p6 + p3) - p2) + p1;
-          } else {
-            // Basis z0 = R3+R5, z1 = R6+R7, z2 = R2-R4, z3 = R1-R3+R4+R7,
-            // decoded as in strassen_pallas.py:744-760.
-            const float z0 = p3 + p5, z1 = p6 + p7, z2 = p2 - p4, z3 = ((p4 - p3) + p7) + p1;
-            q3 = z0;
-            q2 = z3 + z0 * 0.5f;
-            q0 = (z1 + z2) * 0.5f + z0 * 0.25f;
-            q1 = ((z2 - z1) + z3) + z0 * 0.5f;
-          }
-          // Logical quadrant (row, col) lands on physical (row ^ swap_m, col ^ swap_n).
-          if (p.perm & 1) {
-            const float t0 = q0, t1 = q1;
-            q0 = q2;
-            q1 = q3;
-            q2 = t0;
-            q3 = t1;
-          }
-          if (p.perm & 4) {
-            const float t0 = q0, t2 = q2;
-            q0 = q1;
-            q2 = q3;
-            q1 = t0;
-            q3 = t2;
-          }
-        } else {
-          q0 = acc[0][i][j][r];
-          q1 = acc[1][i][j][r];
-          q2 = acc[2][i][j][r];
-          q3 = acc[3][i][j][r];
-          if (pw) {
-            const int poff = ri * ldp + cj;
-            q0 += pw[poff];
-            q1 += pw[poff + hn];
-            q2 += pw[poff + hm_p];
-            q3 += pw[poff + hm_p + hn];
-          }
-        }
-        if constexpr (kGated) {
-          // Quadrants 0/2 are gate, 1/3 up; output [M, N/2].
-          const int off = ri * ldc + cj;
-          cw.put(off, gate_f32<kEpi>(q0) * q1);
-          cw.put(off + hm_c, gate_f32<kEpi>(q2) * q3);
-        } else if constexpr (kEpi == SMX_EPI_QK_NORM_ROPE) {
-          // Normalisation needs whole head segments: keep the quadrant
-          // values and finish below.
-          acc[0][i][j][r] = q0;
-          acc[1][i][j][r] = q1;
-          acc[2][i][j][r] = q2;
-          acc[3][i][j][r] = q3;
-        } else {
-          const int off = ri * ldc + cj;
-          if constexpr (kEpi == SMX_EPI_RESIDUAL_ADD) {
-            const int roff = ri * ldr + cj;
-            q0 += rw.get(roff);
-            q1 += rw.get(roff + hn);
-            q2 += rw.get(roff + hm_r);
-            q3 += rw.get(roff + hm_r + hn);
-          } else if constexpr (kEpi == SMX_EPI_BIAS_ADD) {
-            q0 += bl;
-            q1 += br;
-            q2 += bl;
-            q3 += br;
-          }
-          cw.put(off, q0);
-          cw.put(off + hn, q1);
-          cw.put(off + hm_c, q2);
-          cw.put(off + hm_c + hn, q3);
-        }
-      }
-      // One 32x32 block at a time keeps the epilogue's live set small.
-      __builtin_amdgcn_sched_barrier(0);
+        for (int j = 0; j < kNB; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[q][i][j][r] += get(i, j, r);
+      fence();
     }
   }
 
-  if constexpr (kEpi == SMX_EPI_QK_NORM_ROPE) {
+  if constexpr (kEpi == SMX_EPI_SWIGLU || kEpi == SMX_EPI_GEGLU) {
+    // Quadrants 0/2 are gate, 1/3 up; output [M, N/2].
+    const int64_t ocol = o.tj * hn + cc_base;
+    auto gated = [&](auto gate_q, auto up_q, int64_t row) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < kMB; ++i)
+#pragma unroll
+        for (int j = 0; j < kNB; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) put(i, j, r, gate_f32<kEpi>(value(gate_q, i, j, r)) * value(up_q, i, j, r));
+      emit(row, ocol);
+    };
+    gated(QuadC<0>{}, QuadC<1>{}, row_base);
+    gated(QuadC<2>{}, QuadC<3>{}, row_base + hm);
+  } else if constexpr (kEpi == SMX_EPI_QK_NORM_ROPE) {
     // Per-head RMSNorm then RoPE (strassen_pallas.py:793-835). A head owns
     // head_dim/2 = 64 consecutive columns of a tile half: the wave's column
     // blocks j = 2h, 2h+1 (the caller guarantees kNB % 2 == 0 and 64-aligned
     // wave columns). Quadrants 0/2 hold the a half, 1/3 the b half.
-    static_assert(kEpi != SMX_EPI_QK_NORM_ROPE || kNB % 2 == 0, "qk epilogue needs 64-column waves");
+    static_assert(kNB % 2 == 0, "qk epilogue needs 64-column waves");
+    // The norm spans both quadrants of a tile half and both halves are
+    // needed to the end: the quadrants are formed once, in place in sets
+    // 0-3 (straight-line code), which frees the other three product sets.
+    if constexpr (kQuad == kQuadClassical || kQuad == kQuadGeneric) {
+#pragma unroll
+      for (int i = 0; i < kMB; ++i)
+#pragma unroll
+        for (int j = 0; j < kNB; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float q0 = quadrant_value<kQuad, 0>(p, acc, i, j, r);
+            const float q1 = quadrant_value<kQuad, 1>(p, acc, i, j, r);
+            const float q2 = quadrant_value<kQuad, 2>(p, acc, i, j, r);
+            const float q3 = quadrant_value<kQuad, 3>(p, acc, i, j, r);
+            acc[0][i][j][r] = q0;
+            acc[1][i][j][r] = q1;
+            acc[2][i][j][r] = q2;
+            acc[3][i][j][r] = q3;
+          }
+    }
+    auto qv = [&](auto q, int i, int j, int r) __attribute__((always_inline)) {
+      return acc[decltype(q)::value][i][j][r];
+    };
     const float inv_width = 1.0f / (float)p.head_dim;
+    const int lrow4 = (lane >> 5) * 4;
     // rope tables are [M, hn], indexed by output row and column inside the half
     const uint16_t* const cos_w = p.rope_cos + row_base * hn + cc_base;
     const uint16_t* const sin_w = p.rope_sin + row_base * hn + cc_base;
     const int hm_t = hm * hn;
+    // The a and b outputs of an element go to two blocks: the second staging
+    // tile (this epilogue has two per wave) takes the b block.
+    uint8_t* const tile_b = tile + T::kBytes;
+    uint8_t* const te_b = tile_b + T::lane_part(lane);
+    auto rows = [&](auto qa, auto qb, int half) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < kMB; ++i) {
+      for (int i = 0; i < kMB; ++i) {
 #pragma unroll
-      for (int h = 0; h < kNB / 2; ++h) {
+        for (int h = 0; h < kNB / 2; ++h) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int ri = i * 32 + 8 * (r >> 2) + lrow4 + (r & 3);
-#pragma unroll
-          for (int half = 0; half < 2; ++half) {
-            const int sa = 2 * half, sb = 2 * half + 1;  // a / b quadrant sets
-            const float a0 = acc[sa][i][2 * h][r], a1 = acc[sa][i][2 * h + 1][r];
-            const float b0 = acc[sb][i][2 * h][r], b1 = acc[sb][i][2 * h + 1][r];
+          for (int r = 0; r < 16; ++r) {
+            const int ri = i * 32 + 8 * (r >> 2) + lrow4 + (r & 3);
+            const float a0 = qv(qa, i, 2 * h, r), a1 = qv(qa, i, 2 * h + 1, r);
+            const float b0 = qv(qb, i, 2 * h, r), b1 = qv(qb, i, 2 * h + 1, r);
             const float ssa = half_wave_sum(a0 * a0 + a1 * a1);
             const float ssb = half_wave_sum(b0 * b0 + b1 * b1);
             const float recip = 1.0f / sqrtf((ssa + ssb) * inv_width + p.eps);
@@ -569,17 +640,65 @@ __device__ __forceinline__ void epilogue(const Params& p, const TileOrigin& o, i
               const int toff = ri * hn + cj + half * hm_t;
               const float cs = bf16_to_f32(cos_w[toff]);
               const float sn = bf16_to_f32(sin_w[toff]);
-              const float na = acc[sa][i][j][r] * recip * ga;
-              const float nbv = acc[sb][i][j][r] * recip * gb;
-              const int off = ri * ldc + cj + half * hm_c;
-              cw.put(off, na * cs - nbv * sn);
-              cw.put(off + hn, nbv * cs + na * sn);
+              const float na = qv(qa, i, j, r) * recip * ga;
+              const float nbv = qv(qb, i, j, r) * recip * gb;
+              put(i, j, r, na * cs - nbv * sn);
+              *reinterpret_cast<float*>(te_b + T::at(i, j, r)) = nbv * cs + na * sn;
             }
           }
+          // one head segment at a time keeps the table loads' live set small
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
-    }
+      emit(row_base + half * hm, col_base);
+      tile_store<T>(tile_b, reinterpret_cast<char*>(p.c) + ((row_base + half * hm) * p.ldc + col_base + hn) *
+                                                             (p.out_f32 ? 4 : 2),
+                    p.ldc, p.out_f32, lane);
+      fence();
+    };
+    rows(QuadC<0>{}, QuadC<1>{}, 0);
+    rows(QuadC<2>{}, QuadC<3>{}, 1);
+  } else {
+    auto block = [&](auto q) __attribute__((always_inline)) {
+      constexpr int kQ = decltype(q)::value;
+      if constexpr (kEpi == SMX_EPI_RESIDUAL_ADD) {
+        tile_load<T>(tile, quadrant(p.residual, p.ldr, p.residual_f32 ? 4 : 2, kQ), p.ldr, p.residual_f32, lane);
+        fence();
+      }
+#pragma unroll
+      for (int j = 0; j < kNB; ++j) {
+        float b = 0.f;
+        if constexpr (kEpi == SMX_EPI_BIAS_ADD)
+          b = load_vec(p.bias, p.bias_f32, col_base + (kQ & 1) * hn + j * 32 + lcol);
+#pragma unroll
+        for (int i = 0; i < kMB; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            float v = value(q, i, j, r);
+            if constexpr (kEpi == SMX_EPI_RESIDUAL_ADD) v += get(i, j, r);
+            if constexpr (kEpi == SMX_EPI_BIAS_ADD) v += b;
+            put(i, j, r, v);
+          }
+      }
+      emit(row_base + (kQ >> 1) * hm, col_base + (kQ & 1) * hn);
+    };
+    block(QuadC<0>{});
+    block(QuadC<1>{});
+    block(QuadC<2>{});
+    block(QuadC<3>{});
   }
+}
+
+// The epilogue for the quadrant source kQuad. Each source has a kernel of
+// its own: a runtime choice between bodies would leave the 448 live
+// accumulators to be split across two arms, which spills. The workgroup
+// barrier first makes the LDS free for the staging tiles: every wave has
+// finished its main-loop reads and the last DMA has landed.
+template <int kQuad, int kMB, int kNB, int kEpi, int kNacc>
+__device__ __forceinline__ void epilogue(const Params& p, const TileOrigin& o, int row0, int col0,
+                                         f32x16 (&acc)[kNacc][kMB][kNB], uint8_t* tile) {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  epilogue_body<kMB, kNB, kEpi, kNacc, kQuad>(p, o, row0, col0, acc, tile);
 }
 
 template <int kNacc, int kMB, int kNB>

@@ -108,10 +108,11 @@ __device__ __forceinline__ bf16x8 ld_frag(const uint8_t* p) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(p));
 }
 
-template <int kAlgo, int kEpi, int kCubicSlots = 3>
+template <int kAlgo, int kEpi, int kQuad, int kCubicSlots = 3>
 __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
   using L = Lay<kAlgo, kCubicSlots>;
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+  static_assert(kEpiLds<kEpi, 64, 64> <= 160 * 1024, "epilogue staging fits the LDS");
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int wm = wave >> 1, wn = wave & 1;
@@ -280,7 +281,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
     } while (s < nstages);
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     mfma_drain(acc);
-    epilogue<kAlgo, 2, 2, kEpi>(p, o, wm * 64, wn * 64, acc);
+    epilogue<kQuad, 2, 2, kEpi>(p, o, wm * 64, wn * 64, acc, lds + wave * kEpiTiles<kEpi> * StageTile<64, 64>::kBytes);
     return;
   }
 
@@ -330,7 +331,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
   // The drain also pins every accumulator in its register file up to this
   // point, so the allocator cannot copy them out early.
   mfma_drain(acc);
-  epilogue<kAlgo, 2, 2, kEpi>(p, o, wm * 64, wn * 64, acc);
+  epilogue<kQuad, 2, 2, kEpi>(p, o, wm * 64, wn * 64, acc, lds + wave * kEpiTiles<kEpi> * StageTile<64, 64>::kBytes);
 }
 
 // Packs one operand. kSide 0: A [m, k] row-major (kSide 2: the same A stored

@@ -61,7 +61,7 @@ struct StripFrags {
 // One wave's main loop, accumulator exchange and epilogue. The stage ring
 // holds kNA A stages and kNB B stages (gemm_packed<7>: 2 and 3); each wave
 // moves fragments wave + 4x of every stage.
-template <int kWave, int kEpi, int kNA, int kNB>
+template <int kWave, int kEpi, int kQuad, int kNA, int kNB>
 __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, int nstages, int lane,
                                          const uint8_t* a_src, const uint8_t* b_src, uint8_t* lds) {
   using L = packed::Lay<7>;
@@ -224,10 +224,12 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
     }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
-  epilogue<7, 2, 2, kEpi>(p, o, wm * 64, wn * 64, dst);
+  static_assert(kEpiLds<kEpi, 64, 64> <= 160 * 1024, "epilogue staging fits the LDS");
+  epilogue<kQuad, 2, 2, kEpi>(p, o, wm * 64, wn * 64, dst,
+                              lds + kWave * kEpiTiles<kEpi> * StageTile<64, 64>::kBytes);
 }
 
-template <int kEpi, int kNA = 2, int kNB = 3>
+template <int kEpi, int kQuad, int kNA = 2, int kNB = 3>
 __global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
   using L = packed::Lay<7>;
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
@@ -280,16 +282,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
   // accumulator is live across the branches.
   switch (wave) {
     case 0:
-      run_wave<0, kEpi, kNA, kNB>(p, o, nstages, lane, a_src, b_src, lds);
+      run_wave<0, kEpi, kQuad, kNA, kNB>(p, o, nstages, lane, a_src, b_src, lds);
       break;
     case 1:
-      run_wave<1, kEpi, kNA, kNB>(p, o, nstages, lane, a_src, b_src, lds);
+      run_wave<1, kEpi, kQuad, kNA, kNB>(p, o, nstages, lane, a_src, b_src, lds);
       break;
     case 2:
-      run_wave<2, kEpi, kNA, kNB>(p, o, nstages, lane, a_src, b_src, lds);
+      run_wave<2, kEpi, kQuad, kNA, kNB>(p, o, nstages, lane, a_src, b_src, lds);
       break;
     default:
-      run_wave<3, kEpi, kNA, kNB>(p, o, nstages, lane, a_src, b_src, lds);
+      run_wave<3, kEpi, kQuad, kNA, kNB>(p, o, nstages, lane, a_src, b_src, lds);
       break;
   }
 }

@@ -201,7 +201,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_v1(Params p) {
     mma_slab<C>(lds, acc, wave_m, wave_n);
     __syncthreads();
   }
-  epilogue<C::algo, C::mb, C::nb, kEpi>(p, o, wave_m * C::mb * 32, wave_n * C::nb * 32, acc);
+  using T = StageTile<32 * C::mb, 32 * C::nb>;
+  static_assert(kEpiLds<kEpi, 32 * C::mb, 32 * C::nb> <= 160 * 1024, "epilogue staging fits the LDS");
+  // The compact path runs the classical formula unpermuted (the host sends
+  // formula variants, permutations and partial products to the packed path).
+  constexpr int kQuad = C::algo == 7 ? kQuadClassical : kQuadCubic;
+  epilogue<kQuad, C::mb, C::nb, kEpi>(p, o, wave_m * C::mb * 32, wave_n * C::nb * 32, acc,
+                                      lds + wave * kEpiTiles<kEpi> * T::kBytes);
 }
 
 // The general configuration uses 64x32 wave tiles; the q/k epilogue needs

@@ -103,8 +103,10 @@ int launch_v1(Params p, hipStream_t stream) {
   p.tiles_n = (int)((p.n / 2) / C::TN);
   p.group_m = group_m_setting();
   auto kern = v1::gemm_v1<C, kEpi>;
-  if (int rc = set_lds(kern, C::kLds)) return rc;
-  hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n), dim3(kThreads), C::kLds, stream, p);
+  // operand slabs, then the epilogue's staging tiles, share the LDS
+  constexpr int lds = C::kLds > kEpiLds<kEpi, 32 * C::mb, 32 * C::nb> ? C::kLds : kEpiLds<kEpi, 32 * C::mb, 32 * C::nb>;
+  if (int rc = set_lds(kern, lds)) return rc;
+  hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n), dim3(kThreads), lds, stream, p);
   return check_launch();
 }
 
@@ -113,10 +115,23 @@ int launch_packed(Params p, hipStream_t stream) {
   p.tiles_m = (int)((p.m / 2) / packed::TM);
   p.tiles_n = (int)((p.n / 2) / packed::TN);
   p.group_m = group_m_setting();
-  auto kern = packed::gemm_packed<kAlgo, kEpi>;
-  if constexpr (kAlgo == 7)
-    if (split_kernel_setting()) kern = split::gemm_split<kEpi>;
-  constexpr int lds = packed::Lay<kAlgo>::kLds;
+  // The epilogue's quadrant source is a kernel template argument: the
+  // classical unpermuted Strassen (the hot path) and the cubic without a
+  // partial product have straight-line epilogues of their own.
+  void (*kern)(Params);
+  if constexpr (kAlgo == 7) {
+    if (!split_kernel_setting())
+      kern = packed::gemm_packed<7, kEpi, kQuadGeneric>;
+    else if (p.formula == SMX_FORMULA_CLASSICAL && p.perm == 0)
+      kern = split::gemm_split<kEpi, kQuadClassical>;
+    else
+      kern = split::gemm_split<kEpi, kQuadGeneric>;
+  } else {
+    kern = p.partial ? packed::gemm_packed<8, kEpi, kQuadCubicPartial> : packed::gemm_packed<8, kEpi, kQuadCubic>;
+  }
+  // the stage ring, then the epilogue's staging tiles, share the LDS
+  constexpr int lds = packed::Lay<kAlgo>::kLds > kEpiLds<kEpi, 64, 64> ? packed::Lay<kAlgo>::kLds
+                                                                         : kEpiLds<kEpi, 64, 64>;
   if (int rc = set_lds(kern, lds)) return rc;
   hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n), dim3(kThreads), lds, stream, p);
   return check_launch();
@@ -320,8 +335,10 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
     return fail(SMX_ERR_INVALID, "fused epilogues require a quadrant-basis formula");
   if (d->partial && d->algo != SMX_ALGO_CUBIC)
     return fail(SMX_ERR_INVALID, "an FP32 partial is added by the cubic algorithm only");
-  if (d->partial && (d->ldp < d->n || ((uintptr_t)d->partial & 3)))
-    return fail(SMX_ERR_INVALID, "partial needs ldp >= N and 4-byte alignment");
+  if (d->partial && d->a_layout != SMX_A_PACKED)
+    return fail(SMX_ERR_UNSUPPORTED, "an FP32 partial needs packed operands (smx_pack_operand)");
+  if (d->partial && (d->ldp < d->n || d->ldp % 4 || !aligned16(d->partial)))
+    return fail(SMX_ERR_INVALID, "partial needs ldp >= N, ldp %% 4 == 0 and 16-byte alignment");
   if (d->m <= 0 || d->n <= 0 || d->k <= 0)
     return fail(SMX_ERR_INVALID, "empty problem m=%lld n=%lld k=%lld", (long long)d->m, (long long)d->n,
                 (long long)d->k);
@@ -340,12 +357,14 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
     return fail(SMX_ERR_INVALID, "lda and ldb must be >= K and multiples of 8 elements");
   const int64_t out_cols = (d->epilogue == SMX_EPI_SWIGLU || d->epilogue == SMX_EPI_GEGLU) ? d->n / 2 : d->n;
   if (d->ldc < out_cols) return fail(SMX_ERR_INVALID, "ldc must be >= output width");
-  // The epilogue addresses a tile half with 32-bit element offsets.
-  int64_t widest = d->ldc > d->ldr ? d->ldc : d->ldr;
-  if (d->partial && d->ldp > widest) widest = d->ldp;
-  if ((int64_t)(hm + 128) * widest >= ((int64_t)1 << 31))
-    return fail(SMX_ERR_UNSUPPORTED, "bm/2 * row stride must stay below 2^31 elements (bm=%d, stride=%lld)", d->bm,
-                (long long)widest);
+  // The epilogue moves output (and residual / partial) rows in 16-byte chunks.
+  const bool out_f32 = (d->flags & SMX_FLAG_OUT_F32) != 0;
+  if (!aligned16(c) || d->ldc % (out_f32 ? 4 : 8))
+    return fail(SMX_ERR_INVALID, "C rows must be 16-byte aligned (C 16-byte aligned, ldc %% %d == 0)", out_f32 ? 4 : 8);
+  // The q/k epilogue addresses its RoPE tables ([M, bn/2] per tile half)
+  // with 32-bit element offsets.
+  if ((int64_t)hm * d->bn >= ((int64_t)1 << 31))
+    return fail(SMX_ERR_UNSUPPORTED, "bm/2 * bn must stay below 2^31 (bm=%d, bn=%d)", d->bm, d->bn);
   Params p{};
   p.a = (const uint16_t*)a;
   p.b = (const uint16_t*)b;
@@ -378,6 +397,9 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
     case SMX_EPI_RESIDUAL_ADD:
       if (!residual) return fail(SMX_ERR_INVALID, "residual_add epilogue requires residual");
       if (d->ldr < d->n) return fail(SMX_ERR_INVALID, "ldr must be >= N");
+      if (!aligned16(residual) || d->ldr % (p.residual_f32 ? 4 : 8))
+        return fail(SMX_ERR_INVALID, "residual rows must be 16-byte aligned (residual 16-byte aligned, ldr %% %d == 0)",
+                    p.residual_f32 ? 4 : 8);
       p.residual = residual;
       break;
     case SMX_EPI_BIAS_ADD:

@@ -417,7 +417,8 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
     aux = 0
     if residual is not None:
         residual = _aux_tensor(residual)
-        if residual.stride(1) != 1:
+        # the kernels read residual rows in 16-byte chunks
+        if residual.stride(1) != 1 or (residual.stride(0) * residual.element_size()) % 16 or residual.data_ptr() % 16:
             residual = residual.contiguous()
         if residual.dtype == torch.float32:
             aux |= _lib.SMX_AUX_RESIDUAL_F32

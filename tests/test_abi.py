@@ -257,6 +257,44 @@ def test_partial_product_arguments(fields, match):
     assert match in _lib.last_error()
 
 
+@pytest.mark.parametrize("case,match", [
+    ("c_offset", "C rows must be 16-byte aligned"),
+    ("ldc", "C rows must be 16-byte aligned"),
+    ("ldc_f32", "C rows must be 16-byte aligned"),
+    ("residual_offset", "residual rows must be 16-byte aligned"),
+    ("ldr", "residual rows must be 16-byte aligned"),
+    ("partial_offset", "16-byte alignment"),
+    ("ldp", "ldp % 4"),
+])
+def test_epilogue_rows_are_16_byte_aligned(case, match):
+    """The epilogue moves output, residual and partial rows in 16-byte
+    chunks: their base pointers and row strides must keep rows 16-byte
+    aligned (checked before any launch)."""
+    lib = _lib.load()
+    buf = (ctypes.c_uint8 * 256)()
+    base = (ctypes.addressof(buf) + 15) & ~15
+    good, odd = ctypes.c_void_p(base), ctypes.c_void_p(base + 4)
+    c, residual = good, None
+    d = _desc()
+    if case == "c_offset":
+        c = odd
+    elif case == "ldc":
+        d.ldc = 260
+    elif case == "ldc_f32":
+        d.flags, d.ldc = _lib.SMX_FLAG_OUT_F32, 258
+    elif case in ("residual_offset", "ldr"):
+        d.epilogue = _lib.SMX_EPI["residual_add"]
+        residual = odd if case == "residual_offset" else good
+        if case == "ldr":
+            d.ldr = 260
+    else:
+        d = _desc(algo=_lib.SMX_ALGO_CUBIC, a_layout=_lib.SMX_A_PACKED, b_layout=_lib.SMX_B_PACKED)
+        d.partial = base + 4 if case == "partial_offset" else base
+        d.ldp = 256 if case == "partial_offset" else 258
+    assert lib.smx_gemm(d, good, good, c, residual, None, None, None, None, None) == _lib.SMX_ERR_INVALID
+    assert match in _lib.last_error()
+
+
 def test_inline_asm_kernel_check():
     """The build refuses device code that touches MFMA accumulators between
     the first inline-asm MFMA and the drain."""
@@ -281,3 +319,8 @@ def test_inline_asm_kernel_check():
             build.verify_inline_asm_kernels(text)
     with pytest.raises(RuntimeError):
         build.verify_inline_asm_kernels("no kernels here")
+    # a wave that ends early does not hide another wave's MFMA loop
+    early = ok.replace("; @x\n", "; @x\n\ts_cbranch_scc1 .LBB0_2\n\ts_endpgm\n.LBB0_2:\n")
+    assert build.verify_inline_asm_kernels(early) == 1
+    with pytest.raises(RuntimeError, match="before the MFMA drain"):
+        build.verify_inline_asm_kernels(early.replace(drain, "\tv_accvgpr_read_b32 v0, a0\n" + drain))
