@@ -109,8 +109,9 @@ typedef struct smx_gemm_desc {
   int32_t flags;         /* SMX_FLAG_* bits */
   int32_t formula;       /* SMX_FORMULA_* (Strassen; packed operands built with the same formula) */
   int32_t block_permutation; /* 0..7: bit 0 swaps row halves, bit 1 K halves, bit 2 column halves (:205-226) */
-  /* Cubic only: NULL, or an FP32 [m, n] partial product (row stride ldp >=
-   * n) added to the quadrants before the epilogue. An exact-panel schedule
+  /* Cubic only, packed operands: NULL, or an FP32 [m, n] partial product
+   * (row stride ldp >= n, 16-byte aligned rows) added to the quadrants
+   * before the epilogue. An exact-panel schedule
    * (classical_panels / panel_schedule, :575-586, :713-735) is the Strassen
    * GEMM over the ordinary K panels with an FP32 result, then the cubic GEMM
    * over the exact panels with that result as its partial. */
@@ -127,7 +128,10 @@ typedef struct smx_gemm_desc {
  * SMX_FLAG_OUT_F32. residual: [m, n] (ldr), bf16 or float32
  * (SMX_AUX_RESIDUAL_F32). bias: [n] bf16 or f32. rope_cos / rope_sin: bf16 [m, bn/2] tables
  * indexed by output row (rope_layout_tables). rope_scale: [bn] bf16 or f32
- * (rope_scale_layout). Unused pointers may be NULL.
+ * (rope_scale_layout). Unused pointers may be NULL. The epilogue moves C,
+ * residual and partial rows in 16-byte chunks: those pointers must be 16-byte
+ * aligned and their row strides keep every row 16-byte aligned (ldc, ldr a
+ * multiple of 8 elements for bf16, 4 for float32; ldp a multiple of 4).
  * Returns SMX_OK or an SMX_ERR_* code; smx_last_error() describes it.
  */
 int smx_gemm(const smx_gemm_desc* desc, const void* a, const void* b, void* c, const void* residual,
