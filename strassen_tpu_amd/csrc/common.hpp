@@ -445,20 +445,20 @@ __device__ __forceinline__ void tile_store(const uint8_t* tile, char* dst, int64
 }
 
 // Quadrant sources of the epilogue: the cubic's quadrants (plus an FP32
-// partial product), or Strassen's seven product sets, combined with the
-// classical formula unpermuted (the hot path) or with the call's formula and
-// permutation.
-constexpr int kQuadCubic = 0, kQuadCubicPartial = 1, kQuadClassical = 2, kQuadGeneric = 3;
+// partial product), or Strassen's seven product sets under the classical,
+// dual or powers formula. The block permutation is applied by addressing:
+// it only moves where a quadrant is stored (and which quadrant gates, for
+// SwiGLU / GeGLU, or is the a half, for q/k).
+constexpr int kQuadCubic = 0, kQuadCubicPartial = 1, kQuadClassical = 2, kQuadDual = 3, kQuadPowers = 4;
 
 template <int kQ>
 using QuadC = std::integral_constant<int, kQ>;
 
-// Physical output quadrant kQ of accumulator element (i, j, r). The
+// Logical output quadrant kQ of accumulator element (i, j, r). The
 // accumulators are only read, so no quadrant set is materialised next to
 // the 448 product registers.
 template <int kQuad, int kQ, int kMB, int kNB, int kNacc>
-__device__ __forceinline__ float quadrant_value(const Params& p, const f32x16 (&acc)[kNacc][kMB][kNB], int i, int j,
-                                                int r) {
+__device__ __forceinline__ float quadrant_value(const f32x16 (&acc)[kNacc][kMB][kNB], int i, int j, int r) {
   if constexpr (kQuad == kQuadCubic || kQuad == kQuadCubicPartial) {
     return acc[kQ][i][j][r];
   } else {
@@ -470,25 +470,21 @@ __device__ __forceinline__ float quadrant_value(const Params& p, const f32x16 (&
       if constexpr (kQ == 1) return p5 + p3;
       if constexpr (kQ == 2) return p4 + p2;
       if constexpr (kQ == 3) return ((p6 - p2) + p3) + p1;
+    } else if constexpr (kQuad == kQuadDual) {
+      // C0 = Q1+Q4-Q5+Q7, C1 = Q2+Q4, C2 = Q3+Q5, C3 = Q1-Q2+Q3+Q6
+      if constexpr (kQ == 0) return ((p4 - p5) + p7) + p1;
+      if constexpr (kQ == 1) return p4 + p2;
+      if constexpr (kQ == 2) return p5 + p3;
+      if constexpr (kQ == 3) return ((p6 + p3) - p2) + p1;
     } else {
-      // Logical quadrant (row, col) lands on physical (row ^ swap_m, col ^
-      // swap_n): physical kQ holds logical kQ ^ mask.
-      const int logical = kQ ^ ((p.perm & 1) ? 2 : 0) ^ ((p.perm & 4) ? 1 : 0);
-      const bool dual = p.formula == kFormulaDual, powers = p.formula == kFormulaPowers;
-      // classical and dual share C0 = P1+P4-P5+P7; classical C1 = P3+P5,
-      // C2 = P2+P4, C3 = P1-P2+P3+P6; dual C1 = Q2+Q4, C2 = Q3+Q5,
-      // C3 = Q1-Q2+Q3+Q6
-      const float c0 = ((p4 - p5) + p7) + p1, c1 = p5 + p3, c2 = p4 + p2;
-      const float c3 = ((p6 - p2) + p3) + p1, d3 = ((p6 + p3) - p2) + p1;
       // powers: basis z0 = R3+R5, z1 = R6+R7, z2 = R2-R4, z3 = R1-R3+R4+R7,
       // decoded as in strassen_pallas.py:744-760
-      const float z0 = p3 + p5, z1 = p6 + p7, z2 = p2 - p4, z3 = ((p4 - p3) + p7) + p1;
-      const float w0 = (z1 + z2) * 0.5f + z0 * 0.25f, w1 = ((z2 - z1) + z3) + z0 * 0.5f, w2 = z3 + z0 * 0.5f;
-      const float q0 = powers ? w0 : c0;
-      const float q1 = powers ? w1 : dual ? c2 : c1;
-      const float q2 = powers ? w2 : dual ? c1 : c2;
-      const float q3 = powers ? z0 : dual ? d3 : c3;
-      return logical == 0 ? q0 : logical == 1 ? q1 : logical == 2 ? q2 : q3;
+      const float z0 = p3 + p5;
+      if constexpr (kQ == 3) return z0;
+      const float z1 = p6 + p7, z2 = p2 - p4, z3 = ((p4 - p3) + p7) + p1;
+      if constexpr (kQ == 0) return (z1 + z2) * 0.5f + z0 * 0.25f;
+      if constexpr (kQ == 1) return ((z2 - z1) + z3) + z0 * 0.5f;
+      if constexpr (kQ == 2) return z3 + z0 * 0.5f;
     }
   }
 }
@@ -500,6 +496,11 @@ __device__ __forceinline__ float quadrant_value(const Params& p, const f32x16 (&
 // columns col0 + 32 j, relative to the tile origin o. Accumulator lane
 // layout (v_mfma_f32_32x32x16_bf16): column lane%32, row
 // 8*(r/4) + 4*(lane/32) + r%4 for register r.
+//
+// Logical quadrant (row, col) is stored at physical (row ^ swap_m, col ^
+// swap_n) for the block permutation (strassen_pallas.py:205-226), so the
+// permutation changes addresses only; SwiGLU / GeGLU and q/k, whose roles
+// follow physical columns, swap their two operands with one select.
 //
 // One output block at a time passes through the wave's staging tile `tile`
 // (StageTile<32 kMB, 32 kNB>::kBytes of LDS, private to the wave): a
@@ -517,6 +518,7 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
   asm volatile("" : "+v"(lane));
   const int hm = p.bm / 2, hn = p.bn / 2;
   const int lcol = lane & 31;
+  const int swap_m = p.perm & 1, swap_n = (p.perm >> 2) & 1;
   // Top-left output element of this wave (quadrant 0) and its column inside
   // the tile half.
   const int64_t row_base = o.ti * p.bm + o.tr + row0;
@@ -533,17 +535,17 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
     return *reinterpret_cast<const float*>(te + T::at(i, j, r));
   };
   auto value = [&](auto q, int i, int j, int r) __attribute__((always_inline)) {
-    return quadrant_value<kQuad, decltype(q)::value>(p, acc, i, j, r);
+    return quadrant_value<kQuad, decltype(q)::value>(acc, i, j, r);
   };
-  // Quadrant q of an [M, N] operand (row stride ld, element size es), for
-  // this wave: rows row_base + (q>>1) hm, columns col_base + (q&1) hn.
-  auto quadrant = [&](const void* base, int64_t ld, int es, int q) __attribute__((always_inline)) {
-    return reinterpret_cast<const char*>(base) + ((row_base + (q >> 1) * hm) * ld + col_base + (q & 1) * hn) * es;
+  // Physical quadrant (row half pr, column half pc) of an [M, N] operand
+  // (row stride ld, element size es), for this wave.
+  auto quadrant = [&](const void* base, int64_t ld, int es, int pr, int pc) __attribute__((always_inline)) {
+    return reinterpret_cast<const char*>(base) + ((row_base + pr * hm) * ld + col_base + pc * hn) * es;
   };
-  // The tile -> the output block at (row, col).
-  auto emit = [&](int64_t row, int64_t col) __attribute__((always_inline)) {
+  // The staging tile `t` -> the output block at (row, col).
+  auto emit_from = [&](uint8_t* t, int64_t row, int64_t col) __attribute__((always_inline)) {
     fence();
-    tile_store<T>(tile, reinterpret_cast<char*>(p.c) + (row * p.ldc + col) * (p.out_f32 ? 4 : 2), p.ldc, p.out_f32,
+    tile_store<T>(t, reinterpret_cast<char*>(p.c) + (row * p.ldc + col) * (p.out_f32 ? 4 : 2), p.ldc, p.out_f32,
                   lane);
     fence();
   };
@@ -553,7 +555,7 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
   if constexpr (kQuad == kQuadCubicPartial) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      tile_load<T>(tile, quadrant(p.partial, p.ldp, 4, q), p.ldp, 1, lane);
+      tile_load<T>(tile, quadrant(p.partial, p.ldp, 4, q >> 1, q & 1), p.ldp, 1, lane);
       fence();
 #pragma unroll
       for (int i = 0; i < kMB; ++i)
@@ -566,48 +568,49 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
   }
 
   if constexpr (kEpi == SMX_EPI_SWIGLU || kEpi == SMX_EPI_GEGLU) {
-    // Quadrants 0/2 are gate, 1/3 up; output [M, N/2].
+    // Physical quadrants 0/2 are gate, 1/3 up; output [M, N/2]. Logical row
+    // half lr lands on physical row half lr ^ swap_m; its gate is logical
+    // column swap_n.
     const int64_t ocol = o.tj * hn + cc_base;
-    auto gated = [&](auto gate_q, auto up_q, int64_t row) __attribute__((always_inline)) {
-#pragma unroll
-      for (int i = 0; i < kMB; ++i)
-#pragma unroll
-        for (int j = 0; j < kNB; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) put(i, j, r, gate_f32<kEpi>(value(gate_q, i, j, r)) * value(up_q, i, j, r));
-      emit(row, ocol);
-    };
-    gated(QuadC<0>{}, QuadC<1>{}, row_base);
-    gated(QuadC<2>{}, QuadC<3>{}, row_base + hm);
-  } else if constexpr (kEpi == SMX_EPI_QK_NORM_ROPE) {
-    // Per-head RMSNorm then RoPE (strassen_pallas.py:793-835). A head owns
-    // head_dim/2 = 64 consecutive columns of a tile half: the wave's column
-    // blocks j = 2h, 2h+1 (the caller guarantees kNB % 2 == 0 and 64-aligned
-    // wave columns). Quadrants 0/2 hold the a half, 1/3 the b half.
-    static_assert(kNB % 2 == 0, "qk epilogue needs 64-column waves");
-    // The norm spans both quadrants of a tile half and both halves are
-    // needed to the end: the quadrants are formed once, in place in sets
-    // 0-3 (straight-line code), which frees the other three product sets.
-    if constexpr (kQuad == kQuadClassical || kQuad == kQuadGeneric) {
+    auto gated = [&](auto q_left, auto q_right, int lr) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < kMB; ++i)
 #pragma unroll
         for (int j = 0; j < kNB; ++j)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const float q0 = quadrant_value<kQuad, 0>(p, acc, i, j, r);
-            const float q1 = quadrant_value<kQuad, 1>(p, acc, i, j, r);
-            const float q2 = quadrant_value<kQuad, 2>(p, acc, i, j, r);
-            const float q3 = quadrant_value<kQuad, 3>(p, acc, i, j, r);
+            const float left = value(q_left, i, j, r), right = value(q_right, i, j, r);
+            const float gate = swap_n ? right : left, up = swap_n ? left : right;
+            put(i, j, r, gate_f32<kEpi>(gate) * up);
+          }
+      emit_from(tile, row_base + (lr ^ swap_m) * hm, ocol);
+    };
+    gated(QuadC<0>{}, QuadC<1>{}, 0);
+    gated(QuadC<2>{}, QuadC<3>{}, 1);
+  } else if constexpr (kEpi == SMX_EPI_QK_NORM_ROPE) {
+    // Per-head RMSNorm then RoPE (strassen_pallas.py:793-835). A head owns
+    // head_dim/2 = 64 consecutive columns of a tile half: the wave's column
+    // blocks j = 2h, 2h+1 (the caller guarantees kNB % 2 == 0 and 64-aligned
+    // wave columns). Physical quadrants 0/2 hold the a half, 1/3 the b half.
+    static_assert(kNB % 2 == 0, "qk epilogue needs 64-column waves");
+    // The norm spans both quadrants of a tile half and both halves are
+    // needed to the end: the logical quadrants are formed once, in place in
+    // sets 0-3 (straight-line code), which frees the other three sets.
+    if constexpr (kNacc == 7) {
+#pragma unroll
+      for (int i = 0; i < kMB; ++i)
+#pragma unroll
+        for (int j = 0; j < kNB; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float q0 = value(QuadC<0>{}, i, j, r), q1 = value(QuadC<1>{}, i, j, r);
+            const float q2 = value(QuadC<2>{}, i, j, r), q3 = value(QuadC<3>{}, i, j, r);
             acc[0][i][j][r] = q0;
             acc[1][i][j][r] = q1;
             acc[2][i][j][r] = q2;
             acc[3][i][j][r] = q3;
           }
     }
-    auto qv = [&](auto q, int i, int j, int r) __attribute__((always_inline)) {
-      return acc[decltype(q)::value][i][j][r];
-    };
     const float inv_width = 1.0f / (float)p.head_dim;
     const int lrow4 = (lane >> 5) * 4;
     // rope tables are [M, hn], indexed by output row and column inside the half
@@ -618,7 +621,17 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
     // tile (this epilogue has two per wave) takes the b block.
     uint8_t* const tile_b = tile + T::kBytes;
     uint8_t* const te_b = tile_b + T::lane_part(lane);
-    auto rows = [&](auto qa, auto qb, int half) __attribute__((always_inline)) {
+    // Logical row half lr (sets 2 lr, 2 lr + 1) lands on physical row half
+    // lr ^ swap_m; its a half is logical column swap_n.
+    auto rows = [&](auto q_left, auto q_right, int lr) __attribute__((always_inline)) {
+      constexpr int kL = decltype(q_left)::value, kR = decltype(q_right)::value;
+      const int half = lr ^ swap_m;
+      auto qa = [&](int i, int j, int r) __attribute__((always_inline)) {
+        return swap_n ? acc[kR][i][j][r] : acc[kL][i][j][r];
+      };
+      auto qb = [&](int i, int j, int r) __attribute__((always_inline)) {
+        return swap_n ? acc[kL][i][j][r] : acc[kR][i][j][r];
+      };
 #pragma unroll
       for (int i = 0; i < kMB; ++i) {
 #pragma unroll
@@ -626,8 +639,8 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int ri = i * 32 + 8 * (r >> 2) + lrow4 + (r & 3);
-            const float a0 = qv(qa, i, 2 * h, r), a1 = qv(qa, i, 2 * h + 1, r);
-            const float b0 = qv(qb, i, 2 * h, r), b1 = qv(qb, i, 2 * h + 1, r);
+            const float a0 = qa(i, 2 * h, r), a1 = qa(i, 2 * h + 1, r);
+            const float b0 = qb(i, 2 * h, r), b1 = qb(i, 2 * h + 1, r);
             const float ssa = half_wave_sum(a0 * a0 + a1 * a1);
             const float ssb = half_wave_sum(b0 * b0 + b1 * b1);
             const float recip = 1.0f / sqrtf((ssa + ssb) * inv_width + p.eps);
@@ -640,8 +653,8 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
               const int toff = ri * hn + cj + half * hm_t;
               const float cs = bf16_to_f32(cos_w[toff]);
               const float sn = bf16_to_f32(sin_w[toff]);
-              const float na = qv(qa, i, j, r) * recip * ga;
-              const float nbv = qv(qb, i, j, r) * recip * gb;
+              const float na = qa(i, j, r) * recip * ga;
+              const float nbv = qb(i, j, r) * recip * gb;
               put(i, j, r, na * cs - nbv * sn);
               *reinterpret_cast<float*>(te_b + T::at(i, j, r)) = nbv * cs + na * sn;
             }
@@ -650,26 +663,26 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-      emit(row_base + half * hm, col_base);
-      tile_store<T>(tile_b, reinterpret_cast<char*>(p.c) + ((row_base + half * hm) * p.ldc + col_base + hn) *
-                                                             (p.out_f32 ? 4 : 2),
-                    p.ldc, p.out_f32, lane);
-      fence();
+      emit_from(tile, row_base + half * hm, col_base);
+      emit_from(tile_b, row_base + half * hm, col_base + hn);
     };
     rows(QuadC<0>{}, QuadC<1>{}, 0);
     rows(QuadC<2>{}, QuadC<3>{}, 1);
   } else {
+    // Logical quadrant q -> physical (row half (q >> 1) ^ swap_m, column
+    // half (q & 1) ^ swap_n); the residual and bias are those of the
+    // physical position.
     auto block = [&](auto q) __attribute__((always_inline)) {
       constexpr int kQ = decltype(q)::value;
+      const int pr = (kQ >> 1) ^ swap_m, pc = (kQ & 1) ^ swap_n;
       if constexpr (kEpi == SMX_EPI_RESIDUAL_ADD) {
-        tile_load<T>(tile, quadrant(p.residual, p.ldr, p.residual_f32 ? 4 : 2, kQ), p.ldr, p.residual_f32, lane);
+        tile_load<T>(tile, quadrant(p.residual, p.ldr, p.residual_f32 ? 4 : 2, pr, pc), p.ldr, p.residual_f32, lane);
         fence();
       }
 #pragma unroll
       for (int j = 0; j < kNB; ++j) {
         float b = 0.f;
-        if constexpr (kEpi == SMX_EPI_BIAS_ADD)
-          b = load_vec(p.bias, p.bias_f32, col_base + (kQ & 1) * hn + j * 32 + lcol);
+        if constexpr (kEpi == SMX_EPI_BIAS_ADD) b = load_vec(p.bias, p.bias_f32, col_base + pc * hn + j * 32 + lcol);
 #pragma unroll
         for (int i = 0; i < kMB; ++i)
 #pragma unroll
@@ -680,7 +693,7 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
             put(i, j, r, v);
           }
       }
-      emit(row_base + (kQ >> 1) * hm, col_base + (kQ & 1) * hn);
+      emit_from(tile, row_base + pr * hm, col_base + pc * hn);
     };
     block(QuadC<0>{});
     block(QuadC<1>{});

@@ -115,17 +115,23 @@ int launch_packed(Params p, hipStream_t stream) {
   p.tiles_m = (int)((p.m / 2) / packed::TM);
   p.tiles_n = (int)((p.n / 2) / packed::TN);
   p.group_m = group_m_setting();
-  // The epilogue's quadrant source is a kernel template argument: the
-  // classical unpermuted Strassen (the hot path) and the cubic without a
-  // partial product have straight-line epilogues of their own.
+  // The epilogue's quadrant source (the Strassen formula, or the cubic with
+  // or without a partial product) is a kernel template argument, so every
+  // epilogue is straight-line code; the block permutation is applied by
+  // addressing at run time.
   void (*kern)(Params);
   if constexpr (kAlgo == 7) {
-    if (!split_kernel_setting())
-      kern = packed::gemm_packed<7, kEpi, kQuadGeneric>;
-    else if (p.formula == SMX_FORMULA_CLASSICAL && p.perm == 0)
-      kern = split::gemm_split<kEpi, kQuadClassical>;
-    else
-      kern = split::gemm_split<kEpi, kQuadGeneric>;
+    const bool region = !split_kernel_setting();
+    if (p.formula == SMX_FORMULA_DUAL) {
+      kern = region ? packed::gemm_packed<7, kEpi, kQuadDual> : split::gemm_split<kEpi, kQuadDual>;
+    } else if (p.formula == SMX_FORMULA_POWERS) {
+      if constexpr (kEpi == SMX_EPI_NONE)
+        kern = region ? packed::gemm_packed<7, SMX_EPI_NONE, kQuadPowers> : split::gemm_split<SMX_EPI_NONE, kQuadPowers>;
+      else
+        return fail(SMX_ERR_INVALID, "fused epilogues require a quadrant-basis formula");
+    } else {
+      kern = region ? packed::gemm_packed<7, kEpi, kQuadClassical> : split::gemm_split<kEpi, kQuadClassical>;
+    }
   } else {
     kern = p.partial ? packed::gemm_packed<8, kEpi, kQuadCubicPartial> : packed::gemm_packed<8, kEpi, kQuadCubic>;
   }
