@@ -815,6 +815,35 @@ def test_multi_pass_variants_and_epilogues():
 
 
 # ---------------------------------------------------------------------------
+# Block permutations with every fused epilogue: the permutation moves where a
+# quadrant is stored, and swaps the gate/up and a/b roles of a column swap
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("formula", ["classical", "dual"])
+@pytest.mark.parametrize("perm", range(8))
+def test_permutation_with_every_epilogue(formula, perm):
+    rng, a, b = _gaussian(450 + perm, 512, 1024, 1024)
+    kw = dict(bm=256, bn=512, bk=512, formula_variant=formula, block_permutation=perm)
+    laid = o.swiglu_weight_layout(b, 512)
+    for epi in ("swiglu", "geglu"):
+        got = host(smx.strassen_matmul(dev(a), dev_weight(laid), epilogue=epi, **kw))
+        assert_ulp_close(got, o.strassen_matmul(a, laid, epilogue=epi, **kw), k=1024)
+    got = host(smx.strassen_matmul(dev(a), dev_weight(b), **kw))
+    assert_ulp_close(got, o.strassen_matmul(a, b, **kw), k=1024)
+    r = o.bf16_round(rng.standard_normal((512, 1024)).astype(np.float32))
+    got = host(smx.strassen_matmul(dev(a), dev_weight(b), epilogue="residual_add", residual=dev(r), **kw))
+    assert_ulp_close(got, o.strassen_matmul(a, b, epilogue="residual_add", residual=r, **kw), k=1024)
+    bias = o.bf16_round(rng.standard_normal(1024).astype(np.float32))
+    got = host(smx.strassen_matmul(dev(a), dev_weight(b), epilogue="bias_add", bias=dev(bias), **kw))
+    assert_ulp_close(got, o.strassen_matmul(a, b, epilogue="bias_add", bias=bias, **kw), k=1024)
+    x, w, lq, tcos, tsin, scale = _qk_problem(460 + perm, 2, 256, 8, 1024, 512)
+    qkw = dict(kw, epilogue="qk_norm_rope", rope_head_dim=128, rope_eps=1e-6)
+    got = host(smx.strassen_matmul(dev(x), dev_weight(lq), rope_cos=dev(tcos), rope_sin=dev(tsin),
+                                   rope_scale=dev(scale), **qkw))
+    assert_ulp_close(got, o.strassen_matmul(x, lq, rope_cos=tcos, rope_sin=tsin, rope_scale=scale, **qkw), k=1024)
+
+
+# ---------------------------------------------------------------------------
 # Full Qwen3-32B shapes (8 x 1024 tokens)
 # ---------------------------------------------------------------------------
 
