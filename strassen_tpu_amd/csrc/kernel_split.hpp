@@ -12,6 +12,13 @@
 // the workgroup reads 68 KB of LDS instead of 112 KB (0.61 KB per MFMA
 // instead of 1.0), while the DMA writes are unchanged.
 //
+// Stage ring (all 160 KB of LDS): B holds three stages of its seven
+// operands (prefetched two stages ahead); A holds three stages of operands
+// 0-4 and two of operands 5-6 (prefetched one stage ahead). A full three-
+// stage ring of both (168 KB) does not fit; of the splits that do, this one
+// measured fastest (the weight operand B, streamed from HBM, needs the
+// distance most).
+//
 // After the last stage the waves exchange accumulator blocks through LDS so
 // that wave (wm, wn) holds all seven products of its 64x64 region, the
 // layout gemm_packed ends with; the shared epilogue then combines and
@@ -58,28 +65,45 @@ struct StripFrags {
   bf16x8 b[4];
 };
 
-// One wave's main loop, accumulator exchange and epilogue. The stage ring
-// holds kNA A stages and kNB B stages (gemm_packed<7>: 2 and 3); each wave
-// moves fragments wave + 4x of every stage.
-template <int kWave, int kEpi, int kQuad, int kNA, int kNB>
+// LDS layout of the stage ring. A operand x < kLongOps of stage s sits in
+// slot s % 3 of the long region, operand x >= kLongOps in slot s % 2 of the
+// short region; B stage s in slot s % 3. Each wave moves fragment (op x,
+// row block = wave) of every operand, i.e. 7 DMAs per operand and stage.
+struct Ring {
+  using L = packed::Lay<7>;
+  static constexpr int kLongOps = 5;
+  static constexpr int kShortOps = 7 - kLongOps;
+  static constexpr int kALong = kLongOps * kBlocks * kFrag;    // one A stage, operands 0-4
+  static constexpr int kAShort = kShortOps * kBlocks * kFrag;  // one A stage, operands 5-6
+  static constexpr int kAShortBase = 3 * kALong;
+  static constexpr int kBBase = kAShortBase + 2 * kAShort;
+  static constexpr int kBytes = kBBase + 3 * L::kStage;
+  // Per stage s a wave issues, in this order, A operands 5-6 of stage s+1,
+  // A operands 0-4 of stage s+2 and B of stage s+2; at the barrier only the
+  // last two groups may still be in flight (vmcnt completes in order).
+  static constexpr int kDma = 7 + 7;
+  static constexpr int kPending = kLongOps + 7;
+  static_assert(kBytes <= 160 * 1024, "stage ring exceeds the LDS");
+  static_assert(kPending < 64, "vmcnt range");
+};
+
+// One wave's main loop, accumulator exchange and epilogue.
+template <int kWave, int kEpi, int kQuad>
 __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, int nstages, int lane,
                                          const uint8_t* a_src, const uint8_t* b_src, uint8_t* lds) {
   using L = packed::Lay<7>;
   using P = Plan<kWave>;
-  // The operand with the shorter prefetch distance is issued first each
-  // stage, so the barrier's vmcnt can leave the other one in flight.
-  // VMEM operations issued after the last one stage s+1 needs: with equal
-  // depths N, the 2(N-2) later stage prefetches; otherwise everything after
-  // the shorter operand's stage s+1 prefetch.
-  constexpr int kMin = kNA < kNB ? kNA : kNB;
-  constexpr int kPending = (kNA == kNB ? 2 * (kNA - 2) : 2 * kMin - 3) * L::kDmaPerWave;
-  static_assert(kMin >= 2 && (kNA + kNB) * L::kStage <= 160 * 1024, "ring depth / LDS budget");
-  uint8_t* const a_region = lds;
-  uint8_t* const b_region = lds + kNA * L::kStage;
+  uint8_t* const a_long = lds;
+  uint8_t* const a_short = lds + Ring::kAShortBase;
+  uint8_t* const b_region = lds + Ring::kBBase;
   const uint32_t lane_off = lane * 16;
   const int lo = lane * 16;
-  auto load_a = [&](const uint8_t* sa, int j) {
-    return packed::ld_frag(sa + (P::product(j) * kBlocks + P::row(j)) * kFrag + lo);
+  // Operand and slot choices depend only on the strip (a compile-time
+  // constant after unrolling), so each read is one LDS load from a slot base.
+  auto load_a = [&](const uint8_t* sl, const uint8_t* ss, int j) {
+    constexpr int kL = Ring::kLongOps;
+    return P::product(j) < kL ? packed::ld_frag(sl + (P::product(j) * kBlocks + P::row(j)) * kFrag + lo)
+                              : packed::ld_frag(ss + ((P::product(j) - kL) * kBlocks + P::row(j)) * kFrag + lo);
   };
   auto load_b = [&](const uint8_t* sb, int j, bf16x8 (&b)[4]) {
 #pragma unroll
@@ -103,51 +127,58 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
     }
   };
 
-  // Stage s: prefetch stages s+kNA-1 (A) and s+kNB-1 (B) spread over strips
-  // 0-5, with the next strip's fragments read under the current strip's
-  // MFMAs; barrier; the next stage's strip-0 fragments read under strip 6's
+  // Stage s: the 14 prefetch DMAs spread over strips 0-5 (two or three
+  // after each strip's MFMAs, the short-distance A operands first), with
+  // the next strip's fragments read under the current strip's MFMAs;
+  // barrier; the next stage's strip-0 fragments read under strip 6's
   // MFMAs. The barrier sees every read of stage s complete and every wave's
-  // DMA of stage s+1 landed (vmcnt leaves only the newer prefetches in
-  // flight).
-  int s = 0, a_slot = 0, b_slot = 0;
-  bf16x8 a_cur = load_a(a_region, 0);
+  // DMA of stage s+1 landed.
+  int s = 0, l_slot = 0, s_slot = 0;
+  bf16x8 a_cur = load_a(a_long, a_short, 0);
   bf16x8 b_cur[4];
   load_b(b_region, 0, b_cur);
   do {
-    // Slots of stage s + kN - 1 (the one read at stage s - 1) and s + 1.
-    const int a_fill = a_slot == 0 ? kNA - 1 : a_slot - 1, a_slot1 = a_slot == kNA - 1 ? 0 : a_slot + 1;
-    const int b_fill = b_slot == 0 ? kNB - 1 : b_slot - 1, b_slot1 = b_slot == kNB - 1 ? 0 : b_slot + 1;
-    // The stage's 14 DMA fragments (7 of each operand, the operand with the
-    // shorter prefetch distance first) are issued two or three at a time
-    // after each of strips 0-5, so the vector memory queue never holds a
-    // whole stage in front of the MFMAs; all are issued before the barrier,
-    // whose vmcnt accounting is unchanged.
-    constexpr bool kAFirst = kNA <= kNB;
+    // Long slots: the one read at stage s-1 is refilled with stage s+2;
+    // short slots: the one read at stage s-1 with stage s+1.
+    const int l_fill = l_slot == 0 ? 2 : l_slot - 1, l_next = l_slot == 2 ? 0 : l_slot + 1;
+    const int s_fill = s_slot ^ 1, s_next = s_slot ^ 1;
     // The lane offset is re-derived opaquely each stage: otherwise the
-    // compiler hoists (operand base + lane offset) out of the loop as two
-    // 64-bit per-lane addresses held across it, where the VGPRs next to the
+    // compiler hoists (operand base + lane offset) out of the loop as 64-bit
+    // per-lane addresses held across it, where the VGPRs next to the
     // accumulators cannot afford them; this way the loads take a uniform
     // base plus a 32-bit lane offset.
     uint32_t dma_lane = lane_off;
     asm volatile("" : "+v"(dma_lane));
-    const uint8_t* const a_from = a_src + (int64_t)min(s + kNA - 1, nstages - 1) * L::kStage;
-    const uint8_t* const b_from = b_src + (int64_t)min(s + kNB - 1, nstages - 1) * L::kStage;
-    uint8_t* const a_to = a_region + a_fill * L::kStage + kWave * kFrag;
-    uint8_t* const b_to = b_region + b_fill * L::kStage + kWave * kFrag;
+    const uint8_t* const a_near = a_src + (int64_t)min(s + 1, nstages - 1) * L::kStage;
+    const uint8_t* const a_far = a_src + (int64_t)min(s + 2, nstages - 1) * L::kStage;
+    const uint8_t* const b_far = b_src + (int64_t)min(s + 2, nstages - 1) * L::kStage;
+    uint8_t* const as_to = a_short + s_fill * Ring::kAShort + kWave * kFrag;
+    uint8_t* const al_to = a_long + l_fill * Ring::kALong + kWave * kFrag;
+    uint8_t* const b_to = b_region + l_fill * L::kStage + kWave * kFrag;
     auto dma_op = [&](int q) {
-      const bool is_a = kAFirst ? q < L::kDmaPerWave : q >= L::kDmaPerWave;
-      const int x = q < L::kDmaPerWave ? q : q - L::kDmaPerWave;
-      // uniform base + fragment offset, then the lane's 32-bit offset
-      __builtin_amdgcn_global_load_lds((is_a ? a_from : b_from) + x * 4 * kFrag + dma_lane,
-                                       (__attribute__((address_space(3))) void*)((is_a ? a_to : b_to) + 4 * x * kFrag),
-                                       16, 0, 0);
+      constexpr int kS = Ring::kShortOps, kL = Ring::kLongOps;
+      const uint8_t* from;
+      uint8_t* to;
+      if (q < kS) {
+        from = a_near + (kL + q) * 4 * kFrag;
+        to = as_to + q * 4 * kFrag;
+      } else if (q < 7) {
+        from = a_far + (q - kS) * 4 * kFrag;
+        to = al_to + (q - kS) * 4 * kFrag;
+      } else {
+        from = b_far + (q - 7) * 4 * kFrag;
+        to = b_to + (q - 7) * 4 * kFrag;
+      }
+      // uniform base + operand offset, then the lane's 32-bit offset
+      __builtin_amdgcn_global_load_lds(from + dma_lane, (__attribute__((address_space(3))) void*)to, 16, 0, 0);
     };
     __builtin_amdgcn_sched_barrier(0);
-    const uint8_t* const sa = a_region + a_slot * L::kStage;
-    const uint8_t* const sb = b_region + b_slot * L::kStage;
+    const uint8_t* const sal = a_long + l_slot * Ring::kALong;
+    const uint8_t* const sas = a_short + s_slot * Ring::kAShort;
+    const uint8_t* const sb = b_region + l_slot * L::kStage;
 #pragma unroll
     for (int j = 0; j < 6; ++j) {
-      const bf16x8 a_next = load_a(sa, j + 1);
+      const bf16x8 a_next = load_a(sal, sas, j + 1);
       if (P::opens(j + 1)) {
         bf16x8 b_next_frags[4];
         load_b(sb, j + 1, b_next_frags);
@@ -158,24 +189,22 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
         mfma_strip(j, a_cur, b_cur);
       }
 #pragma unroll
-      for (int q = (2 * L::kDmaPerWave * j) / 6; q < (2 * L::kDmaPerWave * (j + 1)) / 6; ++q) dma_op(q);
+      for (int q = (Ring::kDma * j) / 6; q < (Ring::kDma * (j + 1)) / 6; ++q) dma_op(q);
       __builtin_amdgcn_sched_barrier(0);
       a_cur = a_next;
     }
-    packed::stage_barrier<kPending>();
+    packed::stage_barrier<Ring::kPending>();
     // Stage s+1's strip 0 (past the last stage: a re-loaded copy, unused).
-    const uint8_t* const na = a_region + a_slot1 * L::kStage;
-    const uint8_t* const nb = b_region + b_slot1 * L::kStage;
-    const bf16x8 a_first = load_a(na, 0);
+    const bf16x8 a_first = load_a(a_long + l_next * Ring::kALong, a_short + s_next * Ring::kAShort, 0);
     bf16x8 b_first[4];
-    load_b(nb, 0, b_first);
+    load_b(b_region + l_next * L::kStage, 0, b_first);
     mfma_strip(6, a_cur, b_cur);
     __builtin_amdgcn_sched_barrier(0);
     a_cur = a_first;
 #pragma unroll
     for (int c = 0; c < 4; ++c) b_cur[c] = b_first[c];
-    b_slot = b_slot1;
-    a_slot = a_slot1;
+    l_slot = l_next;
+    s_slot = s_next;
   } while (++s < nstages);
   drain(acc);
 
@@ -229,7 +258,7 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
                               lds + kWave * kEpiTiles<kEpi> * StageTile<64, 64>::kBytes);
 }
 
-template <int kEpi, int kQuad, int kNA = 2, int kNB = 3>
+template <int kEpi, int kQuad>
 __global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
   using L = packed::Lay<7>;
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
@@ -250,48 +279,40 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
   const uint8_t* const b_src =
       reinterpret_cast<const uint8_t*>(p.b) + (int64_t)tile_n * nstages * L::kStage + wave * kFrag;
 
-  // Prologue: A stages 0 .. kNA-2 and B stages 0 .. kNB-2, issued in the
-  // loop's order (shorter distance first) so the barrier's vmcnt matches.
+  // Prologue: stage 0 of everything (A's short operands first, as in the
+  // loop), then stage 1 of A's long operands and of B; stage 0 has landed
+  // once only stage 1 remains in flight.
   const uint32_t lane_off = lane * 16;
-  auto dma = [&](const uint8_t* src, int stage, uint8_t* slot) {
+  auto dma = [&](const uint8_t* src, int stage, int x0, int x1, uint8_t* slot) {
     const uint8_t* from = src + (int64_t)min(stage, nstages - 1) * L::kStage + lane_off;
 #pragma unroll
-    for (int x = 0; x < L::kDmaPerWave; ++x)
+    for (int x = x0; x < x1; ++x)
       __builtin_amdgcn_global_load_lds(from + x * 4 * kFrag,
-                                       (__attribute__((address_space(3))) void*)(slot + (wave + 4 * x) * kFrag), 16,
-                                       0, 0);
+                                       (__attribute__((address_space(3))) void*)(slot + (wave + 4 * (x - x0)) * kFrag),
+                                       16, 0, 0);
   };
-  uint8_t* const b_region = lds + kNA * L::kStage;
-#pragma unroll
-  for (int st = 0; st + 1 < (kNA > kNB ? kNA : kNB); ++st) {
-    if constexpr (kNA <= kNB) {
-      if (st + 1 < kNA) dma(a_src, st, lds + st * L::kStage);
-      if (st + 1 < kNB) dma(b_src, st, b_region + st * L::kStage);
-    } else {
-      if (st + 1 < kNB) dma(b_src, st, b_region + st * L::kStage);
-      if (st + 1 < kNA) dma(a_src, st, lds + st * L::kStage);
-    }
-  }
-  // Stage 0 of both operands has landed once only the later prologue
-  // stages remain in flight.
-  constexpr int kPrologue = (kNA > kNB ? kNA - kNB : kNB - kNA) * L::kDmaPerWave +
-                            ((kNA < kNB ? kNA : kNB) - 2) * 2 * L::kDmaPerWave;
-  packed::stage_barrier<kPrologue>();
+  uint8_t* const b_region = lds + Ring::kBBase;
+  dma(a_src, 0, Ring::kLongOps, 7, lds + Ring::kAShortBase);
+  dma(a_src, 0, 0, Ring::kLongOps, lds);
+  dma(b_src, 0, 0, 7, b_region);
+  dma(a_src, 1, 0, Ring::kLongOps, lds + Ring::kALong);
+  dma(b_src, 1, 0, 7, b_region + L::kStage);
+  packed::stage_barrier<Ring::kPending>();
 
   // One code path per wave (its strip plan is a compile-time constant); no
   // accumulator is live across the branches.
   switch (wave) {
     case 0:
-      run_wave<0, kEpi, kQuad, kNA, kNB>(p, o, nstages, lane, a_src, b_src, lds);
+      run_wave<0, kEpi, kQuad>(p, o, nstages, lane, a_src, b_src, lds);
       break;
     case 1:
-      run_wave<1, kEpi, kQuad, kNA, kNB>(p, o, nstages, lane, a_src, b_src, lds);
+      run_wave<1, kEpi, kQuad>(p, o, nstages, lane, a_src, b_src, lds);
       break;
     case 2:
-      run_wave<2, kEpi, kQuad, kNA, kNB>(p, o, nstages, lane, a_src, b_src, lds);
+      run_wave<2, kEpi, kQuad>(p, o, nstages, lane, a_src, b_src, lds);
       break;
     default:
-      run_wave<3, kEpi, kQuad, kNA, kNB>(p, o, nstages, lane, a_src, b_src, lds);
+      run_wave<3, kEpi, kQuad>(p, o, nstages, lane, a_src, b_src, lds);
       break;
   }
 }

@@ -120,8 +120,13 @@ int launch_packed(Params p, hipStream_t stream) {
   // epilogue is straight-line code; the block permutation is applied by
   // addressing at run time.
   void (*kern)(Params);
+  // the stage ring, then the epilogue's staging tiles, share the LDS; the
+  // product-split kernel's ring fills all of it
+  constexpr int epi_lds = kEpiLds<kEpi, 64, 64>;
+  int lds = packed::Lay<kAlgo>::kLds > epi_lds ? packed::Lay<kAlgo>::kLds : epi_lds;
   if constexpr (kAlgo == 7) {
     const bool region = !split_kernel_setting();
+    if (!region) lds = split::Ring::kBytes > epi_lds ? split::Ring::kBytes : epi_lds;
     if (p.formula == SMX_FORMULA_DUAL) {
       kern = region ? packed::gemm_packed<7, kEpi, kQuadDual> : split::gemm_split<kEpi, kQuadDual>;
     } else if (p.formula == SMX_FORMULA_POWERS) {
@@ -135,9 +140,6 @@ int launch_packed(Params p, hipStream_t stream) {
   } else {
     kern = p.partial ? packed::gemm_packed<8, kEpi, kQuadCubicPartial> : packed::gemm_packed<8, kEpi, kQuadCubic>;
   }
-  // the stage ring, then the epilogue's staging tiles, share the LDS
-  constexpr int lds = packed::Lay<kAlgo>::kLds > kEpiLds<kEpi, 64, 64> ? packed::Lay<kAlgo>::kLds
-                                                                         : kEpiLds<kEpi, 64, 64>;
   if (int rc = set_lds(kern, lds)) return rc;
   hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n), dim3(kThreads), lds, stream, p);
   return check_launch();
