@@ -14,7 +14,8 @@
 //
 // Stage ring (all 160 KB of LDS): B holds three stages of its seven
 // operands (prefetched two stages ahead); A holds three stages of operands
-// 0-4 and two of operands 5-6 (prefetched one stage ahead). A full three-
+// 0-4 and two of operands 5-6 (refilled right after the barrier that frees
+// their slot, one stage and a strip ahead). A full three-
 // stage ring of both (168 KB) does not fit; of the splits that do, this one
 // measured fastest (the weight operand B, streamed from HBM, needs the
 // distance most).
@@ -78,10 +79,12 @@ struct Ring {
   static constexpr int kAShortBase = 3 * kALong;
   static constexpr int kBBase = kAShortBase + 2 * kAShort;
   static constexpr int kBytes = kBBase + 3 * L::kStage;
-  // Per stage s a wave issues, in this order, A operands 5-6 of stage s+1,
-  // A operands 0-4 of stage s+2 and B of stage s+2; at the barrier only the
-  // last two groups may still be in flight (vmcnt completes in order).
-  static constexpr int kDma = 7 + 7;
+  // Each wave issues, in this order: right after the barrier that ends
+  // stage s-1, A operands 5-6 of stage s+1 (into the short slot stage s-1
+  // used); during stage s, A operands 0-4 and B of stage s+2. At the barrier
+  // that ends stage s only the last two groups may still be in flight
+  // (vmcnt completes in order).
+  static constexpr int kLoopDma = kLongOps + 7;
   static constexpr int kPending = kLongOps + 7;
   static_assert(kBytes <= 160 * 1024, "stage ring exceeds the LDS");
   static_assert(kPending < 64, "vmcnt range");
@@ -127,21 +130,21 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
     }
   };
 
-  // Stage s: the 14 prefetch DMAs spread over strips 0-5 (two or three
-  // after each strip's MFMAs, the short-distance A operands first), with
-  // the next strip's fragments read under the current strip's MFMAs;
-  // barrier; the next stage's strip-0 fragments read under strip 6's
+  // Stage s: the 12 long-distance prefetch DMAs spread over strips 0-5 (two
+  // after each strip's MFMAs), with the next strip's fragments read under
+  // the current strip's MFMAs; barrier; the short-distance A prefetch of
+  // stage s+2; the next stage's strip-0 fragments read under strip 6's
   // MFMAs. The barrier sees every read of stage s complete and every wave's
-  // DMA of stage s+1 landed.
+  // DMA of stage s+1 landed. Issuing the short-distance prefetch right
+  // after the barrier, instead of with the others, gave 0.7%.
   int s = 0, l_slot = 0, s_slot = 0;
   bf16x8 a_cur = load_a(a_long, a_short, 0);
   bf16x8 b_cur[4];
   load_b(b_region, 0, b_cur);
   do {
-    // Long slots: the one read at stage s-1 is refilled with stage s+2;
-    // short slots: the one read at stage s-1 with stage s+1.
+    // Long slots: the one read at stage s-1 is refilled with stage s+2.
     const int l_fill = l_slot == 0 ? 2 : l_slot - 1, l_next = l_slot == 2 ? 0 : l_slot + 1;
-    const int s_fill = s_slot ^ 1, s_next = s_slot ^ 1;
+    const int s_next = s_slot ^ 1;
     // The lane offset is re-derived opaquely each stage: otherwise the
     // compiler hoists (operand base + lane offset) out of the loop as 64-bit
     // per-lane addresses held across it, where the VGPRs next to the
@@ -149,25 +152,21 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
     // base plus a 32-bit lane offset.
     uint32_t dma_lane = lane_off;
     asm volatile("" : "+v"(dma_lane));
-    const uint8_t* const a_near = a_src + (int64_t)min(s + 1, nstages - 1) * L::kStage;
     const uint8_t* const a_far = a_src + (int64_t)min(s + 2, nstages - 1) * L::kStage;
     const uint8_t* const b_far = b_src + (int64_t)min(s + 2, nstages - 1) * L::kStage;
-    uint8_t* const as_to = a_short + s_fill * Ring::kAShort + kWave * kFrag;
     uint8_t* const al_to = a_long + l_fill * Ring::kALong + kWave * kFrag;
     uint8_t* const b_to = b_region + l_fill * L::kStage + kWave * kFrag;
+    // q < 5: A operand q; q >= 5: B operand q - 5
     auto dma_op = [&](int q) {
-      constexpr int kS = Ring::kShortOps, kL = Ring::kLongOps;
+      constexpr int kL = Ring::kLongOps;
       const uint8_t* from;
       uint8_t* to;
-      if (q < kS) {
-        from = a_near + (kL + q) * 4 * kFrag;
-        to = as_to + q * 4 * kFrag;
-      } else if (q < 7) {
-        from = a_far + (q - kS) * 4 * kFrag;
-        to = al_to + (q - kS) * 4 * kFrag;
+      if (q < kL) {
+        from = a_far + q * 4 * kFrag;
+        to = al_to + q * 4 * kFrag;
       } else {
-        from = b_far + (q - 7) * 4 * kFrag;
-        to = b_to + (q - 7) * 4 * kFrag;
+        from = b_far + (q - kL) * 4 * kFrag;
+        to = b_to + (q - kL) * 4 * kFrag;
       }
       // uniform base + operand offset, then the lane's 32-bit offset
       __builtin_amdgcn_global_load_lds(from + dma_lane, (__attribute__((address_space(3))) void*)to, 16, 0, 0);
@@ -189,11 +188,20 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
         mfma_strip(j, a_cur, b_cur);
       }
 #pragma unroll
-      for (int q = (Ring::kDma * j) / 6; q < (Ring::kDma * (j + 1)) / 6; ++q) dma_op(q);
+      for (int q = (Ring::kLoopDma * j) / 6; q < (Ring::kLoopDma * (j + 1)) / 6; ++q) dma_op(q);
       __builtin_amdgcn_sched_barrier(0);
       a_cur = a_next;
     }
     packed::stage_barrier<Ring::kPending>();
+    {
+      // A operands 5-6 of stage s+2 into the short slot stage s used.
+      const uint8_t* const a_near = a_src + (int64_t)min(s + 2, nstages - 1) * L::kStage;
+      uint8_t* const as_to = a_short + s_slot * Ring::kAShort + kWave * kFrag;
+#pragma unroll
+      for (int q = 0; q < Ring::kShortOps; ++q)
+        __builtin_amdgcn_global_load_lds(a_near + (Ring::kLongOps + q) * 4 * kFrag + dma_lane,
+                                         (__attribute__((address_space(3))) void*)(as_to + q * 4 * kFrag), 16, 0, 0);
+    }
     // Stage s+1's strip 0 (past the last stage: a re-loaded copy, unused).
     const bf16x8 a_first = load_a(a_long + l_next * Ring::kALong, a_short + s_next * Ring::kAShort, 0);
     bf16x8 b_first[4];
@@ -279,9 +287,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
   const uint8_t* const b_src =
       reinterpret_cast<const uint8_t*>(p.b) + (int64_t)tile_n * nstages * L::kStage + wave * kFrag;
 
-  // Prologue: stage 0 of everything (A's short operands first, as in the
-  // loop), then stage 1 of A's long operands and of B; stage 0 has landed
-  // once only stage 1 remains in flight.
+  // Prologue: stage 0 of everything, then stage 1 of A's long operands, of
+  // B and of A's short operands (the loop's order); stage 0 has landed once
+  // only stage 1 remains in flight.
   const uint32_t lane_off = lane * 16;
   auto dma = [&](const uint8_t* src, int stage, int x0, int x1, uint8_t* slot) {
     const uint8_t* from = src + (int64_t)min(stage, nstages - 1) * L::kStage + lane_off;
@@ -297,7 +305,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
   dma(b_src, 0, 0, 7, b_region);
   dma(a_src, 1, 0, Ring::kLongOps, lds + Ring::kALong);
   dma(b_src, 1, 0, 7, b_region + L::kStage);
-  packed::stage_barrier<Ring::kPending>();
+  dma(a_src, 1, Ring::kLongOps, 7, lds + Ring::kAShortBase + Ring::kAShort);
+  packed::stage_barrier<Ring::kPending + Ring::kShortOps>();
 
   // One code path per wave (its strip plan is a compile-time constant); no
   // accumulator is live across the branches.
