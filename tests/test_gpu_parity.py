@@ -12,6 +12,7 @@ Bars:
   the whole-output error bound against an FP32 product.
 """
 
+import ctypes
 import json
 import os
 
@@ -146,7 +147,40 @@ INT_CASES = [
     ((256, 512, 256), (256, 256, 512)),
     ((512, 1024, 512), (256, 256, 256)),
     ((1024, 2048, 768), (512, 256, 512)),
+    # the fewest K stages the surface allows (bk % 256): 8 stages of 32
+    ((512, 256, 512), (256, 256, 256)),
 ]
+
+
+@pytest.mark.parametrize("k", [64, 128, 192])
+@pytest.mark.parametrize("algo", [7, 8])
+def test_short_k_ring_through_c_abi(k, algo):
+    """2, 4 and 6 K stages (bk = 64, which the C ABI accepts and the surface's
+    TPU rule does not): the stage ring's prologue and the prefetches past the
+    last stage, which re-load it and are never read. Integer operands, so the
+    bf16 output equals the exact product rounded once."""
+    from strassen_tpu_amd import _lib
+
+    m, n, bm, bn, bk = 512, 512, 256, 256, 64
+    rng = np.random.default_rng(511 + k)
+    a = rng.integers(-2, 3, (m, k)).astype(np.float32)
+    b = rng.integers(-2, 3, (k, n)).astype(np.float32)
+    say(f"  algo={algo} shape={(m, k, n)} tile={(bm, bn, bk)}")
+    pa = smx.pack_activation(dev(a), algo, bm, bk)
+    pb = (smx.strassen_weight_layout if algo == 7 else smx.cubic_weight_layout)(dev_weight(b), bn, bk)
+    out = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=DEV)
+    d = _lib.SmxGemmDesc()
+    d.m, d.n, d.k = m, n, k
+    d.lda, d.ldb, d.ldc, d.ldr = k, k, n, 0
+    d.bm, d.bn, d.bk = bm, bn, bk
+    d.algo, d.epilogue = algo, _lib.SMX_EPI[None]
+    d.a_layout, d.b_layout = _lib.SMX_A_PACKED, _lib.SMX_B_PACKED
+    d.rope_head_dim, d.rope_eps = 128, 1e-6
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(_lib.load().smx_gemm(d, _lib.ptr(pa.data), _lib.ptr(pb.data), _lib.ptr(out), None, None, None, None,
+                                    None, ctypes.c_void_p(stream)))
+    want = o.bf16_round((a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32))
+    np.testing.assert_array_equal(host(out), want)
 
 
 @pytest.mark.parametrize("shape,tile", INT_CASES)
