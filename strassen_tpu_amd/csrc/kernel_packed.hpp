@@ -348,6 +348,32 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
 // 32-row product block over kPackStages stages: each lane loads 16 bytes of
 // each quadrant per stage and stores nops 16-byte chunks, so the stores of
 // a wave are whole 1 KB fragments.
+// One lane's share of one packed stage: from the four quadrant values x
+// (A: [row half][K half]; B: [K half][column half]) of its 8 consecutive k,
+// the nops operands of the formula, each stored as 16 bytes at dst + op x 4 KB
+// (lane-contiguous, so every store instruction writes 1 KB).
+template <int kAlgo, int kSide, bool kF32>
+__device__ __forceinline__ void store_fragments(F8 (&x)[4], int formula, int perm, int part, uint8_t* dst) {
+  auto store = [&](int op, const F8& v) {
+    *reinterpret_cast<u32x4*>(dst + op * kBlocks * kFrag) = kF32 ? pack8_part(v, part) : pack8(v);
+  };
+  if constexpr (kAlgo == 7) {
+    F8 ops[7];
+    if constexpr (kSide != 1) {
+      permute_quadrants(x, perm & 1, (perm >> 1) & 1);  // A: (rows, K halves)
+      formula_vals<0, !kF32>(formula, x, ops);
+    } else {
+      permute_quadrants(x, (perm >> 1) & 1, (perm >> 2) & 1);  // B: (K halves, columns)
+      formula_vals<1, !kF32>(formula, x, ops);
+    }
+#pragma unroll
+    for (int op = 0; op < 7; ++op) store(op, ops[op]);
+  } else {
+#pragma unroll
+    for (int op = 0; op < 4; ++op) store(op, x[op]);
+  }
+}
+
 template <int kAlgo, int kSide, bool kF32>
 __global__ __launch_bounds__(256) void pack_operand(const void* __restrict__ src_v, int64_t ld, int64_t rows,
                                                     int64_t k, int32_t tile_rows, int32_t bk, int32_t formula,
@@ -438,25 +464,83 @@ __global__ __launch_bounds__(256) void pack_operand(const void* __restrict__ src
       x[2] = load_row(first, hi);
       x[3] = load_row(second, hi);
     }
-    uint8_t* const dst = dst_tile + st * (int64_t)(nops * kBlocks * kFrag);
-    auto store = [&](int op, const F8& v) {
-      *reinterpret_cast<u32x4*>(dst + op * kBlocks * kFrag) = kF32 ? pack8_part(v, part) : pack8(v);
-    };
-    if constexpr (kAlgo == 7) {
-      F8 ops[7];
-      if constexpr (kSide != 1) {
-        permute_quadrants(x, perm & 1, (perm >> 1) & 1);  // A: (rows, K halves)
-        formula_vals<0, !kF32>(formula, x, ops);
-      } else {
-        permute_quadrants(x, (perm >> 1) & 1, (perm >> 2) & 1);  // B: (K halves, columns)
-        formula_vals<1, !kF32>(formula, x, ops);
-      }
+    store_fragments<kAlgo, kSide, kF32>(x, formula, perm, part, dst_tile + st * (int64_t)(nops * kBlocks * kFrag));
+  }
+}
+
+// pack_operand for bf16 row-major sources (A [rows, k], or a weight stored
+// [n, k]) at one pass, with coalesced reads. pack_operand's lanes read 32
+// source rows per instruction, 32 bytes of each; here a workgroup first
+// copies, for 32 product rows and kRowStages stages, the four source
+// segments of each product row (first / second source row x lower / upper
+// K half, 16 k per stage) into LDS, 16 threads per contiguous 256-byte run.
+// Each wave then forms whole stages from LDS exactly as pack_operand does.
+// The row stride carries a 16-byte pad, so the 8 lanes of one LDS read
+// phase (consecutive rows) fall in distinct banks.
+constexpr int kRowStages = 8;
+constexpr int kRowRun = kRowStages * TK * 2;   // bytes of one segment: 16 k per stage
+constexpr int kRowStride = 4 * kRowRun + 16;  // LDS bytes per product row
+
+template <int kAlgo, int kSide>
+__global__ __launch_bounds__(256) void pack_rows(const uint16_t* __restrict__ src, int64_t ld, int64_t rows,
+                                                 int64_t k, int32_t tile_rows, int32_t bk, int32_t formula,
+                                                 int32_t perm, const int32_t* __restrict__ panels,
+                                                 int32_t src_panels, uint8_t* __restrict__ out) {
+  static_assert(kSide == 0 || kSide == 1, "row-major sources only");
+  static_assert(kRowStages % 4 == 0, "whole stages per wave");
+  __shared__ __attribute__((aligned(16))) uint8_t tile[32 * kRowStride];
+  constexpr int nops = nops_of(kAlgo);
+  const int64_t nstages = k / (2 * TK);
+  const int64_t sgroups = (nstages + kRowStages - 1) / kRowStages;
+  const int64_t rblock = blockIdx.x / sgroups;  // 32-row product block
+  if (rblock >= rows / 64) return;  // uniform per workgroup
+  const int64_t st0 = (blockIdx.x - rblock * sgroups) * kRowStages;
+  const int hr = tile_rows / 2, hk = bk / 2;
+  // Copy: 32 rows x 4 segments x kRowStages stages x two 16-byte pieces.
+  constexpr int kPieces = 32 * 4 * kRowStages * 2;
+  static_assert(kPieces % 256 == 0, "whole copy rounds");
 #pragma unroll
-      for (int op = 0; op < 7; ++op) store(op, ops[op]);
-    } else {
-#pragma unroll
-      for (int op = 0; op < 4; ++op) store(op, x[op]);
+  for (int i = 0; i < kPieces / 256; ++i) {
+    const int piece = i * 256 + (int)threadIdx.x;
+    const int sub = piece & 1, j = (piece >> 1) % kRowStages, rs = (piece >> 1) / kRowStages;
+    const int row = rs >> 2, seg = rs & 3;  // seg bit 1: second source row; bit 0: upper K half
+    const int64_t st = st0 + j;
+    if (st < nstages) {
+      const int64_t r = rblock * 32 + row;
+      const int64_t srow = (r / hr) * tile_rows + r % hr + ((seg & 2) ? hr : 0);
+      // A stage's 16 k never cross a panel half (hk is a multiple of 32).
+      const int64_t kp = st * TK;
+      const int64_t panel = kp / hk;
+      // Map entries are clamped to the source, so a bad map cannot read out of bounds.
+      const int64_t src_panel = panels ? min(max(panels[panel], 0), src_panels - 1) : panel;
+      const int64_t col = src_panel * bk + kp % hk + ((seg & 1) ? hk : 0) + sub * 8;
+      *reinterpret_cast<u32x4*>(tile + row * kRowStride + seg * kRowRun + j * 32 + sub * 16) =
+          *reinterpret_cast<const u32x4*>(src + srow * ld + col);
     }
+  }
+  __syncthreads();
+  const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
+  const uint8_t* const from = tile + (lane & 31) * kRowStride + (lane >> 5) * 16;
+  uint8_t* const dst_tile = out + frag_offset(rblock / 4, 0, nstages, 0, nops, (int)(rblock % 4)) + lane * 16;
+#pragma unroll
+  for (int jj = 0; jj < kRowStages / 4; ++jj) {
+    const int j = jj * 4 + wave;
+    const int64_t st = st0 + j;
+    if (st >= nstages) break;
+    auto seg = [&](int sg) { return unpack8(*reinterpret_cast<const u32x4*>(from + sg * kRowRun + j * 32)); };
+    F8 x[4];
+    if constexpr (kSide == 0) {
+      x[0] = seg(0);  // first row, lower K half
+      x[1] = seg(1);  // first row, upper K half
+      x[2] = seg(2);  // second row, lower K half
+      x[3] = seg(3);  // second row, upper K half
+    } else {
+      x[0] = seg(0);
+      x[1] = seg(2);
+      x[2] = seg(1);
+      x[3] = seg(3);
+    }
+    store_fragments<kAlgo, kSide, false>(x, formula, perm, 0, dst_tile + st * (int64_t)(nops * kBlocks * kFrag));
   }
 }
 

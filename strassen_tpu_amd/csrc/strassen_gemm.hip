@@ -200,6 +200,15 @@ int launch_pack(const void* src, bool src_f32, int64_t ld, int64_t rows, int64_t
                 int32_t formula, int32_t perm, const int32_t* panels, int32_t src_panels, int32_t passes,
                 uint8_t* out, hipStream_t stream) {
   const int64_t nstages = k / (2 * packed::TK);
+  if constexpr (kSide != 2) {
+    if (!src_f32) {  // bf16 row-major source: the LDS-staged kernel
+      const int64_t blocks = (rows / 64) * ((nstages + packed::kRowStages - 1) / packed::kRowStages);
+      if (blocks >= ((int64_t)1 << 31)) return fail(SMX_ERR_UNSUPPORTED, "operand too large to pack");
+      hipLaunchKernelGGL((packed::pack_rows<kAlgo, kSide>), dim3((unsigned)blocks), dim3(256), 0, stream,
+                         (const uint16_t*)src, ld, rows, k, tile_rows, bk, formula, perm, panels, src_panels, out);
+      return check_launch();
+    }
+  }
   const int64_t waves = (rows / 64) * ((nstages + packed::kPackStages - 1) / packed::kPackStages);
   const int64_t blocks = (waves + 3) / 4;
   if (blocks >= ((int64_t)1 << 31)) return fail(SMX_ERR_UNSUPPORTED, "operand too large to pack");
