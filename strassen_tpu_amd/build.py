@@ -105,6 +105,52 @@ def verify_inline_asm_kernels(asm_text):
     return checked
 
 
+# Scratch (private segment) per GEMM kernel, in bytes per lane. The Strassen
+# kernels and the matched cubic keep their accumulators, fragments and
+# addresses in registers: a spill there is reloaded on every tile, so the
+# build refuses it. Two exceptions carry a stated cap: the q/k epilogue of the
+# Strassen kernel (116 bytes: its first exchange round holds the register
+# file's peak) and the cubic that adds an FP32 partial product before its
+# epilogue (the exact-panel path, off the hot path).
+_KERNEL_DESC = re.compile(r"\.amdhsa_kernel (\S+)(.*?)\.end_amdhsa_kernel", re.S)
+_SPLIT = re.compile(r"gemm_splitILi(\d+)ELi(\d+)E")
+_PACKED = re.compile(r"gemm_packedILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)E")
+_EPI_QK = 4
+_QUAD_CUBIC_PARTIAL = 1
+QK_SCRATCH_CAP = 128
+PARTIAL_SCRATCH_CAP = 1024
+
+
+def scratch_limit(name):
+    """Allowed scratch bytes per lane of a kernel (None: not a GEMM kernel)."""
+    m = _SPLIT.search(name)
+    if m:
+        return QK_SCRATCH_CAP if int(m.group(1)) == _EPI_QK else 0
+    m = _PACKED.search(name)
+    if m:
+        return PARTIAL_SCRATCH_CAP if int(m.group(3)) == _QUAD_CUBIC_PARTIAL else 0
+    return None
+
+
+def verify_kernel_scratch(asm_text):
+    """Raise if a GEMM kernel's private segment exceeds its limit; returns the
+    number of GEMM kernels checked."""
+    checked = 0
+    for m in _KERNEL_DESC.finditer(asm_text):
+        limit = scratch_limit(m.group(1))
+        if limit is None:
+            continue
+        size = re.search(r"\.amdhsa_private_segment_fixed_size (\d+)", m.group(2))
+        scratch = int(size.group(1)) if size else 0
+        if scratch > limit:
+            raise RuntimeError(f"{m.group(1)}: {scratch} bytes of scratch per lane (limit {limit}): "
+                               "registers spill; refusing to build")
+        checked += 1
+    if not checked:
+        raise RuntimeError("no GEMM kernel descriptors found in the device assembly")
+    return checked
+
+
 def build(verbose=False):
     """Compile the library; returns its path. Always recompiles."""
     tmp = LIBRARY + ".tmp"
@@ -121,9 +167,11 @@ def build(verbose=False):
         asm = [f for f in os.listdir(scratch) if f.endswith("gfx950.s")]
         if len(asm) != 1:
             raise RuntimeError(f"expected one gfx950 assembly file from -save-temps, found {asm}")
-        checked = verify_inline_asm_kernels(open(os.path.join(scratch, asm[0])).read())
+        text = open(os.path.join(scratch, asm[0])).read()
+        checked = verify_inline_asm_kernels(text)
+        gemms = verify_kernel_scratch(text)
     if verbose:
-        print(f"verified {checked} inline-asm MFMA kernels", file=sys.stderr)
+        print(f"verified {checked} inline-asm MFMA kernels and the scratch of {gemms} GEMM kernels", file=sys.stderr)
     os.replace(tmp, LIBRARY)
     return LIBRARY
 

@@ -322,19 +322,33 @@ struct TileOrigin {
   int64_t tj, tc;  // column tile index and column inside the half
 };
 
+// The origin is uniform over the workgroup. Product-space coordinates fit in
+// 32 bits (the host refuses M/2 or N/2 >= 2^31), so the divisions run on
+// 32-bit values, and readfirstlane moves the results to SGPRs: VGPR copies
+// would stay live across the main loop next to the accumulators and spill.
 __device__ __forceinline__ TileOrigin tile_origin(const Params& p, int64_t prow0, int64_t pcol0) {
-  const int hm = p.bm / 2, hn = p.bn / 2;
+  const uint32_t hm = (uint32_t)(p.bm / 2), hn = (uint32_t)(p.bn / 2);
+  const uint32_t r = (uint32_t)prow0, c = (uint32_t)pcol0;
+  auto uniform = [](uint32_t v) { return (int64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)v); };
   TileOrigin o;
-  o.ti = prow0 / hm;
-  o.tr = prow0 % hm;
-  o.tj = pcol0 / hn;
-  o.tc = pcol0 % hn;
+  o.ti = uniform(r / hm);
+  o.tr = uniform(r % hm);
+  o.tj = uniform(c / hn);
+  o.tc = uniform(c % hn);
   return o;
 }
 
 // ---------------------------------------------------------------------------
 // Epilogue
 // ---------------------------------------------------------------------------
+
+// Lane index within the wave (v_mbcnt over a full mask), as a volatile asm
+// that the compiler can neither hoist nor merge with an earlier lane index.
+__device__ __forceinline__ int opaque_lane_id() {
+  int lane;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+  return lane;
+}
 
 // SiLU as jax.nn.silu computes it, x * sigmoid(x), with sigmoid(x) =
 // 1 / (1 + 2^(-x log2 e)) on the hardware exp2 and reciprocal (each within
@@ -511,11 +525,11 @@ template <int kMB, int kNB, int kEpi, int kNacc, int kQuad>
 __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin& o, int row0, int col0,
                                               f32x16 (&acc)[kNacc][kMB][kNB], uint8_t* tile) {
   using T = StageTile<32 * kMB, 32 * kNB>;
-  // The lane index passes through an empty asm here, after the main loop's
-  // drain: every per-lane epilogue address depends on it, so none can be
-  // computed ahead of the loop and held (or spilled) across it.
-  int lane = threadIdx.x & 63;
-  asm volatile("" : "+v"(lane));
+  // The lane index is produced here by its own volatile asm, after the main
+  // loop's drain: every per-lane epilogue address depends on it, so none can
+  // be computed ahead of the loop and held (or spilled) across it, and the
+  // compiler cannot reuse a lane index it computed before the loop.
+  const int lane = opaque_lane_id();
   const int hm = p.bm / 2, hn = p.bn / 2;
   const int lcol = lane & 31;
   const int swap_m = p.perm & 1, swap_n = (p.perm >> 2) & 1;

@@ -110,6 +110,7 @@ __device__ __forceinline__ bf16x8 ld_frag(const uint8_t* p) {
 
 template <int kAlgo, int kEpi, int kQuad, int kCubicSlots = 3>
 __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
+  static_assert(kAlgo == 8, "the packed kernel serves the cubic; Strassen runs on gemm_split");
   using L = Lay<kAlgo, kCubicSlots>;
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   static_assert(kEpiLds<kEpi, 64, 64> <= 160 * 1024, "epilogue staging fits the LDS");
@@ -181,9 +182,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
   // (benchmark_cubic_control.py:96-106) run one K half at a time, A
   // quadrants (top, bottom) x B quadrants (left, right), every fragment
   // feeding two MFMAs (the cubic loop below).
-  // Strassen products in issue order P4 P6 P5 P2 P7 P3 P1
-  // (strassen_pallas.py:556-565) as operand / accumulator index p-1.
-  constexpr int kOrder[7] = {3, 5, 4, 1, 6, 2, 0};
 
   // Prologue: stages 0..kASlots-2 of A and 0..kBSlots-2 of B.
   dma(a_src, 0, a_region);
@@ -285,53 +283,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
     return;
   }
 
-  // Stage s: prefetch, MFMAs on stage s, barrier. The prefetched slots were
-  // last read at stage s-1, which every wave finished before the previous
-  // barrier. The host guarantees nstages >= 1; a do-while leaves no zero-trip
-  // path whose register assignment would need reconciling copies.
-  // Strassen: a stage's 28 fragments do not fit next to the 448 accumulator
-  // registers, so fragments stream one product ahead, and the software
-  // pipeline is rotated across the barrier: the barrier sits between the
-  // reads and the MFMAs of the last product, and the first product of stage
-  // s+1 is read right after it, under those MFMAs. The barrier sees every
-  // read of stage s complete (lgkmcnt(0)) and every wave's DMA of stage s+1
-  // landed (vmcnt leaves only the newest prefetch in flight).
-  int s = 0, a_slot = 0, b_slot = 0;
-  Frags cur = load_frags(a_region, b_region, kOrder[0], kOrder[0]);
-  do {
-    const int b_next = b_slot == 0 ? 2 : b_slot - 1;  // (s + 2) % 3
-    const int b_slot1 = b_slot == 2 ? 0 : b_slot + 1;
-    dma(a_src, s + 1, a_region + (a_slot ^ 1) * L::kStage);
-    dma(b_src, s + 2, b_region + b_next * L::kStage);
-    __builtin_amdgcn_sched_barrier(0);
-    const uint8_t* const sa = a_region + a_slot * L::kStage;
-    const uint8_t* const sb = b_region + b_slot * L::kStage;
-#pragma unroll
-    for (int x = 0; x < 6; ++x) {
-      const Frags next = load_frags(sa, sb, kOrder[x + 1], kOrder[x + 1]);
-      mfma4(cur, kOrder[x]);
-      __builtin_amdgcn_sched_barrier(0);
-      cur = next;
-    }
-    stage_barrier<L::kPending>();
-    // Stage s+1's first product (past the last stage: a re-loaded copy of
-    // it, never used).
-    const Frags first = load_frags(a_region + (a_slot ^ 1) * L::kStage, b_region + b_slot1 * L::kStage,
-                                   kOrder[0], kOrder[0]);
-    mfma4(cur, kOrder[6]);
-    __builtin_amdgcn_sched_barrier(0);
-    cur = first;
-    b_slot = b_slot1;
-    a_slot ^= 1;
-  } while (++s < nstages);
-  // Let the (unread) prefetches past the last stage land before the
-  // workgroup can finish.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-
-  // The drain also pins every accumulator in its register file up to this
-  // point, so the allocator cannot copy them out early.
-  mfma_drain(acc);
-  epilogue<kQuad, 2, 2, kEpi>(p, o, wm * 64, wn * 64, acc, lds + wave * kEpiTiles<kEpi> * StageTile<64, 64>::kBytes);
 }
 
 // Packs one operand. kSide 0: A [m, k] row-major (kSide 2: the same A stored

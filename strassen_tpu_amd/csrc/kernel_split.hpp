@@ -92,15 +92,19 @@ struct Ring {
 
 // One wave's main loop, accumulator exchange and epilogue.
 template <int kWave, int kEpi, int kQuad>
-__device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, int nstages, int lane,
-                                         const uint8_t* a_src, const uint8_t* b_src, uint8_t* lds) {
+__device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, int nstages, const uint8_t* a_src,
+                                         const uint8_t* b_src, uint8_t* lds) {
   using L = packed::Lay<7>;
   using P = Plan<kWave>;
   uint8_t* const a_long = lds;
   uint8_t* const a_short = lds + Ring::kAShortBase;
   uint8_t* const b_region = lds + Ring::kBBase;
-  const uint32_t lane_off = lane * 16;
-  const int lo = lane * 16;
+  // The lane's byte offset is derived here, inside the wave's own code path:
+  // a value computed before the switch over waves would stay live through
+  // every other wave's path (the branches are laid out one after another)
+  // and spill there.
+  const uint32_t lane_off = opaque_lane_id() * 16;
+  const int lo = (int)lane_off;
   // Operand and slot choices depend only on the strip (a compile-time
   // constant after unrolling), so each read is one LDS load from a slot base.
   auto load_a = [&](const uint8_t* sl, const uint8_t* ss, int j) {
@@ -227,12 +231,32 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
   // product) is one 32x32 FP32 block stored as [4 register groups][64
   // lanes][4 floats]: source and destination share the MFMA accumulator
   // lane layout, so a block moves register for register.
+  //
+  // Each round's block goes through the epilogue as soon as it arrives (the
+  // q/k epilogue, whose heads span 64 columns, takes the blocks (i, 0) and
+  // (i, 1) together), so the products of a finished block are dead before
+  // the next round: holding all seven products of the whole 64x64 region
+  // through the epilogue needed more than the register file and spilled.
+  // The epilogue stages its output in the wave's own receive slots, which
+  // are free from the moment their blocks are read until the barrier that
+  // ends the round (no wave writes them before it).
   constexpr int kBlockBytes = 64 * 16 * 4;
+  constexpr bool kPairs = kEpi == SMX_EPI_QK_NORM_ROPE;
+  static_assert(kEpiTiles<kEpi> * StageTile<32, kPairs ? 64 : 32>::kBytes <= 7 * kBlockBytes,
+                "epilogue staging fits the wave's receive slots");
   const int wm = kWave >> 1, wn = kWave & 1;
-  f32x16 dst[7][2][2];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int i = t >> 1, jj = t & 1;
+  uint8_t* const mine = lds + kWave * 7 * kBlockBytes;
+  // q/k: the four quadrant sets of block (i, 0), formed on arrival, wait
+  // for block (i, 1).
+  f32x16 quads[4][1][2];
+  // The rounds are spelled out with compile-time indices: a loop the
+  // compiler declines to unroll (its body holds the inlined epilogue) would
+  // index the block arrays at run time and move them to scratch.
+  auto round = [&](auto tc) __attribute__((always_inline)) {
+    constexpr int t = decltype(tc)::value, i = t >> 1, jj = t & 1;
+    // the lane's byte offset, re-derived opaquely each round so that no copy
+    // of it stays live through the epilogues
+    const uint32_t lane16 = opaque_lane_id() * 16;
 #pragma unroll
     for (int j = 0; j < 7; ++j) {
       const int r = P::row(j);
@@ -240,7 +264,7 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
 #pragma unroll
       for (int c = jj; c < 4; c += 2) {
         const int dest = 2 * (r / 2) + c / 2;
-        uint8_t* const slot = lds + (dest * 7 + P::product(j)) * kBlockBytes + lane * 16;
+        uint8_t* const slot = lds + (dest * 7 + P::product(j)) * kBlockBytes + lane16;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           f32x4 v = {acc[j][c][4 * g], acc[j][c][4 * g + 1], acc[j][c][4 * g + 2], acc[j][c][4 * g + 3]};
@@ -249,21 +273,40 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
       }
     }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    f32x16 blk[7][1][1];
 #pragma unroll
     for (int q = 0; q < 7; ++q) {
-      const uint8_t* const slot = lds + (kWave * 7 + q) * kBlockBytes + lane * 16;
+      const uint8_t* const slot = mine + q * kBlockBytes + lane16;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const f32x4 v = *reinterpret_cast<const f32x4*>(slot + g * 1024);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) dst[q][i][jj][4 * g + e] = v[e];
+        for (int e = 0; e < 4; ++e) blk[q][0][0][4 * g + e] = v[e];
       }
     }
+    // the block's reads complete before its slots turn into staging tiles
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if constexpr (kPairs) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        quads[0][0][jj][r] = quadrant_value<kQuad, 0>(blk, 0, 0, r);
+        quads[1][0][jj][r] = quadrant_value<kQuad, 1>(blk, 0, 0, r);
+        quads[2][0][jj][r] = quadrant_value<kQuad, 2>(blk, 0, 0, r);
+        quads[3][0][jj][r] = quadrant_value<kQuad, 3>(blk, 0, 0, r);
+      }
+      // the quadrant sets go through the epilogue as the cubic's would
+      if constexpr (jj == 1) epilogue_body<1, 2, kEpi, 4, kQuadCubic>(p, o, wm * 64 + i * 32, wn * 64, quads, mine);
+    } else {
+      epilogue_body<1, 1, kEpi, 7, kQuad>(p, o, wm * 64 + i * 32, wn * 64 + jj * 32, blk, mine);
+    }
+    // every staging access has completed before the next round's blocks
+    // land in these slots
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  }
-  static_assert(kEpiLds<kEpi, 64, 64> <= 160 * 1024, "epilogue staging fits the LDS");
-  epilogue<kQuad, 2, 2, kEpi>(p, o, wm * 64, wn * 64, dst,
-                              lds + kWave * kEpiTiles<kEpi> * StageTile<64, 64>::kBytes);
+  };
+  round(QuadC<0>{});
+  round(QuadC<1>{});
+  round(QuadC<2>{});
+  round(QuadC<3>{});
 }
 
 template <int kEpi, int kQuad>
@@ -312,16 +355,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
   // accumulator is live across the branches.
   switch (wave) {
     case 0:
-      run_wave<0, kEpi, kQuad>(p, o, nstages, lane, a_src, b_src, lds);
+      run_wave<0, kEpi, kQuad>(p, o, nstages, a_src, b_src, lds);
       break;
     case 1:
-      run_wave<1, kEpi, kQuad>(p, o, nstages, lane, a_src, b_src, lds);
+      run_wave<1, kEpi, kQuad>(p, o, nstages, a_src, b_src, lds);
       break;
     case 2:
-      run_wave<2, kEpi, kQuad>(p, o, nstages, lane, a_src, b_src, lds);
+      run_wave<2, kEpi, kQuad>(p, o, nstages, a_src, b_src, lds);
       break;
     default:
-      run_wave<3, kEpi, kQuad>(p, o, nstages, lane, a_src, b_src, lds);
+      run_wave<3, kEpi, kQuad>(p, o, nstages, a_src, b_src, lds);
       break;
   }
 }

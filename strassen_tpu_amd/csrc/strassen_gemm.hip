@@ -27,11 +27,10 @@
 //      seven (product, 32-row strip) pairs of the 128x128 product-space tile
 //      instead of a 64x64 region of all seven products; the accumulators are
 //      regrouped by region through LDS before the shared epilogue.
-//   packed (kernel_packed.hpp): 128x128 product-space tiles, 64x64 waves,
-//      both operands pre-packed (smx_pack_operand: the Strassen operand sums
-//      or the cubic quadrants, in MFMA fragment order) and streamed into an
-//      LDS ring by DMA. The cubic's kernel; for Strassen it is the per-region
-//      design that SMX_STRASSEN_KERNEL=region selects for comparison.
+//   packed (kernel_packed.hpp): the cubic's kernel: 128x128 product-space
+//      tiles, 64x64 waves, both operands pre-packed (smx_pack_operand: the
+//      Strassen operand sums or the cubic quadrants, in MFMA fragment order)
+//      and streamed into an LDS ring by DMA.
 //   v1 (kernel_v1.hpp): 128x64 tiles, row-major A and B^T, both operand sums
 //      formed in registers; serves unpacked calls whose tile the packed
 //      kernels cannot take, or all of them under SMX_PLAIN_WEIGHTS=compact.
@@ -71,17 +70,6 @@ int set_lds(K kern, int bytes) {
 
 // Tile rows per rasterization group; SMX_GROUP_M overrides the default for
 // tuning sweeps.
-// Strassen packed kernel: the product-split kernel by default;
-// SMX_STRASSEN_KERNEL=region selects the per-region kernel (gemm_packed)
-// for comparison.
-bool split_kernel_setting() {
-  static const bool value = [] {
-    const char* env = getenv("SMX_STRASSEN_KERNEL");
-    return !(env && strcmp(env, "region") == 0);
-  }();
-  return value;
-}
-
 int group_m_setting() {
   static const int value = [] {
     const char* env = getenv("SMX_GROUP_M");
@@ -123,19 +111,18 @@ int launch_packed(Params p, hipStream_t stream) {
   // the stage ring, then the epilogue's staging tiles, share the LDS; the
   // product-split kernel's ring fills all of it
   constexpr int epi_lds = kEpiLds<kEpi, 64, 64>;
-  int lds = packed::Lay<kAlgo>::kLds > epi_lds ? packed::Lay<kAlgo>::kLds : epi_lds;
+  int lds = packed::Lay<8>::kLds > epi_lds ? packed::Lay<8>::kLds : epi_lds;
   if constexpr (kAlgo == 7) {
-    const bool region = !split_kernel_setting();
-    if (!region) lds = split::Ring::kBytes > epi_lds ? split::Ring::kBytes : epi_lds;
+    lds = split::Ring::kBytes > epi_lds ? split::Ring::kBytes : epi_lds;
     if (p.formula == SMX_FORMULA_DUAL) {
-      kern = region ? packed::gemm_packed<7, kEpi, kQuadDual> : split::gemm_split<kEpi, kQuadDual>;
+      kern = split::gemm_split<kEpi, kQuadDual>;
     } else if (p.formula == SMX_FORMULA_POWERS) {
       if constexpr (kEpi == SMX_EPI_NONE)
-        kern = region ? packed::gemm_packed<7, SMX_EPI_NONE, kQuadPowers> : split::gemm_split<SMX_EPI_NONE, kQuadPowers>;
+        kern = split::gemm_split<SMX_EPI_NONE, kQuadPowers>;
       else
         return fail(SMX_ERR_INVALID, "fused epilogues require a quadrant-basis formula");
     } else {
-      kern = region ? packed::gemm_packed<7, kEpi, kQuadClassical> : split::gemm_split<kEpi, kQuadClassical>;
+      kern = split::gemm_split<kEpi, kQuadClassical>;
     }
   } else {
     kern = p.partial ? packed::gemm_packed<8, kEpi, kQuadCubicPartial> : packed::gemm_packed<8, kEpi, kQuadCubic>;
@@ -361,6 +348,10 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
                 (long long)d->k);
   if (d->bm <= 0 || d->bn <= 0 || d->bk <= 0 || d->m % d->bm || d->n % d->bn || d->k % d->bk)
     return fail(SMX_ERR_INVALID, "M, N, K must be divisible by bm, bn, bk");
+  // Product-space coordinates (rows of M/2, columns of N/2) are 32-bit in the kernels.
+  if (d->m / 2 >= ((int64_t)1 << 31) || d->n / 2 >= ((int64_t)1 << 31))
+    return fail(SMX_ERR_UNSUPPORTED, "M/2 and N/2 must stay below 2^31 (m=%lld, n=%lld)", (long long)d->m,
+                (long long)d->n);
   int32_t tm, tn, tk;
   tile_of_path(packed_path, &tm, &tn, &tk);
   const int hm = d->bm / 2, hn = d->bn / 2, hk = d->bk / 2;

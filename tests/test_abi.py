@@ -324,3 +324,31 @@ def test_inline_asm_kernel_check():
     assert build.verify_inline_asm_kernels(early) == 1
     with pytest.raises(RuntimeError, match="before the MFMA drain"):
         build.verify_inline_asm_kernels(early.replace(drain, "\tv_accvgpr_read_b32 v0, a0\n" + drain))
+
+
+def test_kernel_scratch_check():
+    """The build refuses GEMM kernels whose registers spill to scratch."""
+    from strassen_tpu_amd import build
+
+    def desc(name, size):
+        return (f"\t.amdhsa_kernel {name}\n\t\t.amdhsa_group_segment_fixed_size 0\n"
+                f"\t\t.amdhsa_private_segment_fixed_size {size}\n\t.end_amdhsa_kernel\n")
+
+    split_swiglu = "_ZN3smx5split10gemm_splitILi1ELi2EEEvNS_6ParamsE"
+    split_qk = "_ZN3smx5split10gemm_splitILi4ELi2EEEvNS_6ParamsE"
+    cubic = "_ZN3smx6packed11gemm_packedILi8ELi2ELi0ELi3EEEvNS_6ParamsE"
+    cubic_partial = "_ZN3smx6packed11gemm_packedILi8ELi2ELi1ELi3EEEvNS_6ParamsE"
+    other = "_ZN3smx6packed9pack_rowsILi7ELi0EEEvPKtlliiiiPKiiPh"
+    assert build.scratch_limit(split_swiglu) == 0
+    assert build.scratch_limit(split_qk) == build.QK_SCRATCH_CAP
+    assert build.scratch_limit(cubic) == 0
+    assert build.scratch_limit(cubic_partial) == build.PARTIAL_SCRATCH_CAP
+    assert build.scratch_limit(other) is None
+    clean = desc(split_swiglu, 0) + desc(split_qk, 116) + desc(cubic, 0) + desc(cubic_partial, 792) + desc(other, 64)
+    assert build.verify_kernel_scratch(clean) == 4
+    for name, size in ((split_swiglu, 8), (split_qk, build.QK_SCRATCH_CAP + 4), (cubic, 4),
+                       (cubic_partial, build.PARTIAL_SCRATCH_CAP + 4)):
+        with pytest.raises(RuntimeError, match="scratch per lane"):
+            build.verify_kernel_scratch(clean + desc(name, size))
+    with pytest.raises(RuntimeError, match="no GEMM kernel"):
+        build.verify_kernel_scratch(desc(other, 0))
