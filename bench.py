@@ -117,8 +117,9 @@ def fused_sites(torch, d, algo):
     """Callables for a fused arm, keyed by site. algo: "strassen" / "cubic"
     (packed weights; each activation is packed once per step, inside the
     step, and shared by the GEMMs that read it) or "strassen_plain" /
-    "cubic_plain" (plain weights, the compact kernel forms the operand sums
-    or quadrants from row-major A and B^T)."""
+    "cubic_plain" (ordinary [in, out] weights, as a drop-in caller passes
+    them: every call packs its weight and its activation, then runs the same
+    packed kernel)."""
     import strassen_tpu_amd as smx
 
     bm, bn, bk = TILE
@@ -263,54 +264,67 @@ def run_block(sites):
     return step
 
 
+def cpu_threads():
+    """Host threads for the CPU baseline: the CPUs this process may run on,
+    capped by OMP_NUM_THREADS when the environment sets a share."""
+    n = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS")
+    if cap and cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return max(n, 1)
+
+
 def cpu_baseline(seconds):
-    """The oracle's Strassen restatement timed on host cores over a bounded
-    sample: 1024x1024 output tiles of the gate|up site (K=5120), repeated for
-    about `seconds`."""
+    """The reference's Strassen path restated in torch on the host cores,
+    at the reference's CPU-runnable configuration: A[1024,1024] ~ N(0,1),
+    B[1024,1024] ~ N(0, 1/32), bf16, seed 0, tile (1024, 1024, 512).
+    Warm-up, then alternating timed calls of the Strassen restatement and the
+    FP32 cubic torch.matmul for about `seconds` in all."""
     import numpy as np
+    import torch
 
     import oracle as o
+    from oracle import strassen_torch_cpu as tc
 
-    try:
-        from threadpoolctl import threadpool_info
-        cores = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
-    except Exception:  # pragma: no cover - informational only
-        cores = os.cpu_count() or 1
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
     rng = np.random.default_rng(0)
-    bm, bn, bk = TILE
-    a = o.bf16_round(rng.standard_normal((bm, HIDDEN)).astype(np.float32))
-    b = o.bf16_round(rng.standard_normal((HIDDEN, bn)).astype(np.float32) * np.float32(0.02))
-    o.strassen_matmul(a, b, bm=bm, bn=bn, bk=bk, interleave_products=True)  # warm-up
-    tiles, t0 = 0, time.perf_counter()
-    while True:
-        o.strassen_matmul(a, b, bm=bm, bn=bn, bk=bk, interleave_products=True)
-        tiles += 1
-        elapsed = time.perf_counter() - t0
-        if elapsed >= seconds:
-            break
-    tflops = tiles * 2.0 * bm * bn * HIDDEN / elapsed / 1e12
-    # Beside it, the FP32 cubic product of the same tile (numpy matmul).
-    a32, b32 = a.astype(np.float32), b.astype(np.float32)
-    np.matmul(a32, b32)
-    cubic_tiles, t1 = 0, time.perf_counter()
-    while True:
-        np.matmul(a32, b32)
-        cubic_tiles += 1
-        cubic_elapsed = time.perf_counter() - t1
-        if cubic_elapsed >= min(seconds, 3.0):
-            break
+    a = torch.from_numpy(o.bf16_round(rng.standard_normal((1024, 1024)).astype(np.float32))).to(torch.bfloat16)
+    b = torch.from_numpy(o.bf16_round((rng.standard_normal((1024, 1024)) / 32).astype(np.float32)))
+    b = b.to(torch.bfloat16)
+    a32, b32 = a.float(), b.float()
+    bm, bn, bk = 1024, 1024, 512
+    for _ in range(2):
+        tc.strassen_matmul(a, b, bm=bm, bn=bn, bk=bk)
+        torch.matmul(a32, b32)
+    strassen_s, cubic_s = [], []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(strassen_s) < 3:
+        t0 = time.perf_counter()
+        tc.strassen_matmul(a, b, bm=bm, bn=bn, bk=bk)
+        t1 = time.perf_counter()
+        torch.matmul(a32, b32)
+        t2 = time.perf_counter()
+        strassen_s.append(t1 - t0)
+        cubic_s.append(t2 - t1)
+    flop = 2.0 * 1024 ** 3
+    median = statistics.median(strassen_s)
     cpu_model = None
     try:
         with open("/proc/cpuinfo") as f:
             cpu_model = next((line.split(":", 1)[1].strip() for line in f if line.startswith("model name")), None)
     except OSError:
         pass
+    ms = [x * 1e3 for x in strassen_s]
     return {
-        "value": tflops, "unit": "TFLOP/s", "cores": int(cores), "kind": "port",
-        "sample": f"{tiles} output tiles of 1024x1024 (K=5120) of the gate|up site, "
-                  f"numpy oracle Strassen restatement, {elapsed:.1f} s",
-        "ms_per_tile": elapsed * 1e3 / tiles,
-        "cubic_fp32_matmul_tflops": cubic_tiles * 2.0 * bm * bn * HIDDEN / cubic_elapsed / 1e12,
+        "value": round(flop / median / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+        "sample": f"{len(strassen_s)} calls of the torch-CPU restatement of the reference Strassen path at "
+                  "1024x1024x1024 (bf16, A~N(0,1), B~N(0,1/32), seed 0, tile 1024x1024x512), "
+                  f"interleaved with FP32 torch.matmul, {sum(strassen_s) + sum(cubic_s):.1f} s",
+        "ms_per_call": {"mean": round(statistics.mean(ms), 3), "median": round(statistics.median(ms), 3),
+                        "std": round(statistics.stdev(ms), 3) if len(ms) > 1 else 0.0, "n": len(ms)},
+        "cubic_fp32_matmul_tflops": round(flop / statistics.median(cubic_s) / 1e12, 5),
+        "affinity_cpus": len(os.sched_getaffinity(0)),
         "cpu_model": cpu_model,
     }
 

@@ -139,42 +139,25 @@ def _is_dtype(x, dtype):
     return x.dtype == dtype
 
 
-def _validate(a, b, *, bm, bn, bk, block_permutation, formula_variant,
-              classical_panels, panel_schedule, epilogue, residual, bias,
-              rope_cos, rope_sin, rope_scale, rope_head_dim, norm_scale,
-              output_dtype, allow_input_fusion, product_aware_swiglu,
-              product_aware_residual):
-    """Argument checks in the order and wording of ``strassen_pallas.py:927-1047``."""
-    if a.dim() != 2 or b.dim() != 2:
-        raise ValueError("strassen_matmul expects two rank-2 matrices")
-    m, k = a.shape
-    k2, n = b.shape
-    if k != k2:
-        raise ValueError(f"inner dimensions disagree: {k} vs {k2}")
-    if a.dtype != b.dtype:
-        raise ValueError(f"input dtypes disagree: {a.dtype} vs {b.dtype}")
-    if a.dtype not in (torch.bfloat16, torch.float32):
-        raise ValueError("inputs must be BF16 or FP32")
-    if not isinstance(block_permutation, int) or not 0 <= block_permutation < 8:
-        raise ValueError("block_permutation must be an integer from 0 through 7")
-    if formula_variant not in ("classical", "dual", "powers"):
-        raise ValueError("formula_variant must be 'classical', 'dual', or 'powers'")
-    classical_panels = tuple(sorted({int(p) for p in classical_panels}))
-    if epilogue is not None:
-        if epilogue not in _EPILOGUES:
-            raise ValueError(
-                f"unknown epilogue {epilogue!r}; choose 'swiglu' or "
-                "'residual_add' or 'bias_add'")
-        if formula_variant == "powers":
-            raise ValueError("fused epilogues require a quadrant-basis formula")
-        if output_dtype is not None and output_dtype != torch.bfloat16:
-            raise ValueError("fused epilogues write a BF16 output tile")
-        if epilogue in ("swiglu", "geglu") and bn % 2:
-            raise ValueError(f"{epilogue} epilogue needs an even bn, got {bn}")
-        if epilogue == "residual_add" and residual is None:
-            raise ValueError("residual_add epilogue requires residual=")
-        if epilogue == "bias_add" and bias is None:
-            raise ValueError("bias_add epilogue requires bias=")
+def _check_epilogue_name(epilogue):
+    if epilogue not in _EPILOGUES:
+        raise ValueError(
+            f"unknown epilogue {epilogue!r}; choose 'swiglu' or "
+            "'residual_add' or 'bias_add'")
+
+
+def _check_epilogue_operands(m, n, bn, *, epilogue, residual, bias, rope_cos, rope_sin, rope_scale,
+                             rope_head_dim, norm_scale):
+    """Presence, pairing and shapes of the epilogue operands for an [m, n]
+    output (the checks of ``strassen_pallas.py:927-1047`` that concern
+    them). The kernels read these operands by address only, so both the
+    Strassen and the cubic entry run these checks before any launch."""
+    if epilogue in ("swiglu", "geglu") and bn % 2:
+        raise ValueError(f"{epilogue} epilogue needs an even bn, got {bn}")
+    if epilogue == "residual_add" and residual is None:
+        raise ValueError("residual_add epilogue requires residual=")
+    if epilogue == "bias_add" and bias is None:
+        raise ValueError("bias_add epilogue requires bias=")
     if residual is not None and epilogue not in ("residual_add", "norm_residual_add"):
         raise ValueError(
             "residual= is only used by the residual_add and "
@@ -212,14 +195,48 @@ def _validate(a, b, *, bm, bn, bk, block_permutation, formula_variant,
                 f"{tuple(rope_scale.shape)}")
     if rope_cos is not None and epilogue != "qk_norm_rope":
         raise ValueError("rope_* are only used by the qk_norm_rope epilogue")
+    if epilogue == "bias_add" and tuple(bias.shape) != (n,):
+        raise ValueError(f"bias shape {tuple(bias.shape)} != output width {(n,)}")
+    if epilogue == "residual_add" and tuple(residual.shape) != (m, n):
+        raise ValueError(f"residual shape {tuple(residual.shape)} != output shape {(m, n)}")
+
+
+def _validate(a, b, *, bm, bn, bk, block_permutation, formula_variant,
+              classical_panels, panel_schedule, epilogue, residual, bias,
+              rope_cos, rope_sin, rope_scale, rope_head_dim, norm_scale,
+              output_dtype, allow_input_fusion, product_aware_swiglu,
+              product_aware_residual):
+    """Argument checks in the order and wording of ``strassen_pallas.py:927-1047``."""
+    if a.dim() != 2 or b.dim() != 2:
+        raise ValueError("strassen_matmul expects two rank-2 matrices")
+    m, k = a.shape
+    k2, n = b.shape
+    if k != k2:
+        raise ValueError(f"inner dimensions disagree: {k} vs {k2}")
+    if a.dtype != b.dtype:
+        raise ValueError(f"input dtypes disagree: {a.dtype} vs {b.dtype}")
+    if a.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("inputs must be BF16 or FP32")
+    if not isinstance(block_permutation, int) or not 0 <= block_permutation < 8:
+        raise ValueError("block_permutation must be an integer from 0 through 7")
+    if formula_variant not in ("classical", "dual", "powers"):
+        raise ValueError("formula_variant must be 'classical', 'dual', or 'powers'")
+    classical_panels = tuple(sorted({int(p) for p in classical_panels}))
+    if epilogue is not None:
+        _check_epilogue_name(epilogue)
+        if formula_variant == "powers":
+            raise ValueError("fused epilogues require a quadrant-basis formula")
+        if output_dtype is not None and output_dtype != torch.bfloat16:
+            raise ValueError("fused epilogues write a BF16 output tile")
+    _check_epilogue_operands(m, n, bn, epilogue=epilogue, residual=residual, bias=bias, rope_cos=rope_cos,
+                             rope_sin=rope_sin, rope_scale=rope_scale, rope_head_dim=rope_head_dim,
+                             norm_scale=norm_scale)
     if product_aware_swiglu and epilogue not in ("swiglu", "geglu"):
         raise ValueError(
             "product_aware_swiglu is only valid with epilogue='swiglu' or 'geglu'")
     if product_aware_residual and epilogue != "residual_add":
         raise ValueError(
             "product_aware_residual is only valid with epilogue='residual_add'")
-    if epilogue == "bias_add" and tuple(bias.shape) != (n,):
-        raise ValueError(f"bias shape {tuple(bias.shape)} != output width {(n,)}")
     operand_count = 3 if epilogue in ("residual_add", "bias_add") else 2
     if epilogue == "norm_residual_add":
         operand_count = 4
@@ -249,8 +266,6 @@ def _validate(a, b, *, bm, bn, bk, block_permutation, formula_variant,
     out = a.dtype if output_dtype is None else output_dtype
     if out not in (torch.bfloat16, torch.float32):
         raise ValueError("output_dtype must be BF16 or FP32")
-    if residual is not None and epilogue == "residual_add" and tuple(residual.shape) != (m, n):
-        raise ValueError(f"residual shape {tuple(residual.shape)} != output shape {(m, n)}")
     nk = k // bk
     if panel_schedule is not None:
         # strassen_pallas.py:1079-1090
@@ -638,8 +653,13 @@ def cubic_matmul(a, b, *, variant="blocked", bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_
     out_dtype = a.dtype if output_dtype is None else output_dtype
     if out_dtype not in (torch.bfloat16, torch.float32):
         raise ValueError("output_dtype must be BF16 or FP32")
-    if epilogue == "norm_residual_add" and (residual is None or norm_scale is None):
-        raise ValueError("norm_residual_add requires residual= and norm_scale=")
+    if epilogue is not None:
+        _check_epilogue_name(epilogue)
+        if output_dtype is not None and output_dtype != torch.bfloat16:
+            raise ValueError("fused epilogues write a BF16 output tile")
+    _check_epilogue_operands(m, n, bn, epilogue=epilogue, residual=residual, bias=bias, rope_cos=rope_cos,
+                             rope_sin=rope_sin, rope_scale=rope_scale, rope_head_dim=rope_head_dim,
+                             norm_scale=norm_scale)
     return _run(_lib.SMX_ALGO_CUBIC, a, b, bm=bm, bn=bn, bk=bk, epilogue=epilogue,
                 residual=residual, bias=bias, rope_cos=rope_cos, rope_sin=rope_sin,
                 rope_scale=rope_scale, rope_head_dim=rope_head_dim, rope_eps=rope_eps,

@@ -21,8 +21,11 @@ For every layer, in order:
 
 After the last layer the final RMSNorm and LM head produce logits per arm.
 The next-token loss, KL to the native arm, top-1 agreement and logit error
-are accumulated over chunks of 256 positions (``:343-378``). With random
-weights and random tokens these are drift measures, not model quality.
+are accumulated over chunks of 256 positions (``:343-378``), and each
+candidate arm gets the reference's task gate (``:444-448``): |loss delta|
+<= 0.01, top-1 agreement >= 0.99, KL <= 0.005 nats. ``main`` exits with 2
+when an arm fails it. With random weights and random tokens these are drift
+measures, not model quality.
 
 ``python -m strassen_tpu_amd.streamed_decoder --layers 64`` prints one JSON
 record per layer and a summary record.
@@ -45,7 +48,7 @@ import torch
 from . import qwen3_block as qb
 from .checkpoint import TENSOR_PREFIX, LocalSafetensors, dims_from_config, load_block_weights
 
-__all__ = ["ARMS", "device_error", "logit_chunk_metrics", "run"]
+__all__ = ["ARMS", "device_error", "logit_chunk_metrics", "passes_task_gate", "run"]
 
 # The reference's arms: regular_xla -> hipBLASLt, gated_cubic, gated_strassen.
 ARMS = ("hipblaslt", "cubic", "strassen")
@@ -106,13 +109,28 @@ def _time_forward(x, block):
     return out, (start, stop)
 
 
+# The reference's task gate (benchmark_qwen3_32b_streamed_inference.py:444-448).
+GATE_LOSS_DELTA = 0.01
+GATE_TOP1 = 0.99
+GATE_KL_NATS = 0.005
+
+
+def passes_task_gate(record):
+    """|loss delta| <= 0.01, top-1 agreement >= 0.99 and mean KL <= 0.005
+    nats against the native arm (``:444-448``)."""
+    return bool(record["absolute_loss_delta"] <= GATE_LOSS_DELTA and record["top1_agreement"] >= GATE_TOP1
+                and record["mean_kl_nats"] <= GATE_KL_NATS)
+
+
 def run(num_layers, *, dims=qb.QWEN3_32B, batch=8, seq=1024, vocab=151936, warmups=1, runs=3, seed=0,
-        tile=(1024, 1024, 512), device="cuda:0", emit=None, checkpoint=None):
+        tile=(1024, 1024, 512), device="cuda:0", emit=None, checkpoint=None, capture=None):
     """Stream ``num_layers`` layers through the three arms; returns the
     summary record (and passes every record to ``emit``). Weights are
     random-init, or read layer by layer from ``checkpoint`` (a
     ``LocalSafetensors`` whose layers match ``dims``); token ids are random
-    either way."""
+    either way. A ``capture`` dict receives the token ids, the initial
+    hidden state, each arm's final hidden state, the final norm scale and
+    the LM head, for a caller that recomputes the forward another way."""
     emit = emit or (lambda record: None)
     dev = torch.device(device)
     gen = torch.Generator(device=dev).manual_seed(seed)
@@ -123,6 +141,8 @@ def run(num_layers, *, dims=qb.QWEN3_32B, batch=8, seq=1024, vocab=151936, warmu
         embeddings = (torch.randn(vocab, dims.hidden, device=dev, generator=gen)).to(torch.bfloat16)
     initial = embeddings[token_ids.reshape(-1)]
     del embeddings
+    if capture is not None:
+        capture["token_ids"], capture["initial"] = token_ids, initial.clone()
     hidden = {arm: initial.clone() for arm in ARMS}
     del initial
     emit({"kind": "metadata", "layers": num_layers, "dims": dataclasses.asdict(dims), "batch": batch, "seq": seq,
@@ -220,6 +240,9 @@ def run(num_layers, *, dims=qb.QWEN3_32B, batch=8, seq=1024, vocab=151936, warmu
             "logit_l2_relative": math.sqrt(delta_sq / max(totals["native_sq"], 1e-30)),
             "logit_maxnorm_relative": max_delta / max(totals["native_max"], 1e-30), "positions": int(count),
         }
+        task[name]["passes_task_gate"] = passes_task_gate(task[name])
+    if capture is not None:
+        capture.update(hidden=hidden, final_norm=final_norm, lm_head=lm_head)
     summary = {"kind": "summary", "layers": num_layers, "all_finite": all_finite, "performance": performance,
                "final_errors_vs_hipblaslt": {arm: device_error(hidden[arm], hidden["hipblaslt"])
                                              for arm in ("cubic", "strassen")},
@@ -256,7 +279,14 @@ def main(argv=None):
         args.layers = min(args.layers, layers)
     summary = run(args.layers, batch=args.batch, seq=args.seq, warmups=args.warmups, runs=args.runs,
                   seed=args.seed, emit=emit, **extra)
-    return 0 if summary["all_finite"] else 1
+    if not summary["all_finite"]:
+        return 1
+    failed = [arm for arm, record in summary["logit_metrics"].items() if not record["passes_task_gate"]]
+    if failed:
+        print(f"task gate failed for {failed} (|loss delta| <= {GATE_LOSS_DELTA}, top-1 >= {GATE_TOP1}, "
+              f"KL <= {GATE_KL_NATS} nats against the hipBLASLt arm)", file=sys.stderr)
+        return 2
+    return 0
 
 
 if __name__ == "__main__":

@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 import torch
 
+from fp32_reference import fp32_block
 from strassen_tpu_amd import qwen3_block as qb
 
 pytestmark = pytest.mark.gpu
@@ -20,35 +21,6 @@ DEV = torch.device("cuda:0")
 
 def say(*args):
     print(*args, flush=True)
-
-
-def fp32_block(x, w, dims, batch, seq):
-    """FP32 CPU restatement: same sites and epilogue semantics, no bf16
-    rounding after the inputs."""
-    f = lambda t: t.detach().float().cpu()
-    x, eps = f(x), dims.eps
-
-    def norm(v, g):
-        return v * torch.rsqrt(v.square().mean(-1, keepdim=True) + eps) * f(g)
-
-    cos, sin = (t.float().cpu() for t in qb.rope_values(seq, dims.head_dim, dims.theta, "cpu"))
-
-    def rope(v):
-        a, b = v.chunk(2, dim=-1)
-        return v * cos[None, :, None, :] + torch.cat((-b, a), -1) * sin[None, :, None, :]
-
-    h = norm(x, w.attention_norm)
-    q = rope(norm((h @ f(w.query)).view(batch, seq, dims.heads, dims.head_dim), w.query_norm))
-    k = rope(norm((h @ f(w.key)).view(batch, seq, dims.kv_heads, dims.head_dim), w.key_norm))
-    v = (h @ f(w.value)).view(batch, seq, dims.kv_heads, dims.head_dim)
-    groups = dims.heads // dims.kv_heads
-    att = torch.nn.functional.scaled_dot_product_attention(
-        q.transpose(1, 2), k.repeat_interleave(groups, 2).transpose(1, 2),
-        v.repeat_interleave(groups, 2).transpose(1, 2), is_causal=True).transpose(1, 2)
-    r = x + att.reshape(batch * seq, -1) @ f(w.attention_output)
-    h2 = norm(r, w.mlp_norm)
-    gate, up = (h2 @ f(w.gate_up)).chunk(2, dim=-1)
-    return r + (torch.nn.functional.silu(gate) * up) @ f(w.mlp_down)
 
 
 @pytest.mark.parametrize("dims,batch,seq,tile", [

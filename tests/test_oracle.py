@@ -641,3 +641,52 @@ def test_multi_pass_packed_planes():
         first = {part: i for i, part in reversed(list(enumerate(parts)))}
         total = sum(six[:, :, first[p] * width:(first[p] + 1) * width].astype(np.float64) for p in range(3))
         np.testing.assert_array_equal(total, ops.astype(np.float64))
+
+
+def test_torch_cpu_restatement_integer_known_answer():
+    """The torch-CPU restatement (the bench's CPU baseline) reproduces A @ B
+    bit for bit on small-integer operands, where every bf16 operand sum and
+    FP32 product is exact (the technique of the reference's
+    Strassen_MM_Focus/tests/test_kernels_v001.py:59-80)."""
+    import torch
+
+    from oracle import strassen_torch_cpu as tc
+
+    rng = np.random.default_rng(187)
+    for (m, k, n), (bm, bn, bk) in (((256, 512, 256), (256, 256, 512)), ((512, 1024, 256), (256, 128, 256))):
+        a = rng.integers(-3, 4, (m, k)).astype(np.float32)
+        b = rng.integers(-3, 4, (k, n)).astype(np.float32)
+        got = tc.strassen_matmul(torch.from_numpy(a), torch.from_numpy(b), bm=bm, bn=bn, bk=bk)
+        assert np.array_equal(got.float().numpy(), o.bf16_round(a @ b))
+        # a planted sign error in one update fails the known answer
+        saved = tc.PRODUCT_UPDATES[5]
+        try:
+            tc.PRODUCT_UPDATES[5] = ((0, +1), (1, +1))
+            bad = tc.strassen_matmul(torch.from_numpy(a), torch.from_numpy(b), bm=bm, bn=bn, bk=bk)
+            assert not np.array_equal(bad.float().numpy(), o.bf16_round(a @ b))
+        finally:
+            tc.PRODUCT_UPDATES[5] = saved
+
+
+def test_torch_cpu_restatement_matches_numpy_oracle():
+    """Random bf16 inputs at the 1024^3 seed-0 configuration: the torch-CPU
+    restatement and the numpy oracle round the same operand sums and add the
+    same products in the same order; only the BLAS libraries' FP32 summation
+    inside each product differs, so results agree to one bf16 ulp on all but
+    a few elements and the accuracy against FP32 is the same."""
+    import torch
+
+    from oracle import strassen_torch_cpu as tc
+
+    rng = np.random.default_rng(0)
+    a = o.bf16_round(rng.standard_normal((1024, 1024)).astype(np.float32))
+    b = o.bf16_round((rng.standard_normal((1024, 1024)) / 32).astype(np.float32))
+    want = o.strassen_matmul(a, b, bm=1024, bn=1024, bk=512, interleave_products=True)
+    got = tc.strassen_matmul(torch.from_numpy(a), torch.from_numpy(b), bm=1024, bn=1024, bk=512).float().numpy()
+    ulp = np.abs(want) * 2.0 ** -7 + 1e-6
+    assert np.all(np.abs(got - want) <= ulp)
+    assert np.mean(got != want) < 0.02
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    e_got = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    e_want = np.linalg.norm(want - ref) / np.linalg.norm(ref)
+    assert abs(e_got - e_want) < 0.02 * e_want

@@ -180,6 +180,36 @@ def test_cubic_surface_checks():
         smx.cubic_matmul(a, w, bm=256, bn=256, bk=512)
 
 
+@pytest.mark.parametrize("kwargs,match", [
+    ({"epilogue": "gelu"}, "unknown epilogue"),
+    ({"epilogue": "swiglu", "output_dtype": torch.float32}, "BF16 output tile"),
+    ({"epilogue": "residual_add"}, "requires residual="),
+    ({"epilogue": "residual_add", "residual": t(256, 128)}, "residual shape"),
+    ({"epilogue": "residual_add", "residual": t(128, 256)}, "residual shape"),
+    ({"epilogue": "bias_add"}, "requires bias="),
+    ({"epilogue": "bias_add", "bias": t(128)}, "bias shape"),
+    ({"bias": t(256)}, "bias= is only used"),
+    ({"residual": t(256, 256)}, "residual= is only used"),
+    ({"epilogue": "qk_norm_rope"}, "requires rope_cos="),
+    ({"epilogue": "qk_norm_rope", "rope_cos": t(64, 128), "rope_sin": t(64, 128), "rope_scale": t(256)},
+     "rope tables must be"),
+    ({"epilogue": "qk_norm_rope", "rope_cos": t(256, 128), "rope_sin": t(256, 128), "rope_scale": t(128)},
+     "rope_scale must be laid out"),
+    ({"rope_cos": t(256, 128)}, "rope_\\* are only used"),
+    ({"epilogue": "norm_residual_add", "residual": t(256, 256)}, "requires residual= and norm_scale="),
+    ({"epilogue": "norm_residual_add", "residual": t(256, 128), "norm_scale": t(256)}, "residual shape"),
+    ({"epilogue": "norm_residual_add", "residual": t(256, 256), "norm_scale": t(128)}, "norm_scale shape"),
+])
+def test_cubic_epilogue_operand_checks(kwargs, match):
+    """The cubic control checks its epilogue operands like strassen_matmul:
+    the kernels read them by address only, so a short bias, residual or
+    table would otherwise be read out of bounds on the device."""
+    base = {"bm": 256, "bn": 256, "bk": 512}
+    base.update(kwargs)
+    with pytest.raises(ValueError, match=match):
+        smx.cubic_matmul(t(256, 512), t(512, 256), **base)
+
+
 def packed_weight(algo=7, n=512, k=512, bn=512, bk=512):
     return smx.PackedOperand(t(n // 2 * k // 2 * (7 if algo == 7 else 4)), algo=algo, side="rhs",
                              rows=n, k=k, tile_rows=bn, bk=bk)
