@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define SMX_VERSION 7
+#define SMX_VERSION 8
 
 /* Status codes. */
 #define SMX_OK 0
@@ -137,6 +137,27 @@ typedef struct smx_gemm_desc {
 int smx_gemm(const smx_gemm_desc* desc, const void* a, const void* b, void* c, const void* residual,
              const void* bias, const void* rope_cos, const void* rope_sin, const void* rope_scale,
              void* stream);
+
+/*
+ * Allocation-free variant of smx_gemm, with no counterpart in the reference:
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). It takes
+ * a row-major bf16 A (desc->a_layout = SMX_A_ROWMAJOR, row stride lda) and a
+ * packed B (desc->b_layout = SMX_B_PACKED, from smx_pack_operand for the
+ * same algo, formula, block permutation and tile), packs A into a device
+ * scratch array that the library holds for the life of the process (256 MiB
+ * on every GPU it runs on), then runs the packed kernel: the result equals
+ * smx_pack_operand of A into a caller buffer followed by smx_gemm. The packed
+ * A needs M/2 * K/2 * nops * 2 bytes (nops 7 for Strassen, 4 for the cubic),
+ * so M * K must stay at or below 76,695,844 (Strassen) or 134,217,728
+ * (cubic); larger calls fail with SMX_ERR_UNSUPPORTED before any launch. No
+ * FP32 partial (desc->partial must be null). Calls allocate nothing. Every
+ * call on one GPU shares that GPU's scratch: calls that overlap on one GPU
+ * (different streams, or another thread) race, so a caller serialises them.
+ */
+int smx_gemm_noalloc(const smx_gemm_desc* desc, const void* a, const void* b, void* c, const void* residual,
+                     const void* bias, const void* rope_cos, const void* rope_sin, const void* rope_scale,
+                     void* stream);
 
 /* Product-space workgroup tile (tm, tn) and K stage (tk) of the kernel that
  * serves (algo, epilogue, b_layout): bm must be a multiple of 2*tm, bn of

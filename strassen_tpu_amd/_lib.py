@@ -45,13 +45,16 @@ SMX_FORMULA = {"classical": 0, "dual": 1, "powers": 2}
 SMX_AUX_BIAS_F32 = 1
 SMX_AUX_SCALE_F32 = 2
 SMX_AUX_RESIDUAL_F32 = 4
+# Largest packed activation smx_gemm_noalloc stages in its device scratch.
+NOALLOC_SCRATCH_BYTES = 256 << 20
+
 SMX_DTYPE_BF16 = 0
 SMX_DTYPE_F32 = 1
 SMX_NRA_SCALE_F32 = 1
 SMX_NRA_RESIDUAL_F32 = 2
 SMX_NRA_OUT_F32 = 4
 
-EXPORTS = ("smx_gemm", "smx_tile_requirements", "smx_packed_bytes", "smx_pack_operand", "smx_norm_residual_add",
+EXPORTS = ("smx_gemm", "smx_gemm_noalloc", "smx_tile_requirements", "smx_packed_bytes", "smx_pack_operand", "smx_norm_residual_add",
            "smx_last_error", "smx_version")
 
 
@@ -87,6 +90,8 @@ def load():
     vp = ctypes.c_void_p
     lib.smx_gemm.argtypes = [ctypes.POINTER(SmxGemmDesc), vp, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.smx_gemm.restype = ctypes.c_int
+    lib.smx_gemm_noalloc.argtypes = [ctypes.POINTER(SmxGemmDesc), vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.smx_gemm_noalloc.restype = ctypes.c_int
     lib.smx_tile_requirements.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                           ctypes.POINTER(ctypes.c_int32),
                                           ctypes.POINTER(ctypes.c_int32),

@@ -42,6 +42,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "common.hpp"
 #include "kernel_v1.hpp"
 #include "kernel_packed.hpp"
@@ -238,6 +240,161 @@ __global__ __launch_bounds__(256) void norm_residual_rows(const float* __restric
   }
 }
 
+// Checks a GEMM descriptor and its operands and fills the kernel parameters;
+// launches nothing. Shared by smx_gemm and smx_gemm_noalloc.
+int gemm_params(const smx_gemm_desc* d, const void* a, const void* b, void* c, const void* residual,
+                const void* bias, const void* rope_cos, const void* rope_sin, const void* rope_scale, Params& p) {
+  if (!d) return fail(SMX_ERR_INVALID, "null descriptor");
+  if (d->algo != SMX_ALGO_STRASSEN && d->algo != SMX_ALGO_CUBIC)
+    return fail(SMX_ERR_INVALID, "algo must be %d (Strassen) or %d (cubic), got %d", SMX_ALGO_STRASSEN,
+                SMX_ALGO_CUBIC, d->algo);
+  if (d->a_layout != SMX_A_ROWMAJOR && d->a_layout != SMX_A_PACKED)
+    return fail(SMX_ERR_INVALID, "a_layout must be SMX_A_ROWMAJOR or SMX_A_PACKED, got %d", d->a_layout);
+  if (d->b_layout != SMX_B_KCONTIG && d->b_layout != SMX_B_PACKED)
+    return fail(SMX_ERR_INVALID, "b_layout must be SMX_B_KCONTIG or SMX_B_PACKED, got %d", d->b_layout);
+  const bool packed_path = d->b_layout == SMX_B_PACKED;
+  if (packed_path != (d->a_layout == SMX_A_PACKED))
+    return fail(SMX_ERR_UNSUPPORTED, "A and B must both be packed (smx_pack_operand) or both unpacked");
+  if (d->flags & ~SMX_FLAG_OUT_F32) return fail(SMX_ERR_INVALID, "unknown flags 0x%x", d->flags);
+  if (int rc = check_variant(d->algo, d->formula, d->block_permutation)) return rc;
+  if ((d->formula || d->block_permutation) && !packed_path)
+    return fail(SMX_ERR_UNSUPPORTED, "formula variants and block permutations run on packed operands");
+  if (d->formula == SMX_FORMULA_POWERS && d->epilogue != SMX_EPI_NONE)
+    return fail(SMX_ERR_INVALID, "fused epilogues require a quadrant-basis formula");
+  if (d->partial && d->algo != SMX_ALGO_CUBIC)
+    return fail(SMX_ERR_INVALID, "an FP32 partial is added by the cubic algorithm only");
+  if (d->partial && d->a_layout != SMX_A_PACKED)
+    return fail(SMX_ERR_UNSUPPORTED, "an FP32 partial needs packed operands (smx_pack_operand)");
+  if (d->partial && (d->ldp < d->n || d->ldp % 4 || !aligned16(d->partial)))
+    return fail(SMX_ERR_INVALID, "partial needs ldp >= N, ldp %% 4 == 0 and 16-byte alignment");
+  if (d->m <= 0 || d->n <= 0 || d->k <= 0)
+    return fail(SMX_ERR_INVALID, "empty problem m=%lld n=%lld k=%lld", (long long)d->m, (long long)d->n,
+                (long long)d->k);
+  if (d->bm <= 0 || d->bn <= 0 || d->bk <= 0 || d->m % d->bm || d->n % d->bn || d->k % d->bk)
+    return fail(SMX_ERR_INVALID, "M, N, K must be divisible by bm, bn, bk");
+  // Product-space coordinates (rows of M/2, columns of N/2) are 32-bit in the kernels.
+  if (d->m / 2 >= ((int64_t)1 << 31) || d->n / 2 >= ((int64_t)1 << 31))
+    return fail(SMX_ERR_UNSUPPORTED, "M/2 and N/2 must stay below 2^31 (m=%lld, n=%lld)", (long long)d->m,
+                (long long)d->n);
+  int32_t tm, tn, tk;
+  tile_of_path(packed_path, &tm, &tn, &tk);
+  const int hm = d->bm / 2, hn = d->bn / 2, hk = d->bk / 2;
+  if (d->bm % 2 || d->bn % 2 || d->bk % 2 || hm % tm || hn % tn || hk % tk)
+    return fail(SMX_ERR_UNSUPPORTED,
+                "tile (bm=%d, bn=%d, bk=%d) unsupported on gfx950: need bm %% %d == 0, bn %% %d == 0, bk %% %d == 0",
+                d->bm, d->bn, d->bk, 2 * tm, 2 * tn, 2 * tk);
+  if (!a || !b || !c) return fail(SMX_ERR_INVALID, "null operand pointer");
+  if (!aligned16(a) || !aligned16(b)) return fail(SMX_ERR_INVALID, "A and B must be 16-byte aligned");
+  if (!packed_path && (d->lda < d->k || d->ldb < d->k || d->lda % 8 || d->ldb % 8))
+    return fail(SMX_ERR_INVALID, "lda and ldb must be >= K and multiples of 8 elements");
+  const int64_t out_cols = (d->epilogue == SMX_EPI_SWIGLU || d->epilogue == SMX_EPI_GEGLU) ? d->n / 2 : d->n;
+  if (d->ldc < out_cols) return fail(SMX_ERR_INVALID, "ldc must be >= output width");
+  // The epilogue moves output (and residual / partial) rows in 16-byte chunks.
+  const bool out_f32 = (d->flags & SMX_FLAG_OUT_F32) != 0;
+  if (!aligned16(c) || d->ldc % (out_f32 ? 4 : 8))
+    return fail(SMX_ERR_INVALID, "C rows must be 16-byte aligned (C 16-byte aligned, ldc %% %d == 0)", out_f32 ? 4 : 8);
+  // The q/k epilogue addresses its RoPE tables ([M, bn/2] per tile half)
+  // with 32-bit element offsets.
+  if ((int64_t)hm * d->bn >= ((int64_t)1 << 31))
+    return fail(SMX_ERR_UNSUPPORTED, "bm/2 * bn must stay below 2^31 (bm=%d, bn=%d)", d->bm, d->bn);
+  p = Params{};
+  p.a = (const uint16_t*)a;
+  p.b = (const uint16_t*)b;
+  p.c = c;
+  p.out_f32 = (d->flags & SMX_FLAG_OUT_F32) ? 1 : 0;
+  p.formula = d->formula;
+  p.perm = d->block_permutation;
+  p.partial = d->partial;
+  p.ldp = d->partial ? d->ldp : 0;
+  p.m = d->m;
+  p.n = d->n;
+  p.k = d->k;
+  p.lda = d->lda;
+  p.ldb = d->ldb;
+  p.ldc = d->ldc;
+  p.ldr = d->ldr;
+  p.bm = d->bm;
+  p.bn = d->bn;
+  p.bk = d->bk;
+  p.head_dim = d->rope_head_dim;
+  p.eps = d->rope_eps;
+  p.bias_f32 = d->aux_f32 & SMX_AUX_BIAS_F32 ? 1 : 0;
+  p.scale_f32 = d->aux_f32 & SMX_AUX_SCALE_F32 ? 1 : 0;
+  p.residual_f32 = d->aux_f32 & SMX_AUX_RESIDUAL_F32 ? 1 : 0;
+  switch (d->epilogue) {
+    case SMX_EPI_NONE:
+    case SMX_EPI_SWIGLU:
+    case SMX_EPI_GEGLU:
+      break;
+    case SMX_EPI_RESIDUAL_ADD:
+      if (!residual) return fail(SMX_ERR_INVALID, "residual_add epilogue requires residual");
+      if (d->ldr < d->n) return fail(SMX_ERR_INVALID, "ldr must be >= N");
+      if (!aligned16(residual) || d->ldr % (p.residual_f32 ? 4 : 8))
+        return fail(SMX_ERR_INVALID, "residual rows must be 16-byte aligned (residual 16-byte aligned, ldr %% %d == 0)",
+                    p.residual_f32 ? 4 : 8);
+      p.residual = residual;
+      break;
+    case SMX_EPI_BIAS_ADD:
+      if (!bias) return fail(SMX_ERR_INVALID, "bias_add epilogue requires bias");
+      p.bias = bias;
+      break;
+    case SMX_EPI_QK_NORM_ROPE:
+      if (!rope_cos || !rope_sin || !rope_scale)
+        return fail(SMX_ERR_INVALID, "qk_norm_rope requires rope_cos, rope_sin and rope_scale");
+      if (d->rope_head_dim != 128)
+        return fail(SMX_ERR_UNSUPPORTED, "qk_norm_rope on gfx950 supports head_dim 128, got %d", d->rope_head_dim);
+      if (d->bn % (2 * d->rope_head_dim))
+        return fail(SMX_ERR_INVALID, "qk_norm_rope needs bn a multiple of 2*head_dim");
+      p.rope_cos = (const uint16_t*)rope_cos;
+      p.rope_sin = (const uint16_t*)rope_sin;
+      p.rope_scale = rope_scale;
+      break;
+    default:
+      return fail(SMX_ERR_INVALID, "unknown epilogue %d", d->epilogue);
+  }
+  return SMX_OK;
+}
+
+int launch_gemm(const Params& p, const smx_gemm_desc& d, hipStream_t s) {
+  const bool packed_path = d.b_layout == SMX_B_PACKED;
+  if (packed_path)
+    return d.algo == SMX_ALGO_STRASSEN ? dispatch_packed<7>(p, d.epilogue, s) : dispatch_packed<8>(p, d.epilogue, s);
+  return d.algo == SMX_ALGO_STRASSEN ? dispatch_v1<7>(p, d.epilogue, s) : dispatch_v1<8>(p, d.epilogue, s);
+}
+
+// Device scratch of smx_gemm_noalloc: the packed activation of one call,
+// at most kNoAllocScratchBytes. Each GPU the library runs on holds its own
+// copy from module load until the process ends. Host code never passes the
+// array's name to a kernel or a copy (on the host it is only a stand-in
+// symbol): scratch_address() looks up the device address once per device,
+// with that device current, and every use goes through that pointer.
+constexpr size_t kNoAllocScratchBytes = (size_t)256 << 20;
+__device__ __attribute__((aligned(256))) uint8_t scratch[kNoAllocScratchBytes];
+// A non-null, 16-byte-aligned placeholder for the packed A while a
+// descriptor is checked (never dereferenced or launched with).
+const void* const kNoAllocScratchProbe = reinterpret_cast<const void*>((uintptr_t)256);
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_address(void** out) {
+  int device = -1;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return fail(SMX_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (device < 0 || device >= kMaxDevices) return fail(SMX_ERR_UNSUPPORTED, "device %d out of range", device);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[device]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(SMX_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+    g_scratch_ptr[device] = ptr;
+  }
+  *out = g_scratch_ptr[device];
+  return SMX_OK;
+}
+
 }  // namespace
 }  // namespace smx
 
@@ -320,119 +477,44 @@ int smx_pack_operand(int32_t algo, int32_t formula, int32_t block_permutation, i
 int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, const void* residual, const void* bias,
              const void* rope_cos, const void* rope_sin, const void* rope_scale, void* stream) {
   g_error[0] = 0;
-  if (!d) return fail(SMX_ERR_INVALID, "null descriptor");
-  if (d->algo != SMX_ALGO_STRASSEN && d->algo != SMX_ALGO_CUBIC)
-    return fail(SMX_ERR_INVALID, "algo must be %d (Strassen) or %d (cubic), got %d", SMX_ALGO_STRASSEN,
-                SMX_ALGO_CUBIC, d->algo);
-  if (d->a_layout != SMX_A_ROWMAJOR && d->a_layout != SMX_A_PACKED)
-    return fail(SMX_ERR_INVALID, "a_layout must be SMX_A_ROWMAJOR or SMX_A_PACKED, got %d", d->a_layout);
-  if (d->b_layout != SMX_B_KCONTIG && d->b_layout != SMX_B_PACKED)
-    return fail(SMX_ERR_INVALID, "b_layout must be SMX_B_KCONTIG or SMX_B_PACKED, got %d", d->b_layout);
-  const bool packed_path = d->b_layout == SMX_B_PACKED;
-  if (packed_path != (d->a_layout == SMX_A_PACKED))
-    return fail(SMX_ERR_UNSUPPORTED, "A and B must both be packed (smx_pack_operand) or both unpacked");
-  if (d->flags & ~SMX_FLAG_OUT_F32) return fail(SMX_ERR_INVALID, "unknown flags 0x%x", d->flags);
-  if (int rc = check_variant(d->algo, d->formula, d->block_permutation)) return rc;
-  if ((d->formula || d->block_permutation) && !packed_path)
-    return fail(SMX_ERR_UNSUPPORTED, "formula variants and block permutations run on packed operands");
-  if (d->formula == SMX_FORMULA_POWERS && d->epilogue != SMX_EPI_NONE)
-    return fail(SMX_ERR_INVALID, "fused epilogues require a quadrant-basis formula");
-  if (d->partial && d->algo != SMX_ALGO_CUBIC)
-    return fail(SMX_ERR_INVALID, "an FP32 partial is added by the cubic algorithm only");
-  if (d->partial && d->a_layout != SMX_A_PACKED)
-    return fail(SMX_ERR_UNSUPPORTED, "an FP32 partial needs packed operands (smx_pack_operand)");
-  if (d->partial && (d->ldp < d->n || d->ldp % 4 || !aligned16(d->partial)))
-    return fail(SMX_ERR_INVALID, "partial needs ldp >= N, ldp %% 4 == 0 and 16-byte alignment");
-  if (d->m <= 0 || d->n <= 0 || d->k <= 0)
-    return fail(SMX_ERR_INVALID, "empty problem m=%lld n=%lld k=%lld", (long long)d->m, (long long)d->n,
-                (long long)d->k);
-  if (d->bm <= 0 || d->bn <= 0 || d->bk <= 0 || d->m % d->bm || d->n % d->bn || d->k % d->bk)
-    return fail(SMX_ERR_INVALID, "M, N, K must be divisible by bm, bn, bk");
-  // Product-space coordinates (rows of M/2, columns of N/2) are 32-bit in the kernels.
-  if (d->m / 2 >= ((int64_t)1 << 31) || d->n / 2 >= ((int64_t)1 << 31))
-    return fail(SMX_ERR_UNSUPPORTED, "M/2 and N/2 must stay below 2^31 (m=%lld, n=%lld)", (long long)d->m,
-                (long long)d->n);
-  int32_t tm, tn, tk;
-  tile_of_path(packed_path, &tm, &tn, &tk);
-  const int hm = d->bm / 2, hn = d->bn / 2, hk = d->bk / 2;
-  if (d->bm % 2 || d->bn % 2 || d->bk % 2 || hm % tm || hn % tn || hk % tk)
-    return fail(SMX_ERR_UNSUPPORTED,
-                "tile (bm=%d, bn=%d, bk=%d) unsupported on gfx950: need bm %% %d == 0, bn %% %d == 0, bk %% %d == 0",
-                d->bm, d->bn, d->bk, 2 * tm, 2 * tn, 2 * tk);
-  if (!a || !b || !c) return fail(SMX_ERR_INVALID, "null operand pointer");
-  if (!aligned16(a) || !aligned16(b)) return fail(SMX_ERR_INVALID, "A and B must be 16-byte aligned");
-  if (!packed_path && (d->lda < d->k || d->ldb < d->k || d->lda % 8 || d->ldb % 8))
-    return fail(SMX_ERR_INVALID, "lda and ldb must be >= K and multiples of 8 elements");
-  const int64_t out_cols = (d->epilogue == SMX_EPI_SWIGLU || d->epilogue == SMX_EPI_GEGLU) ? d->n / 2 : d->n;
-  if (d->ldc < out_cols) return fail(SMX_ERR_INVALID, "ldc must be >= output width");
-  // The epilogue moves output (and residual / partial) rows in 16-byte chunks.
-  const bool out_f32 = (d->flags & SMX_FLAG_OUT_F32) != 0;
-  if (!aligned16(c) || d->ldc % (out_f32 ? 4 : 8))
-    return fail(SMX_ERR_INVALID, "C rows must be 16-byte aligned (C 16-byte aligned, ldc %% %d == 0)", out_f32 ? 4 : 8);
-  // The q/k epilogue addresses its RoPE tables ([M, bn/2] per tile half)
-  // with 32-bit element offsets.
-  if ((int64_t)hm * d->bn >= ((int64_t)1 << 31))
-    return fail(SMX_ERR_UNSUPPORTED, "bm/2 * bn must stay below 2^31 (bm=%d, bn=%d)", d->bm, d->bn);
   Params p{};
-  p.a = (const uint16_t*)a;
-  p.b = (const uint16_t*)b;
-  p.c = c;
-  p.out_f32 = (d->flags & SMX_FLAG_OUT_F32) ? 1 : 0;
-  p.formula = d->formula;
-  p.perm = d->block_permutation;
-  p.partial = d->partial;
-  p.ldp = d->partial ? d->ldp : 0;
-  p.m = d->m;
-  p.n = d->n;
-  p.k = d->k;
-  p.lda = d->lda;
-  p.ldb = d->ldb;
-  p.ldc = d->ldc;
-  p.ldr = d->ldr;
-  p.bm = d->bm;
-  p.bn = d->bn;
-  p.bk = d->bk;
-  p.head_dim = d->rope_head_dim;
-  p.eps = d->rope_eps;
-  p.bias_f32 = d->aux_f32 & SMX_AUX_BIAS_F32 ? 1 : 0;
-  p.scale_f32 = d->aux_f32 & SMX_AUX_SCALE_F32 ? 1 : 0;
-  p.residual_f32 = d->aux_f32 & SMX_AUX_RESIDUAL_F32 ? 1 : 0;
-  switch (d->epilogue) {
-    case SMX_EPI_NONE:
-    case SMX_EPI_SWIGLU:
-    case SMX_EPI_GEGLU:
-      break;
-    case SMX_EPI_RESIDUAL_ADD:
-      if (!residual) return fail(SMX_ERR_INVALID, "residual_add epilogue requires residual");
-      if (d->ldr < d->n) return fail(SMX_ERR_INVALID, "ldr must be >= N");
-      if (!aligned16(residual) || d->ldr % (p.residual_f32 ? 4 : 8))
-        return fail(SMX_ERR_INVALID, "residual rows must be 16-byte aligned (residual 16-byte aligned, ldr %% %d == 0)",
-                    p.residual_f32 ? 4 : 8);
-      p.residual = residual;
-      break;
-    case SMX_EPI_BIAS_ADD:
-      if (!bias) return fail(SMX_ERR_INVALID, "bias_add epilogue requires bias");
-      p.bias = bias;
-      break;
-    case SMX_EPI_QK_NORM_ROPE:
-      if (!rope_cos || !rope_sin || !rope_scale)
-        return fail(SMX_ERR_INVALID, "qk_norm_rope requires rope_cos, rope_sin and rope_scale");
-      if (d->rope_head_dim != 128)
-        return fail(SMX_ERR_UNSUPPORTED, "qk_norm_rope on gfx950 supports head_dim 128, got %d", d->rope_head_dim);
-      if (d->bn % (2 * d->rope_head_dim))
-        return fail(SMX_ERR_INVALID, "qk_norm_rope needs bn a multiple of 2*head_dim");
-      p.rope_cos = (const uint16_t*)rope_cos;
-      p.rope_sin = (const uint16_t*)rope_sin;
-      p.rope_scale = rope_scale;
-      break;
-    default:
-      return fail(SMX_ERR_INVALID, "unknown epilogue %d", d->epilogue);
-  }
-  hipStream_t s = (hipStream_t)stream;
-  if (packed_path)
-    return d->algo == SMX_ALGO_STRASSEN ? dispatch_packed<7>(p, d->epilogue, s)
-                                        : dispatch_packed<8>(p, d->epilogue, s);
-  return d->algo == SMX_ALGO_STRASSEN ? dispatch_v1<7>(p, d->epilogue, s) : dispatch_v1<8>(p, d->epilogue, s);
+  if (int rc = gemm_params(d, a, b, c, residual, bias, rope_cos, rope_sin, rope_scale, p)) return rc;
+  return launch_gemm(p, *d, (hipStream_t)stream);
+}
+
+int smx_gemm_noalloc(const smx_gemm_desc* d, const void* a, const void* b, void* c, const void* residual,
+                     const void* bias, const void* rope_cos, const void* rope_sin, const void* rope_scale,
+                     void* stream) {
+  g_error[0] = 0;
+  if (!d) return fail(SMX_ERR_INVALID, "null descriptor");
+  if (d->a_layout != SMX_A_ROWMAJOR || d->b_layout != SMX_B_PACKED)
+    return fail(SMX_ERR_INVALID,
+                "smx_gemm_noalloc takes a row-major bf16 A (SMX_A_ROWMAJOR) and a packed B (SMX_B_PACKED)");
+  if (d->partial) return fail(SMX_ERR_UNSUPPORTED, "smx_gemm_noalloc takes no FP32 partial");
+  if (!a) return fail(SMX_ERR_INVALID, "null operand pointer");
+  // Every check of the GEMM runs on the descriptor the packed call will see,
+  // before anything is launched; the scratch stands in for the packed A.
+  smx_gemm_desc packed = *d;
+  packed.a_layout = SMX_A_PACKED;
+  Params p{};
+  if (int rc = gemm_params(&packed, kNoAllocScratchProbe, b, c, residual, bias, rope_cos, rope_sin, rope_scale, p))
+    return rc;
+  if (d->lda < d->k || d->lda % 8) return fail(SMX_ERR_INVALID, "lda must be >= K and a multiple of 8 elements");
+  if (!aligned16(a)) return fail(SMX_ERR_INVALID, "A must be 16-byte aligned");
+  const int64_t bytes = (d->m / 2) * (d->k / 2) * packed::nops_of(d->algo) * 2;
+  if (bytes > (int64_t)kNoAllocScratchBytes)
+    return fail(SMX_ERR_UNSUPPORTED,
+                "smx_gemm_noalloc packs A into a %lld-byte device scratch; this call needs %lld bytes "
+                "(M*K <= %lld for algo %d)",
+                (long long)kNoAllocScratchBytes, (long long)bytes,
+                (long long)(kNoAllocScratchBytes / (packed::nops_of(d->algo) / 2.0)), d->algo);
+  void* scratch_ptr = nullptr;
+  if (int rc = scratch_address(&scratch_ptr)) return rc;
+  if (int rc = smx_pack_operand(d->algo, d->formula, d->block_permutation, SMX_SIDE_LHS, d->m, d->k, a,
+                                SMX_DTYPE_BF16, 1, d->lda, d->bm, d->bk, nullptr, 0, scratch_ptr, stream))
+    return rc;
+  p.a = (const uint16_t*)scratch_ptr;
+  return launch_gemm(p, packed, (hipStream_t)stream);
 }
 
 int smx_norm_residual_add(int64_t m, int64_t n, const float* x, int64_t ldx, const void* residual, int64_t ldr,

@@ -352,3 +352,41 @@ def test_kernel_scratch_check():
             build.verify_kernel_scratch(clean + desc(name, size))
     with pytest.raises(RuntimeError, match="no GEMM kernel"):
         build.verify_kernel_scratch(desc(other, 0))
+
+
+def test_noalloc_entry_point_rejects_before_any_launch():
+    """smx_gemm_noalloc checks its descriptor (the smx_gemm checks, on the
+    packed call it will make) and the scratch limit before touching the
+    device: every case here fails without a GPU."""
+    lib = _lib.load()
+    buf = (ctypes.c_uint8 * 4096)()
+    base = ctypes.addressof(buf)
+    p = ctypes.c_void_p(base + (-base) % 256)
+    ok = dict(m=512, n=512, k=512, lda=512, ldc=512, bm=512, bn=512, bk=512, a_layout=_lib.SMX_A_ROWMAJOR,
+              b_layout=_lib.SMX_B_PACKED)
+
+    def call(**kw):
+        fields = dict(ok)
+        fields.update(kw)
+        return lib.smx_gemm_noalloc(_desc(**fields), p, p, p, None, None, None, None, None, None)
+
+    assert call(b_layout=_lib.SMX_B_KCONTIG) == _lib.SMX_ERR_INVALID
+    assert "row-major bf16 A" in _lib.last_error()
+    assert call(a_layout=_lib.SMX_A_PACKED) == _lib.SMX_ERR_INVALID
+    d = _desc(**ok)
+    d.partial, d.ldp = p.value, 512
+    assert lib.smx_gemm_noalloc(d, p, p, p, None, None, None, None, None, None) == _lib.SMX_ERR_UNSUPPORTED
+    assert "partial" in _lib.last_error()
+    assert call(bm=128) == _lib.SMX_ERR_UNSUPPORTED            # the packed kernel's tile rule
+    assert call(epilogue=_lib.SMX_EPI["residual_add"]) == _lib.SMX_ERR_INVALID
+    assert call(lda=500) == _lib.SMX_ERR_INVALID
+    assert "lda" in _lib.last_error()
+    assert lib.smx_gemm_noalloc(_desc(**ok), None, p, p, None, None, None, None, None, None) == _lib.SMX_ERR_INVALID
+    # the scratch limit: M*K beyond 256 MiB of packed Strassen operand sums
+    limit = _lib.NOALLOC_SCRATCH_BYTES
+    m, k = 16384, 5120  # 16384 * 5120 * 3.5 bytes > 256 MiB
+    assert m * k * 7 // 2 > limit
+    assert call(m=m, k=k, lda=k, bm=1024, bn=512, bk=512) == _lib.SMX_ERR_UNSUPPORTED
+    assert "scratch" in _lib.last_error() and str(limit) in _lib.last_error()
+    # the cubic's four quadrants fit where Strassen's seven operand sums do not
+    assert m * k * 2 <= limit
