@@ -1,7 +1,7 @@
 // Packed-operand gfx950 kernel: 128x128 product-space workgroup tile, four
 // waves of 64x64, 16 product-space k per stage, both operands streamed from
-// HBM straight into LDS (global_load_lds_dwordx4, no VGPR staging, no VALU in
-// the main loop).
+// HBM straight into LDS (buffer_load_dwordx4 ... lds, no VGPR staging, no
+// VALU in the main loop).
 //
 // Packed operand layout (written by pack_operand below, once per weight and
 // once per call for the activation). An operand of R product rows (M/2 for
@@ -104,6 +104,34 @@ __device__ __forceinline__ void mfma_drain(f32x16 (&acc)[kSets][2][2]) {
       }
 }
 
+// Operand DMA goes through buffer loads into LDS (buffer_load_dwordx4 ...
+// lds). Measured on gfx950, the FLAT form of the same DMA
+// (global_load_lds_dwordx4) holds back the MFMAs of every wave on the CU
+// while its data arrives: an MFMA stream and a DMA stream on one CU took
+// about the sum of their separate times, at full chip load and on 32 CUs
+// alike; with buffer loads they overlap (1.89 against 1.57 PFLOP/s for 32 KB
+// and 128 MFMAs per CU and stage).
+//
+// A wave's operand panel as a buffer resource: base = the wave's first
+// fragment in the workgroup's packed panel, num_records = the bytes from
+// there to the panel's end. Word 3 selects raw 32-bit-format access (gfx9
+// DATA_FORMAT 32). A load past num_records returns zeros instead of
+// touching memory.
+constexpr int kBufferWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t panel_rsrc(const uint8_t* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), 0, (int)bytes, kBufferWord3);
+}
+
+// One fragment-sized DMA: every lane moves 16 bytes at panel offset
+// soffset (uniform) + voffset (the lane's 16 * lane) into LDS at `to` + 16 *
+// lane.
+__device__ __forceinline__ void dma_frag(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, uint32_t soffset,
+                                         uint8_t* to) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)to, 16, voffset, soffset,
+                                           0, 0);
+}
+
 __device__ __forceinline__ bf16x8 ld_frag(const uint8_t* p) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(p));
 }
@@ -126,23 +154,21 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
   // DMA sources: this workgroup's packed stages are contiguous runs of
   // L::kStage bytes; wave w moves fragments f = w + 4x of each.
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  const uint8_t* const a_src =
-      reinterpret_cast<const uint8_t*>(p.a) + (int64_t)tile_m * nstages * L::kStage + wave_u * kFrag;
-  const uint8_t* const b_src =
-      reinterpret_cast<const uint8_t*>(p.b) + (int64_t)tile_n * nstages * L::kStage + wave_u * kFrag;
+  const uint32_t panel_bytes = (uint32_t)nstages * L::kStage - wave_u * kFrag;
+  const __amdgpu_buffer_rsrc_t a_src = panel_rsrc(
+      reinterpret_cast<const uint8_t*>(p.a) + (int64_t)tile_m * nstages * L::kStage + wave_u * kFrag, panel_bytes);
+  const __amdgpu_buffer_rsrc_t b_src = panel_rsrc(
+      reinterpret_cast<const uint8_t*>(p.b) + (int64_t)tile_n * nstages * L::kStage + wave_u * kFrag, panel_bytes);
   const uint32_t lane_off = lane * 16;
   uint8_t* const a_region = lds;
   uint8_t* const b_region = lds + L::kASlots * L::kStage;
 
   // Prefetches past the last stage re-load it (in bounds, never read)
   // instead of branching.
-  auto dma = [&](const uint8_t* src, int stage, uint8_t* slot) {
-    const uint8_t* from = src + (int64_t)min(stage, nstages - 1) * L::kStage + lane_off;
+  auto dma = [&](__amdgpu_buffer_rsrc_t src, int stage, uint8_t* slot) {
+    const uint32_t from = (uint32_t)min(stage, nstages - 1) * L::kStage;
 #pragma unroll
-    for (int x = 0; x < L::kDmaPerWave; ++x)
-      __builtin_amdgcn_global_load_lds(from + x * 4 * kFrag,
-                                       (__attribute__((address_space(3))) void*)(slot + (wave_u + 4 * x) * kFrag), 16,
-                                       0, 0);
+    for (int x = 0; x < L::kDmaPerWave; ++x) dma_frag(src, lane_off, from + x * 4 * kFrag, slot + (wave_u + 4 * x) * kFrag);
   };
 
   f32x16 acc[L::nops][2][2];
@@ -226,9 +252,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
       // the first half's MFMA groups rather than as one burst ahead of them;
       // all are issued before the mid-stage barrier, so its vmcnt
       // accounting is unchanged.
-      const int stage = min(s + kSlots - 1, nstages - 1);
-      const uint8_t* const a_from = a_src + (int64_t)stage * L::kStage + lane_off;
-      const uint8_t* const b_from = b_src + (int64_t)stage * L::kStage + lane_off;
+      const uint32_t from = (uint32_t)min(s + kSlots - 1, nstages - 1) * L::kStage;
       uint8_t* const a_to = a_region + refill * L::kStage + wave_u * kFrag;
       uint8_t* const b_to = b_region + refill * L::kStage + wave_u * kFrag;
       auto dma_pair = [&](int g) {
@@ -236,10 +260,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
         for (int q = 2 * g; q < 2 * g + 2; ++q) {
           const bool is_a = q < L::kDmaPerWave;
           const int x = is_a ? q : q - L::kDmaPerWave;
-          __builtin_amdgcn_global_load_lds((is_a ? a_from : b_from) + x * 4 * kFrag,
-                                           (__attribute__((address_space(3))) void*)((is_a ? a_to : b_to) +
-                                                                                      4 * x * kFrag),
-                                           16, 0, 0);
+          dma_frag(is_a ? a_src : b_src, lane_off, from + x * 4 * kFrag, (is_a ? a_to : b_to) + 4 * x * kFrag);
         }
       };
       __builtin_amdgcn_sched_barrier(0);

@@ -92,8 +92,8 @@ struct Ring {
 
 // One wave's main loop, accumulator exchange and epilogue.
 template <int kWave, int kEpi, int kQuad>
-__device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, int nstages, const uint8_t* a_src,
-                                         const uint8_t* b_src, uint8_t* lds) {
+__device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, int nstages,
+                                         __amdgpu_buffer_rsrc_t a_src, __amdgpu_buffer_rsrc_t b_src, uint8_t* lds) {
   using L = packed::Lay<7>;
   using P = Plan<kWave>;
   uint8_t* const a_long = lds;
@@ -156,24 +156,16 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
     // base plus a 32-bit lane offset.
     uint32_t dma_lane = lane_off;
     asm volatile("" : "+v"(dma_lane));
-    const uint8_t* const a_far = a_src + (int64_t)min(s + 2, nstages - 1) * L::kStage;
-    const uint8_t* const b_far = b_src + (int64_t)min(s + 2, nstages - 1) * L::kStage;
+    const uint32_t far = (uint32_t)min(s + 2, nstages - 1) * L::kStage;
     uint8_t* const al_to = a_long + l_fill * Ring::kALong + kWave * kFrag;
     uint8_t* const b_to = b_region + l_fill * L::kStage + kWave * kFrag;
     // q < 5: A operand q; q >= 5: B operand q - 5
     auto dma_op = [&](int q) {
       constexpr int kL = Ring::kLongOps;
-      const uint8_t* from;
-      uint8_t* to;
-      if (q < kL) {
-        from = a_far + q * 4 * kFrag;
-        to = al_to + q * 4 * kFrag;
-      } else {
-        from = b_far + (q - kL) * 4 * kFrag;
-        to = b_to + (q - kL) * 4 * kFrag;
-      }
-      // uniform base + operand offset, then the lane's 32-bit offset
-      __builtin_amdgcn_global_load_lds(from + dma_lane, (__attribute__((address_space(3))) void*)to, 16, 0, 0);
+      if (q < kL)
+        packed::dma_frag(a_src, dma_lane, far + q * 4 * kFrag, al_to + q * 4 * kFrag);
+      else
+        packed::dma_frag(b_src, dma_lane, far + (q - kL) * 4 * kFrag, b_to + (q - kL) * 4 * kFrag);
     };
     __builtin_amdgcn_sched_barrier(0);
     const uint8_t* const sal = a_long + l_slot * Ring::kALong;
@@ -199,12 +191,11 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
     packed::stage_barrier<Ring::kPending>();
     {
       // A operands 5-6 of stage s+2 into the short slot stage s used.
-      const uint8_t* const a_near = a_src + (int64_t)min(s + 2, nstages - 1) * L::kStage;
+      const uint32_t near = (uint32_t)min(s + 2, nstages - 1) * L::kStage;
       uint8_t* const as_to = a_short + s_slot * Ring::kAShort + kWave * kFrag;
 #pragma unroll
       for (int q = 0; q < Ring::kShortOps; ++q)
-        __builtin_amdgcn_global_load_lds(a_near + (Ring::kLongOps + q) * 4 * kFrag + dma_lane,
-                                         (__attribute__((address_space(3))) void*)(as_to + q * 4 * kFrag), 16, 0, 0);
+        packed::dma_frag(a_src, dma_lane, near + (Ring::kLongOps + q) * 4 * kFrag, as_to + q * 4 * kFrag);
     }
     // Stage s+1's strip 0 (past the last stage: a re-loaded copy, unused).
     const bf16x8 a_first = load_a(a_long + l_next * Ring::kALong, a_short + s_next * Ring::kAShort, 0);
@@ -325,22 +316,21 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
   const TileOrigin o = tile_origin(p, (int64_t)tile_m * packed::TM, (int64_t)tile_n * packed::TN);
   const int nstages = (int)(p.k / (2 * TK));
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint8_t* const a_src =
-      reinterpret_cast<const uint8_t*>(p.a) + (int64_t)tile_m * nstages * L::kStage + wave * kFrag;
-  const uint8_t* const b_src =
-      reinterpret_cast<const uint8_t*>(p.b) + (int64_t)tile_n * nstages * L::kStage + wave * kFrag;
+  const uint32_t panel_bytes = (uint32_t)nstages * L::kStage - wave * kFrag;
+  const __amdgpu_buffer_rsrc_t a_src = packed::panel_rsrc(
+      reinterpret_cast<const uint8_t*>(p.a) + (int64_t)tile_m * nstages * L::kStage + wave * kFrag, panel_bytes);
+  const __amdgpu_buffer_rsrc_t b_src = packed::panel_rsrc(
+      reinterpret_cast<const uint8_t*>(p.b) + (int64_t)tile_n * nstages * L::kStage + wave * kFrag, panel_bytes);
 
   // Prologue: stage 0 of everything, then stage 1 of A's long operands, of
   // B and of A's short operands (the loop's order); stage 0 has landed once
   // only stage 1 remains in flight.
   const uint32_t lane_off = lane * 16;
-  auto dma = [&](const uint8_t* src, int stage, int x0, int x1, uint8_t* slot) {
-    const uint8_t* from = src + (int64_t)min(stage, nstages - 1) * L::kStage + lane_off;
+  auto dma = [&](__amdgpu_buffer_rsrc_t src, int stage, int x0, int x1, uint8_t* slot) {
+    const uint32_t from = (uint32_t)min(stage, nstages - 1) * L::kStage;
 #pragma unroll
     for (int x = x0; x < x1; ++x)
-      __builtin_amdgcn_global_load_lds(from + x * 4 * kFrag,
-                                       (__attribute__((address_space(3))) void*)(slot + (wave + 4 * (x - x0)) * kFrag),
-                                       16, 0, 0);
+      packed::dma_frag(src, lane_off, from + x * 4 * kFrag, slot + (wave + 4 * (x - x0)) * kFrag);
   };
   uint8_t* const b_region = lds + Ring::kBBase;
   dma(a_src, 0, Ring::kLongOps, 7, lds + Ring::kAShortBase);
