@@ -109,6 +109,25 @@ def make_block(torch, dev, seed=0):
     return d
 
 
+# The six block sites' weights (B operands) as make_block names them.
+SITE_WEIGHTS = ("wq_laid", "wk_laid", "wv", "wo", "wgu_laid", "wd")
+
+
+def weight_memory(d):
+    """HBM bytes the block's six weights occupy in each arm's form: plain
+    bf16, the seven packed Strassen operand sums (7/4 of plain) and the
+    cubic's four packed quadrants (the plain size)."""
+    def total(suffix):
+        return int(sum((d[n + suffix].data if suffix else d[n]).numel() * 2 for n in SITE_WEIGHTS))
+
+    plain, strassen, cubic = total(""), total("_sw"), total("_cw")
+    gu = d["wgu_laid"].numel() * 2
+    return {"plain_bytes": plain, "strassen_packed_bytes": strassen, "cubic_packed_bytes": cubic,
+            "strassen_over_plain": round(strassen / plain, 4),
+            "gate_up_bytes": {"plain": gu, "strassen_packed": int(d["wgu_laid_sw"].data.numel() * 2),
+                              "cubic_packed": int(d["wgu_laid_cw"].data.numel() * 2)}}
+
+
 # Weight suffix and algorithm id of each kernel arm.
 ARM_WEIGHTS = {"strassen": ("_sw", 7), "cubic": ("_cw", 8), "strassen_plain": ("", 7), "cubic_plain": ("", 8)}
 
@@ -514,6 +533,7 @@ def main():
         "roofline": roofline,
         "full_block_ms": {k: round(v, 4) for k, v in full_block.items()},
         "full_block_speedup_vs_cubic": round(full_block["cubic"] / full_block["strassen"], 4),
+        "weight_memory": weight_memory(d),
     }
     if not args.no_cpu_baseline:
         log("timing CPU baseline (oracle)")
