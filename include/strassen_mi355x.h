@@ -16,6 +16,8 @@
  *                with algo = SMX_ALGO_CUBIC (the matched 8-product control).
  *   smx_norm_residual_add <- the norm_residual_add epilogue (strassen_pallas.py:836-866),
  *                run as a second pass over an FP32 smx_gemm result.
+ *   smx_qk_norm_rope <- the qk_norm_rope epilogue (strassen_pallas.py:793-835)
+ *                for head widths other than 128, likewise a second pass.
  *   smx_last_error / status codes <- the ValueError/RuntimeError raised by
  *                strassen_matmul's argument checks (strassen_pallas.py:927-1047).
  *   smx_tile_requirements <- check_tiling (strassen_pallas.py:127-140): the
@@ -39,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SMX_VERSION 8
+#define SMX_VERSION 9
 
 /* Status codes. */
 #define SMX_OK 0
@@ -93,6 +95,10 @@ extern "C" {
 #define SMX_NRA_SCALE_F32 1
 #define SMX_NRA_RESIDUAL_F32 2
 #define SMX_NRA_OUT_F32 4
+
+/* smx_qk_norm_rope dtype bits (else bf16). */
+#define SMX_QK_SCALE_F32 1
+#define SMX_QK_OUT_F32 4
 
 typedef struct smx_gemm_desc {
   int64_t m, n, k;       /* C[m, n] = A[m, k] @ B[k, n] */
@@ -148,9 +154,9 @@ int smx_gemm(const smx_gemm_desc* desc, const void* a, const void* b, void* c, c
  * scratch array that the library holds for the life of the process (256 MiB
  * on every GPU it runs on), then runs the packed kernel: the result equals
  * smx_pack_operand of A into a caller buffer followed by smx_gemm. The packed
- * A needs M/2 * K/2 * nops * 2 bytes (nops 7 for Strassen, 4 for the cubic),
- * so M * K must stay at or below 76,695,844 (Strassen) or 134,217,728
- * (cubic); larger calls fail with SMX_ERR_UNSUPPORTED before any launch. No
+ * A needs smx_packed_bytes(algo, M, K) bytes (about M/2 * K/2 * nops * 2, nops
+ * 7 for Strassen, 4 for the cubic), so M * K must stay at or below about
+ * 76,695,844 (Strassen) or 134,217,728 (cubic); larger calls fail with SMX_ERR_UNSUPPORTED before any launch. No
  * FP32 partial (desc->partial must be null). Calls allocate nothing. Every
  * call on one GPU shares that GPU's scratch: calls that overlap on one GPU
  * (different streams, or another thread) race, so a caller serialises them.
@@ -159,14 +165,18 @@ int smx_gemm_noalloc(const smx_gemm_desc* desc, const void* a, const void* b, vo
                      const void* bias, const void* rope_cos, const void* rope_sin, const void* rope_scale,
                      void* stream);
 
-/* Product-space workgroup tile (tm, tn) and K stage (tk) of the kernel that
- * serves (algo, epilogue, b_layout): bm must be a multiple of 2*tm, bn of
- * 2*tn, bk of 2*tk. */
+/* Tile granules of the kernels that serve (algo, epilogue, b_layout): bm
+ * must be a multiple of 2*tm, bn of 2*tn, bk of 2*tk. Packed operands: 8, 128,
+ * 32 (every bm the reference's check_tiling allows, strassen_pallas.py:127-140;
+ * a bm/2 that is not a multiple of the kernels' 128-row product tile runs
+ * their thin-tiling instantiations); unpacked: 128, 64, 32. */
 int smx_tile_requirements(int32_t algo, int32_t epilogue, int32_t b_layout, int32_t flags, int32_t* tm, int32_t* tn,
                           int32_t* tk);
 
-/* Bytes of the packed form of a [rows, k] operand for algo (rows/2 * k/2 *
- * nops * 2, nops = 7 for Strassen, 4 for the cubic). */
+/* Bytes of the packed form of a [rows, k] operand for algo: R * k/2 * nops *
+ * 2, with R = rows/2 rounded up to a multiple of 128 (product rows of a thin
+ * tiling's last tile are zero padding) and nops = 7 for Strassen, 4 for the
+ * cubic. */
 int smx_packed_bytes(int32_t algo, int64_t rows, int64_t k, int64_t* bytes);
 
 /*
@@ -196,12 +206,14 @@ int smx_packed_bytes(int32_t algo, int64_t rows, int64_t k, int64_t* bytes);
  * the ordinary or the exact panels of an exact-panel schedule (without a map,
  * src_k = k / passes). out
  * (smx_packed_bytes bytes, 16-byte aligned)
- * is laid out [rows/256][k/32][nops][4][64][8] bf16: fragment (tile of 128
- * product rows, stage of 16 product k, operand, 32-row block), lane l holding
- * row l%32, depth 8*(l/32)..+8. Needs rows % tile_rows == 0, k % (passes * bk) == 0,
- * tile_rows % 256 == 0, bk % 64 == 0, ld >= src_k, rows 16-byte aligned (ld % 8 for bf16, % 4 for
- * float32; LHS_T: ld >= m). Asynchronous on
- * stream.
+ * is laid out [R/128][k/32][nops][4][64][8] bf16 (R as in smx_packed_bytes):
+ * fragment (tile of 128 product rows, stage of 16 product k, operand, 32-row
+ * block), lane l holding row l%32, depth 8*(l/32)..+8. Product row P is row
+ * P % (tile_rows/2) of row tile P / (tile_rows/2); rows past rows/2 are
+ * zeros. Needs rows % tile_rows == 0, k % (passes * bk) == 0, tile_rows % 16
+ * == 0 (A sides) or % 256 == 0 (RHS), bk % 64 == 0, ld >= src_k, rows 16-byte
+ * aligned (ld % 8 for bf16, % 4 for float32; LHS_T: ld >= m). Asynchronous
+ * on stream.
  */
 int smx_pack_operand(int32_t algo, int32_t formula, int32_t block_permutation, int32_t side, int64_t rows, int64_t k,
                      const void* src, int32_t src_dtype, int32_t passes, int64_t ld, int32_t tile_rows,
@@ -218,6 +230,24 @@ int smx_pack_operand(int32_t algo, int32_t formula, int32_t block_permutation, i
  */
 int smx_norm_residual_add(int64_t m, int64_t n, const float* x, int64_t ldx, const void* residual, int64_t ldr,
                           const void* scale, int32_t dtypes, float eps, void* out, int64_t ldo, void* stream);
+
+/*
+ * Second pass of the qk_norm_rope epilogue (strassen_pallas.py:793-835) for
+ * head widths the fused epilogue does not take (it fuses head_dim 128): from
+ * the FP32 product x [m, n] (an smx_gemm with SMX_FLAG_OUT_F32 and no
+ * epilogue, on the rope-laid-out weight) writes out [m, n]. In each column
+ * tile of bn, head h of the bn / head_dim heads pairs columns c in
+ * [h head_dim/2, (h+1) head_dim/2) of the first half (a) and the second half
+ * (b): recip = 1/sqrt((sum a^2 + sum b^2)/head_dim + eps), na = a recip
+ * scale[c], nb = b recip scale[bn/2 + c], out_a = na cos - nb sin, out_b =
+ * nb cos + na sin, with rope_cos / rope_sin bf16 [m, bn/2] at (row, c) and
+ * rope_scale [bn] (the layouts of rope_layout_tables / rope_scale_layout).
+ * dtypes: SMX_QK_* bits. Needs bn % (2 head_dim) == 0, n % bn == 0 and
+ * (bn + bn/head_dim) * 4 <= 65536. Asynchronous on stream.
+ */
+int smx_qk_norm_rope(int64_t m, int64_t n, const float* x, int64_t ldx, const void* rope_cos, const void* rope_sin,
+                     const void* rope_scale, int32_t dtypes, int32_t bn, int32_t head_dim, float eps, void* out,
+                     int64_t ldo, void* stream);
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* smx_last_error(void);

@@ -417,9 +417,16 @@ def packed_operand(x, algo, side, tile_rows, bk, formula="classical", block_perm
                    input_dtype="bfloat16", dot_precision=None):
     """``smx_pack_operand``'s output as a flat float32 array of bf16 values:
     ``[R/128][K/32][nops][4][64][8]``, lane l of a fragment holding product
-    row l%32 of its 32-row block and depth 8*(l//32)..+8 of its stage."""
+    row l%32 of its 32-row block and depth 8*(l//32)..+8 of its stage; R is
+    the product rows rounded up to 128, the rows past them zeros."""
     planes = operand_planes(x, algo, side, tile_rows, bk, formula, block_permutation, input_dtype, dot_precision)
     nops, rows, depth = planes.shape
+    # A thin tiling (tile_rows/2 not a multiple of 128) leaves a partial last
+    # product tile: its missing rows are zeros (smx_packed_bytes counts them).
+    padded = -(-rows // PACK_TILE) * PACK_TILE
+    if padded != rows:
+        planes = np.concatenate([planes, np.zeros((nops, padded - rows, depth), np.float32)], axis=1)
+        rows = padded
     v = planes.reshape(nops, rows // PACK_TILE, 4, 32, depth // PACK_STAGE, 2, 8)
     # (op, tile, block, row32, stage, half, e) -> (tile, stage, op, block, half, row32, e)
     return np.ascontiguousarray(v.transpose(1, 4, 0, 2, 5, 3, 6)).reshape(-1)

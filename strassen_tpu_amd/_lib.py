@@ -53,9 +53,11 @@ SMX_DTYPE_F32 = 1
 SMX_NRA_SCALE_F32 = 1
 SMX_NRA_RESIDUAL_F32 = 2
 SMX_NRA_OUT_F32 = 4
+SMX_QK_SCALE_F32 = 1
+SMX_QK_OUT_F32 = 4
 
-EXPORTS = ("smx_gemm", "smx_gemm_noalloc", "smx_tile_requirements", "smx_packed_bytes", "smx_pack_operand", "smx_norm_residual_add",
-           "smx_last_error", "smx_version")
+EXPORTS = ("smx_gemm", "smx_gemm_noalloc", "smx_tile_requirements", "smx_packed_bytes", "smx_pack_operand",
+           "smx_norm_residual_add", "smx_qk_norm_rope", "smx_last_error", "smx_version")
 
 
 class SmxGemmDesc(ctypes.Structure):
@@ -105,6 +107,8 @@ def load():
     f32 = ctypes.c_float
     lib.smx_norm_residual_add.argtypes = [i64, i64, vp, i64, vp, i64, vp, i32, f32, vp, i64, vp]
     lib.smx_norm_residual_add.restype = ctypes.c_int
+    lib.smx_qk_norm_rope.argtypes = [i64, i64, vp, i64, vp, vp, vp, i32, i32, i32, f32, vp, i64, vp]
+    lib.smx_qk_norm_rope.restype = ctypes.c_int
     lib.smx_last_error.argtypes = []
     lib.smx_last_error.restype = ctypes.c_char_p
     lib.smx_version.argtypes = []

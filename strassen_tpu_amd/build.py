@@ -1,14 +1,17 @@
 """Build the gfx950 C-ABI library in-tree.
 
-``python -m strassen_tpu_amd.build`` (or ``build()``) compiles
-``csrc/strassen_gemm.hip`` with hipcc into ``libstrassen_mi355x.so`` next to
-this file. hipcc cross-compiles for gfx950 without a GPU.
+``python -m strassen_tpu_amd.build`` (or ``build()``) compiles the C ABI's
+translation unit (``csrc/strassen_gemm.hip``) and the four units that
+instantiate the GEMM kernels (``csrc/gemm_*.hip``) with hipcc, in parallel,
+checks each unit's device assembly, and links ``libstrassen_mi355x.so`` next
+to this file. hipcc cross-compiles for gfx950 without a GPU.
 """
 
 from __future__ import annotations
 
 import os
 import re
+from concurrent.futures import ThreadPoolExecutor
 import shutil
 import subprocess
 import sys
@@ -16,7 +19,8 @@ import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
-SOURCE = os.path.join(HERE, "csrc", "strassen_gemm.hip")
+SOURCES = tuple(os.path.join(HERE, "csrc", name) for name in (
+    "strassen_gemm.hip", "gemm_strassen.hip", "gemm_strassen_thin.hip", "gemm_cubic.hip", "gemm_cubic_thin.hip"))
 LIBRARY = os.path.join(HERE, "libstrassen_mi355x.so")
 INCLUDE = os.path.join(REPO, "include")
 
@@ -32,16 +36,21 @@ def hipcc_path():
     return found
 
 
-def compile_command(output=LIBRARY, extra=()):
+def compile_command(source, output, extra=()):
+    """hipcc command compiling one translation unit to an object file."""
     return [
-        hipcc_path(), "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+        hipcc_path(), "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-c",
         # Code object v5 is accepted by both the ROCm 7.0 runtime bundled with
         # torch and the system ROCm 7.2 runtime.
         "-mcode-object-version=5",
         # Packed FP32 VALU ops (v_pk_add_f32 and friends) stay disabled.
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        "-I", INCLUDE, *extra, SOURCE, "-o", output,
+        "-I", INCLUDE, *extra, source, "-o", output,
     ]
+
+
+def link_command(objects, output):
+    return [hipcc_path(), "--offload-arch=gfx950", "-fPIC", "-shared", *objects, "-o", output]
 
 
 # The pre-summed Strassen kernel issues its MFMAs through inline asm (to pin
@@ -108,16 +117,18 @@ def verify_inline_asm_kernels(asm_text):
 # Scratch (private segment) per GEMM kernel, in bytes per lane. The Strassen
 # kernels and the matched cubic keep their accumulators, fragments and
 # addresses in registers: a spill there is reloaded on every tile, so the
-# build refuses it. Two exceptions carry a stated cap: the q/k epilogue of the
-# Strassen kernel (116 bytes: its first exchange round holds the register
-# file's peak) and the cubic that adds an FP32 partial product before its
-# epilogue (the exact-panel path, off the hot path).
+# build refuses it. Three exceptions carry a stated cap: the q/k epilogue of
+# the Strassen kernel (116 bytes: its first exchange round holds the register
+# file's peak; 164 bytes in a thin tiling, whose per-row table addresses need
+# more registers, off the hot path) and the cubic that adds an FP32 partial
+# product before its epilogue (the exact-panel path, off the hot path).
 _KERNEL_DESC = re.compile(r"\.amdhsa_kernel (\S+)(.*?)\.end_amdhsa_kernel", re.S)
-_SPLIT = re.compile(r"gemm_splitILi(\d+)ELi(\d+)E")
-_PACKED = re.compile(r"gemm_packedILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)E")
+_SPLIT = re.compile(r"gemm_splitILi(\d+)ELi(\d+)ELb(\d)E")
+_PACKED = re.compile(r"gemm_packedILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb(\d)E")
 _EPI_QK = 4
 _QUAD_CUBIC_PARTIAL = 1
 QK_SCRATCH_CAP = 128
+THIN_QK_SCRATCH_CAP = 192
 PARTIAL_SCRATCH_CAP = 1024
 
 
@@ -125,16 +136,18 @@ def scratch_limit(name):
     """Allowed scratch bytes per lane of a kernel (None: not a GEMM kernel)."""
     m = _SPLIT.search(name)
     if m:
-        return QK_SCRATCH_CAP if int(m.group(1)) == _EPI_QK else 0
+        if int(m.group(1)) != _EPI_QK:
+            return 0
+        return THIN_QK_SCRATCH_CAP if m.group(3) == "1" else QK_SCRATCH_CAP
     m = _PACKED.search(name)
     if m:
         return PARTIAL_SCRATCH_CAP if int(m.group(3)) == _QUAD_CUBIC_PARTIAL else 0
     return None
 
 
-def verify_kernel_scratch(asm_text):
+def verify_kernel_scratch(asm_text, require=True):
     """Raise if a GEMM kernel's private segment exceeds its limit; returns the
-    number of GEMM kernels checked."""
+    number of GEMM kernels checked (with require, at least one)."""
     checked = 0
     for m in _KERNEL_DESC.finditer(asm_text):
         limit = scratch_limit(m.group(1))
@@ -146,30 +159,52 @@ def verify_kernel_scratch(asm_text):
             raise RuntimeError(f"{m.group(1)}: {scratch} bytes of scratch per lane (limit {limit}): "
                                "registers spill; refusing to build")
         checked += 1
-    if not checked:
+    if require and not checked:
         raise RuntimeError("no GEMM kernel descriptors found in the device assembly")
     return checked
 
 
-def build(verbose=False):
+def _compile_unit(source, workdir):
+    """Compiles one unit in its own directory (-save-temps keeps its device
+    assembly); returns (object path, assembly text, compiler messages)."""
+    os.makedirs(workdir)
+    obj = os.path.join(workdir, os.path.basename(source).replace(".hip", ".o"))
+    cmd = compile_command(source, obj, extra=("-save-temps",))
+    result = subprocess.run(cmd, capture_output=True, text=True, cwd=workdir)
+    noise = "packed-fp32-ops"
+    stderr = "\n".join(l for l in result.stderr.splitlines() if noise not in l)
+    if result.returncode != 0:
+        raise RuntimeError("hipcc failed:\n" + " ".join(cmd) + "\n" + stderr)
+    asm = [f for f in os.listdir(workdir) if f.endswith("gfx950.s")]
+    if len(asm) != 1:
+        raise RuntimeError(f"expected one gfx950 assembly file from -save-temps of {source}, found {asm}")
+    with open(os.path.join(workdir, asm[0])) as f:
+        return obj, f.read(), stderr
+
+
+def build(verbose=False, jobs=None):
     """Compile the library; returns its path. Always recompiles."""
     tmp = LIBRARY + ".tmp"
+    jobs = jobs or min(len(SOURCES), os.cpu_count() or 1)
     with tempfile.TemporaryDirectory() as scratch:
-        # --save-temps keeps the device assembly for the inline-asm check.
-        cmd = compile_command(tmp, extra=("-save-temps",))
+        dirs = [os.path.join(scratch, f"unit{i}") for i in range(len(SOURCES))]
+        with ThreadPoolExecutor(max_workers=jobs) as pool:
+            units = list(pool.map(_compile_unit, SOURCES, dirs))
+        checked = gemms = 0
+        for source, (_, text, stderr) in zip(SOURCES, units):
+            if verbose and stderr.strip():
+                print(stderr, file=sys.stderr)
+            # The C ABI's unit holds the compact kernels and the packers; the
+            # inline-asm MFMA kernels and the GEMM scratch limits live in the
+            # kernel units, each of which must hold some.
+            kernel_unit = os.path.basename(source) != "strassen_gemm.hip"
+            if kernel_unit:
+                checked += verify_inline_asm_kernels(text)
+            gemms += verify_kernel_scratch(text, require=kernel_unit)
+        cmd = link_command([obj for obj, _, _ in units], tmp)
         result = subprocess.run(cmd, capture_output=True, text=True, cwd=scratch)
-        noise = "packed-fp32-ops"
-        stderr = "\n".join(l for l in result.stderr.splitlines() if noise not in l)
         if result.returncode != 0:
-            raise RuntimeError("hipcc failed:\n" + " ".join(cmd) + "\n" + stderr)
-        if verbose and stderr.strip():
-            print(stderr, file=sys.stderr)
-        asm = [f for f in os.listdir(scratch) if f.endswith("gfx950.s")]
-        if len(asm) != 1:
-            raise RuntimeError(f"expected one gfx950 assembly file from -save-temps, found {asm}")
-        text = open(os.path.join(scratch, asm[0])).read()
-        checked = verify_inline_asm_kernels(text)
-        gemms = verify_kernel_scratch(text)
+            raise RuntimeError("link failed:\n" + " ".join(cmd) + "\n" + result.stderr)
     if verbose:
         print(f"verified {checked} inline-asm MFMA kernels and the scratch of {gemms} GEMM kernels", file=sys.stderr)
     os.replace(tmp, LIBRARY)

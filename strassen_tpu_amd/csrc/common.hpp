@@ -318,7 +318,7 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int g
 
 // Physical origin of a product-space workgroup tile (prow0, pcol0).
 struct TileOrigin {
-  int64_t ti, tr;  // row tile index and row inside the half
+  int64_t ti, tr;  // row tile index and row inside the half (thin tilings: 0 and the product row)
   int64_t tj, tc;  // column tile index and column inside the half
 };
 
@@ -326,17 +326,42 @@ struct TileOrigin {
 // 32 bits (the host refuses M/2 or N/2 >= 2^31), so the divisions run on
 // 32-bit values, and readfirstlane moves the results to SGPRs: VGPR copies
 // would stay live across the main loop next to the accumulators and spill.
+// kThin: bm/2 is not a multiple of the product tile's rows, so the tile's
+// rows belong to several row tiles; the origin keeps the product row and the
+// epilogue maps every row on its own (ThinRows).
+template <bool kThin = false>
 __device__ __forceinline__ TileOrigin tile_origin(const Params& p, int64_t prow0, int64_t pcol0) {
   const uint32_t hm = (uint32_t)(p.bm / 2), hn = (uint32_t)(p.bn / 2);
   const uint32_t r = (uint32_t)prow0, c = (uint32_t)pcol0;
   auto uniform = [](uint32_t v) { return (int64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)v); };
   TileOrigin o;
-  o.ti = uniform(r / hm);
-  o.tr = uniform(r % hm);
+  if constexpr (kThin) {
+    o.ti = 0;
+    o.tr = uniform(r);
+  } else {
+    o.ti = uniform(r / hm);
+    o.tr = uniform(r % hm);
+  }
   o.tj = uniform(c / hn);
   o.tc = uniform(c % hn);
   return o;
 }
+
+// Output rows of a thin tiling. Product row P (of M/2) is row P % hm of row
+// tile P / hm, whose two row halves are output rows (P / hm) * bm + P % hm
+// and that plus hm (strassen_pallas.py:188-204 splits every bm-row tile into
+// those halves). The packed A holds its rows in product order, zero-padded
+// to whole 128-row product tiles, so the main loop is that of any tiling;
+// only the epilogue's row addresses change, and padding rows (P >= M/2) are
+// neither read nor written.
+struct ThinRows {
+  uint32_t hm, bm, prows;
+  __device__ __forceinline__ int64_t row(uint32_t prow, int half) const {
+    const uint32_t t = prow / hm;
+    return (int64_t)t * bm + (int64_t)half * hm + (prow - t * hm);
+  }
+  __device__ __forceinline__ bool valid(uint32_t prow) const { return prow < prows; }
+};
 
 // ---------------------------------------------------------------------------
 // Epilogue
@@ -458,6 +483,60 @@ __device__ __forceinline__ void tile_store(const uint8_t* tile, char* dst, int64
   }
 }
 
+// tile_load / tile_store over rows at arbitrary addresses: row_at(row) gives
+// the row's first element (already offset to the tile's first column), or
+// null for a row that is skipped (its staging row is left as it is).
+template <class T, class RowAt>
+__device__ __forceinline__ void tile_load_rows(uint8_t* tile, RowAt row_at, int f32, int lane) {
+  if (f32) {
+    constexpr int kChunks = T::kCols / 4;
+#pragma unroll
+    for (int t = 0; t < T::kRows * kChunks / 64; ++t) {
+      const int idx = lane + 64 * t, row = idx / kChunks, ch = idx % kChunks;
+      const char* const src = row_at(row);
+      if (src) *reinterpret_cast<f32x4*>(tile + row * T::kStride + ch * 16) =
+          *reinterpret_cast<const f32x4*>(src + ch * 16);
+    }
+  } else {
+    constexpr int kChunks = T::kCols / 8;
+#pragma unroll
+    for (int t = 0; t < T::kRows * kChunks / 64; ++t) {
+      const int idx = lane + 64 * t, row = idx / kChunks, ch = idx % kChunks;
+      const char* const src = row_at(row);
+      if (!src) continue;
+      const F8 f = unpack8(*reinterpret_cast<const u32x4*>(src + ch * 16));
+      const f32x4 v0 = {f.v[0], f.v[1], f.v[2], f.v[3]}, v1 = {f.v[4], f.v[5], f.v[6], f.v[7]};
+      *reinterpret_cast<f32x4*>(tile + row * T::kStride + ch * 32) = v0;
+      *reinterpret_cast<f32x4*>(tile + row * T::kStride + ch * 32 + 16) = v1;
+    }
+  }
+}
+
+template <class T, class RowAt>
+__device__ __forceinline__ void tile_store_rows(const uint8_t* tile, RowAt row_at, int f32, int lane) {
+  constexpr int kChunks = T::kCols / 8;
+#pragma unroll
+  for (int t = 0; t < T::kRows * kChunks / 64; ++t) {
+    const int idx = lane + 64 * t, row = idx / kChunks, ch = idx % kChunks;
+    char* const dst = row_at(row);
+    if (!dst) continue;
+    const f32x4 v0 = *reinterpret_cast<const f32x4*>(tile + row * T::kStride + ch * 32);
+    const f32x4 v1 = *reinterpret_cast<const f32x4*>(tile + row * T::kStride + ch * 32 + 16);
+    if (f32) {
+      *reinterpret_cast<f32x4*>(dst + ch * 32) = v0;
+      *reinterpret_cast<f32x4*>(dst + ch * 32 + 16) = v1;
+    } else {
+      F8 f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f.v[e] = v0[e];
+        f.v[4 + e] = v1[e];
+      }
+      *reinterpret_cast<u32x4*>(dst + ch * 16) = pack8(f);
+    }
+  }
+}
+
 // Quadrant sources of the epilogue: the cubic's quadrants (plus an FP32
 // partial product), or Strassen's seven product sets under the classical,
 // dual or powers formula. The block permutation is applied by addressing:
@@ -521,7 +600,10 @@ __device__ __forceinline__ float quadrant_value(const f32x16 (&acc)[kNacc][kMB][
 // residual block is loaded into it, each element's result replaces the
 // element in place, and the block is stored. Registers meet LDS at
 // compile-time offsets; global memory sees whole 16-byte row chunks.
-template <int kMB, int kNB, int kEpi, int kNacc, int kQuad>
+//
+// kThin: the rows of a thin tiling go through ThinRows one by one (o.tr is
+// then the tile's first product row).
+template <int kMB, int kNB, int kEpi, int kNacc, int kQuad, bool kThin = false>
 __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin& o, int row0, int col0,
                                               f32x16 (&acc)[kNacc][kMB][kNB], uint8_t* tile) {
   using T = StageTile<32 * kMB, 32 * kNB>;
@@ -538,6 +620,8 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
   const int64_t row_base = o.ti * p.bm + o.tr + row0;
   const int64_t cc_base = o.tc + col0;
   const int64_t col_base = o.tj * p.bn + cc_base;
+  // thin tilings: row_base is the wave's first product row
+  const ThinRows thin{(uint32_t)hm, (uint32_t)p.bm, (uint32_t)(p.m / 2)};
   uint8_t* const te = tile + T::lane_part(lane);
   // LDS operations of one wave complete in order; this keeps the compiler
   // from moving one lane's tile access across another lane's.
@@ -552,15 +636,33 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
     return quadrant_value<kQuad, decltype(q)::value>(acc, i, j, r);
   };
   // Physical quadrant (row half pr, column half pc) of an [M, N] operand
-  // (row stride ld, element size es), for this wave.
-  auto quadrant = [&](const void* base, int64_t ld, int es, int pr, int pc) __attribute__((always_inline)) {
-    return reinterpret_cast<const char*>(base) + ((row_base + pr * hm) * ld + col_base + pc * hn) * es;
+  // (row stride ld, element size es, float when f32) -> the staging tile.
+  auto load_quadrant = [&](const void* base, int64_t ld, int es, int f32, int pr, int pc)
+                           __attribute__((always_inline)) {
+    const char* const cols = reinterpret_cast<const char*>(base) + (col_base + pc * hn) * es;
+    if constexpr (kThin) {
+      tile_load_rows<T>(tile, [&](int row) __attribute__((always_inline)) -> const char* {
+        const uint32_t prow = (uint32_t)(row_base + row);
+        return thin.valid(prow) ? cols + thin.row(prow, pr) * ld * es : nullptr;
+      }, f32, lane);
+    } else {
+      tile_load<T>(tile, cols + (row_base + pr * hm) * ld * es, ld, f32, lane);
+    }
   };
-  // The staging tile `t` -> the output block at (row, col).
-  auto emit_from = [&](uint8_t* t, int64_t row, int64_t col) __attribute__((always_inline)) {
+  // The staging tile `t` -> the output block in row half `half` at column col.
+  auto emit_from = [&](uint8_t* t, int half, int64_t col) __attribute__((always_inline)) {
     fence();
-    tile_store<T>(t, reinterpret_cast<char*>(p.c) + (row * p.ldc + col) * (p.out_f32 ? 4 : 2), p.ldc, p.out_f32,
-                  lane);
+    const int es = p.out_f32 ? 4 : 2;
+    if constexpr (kThin) {
+      char* const cols = reinterpret_cast<char*>(p.c) + col * es;
+      tile_store_rows<T>(t, [&](int row) __attribute__((always_inline)) -> char* {
+        const uint32_t prow = (uint32_t)(row_base + row);
+        return thin.valid(prow) ? cols + thin.row(prow, half) * p.ldc * es : nullptr;
+      }, p.out_f32, lane);
+    } else {
+      tile_store<T>(t, reinterpret_cast<char*>(p.c) + ((row_base + half * hm) * p.ldc + col) * es, p.ldc,
+                    p.out_f32, lane);
+    }
     fence();
   };
 
@@ -569,7 +671,7 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
   if constexpr (kQuad == kQuadCubicPartial) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      tile_load<T>(tile, quadrant(p.partial, p.ldp, 4, q >> 1, q & 1), p.ldp, 1, lane);
+      load_quadrant(p.partial, p.ldp, 4, 1, q >> 1, q & 1);
       fence();
 #pragma unroll
       for (int i = 0; i < kMB; ++i)
@@ -597,7 +699,7 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
             const float gate = swap_n ? right : left, up = swap_n ? left : right;
             put(i, j, r, gate_f32<kEpi>(gate) * up);
           }
-      emit_from(tile, row_base + (lr ^ swap_m) * hm, ocol);
+      emit_from(tile, lr ^ swap_m, ocol);
     };
     gated(QuadC<0>{}, QuadC<1>{}, 0);
     gated(QuadC<2>{}, QuadC<3>{}, 1);
@@ -631,6 +733,13 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
     const uint16_t* const cos_w = p.rope_cos + row_base * hn + cc_base;
     const uint16_t* const sin_w = p.rope_sin + row_base * hn + cc_base;
     const int hm_t = hm * hn;
+    // thin tilings: element offset of the table row of product row prow in
+    // row half `half`, in 32 bits (the host keeps M * bn/2 below 2^31);
+    // padding rows read the last real row and are not stored
+    auto table_row = [&](uint32_t prow, int half) __attribute__((always_inline)) {
+      const uint32_t pr = min(prow, thin.prows - 1), t = pr / thin.hm;
+      return (t * thin.bm + (uint32_t)half * thin.hm + (pr - t * thin.hm)) * (uint32_t)hn + (uint32_t)cc_base;
+    };
     // The a and b outputs of an element go to two blocks: the second staging
     // tile (this epilogue has two per wave) takes the b block.
     uint8_t* const tile_b = tile + T::kBytes;
@@ -664,9 +773,16 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
               const int cj = j * 32 + lcol;
               const float ga = load_vec(p.rope_scale, p.scale_f32, cc_base + cj);
               const float gb = load_vec(p.rope_scale, p.scale_f32, hn + cc_base + cj);
-              const int toff = ri * hn + cj + half * hm_t;
-              const float cs = bf16_to_f32(cos_w[toff]);
-              const float sn = bf16_to_f32(sin_w[toff]);
+              float cs, sn;
+              if constexpr (kThin) {
+                const uint32_t toff = table_row((uint32_t)(row_base + ri), half) + (uint32_t)cj;
+                cs = bf16_to_f32(p.rope_cos[toff]);
+                sn = bf16_to_f32(p.rope_sin[toff]);
+              } else {
+                const int toff = ri * hn + cj + half * hm_t;
+                cs = bf16_to_f32(cos_w[toff]);
+                sn = bf16_to_f32(sin_w[toff]);
+              }
               const float na = qa(i, j, r) * recip * ga;
               const float nbv = qb(i, j, r) * recip * gb;
               put(i, j, r, na * cs - nbv * sn);
@@ -677,8 +793,8 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-      emit_from(tile, row_base + half * hm, col_base);
-      emit_from(tile_b, row_base + half * hm, col_base + hn);
+      emit_from(tile, half, col_base);
+      emit_from(tile_b, half, col_base + hn);
     };
     rows(QuadC<0>{}, QuadC<1>{}, 0);
     rows(QuadC<2>{}, QuadC<3>{}, 1);
@@ -690,7 +806,7 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
       constexpr int kQ = decltype(q)::value;
       const int pr = (kQ >> 1) ^ swap_m, pc = (kQ & 1) ^ swap_n;
       if constexpr (kEpi == SMX_EPI_RESIDUAL_ADD) {
-        tile_load<T>(tile, quadrant(p.residual, p.ldr, p.residual_f32 ? 4 : 2, pr, pc), p.ldr, p.residual_f32, lane);
+        load_quadrant(p.residual, p.ldr, p.residual_f32 ? 4 : 2, p.residual_f32, pr, pc);
         fence();
       }
 #pragma unroll
@@ -707,7 +823,7 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
             put(i, j, r, v);
           }
       }
-      emit_from(tile, row_base + pr * hm, col_base + pc * hn);
+      emit_from(tile, pr, col_base + pc * hn);
     };
     block(QuadC<0>{});
     block(QuadC<1>{});
@@ -721,11 +837,11 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
 // accumulators to be split across two arms, which spills. The workgroup
 // barrier first makes the LDS free for the staging tiles: every wave has
 // finished its main-loop reads and the last DMA has landed.
-template <int kQuad, int kMB, int kNB, int kEpi, int kNacc>
+template <int kQuad, int kMB, int kNB, int kEpi, int kNacc, bool kThin = false>
 __device__ __forceinline__ void epilogue(const Params& p, const TileOrigin& o, int row0, int col0,
                                          f32x16 (&acc)[kNacc][kMB][kNB], uint8_t* tile) {
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  epilogue_body<kMB, kNB, kEpi, kNacc, kQuad>(p, o, row0, col0, acc, tile);
+  epilogue_body<kMB, kNB, kEpi, kNacc, kQuad, kThin>(p, o, row0, col0, acc, tile);
 }
 
 template <int kNacc, int kMB, int kNB>

@@ -1,0 +1,5 @@
+// The matched cubic kernels, thin tilings (bm/2 not a multiple of 128):
+// instantiated, registered and launched here (launch.hpp).
+#include "gemm_launch.hpp"
+
+template int smx::launch_cubic<true>(const smx::Params&, int, hipStream_t);

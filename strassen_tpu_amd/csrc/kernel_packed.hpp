@@ -35,6 +35,10 @@ constexpr int kPackStages = 4;  // stages one pack wave handles (128 B per sourc
 
 __host__ __device__ constexpr int nops_of(int algo) { return algo == 7 ? 7 : 4; }
 
+// Product rows of a packed [rows, k] operand: rows/2 rounded up to whole
+// 128-row tiles (a thin tiling's last tile is zero-padded).
+__host__ __device__ constexpr int64_t padded_product_rows(int64_t rows) { return (rows / 2 + TM - 1) / TM * TM; }
+
 // Byte offset of fragment (tile, stage, op, block) in a packed operand.
 __host__ __device__ inline int64_t frag_offset(int64_t tile, int64_t stage, int64_t nstages, int op, int nops,
                                                int block) {
@@ -136,7 +140,8 @@ __device__ __forceinline__ bf16x8 ld_frag(const uint8_t* p) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(p));
 }
 
-template <int kAlgo, int kEpi, int kQuad, int kCubicSlots = 3>
+// kThin: a tiling whose bm/2 is not a multiple of 128 (ThinRows).
+template <int kAlgo, int kEpi, int kQuad, int kCubicSlots = 3, bool kThin = false>
 __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
   static_assert(kAlgo == 8, "the packed kernel serves the cubic; Strassen runs on gemm_split");
   using L = Lay<kAlgo, kCubicSlots>;
@@ -148,7 +153,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
 
   int tile_m, tile_n;
   tile_of(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tile_m, tile_n);
-  const TileOrigin o = tile_origin(p, (int64_t)tile_m * TM, (int64_t)tile_n * TN);
+  const TileOrigin o = tile_origin<kThin>(p, (int64_t)tile_m * TM, (int64_t)tile_n * TN);
   const int nstages = (int)(p.k / (2 * TK));
 
   // DMA sources: this workgroup's packed stages are contiguous runs of
@@ -300,7 +305,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
     } while (s < nstages);
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     mfma_drain(acc);
-    epilogue<kQuad, 2, 2, kEpi>(p, o, wm * 64, wn * 64, acc, lds + wave * kEpiTiles<kEpi> * StageTile<64, 64>::kBytes);
+    epilogue<kQuad, 2, 2, kEpi, L::nops, kThin>(p, o, wm * 64, wn * 64, acc,
+                                                lds + wave * kEpiTiles<kEpi> * StageTile<64, 64>::kBytes);
     return;
   }
 
@@ -365,11 +371,14 @@ __global__ __launch_bounds__(256) void pack_operand(const void* __restrict__ src
   const int64_t nstages = k / (2 * TK);
   const int64_t sgroups = (nstages + kPackStages - 1) / kPackStages;
   const int64_t rblock = gwave / sgroups;  // 32-row product block
-  if (rblock >= rows / 64) return;
+  if (rblock >= padded_product_rows(rows) / 32) return;
   const int64_t sg = gwave - rblock * sgroups;
   const int hr = tile_rows / 2, hk = bk / 2;
   const int64_t r = rblock * 32 + (lane & 31);
-  const int64_t row_first = (r / hr) * tile_rows + r % hr, row_second = row_first + hr;
+  // Product rows past rows/2 pad the last 128-row tile: they pack as zeros
+  // (their source rows are clamped to row 0 and the values replaced).
+  const bool pad = r >= rows / 2;
+  const int64_t row_first = pad ? 0 : (r / hr) * tile_rows + r % hr, row_second = row_first + hr;
   const Elem* const first = src + row_first * ld;
   const Elem* const second = first + (int64_t)hr * ld;
   // Eight consecutive elements (columns col0 .. col0+7) of a row-major row.
@@ -420,7 +429,12 @@ __global__ __launch_bounds__(256) void pack_operand(const void* __restrict__ src
     const int64_t src_panel = panels ? min(max(panels[slot], 0), src_panels - 1) : slot;
     const int64_t lo = src_panel * bk + kp % hk, hi = lo + hk;
     F8 x[4];
-    if constexpr (kSide == 2) {
+    if (pad) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[q].v[e] = 0.0f;
+    } else if constexpr (kSide == 2) {
       x[0] = gather(row_first, lo);
       x[1] = gather(row_first, hi);
       x[2] = gather(row_second, lo);
@@ -465,7 +479,7 @@ __global__ __launch_bounds__(256) void pack_rows(const uint16_t* __restrict__ sr
   const int64_t nstages = k / (2 * TK);
   const int64_t sgroups = (nstages + kRowStages - 1) / kRowStages;
   const int64_t rblock = blockIdx.x / sgroups;  // 32-row product block
-  if (rblock >= rows / 64) return;  // uniform per workgroup
+  if (rblock >= padded_product_rows(rows) / 32) return;  // uniform per workgroup
   const int64_t st0 = (blockIdx.x - rblock * sgroups) * kRowStages;
   const int hr = tile_rows / 2, hk = bk / 2;
   // Copy: 32 rows x 4 segments x kRowStages stages x two 16-byte pieces.
@@ -479,6 +493,11 @@ __global__ __launch_bounds__(256) void pack_rows(const uint16_t* __restrict__ sr
     const int64_t st = st0 + j;
     if (st < nstages) {
       const int64_t r = rblock * 32 + row;
+      uint8_t* const to = tile + row * kRowStride + seg * kRowRun + j * 32 + sub * 16;
+      if (r >= rows / 2) {  // padding of the last 128-row product tile: zeros
+        *reinterpret_cast<u32x4*>(to) = u32x4{0u, 0u, 0u, 0u};
+        continue;
+      }
       const int64_t srow = (r / hr) * tile_rows + r % hr + ((seg & 2) ? hr : 0);
       // A stage's 16 k never cross a panel half (hk is a multiple of 32).
       const int64_t kp = st * TK;
@@ -486,8 +505,7 @@ __global__ __launch_bounds__(256) void pack_rows(const uint16_t* __restrict__ sr
       // Map entries are clamped to the source, so a bad map cannot read out of bounds.
       const int64_t src_panel = panels ? min(max(panels[panel], 0), src_panels - 1) : panel;
       const int64_t col = src_panel * bk + kp % hk + ((seg & 1) ? hk : 0) + sub * 8;
-      *reinterpret_cast<u32x4*>(tile + row * kRowStride + seg * kRowRun + j * 32 + sub * 16) =
-          *reinterpret_cast<const u32x4*>(src + srow * ld + col);
+      *reinterpret_cast<u32x4*>(to) = *reinterpret_cast<const u32x4*>(src + srow * ld + col);
     }
   }
   __syncthreads();

@@ -91,7 +91,7 @@ struct Ring {
 };
 
 // One wave's main loop, accumulator exchange and epilogue.
-template <int kWave, int kEpi, int kQuad>
+template <int kWave, int kEpi, int kQuad, bool kThin>
 __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, int nstages,
                                          __amdgpu_buffer_rsrc_t a_src, __amdgpu_buffer_rsrc_t b_src, uint8_t* lds) {
   using L = packed::Lay<7>;
@@ -286,9 +286,10 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
         quads[3][0][jj][r] = quadrant_value<kQuad, 3>(blk, 0, 0, r);
       }
       // the quadrant sets go through the epilogue as the cubic's would
-      if constexpr (jj == 1) epilogue_body<1, 2, kEpi, 4, kQuadCubic>(p, o, wm * 64 + i * 32, wn * 64, quads, mine);
+      if constexpr (jj == 1)
+        epilogue_body<1, 2, kEpi, 4, kQuadCubic, kThin>(p, o, wm * 64 + i * 32, wn * 64, quads, mine);
     } else {
-      epilogue_body<1, 1, kEpi, 7, kQuad>(p, o, wm * 64 + i * 32, wn * 64 + jj * 32, blk, mine);
+      epilogue_body<1, 1, kEpi, 7, kQuad, kThin>(p, o, wm * 64 + i * 32, wn * 64 + jj * 32, blk, mine);
     }
     // every staging access has completed before the next round's blocks
     // land in these slots
@@ -300,7 +301,8 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
   round(QuadC<3>{});
 }
 
-template <int kEpi, int kQuad>
+// kThin: a tiling whose bm/2 is not a multiple of 128 (ThinRows).
+template <int kEpi, int kQuad, bool kThin = false>
 __global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
   using L = packed::Lay<7>;
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
@@ -313,7 +315,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
   // derived from them) to SGPRs, which keeps VGPRs for the accumulators.
   tile_m = __builtin_amdgcn_readfirstlane(tile_m);
   tile_n = __builtin_amdgcn_readfirstlane(tile_n);
-  const TileOrigin o = tile_origin(p, (int64_t)tile_m * packed::TM, (int64_t)tile_n * packed::TN);
+  const TileOrigin o = tile_origin<kThin>(p, (int64_t)tile_m * packed::TM, (int64_t)tile_n * packed::TN);
   const int nstages = (int)(p.k / (2 * TK));
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t panel_bytes = (uint32_t)nstages * L::kStage - wave * kFrag;
@@ -345,16 +347,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
   // accumulator is live across the branches.
   switch (wave) {
     case 0:
-      run_wave<0, kEpi, kQuad>(p, o, nstages, a_src, b_src, lds);
+      run_wave<0, kEpi, kQuad, kThin>(p, o, nstages, a_src, b_src, lds);
       break;
     case 1:
-      run_wave<1, kEpi, kQuad>(p, o, nstages, a_src, b_src, lds);
+      run_wave<1, kEpi, kQuad, kThin>(p, o, nstages, a_src, b_src, lds);
       break;
     case 2:
-      run_wave<2, kEpi, kQuad>(p, o, nstages, a_src, b_src, lds);
+      run_wave<2, kEpi, kQuad, kThin>(p, o, nstages, a_src, b_src, lds);
       break;
     default:
-      run_wave<3, kEpi, kQuad>(p, o, nstages, a_src, b_src, lds);
+      run_wave<3, kEpi, kQuad, kThin>(p, o, nstages, a_src, b_src, lds);
       break;
   }
 }

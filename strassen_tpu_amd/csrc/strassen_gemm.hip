@@ -34,6 +34,11 @@
 //   v1 (kernel_v1.hpp): 128x64 tiles, row-major A and B^T, both operand sums
 //      formed in registers; serves unpacked calls whose tile the packed
 //      kernels cannot take, or all of them under SMX_PLAIN_WEIGHTS=compact.
+// The split and packed kernels are instantiated in translation units of
+// their own (gemm_strassen*.hip, gemm_cubic*.hip) and reached through the
+// launchers of launch.hpp; a thin tiling (bm/2 not a multiple of the 128-row
+// product tile, bm % 16 == 0 as the reference allows) runs their kThin
+// instantiations, whose epilogues map rows one by one (ThinRows).
 
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
@@ -45,16 +50,15 @@
 #include <mutex>
 
 #include "common.hpp"
-#include "kernel_v1.hpp"
 #include "kernel_packed.hpp"
-#include "kernel_split.hpp"
+#include "kernel_v1.hpp"
+#include "launch.hpp"
 
 namespace smx {
 namespace {
-
 thread_local char g_error[512] = "";
+}  // namespace
 
-int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -62,6 +66,8 @@ int fail(int code, const char* fmt, ...) {
   va_end(ap);
   return code;
 }
+
+namespace {
 
 template <class K>
 int set_lds(K kern, int bytes) {
@@ -81,12 +87,6 @@ int group_m_setting() {
   return value;
 }
 
-int check_launch() {
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(SMX_ERR_LAUNCH, "kernel launch: %s", hipGetErrorString(e));
-  return SMX_OK;
-}
-
 template <class C, int kEpi>
 int launch_v1(Params p, hipStream_t stream) {
   p.tiles_m = (int)((p.m / 2) / C::TM);
@@ -95,40 +95,6 @@ int launch_v1(Params p, hipStream_t stream) {
   auto kern = v1::gemm_v1<C, kEpi>;
   // operand slabs, then the epilogue's staging tiles, share the LDS
   constexpr int lds = C::kLds > kEpiLds<kEpi, 32 * C::mb, 32 * C::nb> ? C::kLds : kEpiLds<kEpi, 32 * C::mb, 32 * C::nb>;
-  if (int rc = set_lds(kern, lds)) return rc;
-  hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n), dim3(kThreads), lds, stream, p);
-  return check_launch();
-}
-
-template <int kAlgo, int kEpi>
-int launch_packed(Params p, hipStream_t stream) {
-  p.tiles_m = (int)((p.m / 2) / packed::TM);
-  p.tiles_n = (int)((p.n / 2) / packed::TN);
-  p.group_m = group_m_setting();
-  // The epilogue's quadrant source (the Strassen formula, or the cubic with
-  // or without a partial product) is a kernel template argument, so every
-  // epilogue is straight-line code; the block permutation is applied by
-  // addressing at run time.
-  void (*kern)(Params);
-  // the stage ring, then the epilogue's staging tiles, share the LDS; the
-  // product-split kernel's ring fills all of it
-  constexpr int epi_lds = kEpiLds<kEpi, 64, 64>;
-  int lds = packed::Lay<8>::kLds > epi_lds ? packed::Lay<8>::kLds : epi_lds;
-  if constexpr (kAlgo == 7) {
-    lds = split::Ring::kBytes > epi_lds ? split::Ring::kBytes : epi_lds;
-    if (p.formula == SMX_FORMULA_DUAL) {
-      kern = split::gemm_split<kEpi, kQuadDual>;
-    } else if (p.formula == SMX_FORMULA_POWERS) {
-      if constexpr (kEpi == SMX_EPI_NONE)
-        kern = split::gemm_split<SMX_EPI_NONE, kQuadPowers>;
-      else
-        return fail(SMX_ERR_INVALID, "fused epilogues require a quadrant-basis formula");
-    } else {
-      kern = split::gemm_split<kEpi, kQuadClassical>;
-    }
-  } else {
-    kern = p.partial ? packed::gemm_packed<8, kEpi, kQuadCubicPartial> : packed::gemm_packed<8, kEpi, kQuadCubic>;
-  }
   if (int rc = set_lds(kern, lds)) return rc;
   hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n), dim3(kThreads), lds, stream, p);
   return check_launch();
@@ -147,22 +113,14 @@ int dispatch_v1(const Params& p, int epilogue, hipStream_t s) {
   return fail(SMX_ERR_INVALID, "unknown epilogue %d", epilogue);
 }
 
-template <int kAlgo>
-int dispatch_packed(const Params& p, int epilogue, hipStream_t s) {
-  switch (epilogue) {
-    case SMX_EPI_NONE: return launch_packed<kAlgo, SMX_EPI_NONE>(p, s);
-    case SMX_EPI_SWIGLU: return launch_packed<kAlgo, SMX_EPI_SWIGLU>(p, s);
-    case SMX_EPI_GEGLU: return launch_packed<kAlgo, SMX_EPI_GEGLU>(p, s);
-    case SMX_EPI_RESIDUAL_ADD: return launch_packed<kAlgo, SMX_EPI_RESIDUAL_ADD>(p, s);
-    case SMX_EPI_BIAS_ADD: return launch_packed<kAlgo, SMX_EPI_BIAS_ADD>(p, s);
-    case SMX_EPI_QK_NORM_ROPE: return launch_packed<kAlgo, SMX_EPI_QK_NORM_ROPE>(p, s);
-  }
-  return fail(SMX_ERR_INVALID, "unknown epilogue %d", epilogue);
-}
+// Tile granules of a path: bm % (2 tm), bn % (2 tn), bk % (2 tk). Packed
+// operands take any bm the reference allows (bm % 16; thin tilings map rows
+// in the epilogue); the v1 kernels need whole 128-row product tiles.
+constexpr int32_t kThinRowGranule = 8;
 
 void tile_of_path(bool packed_path, int32_t* tm, int32_t* tn, int32_t* tk) {
   if (packed_path) {
-    *tm = packed::TM;
+    *tm = kThinRowGranule;
     *tn = packed::TN;
     *tk = packed::kKGranule;
   } else {  // both v1 configurations are 128 x 64 x 32
@@ -191,14 +149,16 @@ int launch_pack(const void* src, bool src_f32, int64_t ld, int64_t rows, int64_t
   const int64_t nstages = k / (2 * packed::TK);
   if constexpr (kSide != 2) {
     if (!src_f32) {  // bf16 row-major source: the LDS-staged kernel
-      const int64_t blocks = (rows / 64) * ((nstages + packed::kRowStages - 1) / packed::kRowStages);
+      const int64_t blocks =
+          (packed::padded_product_rows(rows) / 32) * ((nstages + packed::kRowStages - 1) / packed::kRowStages);
       if (blocks >= ((int64_t)1 << 31)) return fail(SMX_ERR_UNSUPPORTED, "operand too large to pack");
       hipLaunchKernelGGL((packed::pack_rows<kAlgo, kSide>), dim3((unsigned)blocks), dim3(256), 0, stream,
                          (const uint16_t*)src, ld, rows, k, tile_rows, bk, formula, perm, panels, src_panels, out);
       return check_launch();
     }
   }
-  const int64_t waves = (rows / 64) * ((nstages + packed::kPackStages - 1) / packed::kPackStages);
+  const int64_t waves =
+      (packed::padded_product_rows(rows) / 32) * ((nstages + packed::kPackStages - 1) / packed::kPackStages);
   const int64_t blocks = (waves + 3) / 4;
   if (blocks >= ((int64_t)1 << 31)) return fail(SMX_ERR_UNSUPPORTED, "operand too large to pack");
   if (src_f32)
@@ -297,6 +257,9 @@ int gemm_params(const smx_gemm_desc* d, const void* a, const void* b, void* c, c
   // with 32-bit element offsets.
   if ((int64_t)hm * d->bn >= ((int64_t)1 << 31))
     return fail(SMX_ERR_UNSUPPORTED, "bm/2 * bn must stay below 2^31 (bm=%d, bn=%d)", d->bm, d->bn);
+  // A thin tiling's q/k epilogue addresses the whole [M, bn/2] tables so.
+  if (packed_path && hm % packed::TM && d->epilogue == SMX_EPI_QK_NORM_ROPE && d->m * (d->bn / 2) >= ((int64_t)1 << 31))
+    return fail(SMX_ERR_UNSUPPORTED, "thin tilings (bm/2 %% 128 != 0) with qk_norm_rope need M * bn/2 below 2^31");
   p = Params{};
   p.a = (const uint16_t*)a;
   p.b = (const uint16_t*)b;
@@ -342,7 +305,10 @@ int gemm_params(const smx_gemm_desc* d, const void* a, const void* b, void* c, c
       if (!rope_cos || !rope_sin || !rope_scale)
         return fail(SMX_ERR_INVALID, "qk_norm_rope requires rope_cos, rope_sin and rope_scale");
       if (d->rope_head_dim != 128)
-        return fail(SMX_ERR_UNSUPPORTED, "qk_norm_rope on gfx950 supports head_dim 128, got %d", d->rope_head_dim);
+        return fail(SMX_ERR_UNSUPPORTED,
+                    "the fused qk_norm_rope takes head_dim 128, got %d: run smx_gemm with SMX_FLAG_OUT_F32 and no "
+                    "epilogue, then smx_qk_norm_rope",
+                    d->rope_head_dim);
       if (d->bn % (2 * d->rope_head_dim))
         return fail(SMX_ERR_INVALID, "qk_norm_rope needs bn a multiple of 2*head_dim");
       p.rope_cos = (const uint16_t*)rope_cos;
@@ -355,11 +321,16 @@ int gemm_params(const smx_gemm_desc* d, const void* a, const void* b, void* c, c
   return SMX_OK;
 }
 
-int launch_gemm(const Params& p, const smx_gemm_desc& d, hipStream_t s) {
-  const bool packed_path = d.b_layout == SMX_B_PACKED;
-  if (packed_path)
-    return d.algo == SMX_ALGO_STRASSEN ? dispatch_packed<7>(p, d.epilogue, s) : dispatch_packed<8>(p, d.epilogue, s);
-  return d.algo == SMX_ALGO_STRASSEN ? dispatch_v1<7>(p, d.epilogue, s) : dispatch_v1<8>(p, d.epilogue, s);
+int launch_gemm(Params p, const smx_gemm_desc& d, hipStream_t s) {
+  if (d.b_layout != SMX_B_PACKED)
+    return d.algo == SMX_ALGO_STRASSEN ? dispatch_v1<7>(p, d.epilogue, s) : dispatch_v1<8>(p, d.epilogue, s);
+  p.tiles_m = (int)(packed::padded_product_rows(p.m) / packed::TM);
+  p.tiles_n = (int)((p.n / 2) / packed::TN);
+  p.group_m = group_m_setting();
+  const bool thin = (p.bm / 2) % packed::TM != 0;
+  if (d.algo == SMX_ALGO_STRASSEN)
+    return thin ? launch_strassen<true>(p, d.epilogue, s) : launch_strassen<false>(p, d.epilogue, s);
+  return thin ? launch_cubic<true>(p, d.epilogue, s) : launch_cubic<false>(p, d.epilogue, s);
 }
 
 // Device scratch of smx_gemm_noalloc: the packed activation of one call,
@@ -395,6 +366,61 @@ int scratch_address(void** out) {
   return SMX_OK;
 }
 
+// qk_norm_rope's second pass (strassen_pallas.py:793-835) for head widths
+// the fused epilogue does not take: one workgroup per (output row, column
+// tile of bn). A tile half holds bn / head_dim heads of head_dim/2 columns;
+// head h pairs its columns c of the first half (a) with the same columns of
+// the second half (b). recip = 1 / sqrt((sum a^2 + sum b^2) / head_dim + eps)
+// over the head; na = a recip scale[c], nb = b recip scale[bn/2 + c];
+// out_a = na cos - nb sin, out_b = nb cos + na sin, with cos, sin [m, bn/2] at
+// (row, c). Squares go to LDS ([a^2 | b^2], bn floats), one thread per head
+// sums its segment (first half, then second, in column order), and the
+// reciprocals ([bn / head_dim]) follow them in LDS.
+__global__ __launch_bounds__(256) void qk_norm_rope_rows(const float* __restrict__ x, int64_t ldx,
+                                                         const uint16_t* __restrict__ cos_t,
+                                                         const uint16_t* __restrict__ sin_t,
+                                                         const void* __restrict__ scale, int32_t dtypes, int32_t bn,
+                                                         int32_t head_dim, float eps, void* __restrict__ out,
+                                                         int64_t ldo) {
+  extern __shared__ float sq[];
+  const int64_t row = blockIdx.x;
+  const int hn = bn / 2, seg = head_dim / 2, heads = hn / seg;
+  const float* const xa = x + row * ldx + (int64_t)blockIdx.y * bn;
+  const float* const xb = xa + hn;
+  for (int c = threadIdx.x; c < hn; c += blockDim.x) {
+    sq[c] = xa[c] * xa[c];
+    sq[hn + c] = xb[c] * xb[c];
+  }
+  __syncthreads();
+  float* const recip = sq + bn;
+  const float inv_width = 1.0f / (float)head_dim;
+  for (int h = threadIdx.x; h < heads; h += blockDim.x) {
+    float ssa = 0.f, ssb = 0.f;
+    for (int c = 0; c < seg; ++c) {
+      ssa += sq[h * seg + c];
+      ssb += sq[hn + h * seg + c];
+    }
+    recip[h] = 1.0f / sqrtf((ssa + ssb) * inv_width + eps);
+  }
+  __syncthreads();
+  const int scale_f32 = dtypes & SMX_QK_SCALE_F32;
+  const int64_t out0 = row * ldo + (int64_t)blockIdx.y * bn;
+  for (int c = threadIdx.x; c < hn; c += blockDim.x) {
+    const float r = recip[c / seg];
+    const float na = xa[c] * r * load_vec(scale, scale_f32, c);
+    const float nb = xb[c] * r * load_vec(scale, scale_f32, hn + c);
+    const float cs = bf16_to_f32(cos_t[row * hn + c]), sn = bf16_to_f32(sin_t[row * hn + c]);
+    const float oa = na * cs - nb * sn, ob = nb * cs + na * sn;
+    if (dtypes & SMX_QK_OUT_F32) {
+      reinterpret_cast<float*>(out)[out0 + c] = oa;
+      reinterpret_cast<float*>(out)[out0 + hn + c] = ob;
+    } else {
+      reinterpret_cast<uint16_t*>(out)[out0 + c] = f32_to_bf16(oa);
+      reinterpret_cast<uint16_t*>(out)[out0 + hn + c] = f32_to_bf16(ob);
+    }
+  }
+}
+
 }  // namespace
 }  // namespace smx
 
@@ -426,7 +452,7 @@ int smx_packed_bytes(int32_t algo, int64_t rows, int64_t k, int64_t* bytes) {
   if (algo != SMX_ALGO_STRASSEN && algo != SMX_ALGO_CUBIC) return fail(SMX_ERR_INVALID, "algo must be 7 or 8");
   if (rows <= 0 || k <= 0 || rows % 2 || k % 2) return fail(SMX_ERR_INVALID, "rows and k must be positive and even");
   if (!bytes) return fail(SMX_ERR_INVALID, "null output");
-  *bytes = (rows / 2) * (k / 2) * packed::nops_of(algo) * 2;
+  *bytes = packed::padded_product_rows(rows) * (k / 2) * packed::nops_of(algo) * 2;
   return SMX_OK;
 }
 
@@ -440,9 +466,11 @@ int smx_pack_operand(int32_t algo, int32_t formula, int32_t block_permutation, i
     return fail(SMX_ERR_INVALID, "side must be LHS (0), RHS (1) or LHS_T (2)");
   if (rows <= 0 || k <= 0 || tile_rows <= 0 || bk <= 0 || rows % tile_rows || k % bk)
     return fail(SMX_ERR_INVALID, "packing needs rows %% tile_rows == 0 and K %% bk == 0");
-  if (tile_rows % (2 * packed::TM) || bk % (2 * packed::kKGranule))
+  // A's tile rows may be thin (ThinRows); B's must fill whole product tiles.
+  const int32_t row_granule = side == SMX_SIDE_RHS ? 2 * packed::TN : 2 * kThinRowGranule;
+  if (tile_rows % row_granule || bk % (2 * packed::kKGranule))
     return fail(SMX_ERR_UNSUPPORTED, "packed tiles need %s %% %d == 0 and bk %% %d == 0 (got %d, %d)",
-                side == SMX_SIDE_LHS ? "bm" : "bn", 2 * packed::TM, 2 * packed::kKGranule, tile_rows, bk);
+                side == SMX_SIDE_RHS ? "bn" : "bm", row_granule, 2 * packed::kKGranule, tile_rows, bk);
   if (!src || !out) return fail(SMX_ERR_INVALID, "null pointer");
   if (!aligned16(src) || !aligned16(out)) return fail(SMX_ERR_INVALID, "pointers must be 16-byte aligned");
   if (src_dtype != SMX_DTYPE_BF16 && src_dtype != SMX_DTYPE_F32)
@@ -501,7 +529,7 @@ int smx_gemm_noalloc(const smx_gemm_desc* d, const void* a, const void* b, void*
     return rc;
   if (d->lda < d->k || d->lda % 8) return fail(SMX_ERR_INVALID, "lda must be >= K and a multiple of 8 elements");
   if (!aligned16(a)) return fail(SMX_ERR_INVALID, "A must be 16-byte aligned");
-  const int64_t bytes = (d->m / 2) * (d->k / 2) * packed::nops_of(d->algo) * 2;
+  const int64_t bytes = packed::padded_product_rows(d->m) * (d->k / 2) * packed::nops_of(d->algo) * 2;
   if (bytes > (int64_t)kNoAllocScratchBytes)
     return fail(SMX_ERR_UNSUPPORTED,
                 "smx_gemm_noalloc packs A into a %lld-byte device scratch; this call needs %lld bytes "
@@ -528,6 +556,29 @@ int smx_norm_residual_add(int64_t m, int64_t n, const float* x, int64_t ldx, con
     return fail(SMX_ERR_INVALID, "unknown dtype bits 0x%x", dtypes);
   hipLaunchKernelGGL(norm_residual_rows, dim3((unsigned)m), dim3(256), 0, (hipStream_t)stream, x, ldx,
                      residual, ldr, scale, dtypes, eps, n, out, ldo);
+  return check_launch();
+}
+
+int smx_qk_norm_rope(int64_t m, int64_t n, const float* x, int64_t ldx, const void* rope_cos, const void* rope_sin,
+                     const void* rope_scale, int32_t dtypes, int32_t bn, int32_t head_dim, float eps, void* out,
+                     int64_t ldo, void* stream) {
+  g_error[0] = 0;
+  if (m <= 0 || n <= 0) return fail(SMX_ERR_INVALID, "empty problem m=%lld n=%lld", (long long)m, (long long)n);
+  if (!x || !rope_cos || !rope_sin || !rope_scale || !out) return fail(SMX_ERR_INVALID, "null pointer");
+  if (head_dim <= 0 || head_dim % 2 || bn <= 0 || bn % (2 * head_dim))
+    return fail(SMX_ERR_INVALID, "qk_norm_rope needs an even head_dim and bn a multiple of 2*head_dim (bn=%d, "
+                "head_dim=%d)", bn, head_dim);
+  if (n % bn) return fail(SMX_ERR_INVALID, "N=%lld is not divisible by bn=%d", (long long)n, bn);
+  if (ldx < n || ldo < n) return fail(SMX_ERR_INVALID, "row strides must be >= n");
+  if (dtypes & ~(SMX_QK_SCALE_F32 | SMX_QK_OUT_F32)) return fail(SMX_ERR_INVALID, "unknown dtype bits 0x%x", dtypes);
+  // LDS: the tile's bn squares and its bn / head_dim reciprocals.
+  const int64_t lds = ((int64_t)bn + bn / head_dim) * 4;
+  if (lds > 64 * 1024)
+    return fail(SMX_ERR_UNSUPPORTED, "bn=%d: the row pass holds bn + bn/head_dim floats in at most 64 KiB of LDS", bn);
+  if (m >= ((int64_t)1 << 31) || n / bn >= 65536) return fail(SMX_ERR_UNSUPPORTED, "too many rows or tiles");
+  hipLaunchKernelGGL(qk_norm_rope_rows, dim3((unsigned)m, (unsigned)(n / bn)), dim3(256), (unsigned)lds,
+                     (hipStream_t)stream, x, ldx, (const uint16_t*)rope_cos, (const uint16_t*)rope_sin, rope_scale,
+                     dtypes, bn, head_dim, eps, out, ldo);
   return check_launch();
 }
 

@@ -32,7 +32,9 @@ Differences a caller can observe, all raised as exceptions (never silent):
   formula raises ``ValueError`` (the reference would add raw quadrant
   products into its encoded basis).
 * ``norm_residual_add`` runs as the GEMM with an FP32 result followed by a
-  row-norm pass (one bf16 rounding, as in the reference).
+  row-norm pass (one bf16 rounding, as in the reference). So does
+  ``qk_norm_rope`` for a ``rope_head_dim`` other than 128 (the fused q/k
+  epilogue's head width), followed by a per-head norm and RoPE pass.
 * ``formula_variant`` "dual" / "powers" and ``block_permutation`` run on
   packed operands: a plain weight is packed for the call (pack it once with
   ``strassen_weight_layout(..., formula_variant=, block_permutation=)``).
@@ -44,9 +46,12 @@ Differences a caller can observe, all raised as exceptions (never silent):
   the quadrants once after the last K panel, so ``interleave_products`` and
   the ``product_aware_*`` schedules (which only reorder FP32 additions in
   the reference) are validated and accepted but select the same kernel.
-* Tiles must additionally satisfy the gfx950 kernels' divisibility rule
-  (``smx_tile_requirements``): bm % 256 == 0 always; bn % 128 and bk % 64 for
-  a plain weight; bn % 256 and bk % 64 for a packed weight.
+* Every tile the reference's ``check_tiling`` accepts runs (bm % 16, bn % 256,
+  bk % 256): the packed kernels take bm % 16, bn % 256, bk % 64. A bm whose
+  half is not a multiple of 128 (decode-sized M, for one) runs their
+  thin-tiling instantiations, which map output rows one by one. The compact
+  kernel (``plain_weight_kernel("compact")``) needs bm % 256 and takes
+  bn % 128; a tile it cannot take runs packed.
 """
 
 from __future__ import annotations
@@ -130,9 +135,19 @@ def plain_weight_kernel(kind):
         PLAIN_WEIGHTS = previous
 
 
-def _fits_packed(algo, epilogue, bm, bn, bk):
-    tm, tn, tk = _lib.tile_requirements(algo, epilogue, _lib.SMX_B_PACKED)
+def _fits(algo, epilogue, bm, bn, bk, b_layout):
+    tm, tn, tk = _lib.tile_requirements(algo, epilogue, b_layout)
     return bm % (2 * tm) == 0 and bn % (2 * tn) == 0 and bk % (2 * tk) == 0
+
+
+def _fits_packed(algo, epilogue, bm, bn, bk):
+    return _fits(algo, epilogue, bm, bn, bk, _lib.SMX_B_PACKED)
+
+
+# Head width of the fused q/k epilogue: a head's half (64 columns) is two of
+# the kernels' 32-column accumulator blocks. Other widths run the GEMM with an
+# FP32 result and the per-head pass smx_qk_norm_rope.
+FUSED_QK_HEAD_DIM = 128
 
 
 def _is_dtype(x, dtype):
@@ -359,10 +374,38 @@ def _norm_residual_add(algo, a, b, *, residual, norm_scale, norm_eps, **kw):
     return out
 
 
+def _qk_norm_rope(algo, a, b, *, rope_cos, rope_sin, rope_scale, rope_head_dim, rope_eps, **kw):
+    """``qk_norm_rope`` (``strassen_pallas.py:793-835``) for head widths the
+    fused epilogue does not take, in two passes: the GEMM stores its FP32
+    result, then ``smx_qk_norm_rope`` applies each head's RMSNorm (over its
+    columns in both tile halves) and the rotation, rounding once."""
+    out_dtype = kw.pop("out_dtype", torch.bfloat16)
+    product = _run(algo, a, b, out_dtype=torch.float32, **kw)
+    m, n = product.shape
+    _require_device(rope_cos, rope_sin, rope_scale)
+    cos = rope_cos.to(torch.bfloat16).contiguous()
+    sin = rope_sin.to(torch.bfloat16).contiguous()
+    scale = _aux_tensor(rope_scale.contiguous())
+    out = torch.empty((m, n), dtype=out_dtype, device=product.device)
+    dtypes = ((_lib.SMX_QK_SCALE_F32 if scale.dtype == torch.float32 else 0)
+              | (_lib.SMX_QK_OUT_F32 if out_dtype == torch.float32 else 0))
+    stream = torch.cuda.current_stream(product.device).cuda_stream
+    rc = _lib.load().smx_qk_norm_rope(m, n, _lib.ptr(product), product.stride(0), _lib.ptr(cos), _lib.ptr(sin),
+                                      _lib.ptr(scale), dtypes, kw["bn"], rope_head_dim, float(rope_eps),
+                                      _lib.ptr(out), out.stride(0), stream)
+    _lib.check(rc)
+    return out
+
+
 def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
          rope_cos=None, rope_sin=None, rope_scale=None, rope_head_dim=128,
          rope_eps=1e-6, out_dtype=torch.bfloat16, formula="classical", block_permutation=0,
          norm_scale=None, norm_eps=1e-6, schedule=None, partial=None, dot_precision=None):
+    if epilogue == "qk_norm_rope" and rope_head_dim != FUSED_QK_HEAD_DIM:
+        return _qk_norm_rope(algo, a, b, rope_cos=rope_cos, rope_sin=rope_sin, rope_scale=rope_scale,
+                             rope_head_dim=rope_head_dim, rope_eps=rope_eps, bm=bm, bn=bn, bk=bk,
+                             out_dtype=out_dtype, formula=formula, block_permutation=block_permutation,
+                             schedule=schedule, partial=partial, dot_precision=dot_precision)
     if epilogue == "norm_residual_add":
         return _norm_residual_add(algo, a, b, residual=residual, norm_scale=norm_scale, norm_eps=norm_eps,
                                   bm=bm, bn=bn, bk=bk, formula=formula, block_permutation=block_permutation,
@@ -385,6 +428,9 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
     packed = isinstance(b, PackedOperand) or formula != "classical" or block_permutation != 0
     if not packed and PLAIN_WEIGHTS == "pack" and _fits_packed(algo, epilogue, bm, bn, bk):
         packed = True
+    if not packed and not _fits(algo, epilogue, bm, bn, bk, _lib.SMX_B_KCONTIG) and _fits_packed(
+            algo, epilogue, bm, bn, bk):
+        packed = True  # a tile the compact kernel cannot take (a thin bm, for one)
     if not packed and (a.dtype == torch.float32 or b.dtype == torch.float32):
         packed = True  # FP32 inputs reach the kernels through the packing pass only
     if isinstance(a, PackedOperand) and not packed:

@@ -15,8 +15,10 @@ Restates two pieces of the reference for gfx950:
   satisfy the kernels' tile rule and admit the paired gate|up layout; give
   every surviving candidate exactly ``warmups`` + ``runs`` timed calls per
   arm; record failures in-band; the winner per arm is the lowest mean, ties
-  to the earlier candidate, with no re-timing. On gfx950 the tile rule is
-  the packed kernel's (``bm % 256``, ``bn % 256``, ``bk % 64``); there is no
+  to the earlier candidate, with no re-timing. On gfx950 the screen keeps
+  the packed kernel's full-tile rule (``bm % 256``, ``bn % 256``,
+  ``bk % 64``): thin tilings (``bm % 16``) run as well, but they exist for
+  an M that no full-tile bm divides, not as faster candidates; there is no
   VMEM budget to screen against, because the kernel's LDS footprint is fixed
   by its 128 x 128 product-space workgroup tile, not by ``(bm, bn, bk)``.
 
@@ -46,8 +48,9 @@ __all__ = ["TILE_RULE", "enumerate_candidates", "time_calls", "screen_tiles", "m
 HERE = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_TABLE = os.path.join(HERE, "tuned_shapes.json")
 
-# The packed kernel's tile rule (smx_tile_requirements): bm, bn multiples of
-# 2 x 128 product rows / columns, bk of 2 x 32 product depth.
+# The screened tile rule: bm, bn multiples of 2 x 128 product rows / columns
+# (whole product tiles; smx_tile_requirements also admits thin bm % 16), bk of
+# 2 x 32 product depth.
 TILE_RULE = (256, 256, 64)
 BM_CANDIDATES = (512, 1024, 2048)
 BN_CANDIDATES = (512, 1024, 2048, 2560)

@@ -115,6 +115,50 @@ def test_invalid_descriptors_are_rejected_before_any_launch(field, value, code):
     assert _lib.last_error()
 
 
+@pytest.mark.parametrize("fields,code,match", [
+    (dict(bm=8), _lib.SMX_ERR_UNSUPPORTED, "bm % 16"),       # below the reference's bm % 16
+    (dict(bm=24, m=240), _lib.SMX_ERR_UNSUPPORTED, "bm % 16"),
+    (dict(bn=128), _lib.SMX_ERR_UNSUPPORTED, "bn % 256"),
+    (dict(bk=32), _lib.SMX_ERR_UNSUPPORTED, "bk % 64"),
+    (dict(epilogue=_lib.SMX_EPI["qk_norm_rope"], rope_head_dim=64), _lib.SMX_ERR_UNSUPPORTED, "smx_qk_norm_rope"),
+])
+def test_packed_tile_rule(fields, code, match):
+    """Packed operands take bm % 16 (thin tilings included), bn % 256 and
+    bk % 64; the fused q/k epilogue takes head_dim 128 and names the
+    two-pass route for other widths."""
+    lib = _lib.load()
+    buf = (ctypes.c_uint8 * 64)()
+    base = ctypes.addressof(buf)
+    p = ctypes.c_void_p(base + (-base) % 16)
+    kw = dict(a_layout=_lib.SMX_A_PACKED, b_layout=_lib.SMX_B_PACKED)
+    kw.update(fields)
+    rc = lib.smx_gemm(_desc(**kw), p, p, p, None, None, p, p, p, None)
+    assert rc == code
+    assert match in _lib.last_error()
+
+
+@pytest.mark.parametrize("args,match", [
+    (dict(m=0), "empty"),
+    (dict(head_dim=3), "even head_dim"),
+    (dict(head_dim=96), "multiple of 2*head_dim"),   # bn 256 % 192
+    (dict(n=384), "not divisible"),
+    (dict(ldx=100), "row strides"),
+    (dict(dtypes=2), "dtype bits"),
+    (dict(bn=16384, n=16384, ldx=16384, ldo=16384), "LDS"),
+])
+def test_qk_norm_rope_rejects_bad_arguments(args, match):
+    lib = _lib.load()
+    buf = (ctypes.c_uint8 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    a = dict(m=16, n=512, ldx=512, bn=256, head_dim=64, dtypes=0, ldo=512)
+    a.update(args)
+    rc = lib.smx_qk_norm_rope(a["m"], a["n"], p, a["ldx"], p, p, p, a["dtypes"], a["bn"], a["head_dim"], 1e-6, p,
+                              a["ldo"], None)
+    assert rc == _lib.SMX_ERR_INVALID or rc == _lib.SMX_ERR_UNSUPPORTED
+    assert match in _lib.last_error()
+    assert lib.smx_qk_norm_rope(16, 512, None, 512, p, p, p, 0, 256, 64, 1e-6, p, 512, None) == _lib.SMX_ERR_INVALID
+
+
 def test_null_pointers_and_missing_epilogue_operands():
     lib = _lib.load()
     assert lib.smx_gemm(None, None, None, None, None, None, None, None, None, None) == _lib.SMX_ERR_INVALID
@@ -133,7 +177,8 @@ def test_tile_requirements():
     # Both algorithms share each kernel's tiling.
     assert plain == _lib.tile_requirements(_lib.SMX_ALGO_CUBIC, None, _lib.SMX_B_KCONTIG)
     assert packed == _lib.tile_requirements(_lib.SMX_ALGO_CUBIC, None, _lib.SMX_B_PACKED)
-    assert packed == (128, 128, 32) and plain == (128, 64, 32)
+    # packed: every bm the reference allows (bm % 16), thin tilings included
+    assert packed == (8, 128, 32) and plain == (128, 64, 32)
     with pytest.raises(ValueError):
         _lib.tile_requirements(3, None)
     with pytest.raises(ValueError):
@@ -149,6 +194,11 @@ def test_packed_bytes():
     assert out.value == 512 * 256 * 2
     assert lib.smx_packed_bytes(5, 512, 256, ctypes.byref(out)) == _lib.SMX_ERR_INVALID
     assert lib.smx_packed_bytes(7, 511, 256, ctypes.byref(out)) == _lib.SMX_ERR_INVALID
+    # a thin tiling's product rows are padded to whole 128-row tiles
+    assert lib.smx_packed_bytes(7, 32, 256, ctypes.byref(out)) == _lib.SMX_OK
+    assert out.value == 128 * 128 * 7 * 2
+    assert lib.smx_packed_bytes(8, 272 * 2, 256, ctypes.byref(out)) == _lib.SMX_OK
+    assert out.value == 384 * 128 * 4 * 2
 
 
 @pytest.mark.parametrize("args,code", [
@@ -157,7 +207,8 @@ def test_packed_bytes():
     ((7, 3, 512, 512, 512, 256, 512), _lib.SMX_ERR_INVALID),      # side
     ((7, 2, 512, 512, 256, 256, 512), _lib.SMX_ERR_INVALID),      # transposed A: ld < rows
     ((6, 0, 512, 512, 512, 256, 512), _lib.SMX_ERR_INVALID),      # algo
-    ((7, 0, 512, 512, 512, 128, 512), _lib.SMX_ERR_UNSUPPORTED),  # tile_rows % 256
+    ((7, 0, 480, 512, 512, 24, 512), _lib.SMX_ERR_UNSUPPORTED),   # A: tile_rows % 16
+    ((7, 1, 512, 512, 512, 128, 512), _lib.SMX_ERR_UNSUPPORTED),  # B: tile_rows % 256
     ((8, 1, 512, 512, 512, 256, 48), _lib.SMX_ERR_INVALID),       # k % bk
     ((8, 1, 512, 480, 480, 256, 48), _lib.SMX_ERR_UNSUPPORTED),   # bk % 64
     ((7, 0, 512, 480, 480, 256, 96), _lib.SMX_ERR_UNSUPPORTED),   # bk % 64
@@ -334,22 +385,31 @@ def test_kernel_scratch_check():
         return (f"\t.amdhsa_kernel {name}\n\t\t.amdhsa_group_segment_fixed_size 0\n"
                 f"\t\t.amdhsa_private_segment_fixed_size {size}\n\t.end_amdhsa_kernel\n")
 
-    split_swiglu = "_ZN3smx5split10gemm_splitILi1ELi2EEEvNS_6ParamsE"
-    split_qk = "_ZN3smx5split10gemm_splitILi4ELi2EEEvNS_6ParamsE"
-    cubic = "_ZN3smx6packed11gemm_packedILi8ELi2ELi0ELi3EEEvNS_6ParamsE"
-    cubic_partial = "_ZN3smx6packed11gemm_packedILi8ELi2ELi1ELi3EEEvNS_6ParamsE"
+    split_swiglu = "_ZN3smx5split10gemm_splitILi1ELi2ELb0EEEvNS_6ParamsE"
+    split_qk = "_ZN3smx5split10gemm_splitILi4ELi2ELb0EEEvNS_6ParamsE"
+    thin_swiglu = "_ZN3smx5split10gemm_splitILi1ELi2ELb1EEEvNS_6ParamsE"
+    thin_qk = "_ZN3smx5split10gemm_splitILi4ELi2ELb1EEEvNS_6ParamsE"
+    cubic = "_ZN3smx6packed11gemm_packedILi8ELi2ELi0ELi3ELb0EEEvNS_6ParamsE"
+    cubic_partial = "_ZN3smx6packed11gemm_packedILi8ELi2ELi1ELi3ELb0EEEvNS_6ParamsE"
+    thin_cubic = "_ZN3smx6packed11gemm_packedILi8ELi2ELi0ELi3ELb1EEEvNS_6ParamsE"
     other = "_ZN3smx6packed9pack_rowsILi7ELi0EEEvPKtlliiiiPKiiPh"
     assert build.scratch_limit(split_swiglu) == 0
     assert build.scratch_limit(split_qk) == build.QK_SCRATCH_CAP
+    assert build.scratch_limit(thin_swiglu) == 0
+    assert build.scratch_limit(thin_qk) == build.THIN_QK_SCRATCH_CAP
     assert build.scratch_limit(cubic) == 0
     assert build.scratch_limit(cubic_partial) == build.PARTIAL_SCRATCH_CAP
+    assert build.scratch_limit(thin_cubic) == 0
     assert build.scratch_limit(other) is None
-    clean = desc(split_swiglu, 0) + desc(split_qk, 116) + desc(cubic, 0) + desc(cubic_partial, 792) + desc(other, 64)
-    assert build.verify_kernel_scratch(clean) == 4
-    for name, size in ((split_swiglu, 8), (split_qk, build.QK_SCRATCH_CAP + 4), (cubic, 4),
+    clean = (desc(split_swiglu, 0) + desc(split_qk, 116) + desc(thin_qk, 164) + desc(cubic, 0)
+             + desc(cubic_partial, 792) + desc(other, 64))
+    assert build.verify_kernel_scratch(clean) == 5
+    for name, size in ((split_swiglu, 8), (split_qk, build.QK_SCRATCH_CAP + 4), (thin_swiglu, 4),
+                       (thin_qk, build.THIN_QK_SCRATCH_CAP + 4), (cubic, 4), (thin_cubic, 4),
                        (cubic_partial, build.PARTIAL_SCRATCH_CAP + 4)):
         with pytest.raises(RuntimeError, match="scratch per lane"):
             build.verify_kernel_scratch(clean + desc(name, size))
+    assert build.verify_kernel_scratch(desc(other, 0), require=False) == 0
     with pytest.raises(RuntimeError, match="no GEMM kernel"):
         build.verify_kernel_scratch(desc(other, 0))
 
@@ -377,7 +437,8 @@ def test_noalloc_entry_point_rejects_before_any_launch():
     d.partial, d.ldp = p.value, 512
     assert lib.smx_gemm_noalloc(d, p, p, p, None, None, None, None, None, None) == _lib.SMX_ERR_UNSUPPORTED
     assert "partial" in _lib.last_error()
-    assert call(bm=128) == _lib.SMX_ERR_UNSUPPORTED            # the packed kernel's tile rule
+    assert call(bn=128) == _lib.SMX_ERR_UNSUPPORTED            # the packed kernel's tile rule
+    assert call(bm=8) == _lib.SMX_ERR_UNSUPPORTED
     assert call(epilogue=_lib.SMX_EPI["residual_add"]) == _lib.SMX_ERR_INVALID
     assert call(lda=500) == _lib.SMX_ERR_INVALID
     assert "lda" in _lib.last_error()

@@ -86,6 +86,81 @@ def test_cubic_exact_integer_kat(shape, tile):
     assert np.array_equal(got, a @ b)
 
 
+def _textbook_tile_strassen(a, b, bm, bn, bk):
+    """One-level Strassen on every (bm, bn) output tile from the textbook
+    formulas (M1..M7 and the four quadrant sums of Strassen 1969, as in
+    Cormen et al., ch. 4.2) written on explicit per-tile slices, with every
+    operand sum rounded once to bf16 as the reference's bf16 path does; the
+    products and their combination in float64."""
+    m, k = a.shape
+    n = b.shape[1]
+    hm, hn, hk = bm // 2, bn // 2, bk // 2
+
+    def r(x):
+        return o.bf16_round(x.astype(np.float32)).astype(np.float64)
+
+    out = np.zeros((m, n))
+    for i in range(m // bm):
+        for j in range(n // bn):
+            c11 = c12 = c21 = c22 = 0.0
+            for p in range(k // bk):
+                A = a[i * bm:(i + 1) * bm, p * bk:(p + 1) * bk].astype(np.float64)
+                B = b[p * bk:(p + 1) * bk, j * bn:(j + 1) * bn].astype(np.float64)
+                A11, A12, A21, A22 = A[:hm, :hk], A[:hm, hk:], A[hm:, :hk], A[hm:, hk:]
+                B11, B12, B21, B22 = B[:hk, :hn], B[:hk, hn:], B[hk:, :hn], B[hk:, hn:]
+                M1 = r(A11 + A22) @ r(B11 + B22)
+                M2 = r(A21 + A22) @ B11
+                M3 = A11 @ r(B12 - B22)
+                M4 = A22 @ r(B21 - B11)
+                M5 = r(A11 + A12) @ B22
+                M6 = r(A21 - A11) @ r(B11 + B12)
+                M7 = r(A12 - A22) @ r(B21 + B22)
+                c11, c12 = c11 + M1 + M4 - M5 + M7, c12 + M3 + M5
+                c21, c22 = c21 + M2 + M4, c22 + M1 - M2 + M3 + M6
+            out[i * bm:i * bm + hm, j * bn:j * bn + hn] = c11
+            out[i * bm:i * bm + hm, j * bn + hn:(j + 1) * bn] = c12
+            out[i * bm + hm:(i + 1) * bm, j * bn:j * bn + hn] = c21
+            out[i * bm + hm:(i + 1) * bm, j * bn + hn:(j + 1) * bn] = c22
+    return out
+
+
+@pytest.mark.parametrize("bm", [16, 48])
+def test_thin_tile_row_pairing_against_textbook_tiles(bm):
+    """Which rows meet in an operand sum (row r and r + bm/2 of each bm-row
+    tile, strassen_pallas.py:188-204) changes the bf16 rounding of the sums
+    only, so integer KATs cannot see it. The oracle's FP32 output agrees with
+    the per-tile textbook computation to float32 summation noise (about
+    1e-7), while the tilings that pair other rows differ by about 5e-3."""
+    rng = np.random.default_rng(0)
+    m, k, n = 96, 512, 256
+    a = o.bf16_round(rng.standard_normal((m, k)).astype(np.float32))
+    b = o.bf16_round((rng.standard_normal((k, n)) * 0.05).astype(np.float32))
+    got = o.strassen_matmul(a, b, bm=bm, bn=256, bk=256, output_dtype="float32").astype(np.float64)
+
+    def rel(x, y):
+        return float(np.linalg.norm(x - y) / np.linalg.norm(y))
+
+    assert rel(got, _textbook_tile_strassen(a, b, bm, 256, 256)) < 1e-6
+    for other in (16, 32, 48, 96):
+        if other != bm:
+            assert rel(got, _textbook_tile_strassen(a, b, other, 256, 256)) > 1e-3
+
+
+def test_thin_packed_operand_pads_zero_rows():
+    """smx_pack_operand's layout restated for a thin tiling: the product
+    rows in order (those of operand_planes), then zero rows up to a whole
+    128-row tile."""
+    rng = np.random.default_rng(2)
+    a = o.bf16_round(rng.standard_normal((48, 512)).astype(np.float32))
+    for algo, nops in ((7, 7), (8, 4)):
+        planes = o.operand_planes(a, algo, "lhs", 16, 256)
+        assert planes.shape == (nops, 24, 256)
+        flat = o.packed_operand(a, algo, "lhs", 16, 256)
+        unpacked = o.unpack_operand(flat, nops, 128, 256)
+        assert np.array_equal(unpacked[:, :24], planes)
+        assert not unpacked[:, 24:].any()
+
+
 def test_kat_detects_planted_sign_error(monkeypatch):
     """A wrong sign in one operand sum must fail the integer KAT."""
     original = ref.strassen_products
@@ -291,14 +366,16 @@ def test_product_aware_swiglu_within_reference_gate():
     assert e_std < 2e-2
 
 
-def test_qk_norm_rope_matches_unfused_semantics():
+@pytest.mark.parametrize("hd,bn,heads", [(128, 256, 4), (64, 256, 4), (96, 768, 8), (256, 512, 4)])
+def test_qk_norm_rope_matches_unfused_semantics(hd, bn, heads):
     """Fused per-head RMSNorm+RoPE on the rope layout equals the reference's
     unfused path (projection -> rms_norm per head -> apply_rope,
     benchmark_qwen3_32b_layer.py:270-284, 354-366) after rope_layout_to_heads,
-    up to the bf16 roundings the unfused path adds."""
+    up to the bf16 roundings the unfused path adds, for head widths whose
+    halves fill, share or straddle 32-column blocks."""
     rng = np.random.default_rng(11)
-    batch, seq, heads, hd = 2, 16, 4, 128
-    tokens, n, k, bn = batch * seq, heads * hd, 512, 256
+    batch, seq = 2, 16
+    tokens, n, k = batch * seq, heads * hd, 512
     x = o.bf16_round(rng.standard_normal((tokens, k)).astype(np.float32))
     w = o.bf16_round(rng.standard_normal((k, n)).astype(np.float32) * np.float32(0.05))
     gamma = o.bf16_round((1.0 + 0.1 * rng.standard_normal(hd)).astype(np.float32))
