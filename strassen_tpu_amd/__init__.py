@@ -16,9 +16,10 @@ from .strassen import (  # noqa: F401
 )
 
 from .packing import (  # noqa: F401
-    ExactSchedule, PackedOperand, SplitOperand, cubic_weight_layout, pack_activation, pack_operand,
-    precision_passes, strassen_weight_layout,
+    ExactSchedule, PackedOperand, SplitOperand, cache_packed_weights, cubic_weight_layout, pack_activation,
+    pack_operand, packed_weight_cache_info, precision_passes, strassen_weight_layout,
 )
+from .strassen import PlainWeightPackWarning  # noqa: F401
 from .tuning import tuned_matmul  # noqa: F401
 
 __version__ = "0.5.0"

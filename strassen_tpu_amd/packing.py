@@ -25,14 +25,17 @@ panels, which adds the partial before the epilogue.
 
 from __future__ import annotations
 
+import collections
 import ctypes
+import os
 
 import torch
 
 from . import _lib
 
 __all__ = ["PackedOperand", "SplitOperand", "ExactSchedule", "exact_schedule", "pack_operand", "precision_passes",
-           "strassen_weight_layout", "cubic_weight_layout", "pack_activation"]
+           "strassen_weight_layout", "cubic_weight_layout", "pack_activation", "cache_packed_weights",
+           "packed_weight_cache_info", "pack_weight_for_call"]
 
 _ALGOS = {_lib.SMX_ALGO_STRASSEN: "strassen", _lib.SMX_ALGO_CUBIC: "cubic"}
 
@@ -271,6 +274,111 @@ def pack_operand(x, *, algo, side, tile_rows, bk, formula="classical", block_per
     common["side"] = "rhs" if side == "rhs" else "lhs"
     return SplitOperand(ordinary, exact, formula=formula, block_permutation=block_permutation, schedule=schedule,
                         **common)
+
+
+class _WeightCache:
+    """Packed forms of plain weights, reused while a weight is unchanged.
+
+    A call that passes an ordinary ``[K, N]`` weight packs it (the seven
+    Strassen operand sums, 7/4 of its bytes, or the cubic's quadrants) before
+    the GEMM; with the cache enabled the packed form of the same weight is
+    reused on later calls. Key: the weight's data address, view geometry,
+    dtype and device, and the packing (algorithm, tile, formula, block
+    permutation, exact panels, bf16 passes). An entry keeps the weight tensor
+    alive, so its storage cannot be freed and its address taken by another
+    tensor while the entry lives, and records torch's version counter at
+    packing: an in-place update of the weight through it or any view of it
+    bumps the counter and the next call packs again. Writes that bypass the
+    counter (through ``.data``, or from outside torch) are not seen.
+    Least-recently used entries are dropped beyond the capacity (bytes of
+    packed data); an operand larger than the capacity is not kept. Not
+    thread-safe."""
+
+    def __init__(self, capacity):
+        self.capacity = int(capacity)
+        self.entries = collections.OrderedDict()
+        self.bytes = 0
+        self.hits = self.misses = self.stale = 0
+
+    @staticmethod
+    def _nbytes(packed):
+        parts = [packed.ordinary, packed.exact] if isinstance(packed, SplitOperand) else [packed]
+        return sum(p.data.numel() * p.data.element_size() for p in parts if p is not None)
+
+    def resize(self, capacity):
+        self.capacity = int(capacity)
+        self._evict()
+
+    def _evict(self):
+        while self.entries and self.bytes > self.capacity:
+            _, (_, _, _, nbytes) = self.entries.popitem(last=False)
+            self.bytes -= nbytes
+
+    def lookup(self, x, packing, make):
+        if self.capacity <= 0:
+            return make()
+        key = (x.data_ptr(), tuple(x.shape), tuple(x.stride()), x.dtype, str(x.device), packing)
+        entry = self.entries.get(key)
+        if entry is not None:
+            tensor, version, packed, nbytes = entry
+            if tensor._version == version:
+                self.entries.move_to_end(key)
+                self.hits += 1
+                return packed
+            self.stale += 1
+            del self.entries[key]
+            self.bytes -= nbytes
+        self.misses += 1
+        version = x._version
+        packed = make()
+        nbytes = self._nbytes(packed)
+        if nbytes <= self.capacity:
+            self.entries[key] = (x, version, packed, nbytes)
+            self.bytes += nbytes
+            self._evict()
+        return packed
+
+
+_WEIGHT_CACHE = _WeightCache(int(os.environ.get("SMX_WEIGHT_CACHE_BYTES", "0") or 0))
+
+
+def cache_packed_weights(capacity_bytes):
+    """Keep the packed forms of plain weights that ``strassen_matmul`` /
+    ``cubic_matmul`` calls pack, up to ``capacity_bytes`` of packed data
+    (0, the default unless ``SMX_WEIGHT_CACHE_BYTES`` sets one, packs on
+    every call and empties the cache). Returns the previous capacity. Size it
+    to hold every weight of the working set (a Strassen weight packs to 7/4
+    of its bytes); a cache that evicts before reuse only adds bookkeeping.
+    Packing weights once with ``strassen_weight_layout`` /
+    ``cubic_weight_layout`` needs no cache."""
+    previous = _WEIGHT_CACHE.capacity
+    _WEIGHT_CACHE.resize(capacity_bytes)
+    return previous
+
+
+def packed_weight_cache_info():
+    """Hits, misses, stale entries (weights updated in place), entries held,
+    bytes held and capacity of the packed-weight cache."""
+    c = _WEIGHT_CACHE
+    return {"hits": c.hits, "misses": c.misses, "stale": c.stale, "entries": len(c.entries), "bytes": c.bytes,
+            "capacity": c.capacity}
+
+
+def pack_weight_for_call(b, *, algo, bn, bk, formula="classical", block_permutation=0, classical_panels=(),
+                         panel_schedule=None, dot_precision=None):
+    """The packed weight a GEMM call on a plain weight ``b [K, N]`` needs:
+    from the packed-weight cache when it holds ``b`` unchanged, else packed
+    now (and kept when the cache is enabled)."""
+    def make():
+        return pack_operand(b, algo=algo, side="rhs", tile_rows=bn, bk=bk, formula=formula,
+                            block_permutation=block_permutation, classical_panels=classical_panels,
+                            panel_schedule=panel_schedule, dot_precision=dot_precision)
+
+    if panel_schedule is not None and not isinstance(panel_schedule, ExactSchedule):
+        return make()  # a schedule still to be read from the device: packed per call
+    exact = panel_schedule.exact if panel_schedule is not None else None
+    packing = (algo, bn, bk, formula, block_permutation, tuple(classical_panels), exact, dot_precision)
+    return _WEIGHT_CACHE.lookup(b, packing, make)
 
 
 def strassen_weight_layout(b, bn, bk, *, formula_variant="classical", block_permutation=0, classical_panels=(),

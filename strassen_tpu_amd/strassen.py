@@ -58,13 +58,15 @@ from __future__ import annotations
 
 import contextlib
 import os
+import warnings
 
 import numpy as np
 import torch
 
 from . import _lib
 from .layouts import is_k_contiguous
-from .packing import PackedOperand, SplitOperand, exact_schedule, pack_operand, precision_passes
+from .packing import (PackedOperand, SplitOperand, exact_schedule, pack_operand, pack_weight_for_call,
+                      packed_weight_cache_info, precision_passes)
 
 __all__ = [
     "strassen_matmul", "strassen_matmul_lhs_transposed", "cubic_matmul", "native_matmul", "check_tiling",
@@ -142,6 +144,26 @@ def _fits(algo, epilogue, bm, bn, bk, b_layout):
 
 def _fits_packed(algo, epilogue, bm, bn, bk):
     return _fits(algo, epilogue, bm, bn, bk, _lib.SMX_B_PACKED)
+
+
+class PlainWeightPackWarning(UserWarning):
+    """A call packed an ordinary weight for itself (no packed-weight cache)."""
+
+
+_PLAIN_PACK_WARNED = False
+
+
+def _plain_weight(b, **packing):
+    """The packed form of a plain weight for one call (through the
+    packed-weight cache when enabled). The first per-call pack of a process
+    without a cache warns once: it repeats on every call."""
+    global _PLAIN_PACK_WARNED
+    if not _PLAIN_PACK_WARNED and packed_weight_cache_info()["capacity"] <= 0:
+        _PLAIN_PACK_WARNED = True
+        warnings.warn("a plain weight is packed on every call (a Strassen weight packs to 7/4 of its bytes): "
+                      "pack it once with strassen_weight_layout / cubic_weight_layout, or keep packed weights "
+                      "with cache_packed_weights(capacity_bytes)", PlainWeightPackWarning, stacklevel=4)
+    return pack_weight_for_call(b, **packing)
 
 
 # Head width of the fused q/k epilogue: a head's half (64 columns) is two of
@@ -447,7 +469,7 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
                     residual, bias, rope_cos, rope_sin, rope_scale)
     if packed:
         if not isinstance(b, PackedOperand):
-            b = pack_operand(b, algo=algo, side="rhs", tile_rows=bn, bk=bk, dot_precision=dot_precision, **variant)
+            b = _plain_weight(b, algo=algo, bn=bn, bk=bk, dot_precision=dot_precision, **variant)
         if not isinstance(a, PackedOperand):
             a = pack_operand(a, algo=algo, side="lhs", tile_rows=bm, bk=bk, dot_precision=dot_precision, **variant)
         a_ptr, b_ptr, lda, ldb = a.data, b.data, k * passes, k * passes
@@ -537,8 +559,8 @@ def _run_split(a, b, *, bm, bn, bk, schedule, formula, block_permutation, out_dt
         a = pack_operand(a, algo=_lib.SMX_ALGO_STRASSEN, side="lhs", tile_rows=bm, bk=bk, panel_schedule=schedule,
                          dot_precision=dot_precision, **variant)
     if not isinstance(b, SplitOperand):
-        b = pack_operand(b, algo=_lib.SMX_ALGO_STRASSEN, side="rhs", tile_rows=bn, bk=bk, panel_schedule=schedule,
-                         dot_precision=dot_precision, **variant)
+        b = _plain_weight(b, algo=_lib.SMX_ALGO_STRASSEN, bn=bn, bk=bk, panel_schedule=schedule,
+                          dot_precision=dot_precision, **variant)
     partial = None
     if a.ordinary is not None:
         partial = _run(_lib.SMX_ALGO_STRASSEN, a.ordinary, b.ordinary, bm=bm, bn=bn, bk=bk,
@@ -651,7 +673,7 @@ def strassen_matmul_lhs_transposed(a, b, *, bm=TUNED_BM, bn=TUNED_BN, bk=TUNED_B
     packed_a = pack_operand(a, algo=_lib.SMX_ALGO_STRASSEN, side="lhs_t", tile_rows=bm, bk=bk,
                             dot_precision=dot_precision)
     if not isinstance(b, PackedOperand):
-        b = pack_operand(b, algo=_lib.SMX_ALGO_STRASSEN, side="rhs", tile_rows=bn, bk=bk, dot_precision=dot_precision)
+        b = _plain_weight(b, algo=_lib.SMX_ALGO_STRASSEN, bn=bn, bk=bk, dot_precision=dot_precision)
     return _run(_lib.SMX_ALGO_STRASSEN, packed_a, b, bm=bm, bn=bn, bk=bk, out_dtype=out_dtype,
                 dot_precision=dot_precision)
 

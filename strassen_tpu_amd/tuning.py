@@ -39,7 +39,7 @@ import torch
 
 from . import _lib
 from .layouts import swiglu_weight_layout
-from .packing import cubic_weight_layout, strassen_weight_layout
+from .packing import cache_packed_weights, cubic_weight_layout, strassen_weight_layout
 from .strassen import cubic_matmul, native_matmul, strassen_matmul
 
 __all__ = ["TILE_RULE", "enumerate_candidates", "time_calls", "screen_tiles", "measure_dispatch",
@@ -190,10 +190,14 @@ def screen_tiles(m, k, n, *, swiglu=True, seed=20260907, warmups=2, runs=5, devi
 def measure_dispatch(shapes, *, tile=(1024, 1024, 512), margin=0.02, seed=0, warmups=2, runs=10, device="cuda",
                      emit=None):
     """Same-run comparison of ``strassen_matmul`` (plain weight, as
-    ``tuned_matmul`` calls it) against ``native_matmul`` per ``(m, k, n)``,
-    with calls interleaved per sample. A shape enters the table only when
-    Strassen's mean is lower than native's by more than ``margin``. Returns
-    the table ``{"shapes": {"m,k,n": {"tile": [...], ...}}, ...}``."""
+    ``tuned_matmul`` calls it: the weight packed for every call) against
+    ``native_matmul`` per ``(m, k, n)``, with calls interleaved per sample.
+    A third arm, ``strassen_cached``, runs the same call with the
+    packed-weight cache holding the weight (only the activation is packed
+    per call); it is recorded, not used for the table. A shape enters the
+    table only when Strassen's mean is lower than native's by more than
+    ``margin``. Returns the table
+    ``{"shapes": {"m,k,n": {"tile": [...], ...}}, ...}``."""
     emit = emit or (lambda record: None)
     device = torch.device(device)
     bm, bn, bk = tile
@@ -205,16 +209,31 @@ def measure_dispatch(shapes, *, tile=(1024, 1024, 512), margin=0.02, seed=0, war
             emit({"kind": "dispatch_skip", "shape": [m, k, n], "reason": f"does not tile by {tuple(tile)}"})
             continue
         x, w = _inputs(m, k, n, seed, device)
-        for _ in range(warmups):
-            native_matmul(x, w)
-            strassen_matmul(x, w, bm=bm, bn=bn, bk=bk)
-        samples = {"native": [], "strassen": []}
-        for r in range(runs):
-            order = ("native", "strassen") if r % 2 == 0 else ("strassen", "native")
-            for arm in order:
-                call = (lambda: native_matmul(x, w)) if arm == "native" else \
-                    (lambda: strassen_matmul(x, w, bm=bm, bn=bn, bk=bk))
-                samples[arm] += time_calls(call, 0, 1)
+
+        calls = {"native": lambda: native_matmul(x, w),
+                 "strassen": lambda: strassen_matmul(x, w, bm=bm, bn=bn, bk=bk)}
+        calls["strassen_cached"] = calls["strassen"]
+        samples = {arm: [] for arm in calls}
+
+        def phase(arms, cache_bytes):
+            """Interleaved samples of ``arms`` with the packed-weight cache at
+            ``cache_bytes`` (0: the weight packed on every call)."""
+            previous = cache_packed_weights(cache_bytes)
+            try:
+                for _ in range(warmups):
+                    for arm in arms:
+                        calls[arm]()
+                for r in range(runs):
+                    for arm in (arms if r % 2 == 0 else arms[::-1]):
+                        samples[arm] += time_calls(calls[arm], 0, 1)
+            finally:
+                cache_packed_weights(0)
+                cache_packed_weights(previous)
+
+        phase(("native", "strassen"), 0)
+        # room for the packed weight (7/4 of its bytes): only the activation
+        # is packed per call
+        phase(("native", "strassen_cached"), 2 * k * n * 2)
         means = {arm: statistics.fmean(v) for arm, v in samples.items()}
         wins = means["strassen"] < (1.0 - margin) * means["native"]
         record = {"kind": "dispatch", "shape": [m, k, n], "mean_ms": means, "samples_ms": samples,

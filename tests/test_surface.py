@@ -378,3 +378,54 @@ def test_norm_residual_add_surface_checks():
         smx.strassen_matmul(a, b, residual=t(256, 256), norm_scale=t(128), **kw)
     with pytest.raises(ValueError, match="HIP device"):
         smx.strassen_matmul(a, b, residual=t(256, 256), norm_scale=t(256), **kw)
+
+
+def test_packed_weight_cache_logic():
+    """The packed-weight cache (CPU tensors stand in for device weights;
+    ``make`` counts packings): disabled by default, hits on a fresh view of
+    the same weight, repacks after an in-place update, least-recently used
+    eviction by packed bytes, and no entry for an operand above capacity."""
+    from strassen_tpu_amd.packing import PackedOperand, _WeightCache
+
+    made = []
+
+    def maker(nbytes):
+        def make():
+            made.append(nbytes)
+            return PackedOperand(torch.empty(nbytes // 2, dtype=torch.bfloat16), algo=7, side="rhs", rows=256,
+                                 k=256, tile_rows=256, bk=256)
+        return make
+
+    w = torch.zeros(256, 256, dtype=torch.bfloat16)
+    off = _WeightCache(0)
+    off.lookup(w.t(), ("p",), maker(1000))
+    off.lookup(w.t(), ("p",), maker(1000))
+    assert len(made) == 2 and not off.entries
+
+    cache = _WeightCache(3000)
+    first = cache.lookup(w.t(), ("p",), maker(1000))
+    again = cache.lookup(w.t(), ("p",), maker(1000))  # a new view of the same storage
+    assert again is first and len(made) == 3 and cache.hits == 1
+    cache.lookup(w.t(), ("other tile",), maker(1000))  # another packing of the same weight
+    assert len(made) == 4 and cache.bytes == 2000
+    w.add_(1)  # in-place update: the version counter moves
+    repacked = cache.lookup(w.t(), ("p",), maker(1000))
+    assert repacked is not first and cache.stale == 1 and len(made) == 5
+    v = torch.ones(256, 256, dtype=torch.bfloat16)
+    cache.lookup(v, ("p",), maker(1500))  # 3500 bytes > 3000: the least recently used entry goes
+    assert cache.bytes <= 3000 and len(cache.entries) == 2
+    cache.lookup(v, ("big",), maker(4000))  # above capacity: packed, not kept
+    assert all(key[-1] != ("big",) for key in cache.entries)
+    cache.resize(0)
+    assert not cache.entries and cache.bytes == 0
+
+
+def test_cache_packed_weights_api():
+    previous = smx.cache_packed_weights(1 << 20)
+    try:
+        info = smx.packed_weight_cache_info()
+        assert info["capacity"] == 1 << 20
+        assert set(info) == {"hits", "misses", "stale", "entries", "bytes", "capacity"}
+    finally:
+        smx.cache_packed_weights(previous)
+    assert smx.packed_weight_cache_info()["capacity"] == previous
