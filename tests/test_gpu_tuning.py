@@ -47,7 +47,11 @@ def test_dispatch_measurement_records():
     records = []
     table = tuning.measure_dispatch([(512, 1024, 1024), (500, 1024, 1024)], tile=(256, 256, 512), runs=2,
                                     emit=records.append)
-    assert records[0]["kind"] == "dispatch" and len(records[0]["samples_ms"]["native"]) == 2
+    assert records[0]["kind"] == "dispatch"
+    samples = records[0]["samples_ms"]
+    # hipBLASLt is sampled in both phases (per-call packing, cached weight)
+    assert len(samples["native"]) == 4 and len(samples["strassen"]) == 2 and len(samples["strassen_cached"]) == 2
+    assert smx.packed_weight_cache_info()["entries"] == 0  # the measurement leaves the cache as it found it
     assert records[1]["kind"] == "dispatch_skip"
     for key, entry in table["shapes"].items():
         assert entry["strassen_ms"] < entry["native_ms"]

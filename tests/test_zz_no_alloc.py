@@ -1,9 +1,10 @@
 """The allocation-free entry point smx_gemm_noalloc on the GPU, through the
 C ABI: its result equals that of the existing path it replaces for callers
 that cannot allocate (smx_pack_operand of A into a caller buffer, then
-smx_gemm), bit for bit, for the Strassen and the cubic algorithm, on two
-calls in a row whose second is smaller (the device scratch keeps the first
-call's contents). Named to be collected after every other test."""
+smx_gemm), bit for bit, for the Strassen and the cubic algorithm, on calls in
+a row that each get smaller (the device scratch keeps the previous call's
+contents), the last on a thin tiling. Named to be collected after every other
+test."""
 
 import ctypes
 
@@ -86,6 +87,9 @@ def test_noalloc_matches_existing_entry_point(algo):
     compare(lib, algo, 2048, 2048, 2048, (1024, 1024, 512), "swiglu", seed=1)
     compare(lib, algo, 512, 1024, 1024, (512, 512, 512), "residual_add", seed=2)
     compare(lib, algo, 256, 512, 512, (256, 256, 512), None, seed=3)
+    # a thin tiling (bm = 16): the packed A is zero-padded to a whole
+    # 128-row product tile inside the scratch, and only real rows are stored
+    compare(lib, algo, 48, 512, 512, (16, 256, 512), "residual_add", seed=4)
 
 
 def test_noalloc_refuses_calls_beyond_its_scratch():
