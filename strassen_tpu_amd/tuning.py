@@ -39,7 +39,7 @@ import torch
 
 from . import _lib
 from .layouts import swiglu_weight_layout
-from .packing import cache_packed_weights, cubic_weight_layout, strassen_weight_layout
+from .packing import cache_packed_weights, cubic_weight_layout, pack_activation, strassen_weight_layout
 from .strassen import cubic_matmul, native_matmul, strassen_matmul
 
 __all__ = ["TILE_RULE", "enumerate_candidates", "time_calls", "screen_tiles", "measure_dispatch",
@@ -87,9 +87,12 @@ def enumerate_candidates(m, k, n, *, paired_width=None, bm_candidates=BM_CANDIDA
     return kept, filtered
 
 
-def time_calls(function, warmups, runs):
-    """``warmups`` untimed calls, then ``runs`` calls timed one by one with
-    HIP events; returns milliseconds per call."""
+def time_calls(function, warmups, runs, batch=1):
+    """``warmups`` untimed calls, then ``runs`` samples timed with HIP
+    events, each over ``batch`` back-to-back calls; returns milliseconds per
+    call of each sample. A batch keeps the device busy while the host issues
+    the next call, so short kernels are timed without the host's per-call
+    work between them."""
     for _ in range(warmups):
         function()
     torch.cuda.synchronize()
@@ -97,11 +100,12 @@ def time_calls(function, warmups, runs):
     for _ in range(runs):
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
-        function()
+        for _ in range(batch):
+            function()
         stop.record()
         events.append((start, stop))
     torch.cuda.synchronize()
-    return [start.elapsed_time(stop) for start, stop in events]
+    return [start.elapsed_time(stop) / batch for start, stop in events]
 
 
 def _device_name(device):
@@ -187,8 +191,8 @@ def screen_tiles(m, k, n, *, swiglu=True, seed=20260907, warmups=2, runs=5, devi
     return chosen
 
 
-def measure_dispatch(shapes, *, tile=(1024, 1024, 512), margin=0.02, seed=0, warmups=2, runs=10, device="cuda",
-                     emit=None):
+def measure_dispatch(shapes, *, tile=(1024, 1024, 512), margin=0.02, seed=0, warmups=2, runs=10, batch=5,
+                     device="cuda", emit=None):
     """Same-run comparison of ``strassen_matmul`` (plain weight, as
     ``tuned_matmul`` calls it: the weight packed for every call) against
     ``native_matmul`` per ``(m, k, n)``, with calls interleaved per sample.
@@ -196,8 +200,8 @@ def measure_dispatch(shapes, *, tile=(1024, 1024, 512), margin=0.02, seed=0, war
     packed-weight cache holding the weight (only the activation is packed
     per call); it is recorded, not used for the table. A shape enters the
     table only when Strassen's mean is lower than native's by more than
-    ``margin``. Returns the table
-    ``{"shapes": {"m,k,n": {"tile": [...], ...}}, ...}``."""
+    ``margin``. Each sample times ``batch`` back-to-back calls. Returns the
+    table ``{"shapes": {"m,k,n": {"tile": [...], ...}}, ...}``."""
     emit = emit or (lambda record: None)
     device = torch.device(device)
     bm, bn, bk = tile
@@ -225,7 +229,7 @@ def measure_dispatch(shapes, *, tile=(1024, 1024, 512), margin=0.02, seed=0, war
                         calls[arm]()
                 for r in range(runs):
                     for arm in (arms if r % 2 == 0 else arms[::-1]):
-                        samples[arm] += time_calls(calls[arm], 0, 1)
+                        samples[arm] += time_calls(calls[arm], 0, 1, batch=batch)
             finally:
                 cache_packed_weights(0)
                 cache_packed_weights(previous)
@@ -244,6 +248,89 @@ def measure_dispatch(shapes, *, tile=(1024, 1024, 512), margin=0.02, seed=0, war
                                                "native_ms": means["native"]}
         del x, w
     return table
+
+
+# Launches that fill part of the chip: tile counts (128 x 128 product-space
+# tiles, i.e. 256 x 256 outputs) of half a round, one round and 1.875, 2.5 and
+# 3.125 rounds of a 256-CU MI355X.
+OCCUPANCY_SHAPES = ((8192, 5120, 1024), (8192, 5120, 2048), (6144, 8192, 5120), (8192, 8192, 5120),
+                    (10240, 8192, 5120))
+
+
+def measure_occupancy(shapes=OCCUPANCY_SHAPES, *, tile=(1024, 1024, 512), seed=0, warmups=3, runs=20, batch=10,
+                      device="cuda", emit=None):
+    """Strassen and the matched cubic per shape on operands packed once
+    (outside the timing), the arms alternating per sample of ``batch``
+    back-to-back calls: the time per call, the tile count in rounds of the
+    device's CUs, and the time per round of work."""
+    emit = emit or (lambda record: None)
+    device = torch.device(device)
+    bm, bn, bk = tile
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    results = []
+    for m, k, n in shapes:
+        x, w = _inputs(m, k, n, seed, device)
+        operands = {"strassen": (pack_activation(x, _lib.SMX_ALGO_STRASSEN, bm, bk), strassen_weight_layout(w, bn, bk)),
+                    "cubic": (pack_activation(x, _lib.SMX_ALGO_CUBIC, bm, bk), cubic_weight_layout(w, bn, bk))}
+        calls = {"strassen": lambda: strassen_matmul(*operands["strassen"], bm=bm, bn=bn, bk=bk),
+                 "cubic": lambda: cubic_matmul(*operands["cubic"], bm=bm, bn=bn, bk=bk)}
+        for call in calls.values():
+            time_calls(call, warmups, 0)
+        samples = {arm: [] for arm in calls}
+        for r in range(runs):
+            for arm in (("strassen", "cubic") if r % 2 == 0 else ("cubic", "strassen")):
+                samples[arm] += time_calls(calls[arm], 0, 1, batch=batch)
+        means = {arm: statistics.fmean(v) for arm, v in samples.items()}
+        tiles = (m // 256) * (n // 256)
+        rounds = tiles / cus
+        record = {"kind": "occupancy", "shape": [m, k, n], "tile": list(tile), "tiles": tiles, "cus": cus,
+                  "rounds": rounds, "mean_ms": means, "ms_per_round_of_work": {a: v / rounds for a, v in means.items()},
+                  "strassen_speed_over_cubic": means["cubic"] / means["strassen"], "samples_ms": samples}
+        emit(record)
+        results.append(record)
+        del operands, x, w
+    return results
+
+
+DECODE_TOKENS = (16, 64, 128)
+
+
+def measure_decode(tokens=DECODE_TOKENS, *, k=5120, n=51200, bn=1024, bk=512, seed=0, warmups=5, runs=30, batch=10,
+                   device="cuda", emit=None):
+    """The Qwen3-32B gate|up site with SwiGLU at decode-sized M, a thin
+    tiling (bm = 16): Strassen and the cubic on weights packed once against
+    hipBLASLt's GEMM followed by torch's SwiGLU, the arms rotating per sample
+    of ``batch`` back-to-back calls, with the weight bytes each arm streams
+    and the rate they imply."""
+    emit = emit or (lambda record: None)
+    device = torch.device(device)
+    _, w = _inputs(16, k, n, seed, device)
+    laid = swiglu_weight_layout(w, bn)
+    weights = {"strassen": strassen_weight_layout(laid, bn, bk), "cubic": cubic_weight_layout(laid, bn, bk)}
+    weight_bytes = {"strassen": weights["strassen"].data.numel() * 2, "cubic": weights["cubic"].data.numel() * 2,
+                    "hipblaslt": w.numel() * 2}
+    results = []
+    for m in tokens:
+        g = torch.Generator(device=device).manual_seed(seed + m)
+        x = torch.randn(m, k, device=device, generator=g).to(torch.bfloat16)
+        calls = {"strassen": lambda: strassen_matmul(x, weights["strassen"], bm=16, bn=bn, bk=bk, epilogue="swiglu"),
+                 "cubic": lambda: cubic_matmul(x, weights["cubic"], bm=16, bn=bn, bk=bk, epilogue="swiglu"),
+                 "hipblaslt": lambda: _activate(native_matmul(x, w))}
+        for call in calls.values():
+            time_calls(call, warmups, 0)
+        samples = {arm: [] for arm in calls}
+        names = list(calls)
+        for r in range(runs):
+            for arm in names[r % 3:] + names[:r % 3]:
+                samples[arm] += time_calls(calls[arm], 0, 1, batch=batch)
+        means = {arm: statistics.fmean(v) for arm, v in samples.items()}
+        record = {"kind": "decode", "shape": [m, k, n], "tile": [16, bn, bk], "mean_ms": means,
+                  "weight_bytes": weight_bytes,
+                  "weight_stream_tb_per_s": {a: weight_bytes[a] / (v * 1e-3) / 1e12 for a, v in means.items()},
+                  "samples_ms": samples}
+        emit(record)
+        results.append(record)
+    return results
 
 
 _TABLE = None
@@ -300,7 +387,11 @@ def main(argv=None):
     dispatch = sub.add_parser("dispatch", help="measure Strassen against the native GEMM per shape")
     dispatch.add_argument("--runs", type=int, default=10)
     dispatch.add_argument("--table", default=None, help="write the dispatch table here")
-    for p in (screen, dispatch):
+    occupancy = sub.add_parser("occupancy", help="Strassen and cubic on launches that fill part of the chip")
+    occupancy.add_argument("--runs", type=int, default=20)
+    decode = sub.add_parser("decode", help="the gate|up site with SwiGLU at decode-sized M (thin tiling)")
+    decode.add_argument("--runs", type=int, default=30)
+    for p in (screen, dispatch, occupancy, decode):
         p.add_argument("--out", default=None, help="also append the JSON records to this file")
     args = ap.parse_args(argv)
     sink = open(args.out, "a") if args.out else None
@@ -316,6 +407,10 @@ def main(argv=None):
     if args.command == "screen":
         m, k, n = (int(v) for v in args.shape.split(","))
         screen_tiles(m, k, n, swiglu=not args.no_swiglu, warmups=args.warmups, runs=args.runs, emit=emit)
+    elif args.command == "occupancy":
+        measure_occupancy(runs=args.runs, emit=emit)
+    elif args.command == "decode":
+        measure_decode(runs=args.runs, emit=emit)
     else:
         table = measure_dispatch(DISPATCH_SHAPES, runs=args.runs, emit=emit)
         emit({"kind": "table", **table})

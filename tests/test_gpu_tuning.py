@@ -55,3 +55,15 @@ def test_dispatch_measurement_records():
     assert records[1]["kind"] == "dispatch_skip"
     for key, entry in table["shapes"].items():
         assert entry["strassen_ms"] < entry["native_ms"]
+
+
+def test_occupancy_and_decode_measurements():
+    """The occupancy and decode measurements run and record what they
+    claim (small shapes, two samples each)."""
+    occ = tuning.measure_occupancy([(512, 1024, 512)], tile=(256, 256, 512), warmups=1, runs=2)
+    assert occ[0]["tiles"] == 4 and occ[0]["rounds"] == 4 / occ[0]["cus"]
+    assert set(occ[0]["mean_ms"]) == {"strassen", "cubic"} and all(v > 0 for v in occ[0]["mean_ms"].values())
+    dec = tuning.measure_decode((16,), k=1024, n=2048, bn=512, bk=512, warmups=1, runs=3)
+    assert dec[0]["shape"] == [16, 1024, 2048]
+    assert dec[0]["weight_bytes"]["strassen"] == 7 * dec[0]["weight_bytes"]["hipblaslt"] // 4
+    assert all(len(v) == 3 for v in dec[0]["samples_ms"].values())
