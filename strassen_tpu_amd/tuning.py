@@ -250,11 +250,14 @@ def measure_dispatch(shapes, *, tile=(1024, 1024, 512), margin=0.02, seed=0, war
     return table
 
 
-# Launches that fill part of the chip: tile counts (128 x 128 product-space
-# tiles, i.e. 256 x 256 outputs) of half a round, one round and 1.875, 2.5 and
-# 3.125 rounds of a 256-CU MI355X.
-OCCUPANCY_SHAPES = ((8192, 5120, 1024), (8192, 5120, 2048), (6144, 8192, 5120), (8192, 8192, 5120),
-                    (10240, 8192, 5120))
+# Launches of different lengths and fill on a 256-CU MI355X (tiles are 128 x
+# 128 product-space workgroups, i.e. 256 x 256 outputs): half a round and one
+# round at K = 5120; one round at K = 8192, 16384 and 25600; 1.875, 2.5 and
+# 3.125 rounds at K = 8192; 2.5 and 10 rounds at K = 5120.
+OCCUPANCY_SHAPES = ((8192, 5120, 1024), (8192, 5120, 2048),
+                    (8192, 8192, 2048), (8192, 16384, 2048), (8192, 25600, 2048),
+                    (6144, 8192, 5120), (8192, 8192, 5120), (10240, 8192, 5120),
+                    (8192, 5120, 5120), (8192, 5120, 20480))
 
 
 def measure_occupancy(shapes=OCCUPANCY_SHAPES, *, tile=(1024, 1024, 512), seed=0, warmups=3, runs=20, batch=10,
