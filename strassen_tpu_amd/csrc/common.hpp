@@ -401,10 +401,23 @@ __device__ __forceinline__ float load_vec(const void* v, int is_f32, int64_t i) 
   return is_f32 ? reinterpret_cast<const float*>(v)[i] : bf16_to_f32(reinterpret_cast<const uint16_t*>(v)[i]);
 }
 
-// Sum over the 32 lanes of a half-wave (lanes sharing lane>>5).
+// Sum over the 32 lanes of a half-wave (lanes sharing lane>>5), the same
+// total in every lane. DPP adds within rows of 16 lanes (quad_perm
+// [1,0,3,2] and [2,3,0,1]: pairs and quads; row_half_mirror: lane i with
+// 7-i, halves of 8; row_mirror: lane i with 15-i, rows of 16), then
+// ds_swizzle in bit-mask mode (and 0x1f, xor 0x10: lane i with i ^ 16 within
+// each 32-lane group) adds the two rows. Every step adds two partial sums
+// that their partner lane adds in the other order, and float addition is
+// commutative, so all 32 lanes end with bit-identical totals. DPP steps are
+// plain VALU ops; only the last step uses the LDS crossbar.
 __device__ __forceinline__ float half_wave_sum(float x) {
-#pragma unroll
-  for (int s = 16; s >= 1; s >>= 1) x += __shfl_xor(x, s, 64);
+  auto as_int = [](float v) __attribute__((always_inline)) { return __builtin_bit_cast(int, v); };
+  auto as_float = [](int v) __attribute__((always_inline)) { return __builtin_bit_cast(float, v); };
+  x += as_float(__builtin_amdgcn_update_dpp(0, as_int(x), 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+  x += as_float(__builtin_amdgcn_update_dpp(0, as_int(x), 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+  x += as_float(__builtin_amdgcn_update_dpp(0, as_int(x), 0x141, 0xF, 0xF, false));  // row_half_mirror
+  x += as_float(__builtin_amdgcn_update_dpp(0, as_int(x), 0x140, 0xF, 0xF, false));  // row_mirror
+  x += as_float(__builtin_amdgcn_ds_swizzle(as_int(x), 0x401F));                     // lane ^ 16
   return x;
 }
 
@@ -728,22 +741,73 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
           }
     }
     const float inv_width = 1.0f / (float)p.head_dim;
-    const int lrow4 = (lane >> 5) * 4;
-    // rope tables are [M, hn], indexed by output row and column inside the half
-    const uint16_t* const cos_w = p.rope_cos + row_base * hn + cc_base;
-    const uint16_t* const sin_w = p.rope_sin + row_base * hn + cc_base;
-    const int hm_t = hm * hn;
-    // thin tilings: element offset of the table row of product row prow in
-    // row half `half`, in 32 bits (the host keeps M * bn/2 below 2^31);
-    // padding rows read the last real row and are not stored
-    auto table_row = [&](uint32_t prow, int half) __attribute__((always_inline)) {
-      const uint32_t pr = min(prow, thin.prows - 1), t = pr / thin.hm;
-      return (t * thin.bm + (uint32_t)half * thin.hm + (pr - t * thin.hm)) * (uint32_t)hn + (uint32_t)cc_base;
-    };
-    // The a and b outputs of an element go to two blocks: the second staging
-    // tile (this epilogue has two per wave) takes the b block.
+    // Two staging tiles per wave: the a and b halves of each row, first as
+    // a * recip and b * recip (FP32, exact), then rotated and stored by the
+    // pass below.
     uint8_t* const tile_b = tile + T::kBytes;
     uint8_t* const te_b = tile_b + T::lane_part(lane);
+    // Rotation and store by 16-byte row chunks (the staging tile's store
+    // pattern). A lane always takes the same chunk column, eight columns c0..
+    // of the tile half: it reads their scale (gamma) once per row half, and
+    // the RoPE tables ([M, hn] bf16, by output row and column inside the
+    // half) eight values per load. out_a = a' cos - b' sin and out_b =
+    // b' cos + a' sin with a' = (a * recip) * gamma_a, b' = (b * recip) *
+    // gamma_b, as the reference orders them (strassen_pallas.py:821-827).
+    constexpr int kChunks = T::kCols / 8;
+    static_assert(64 % kChunks == 0, "a lane keeps one chunk column");
+    const int ch = lane % kChunks;
+    const int64_t c0 = cc_base + ch * 8;
+    auto rotate_store = [&](int half) __attribute__((always_inline)) {
+      fence();
+      float ga[8], gb[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        ga[e] = load_vec(p.rope_scale, p.scale_f32, c0 + e);
+        gb[e] = load_vec(p.rope_scale, p.scale_f32, hn + c0 + e);
+      }
+      const int es = p.out_f32 ? 4 : 2;
+      char* const out_cols = reinterpret_cast<char*>(p.c) + (col_base + ch * 8) * es;
+#pragma unroll
+      for (int t = 0; t < T::kRows * kChunks / 64; ++t) {
+        const int row = (lane + 64 * t) / kChunks;
+        int64_t orow;
+        bool store = true;
+        if constexpr (kThin) {
+          const uint32_t prow = (uint32_t)(row_base + row);
+          store = thin.valid(prow);
+          orow = thin.row(store ? prow : thin.prows - 1, half);  // padding rows read a real table row
+        } else {
+          orow = row_base + half * hm + row;
+        }
+        const F8 cs = unpack8(*reinterpret_cast<const u32x4*>(p.rope_cos + orow * hn + c0));
+        const F8 sn = unpack8(*reinterpret_cast<const u32x4*>(p.rope_sin + orow * hn + c0));
+        const uint8_t* const sa = tile + row * T::kStride + ch * 32;
+        const uint8_t* const sb = tile_b + row * T::kStride + ch * 32;
+        const f32x4 a_lo = *reinterpret_cast<const f32x4*>(sa), a_hi = *reinterpret_cast<const f32x4*>(sa + 16);
+        const f32x4 b_lo = *reinterpret_cast<const f32x4*>(sb), b_hi = *reinterpret_cast<const f32x4*>(sb + 16);
+        F8 oa, ob;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float na = (e < 4 ? a_lo[e & 3] : a_hi[e & 3]) * ga[e];
+          const float nb = (e < 4 ? b_lo[e & 3] : b_hi[e & 3]) * gb[e];
+          oa.v[e] = na * cs.v[e] - nb * sn.v[e];
+          ob.v[e] = nb * cs.v[e] + na * sn.v[e];
+        }
+        if (!store) continue;
+        char* const out_a = out_cols + orow * p.ldc * es;
+        char* const out_b = out_a + (int64_t)hn * es;
+        if (p.out_f32) {
+          *reinterpret_cast<f32x4*>(out_a) = f32x4{oa.v[0], oa.v[1], oa.v[2], oa.v[3]};
+          *reinterpret_cast<f32x4*>(out_a + 16) = f32x4{oa.v[4], oa.v[5], oa.v[6], oa.v[7]};
+          *reinterpret_cast<f32x4*>(out_b) = f32x4{ob.v[0], ob.v[1], ob.v[2], ob.v[3]};
+          *reinterpret_cast<f32x4*>(out_b + 16) = f32x4{ob.v[4], ob.v[5], ob.v[6], ob.v[7]};
+        } else {
+          *reinterpret_cast<u32x4*>(out_a) = pack8(oa);
+          *reinterpret_cast<u32x4*>(out_b) = pack8(ob);
+        }
+      }
+      fence();
+    };
     // Logical row half lr (sets 2 lr, 2 lr + 1) lands on physical row half
     // lr ^ swap_m; its a half is logical column swap_n.
     auto rows = [&](auto q_left, auto q_right, int lr) __attribute__((always_inline)) {
@@ -761,7 +825,6 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
         for (int h = 0; h < kNB / 2; ++h) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int ri = i * 32 + 8 * (r >> 2) + lrow4 + (r & 3);
             const float a0 = qa(i, 2 * h, r), a1 = qa(i, 2 * h + 1, r);
             const float b0 = qb(i, 2 * h, r), b1 = qb(i, 2 * h + 1, r);
             const float ssa = half_wave_sum(a0 * a0 + a1 * a1);
@@ -770,31 +833,13 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj) {
               const int j = 2 * h + jj;
-              const int cj = j * 32 + lcol;
-              const float ga = load_vec(p.rope_scale, p.scale_f32, cc_base + cj);
-              const float gb = load_vec(p.rope_scale, p.scale_f32, hn + cc_base + cj);
-              float cs, sn;
-              if constexpr (kThin) {
-                const uint32_t toff = table_row((uint32_t)(row_base + ri), half) + (uint32_t)cj;
-                cs = bf16_to_f32(p.rope_cos[toff]);
-                sn = bf16_to_f32(p.rope_sin[toff]);
-              } else {
-                const int toff = ri * hn + cj + half * hm_t;
-                cs = bf16_to_f32(cos_w[toff]);
-                sn = bf16_to_f32(sin_w[toff]);
-              }
-              const float na = qa(i, j, r) * recip * ga;
-              const float nbv = qb(i, j, r) * recip * gb;
-              put(i, j, r, na * cs - nbv * sn);
-              *reinterpret_cast<float*>(te_b + T::at(i, j, r)) = nbv * cs + na * sn;
+              put(i, j, r, qa(i, j, r) * recip);
+              *reinterpret_cast<float*>(te_b + T::at(i, j, r)) = qb(i, j, r) * recip;
             }
           }
-          // one head segment at a time keeps the table loads' live set small
-          __builtin_amdgcn_sched_barrier(0);
         }
       }
-      emit_from(tile, half, col_base);
-      emit_from(tile_b, half, col_base + hn);
+      rotate_store(half);
     };
     rows(QuadC<0>{}, QuadC<1>{}, 0);
     rows(QuadC<2>{}, QuadC<3>{}, 1);

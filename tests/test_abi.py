@@ -401,7 +401,7 @@ def test_kernel_scratch_check():
     assert build.scratch_limit(cubic_partial) == build.PARTIAL_SCRATCH_CAP
     assert build.scratch_limit(thin_cubic) == 0
     assert build.scratch_limit(other) is None
-    clean = (desc(split_swiglu, 0) + desc(split_qk, 116) + desc(thin_qk, 164) + desc(cubic, 0)
+    clean = (desc(split_swiglu, 0) + desc(split_qk, 20) + desc(thin_qk, 20) + desc(cubic, 0)
              + desc(cubic_partial, 792) + desc(other, 64))
     assert build.verify_kernel_scratch(clean) == 5
     for name, size in ((split_swiglu, 8), (split_qk, build.QK_SCRATCH_CAP + 4), (thin_swiglu, 4),
