@@ -198,7 +198,8 @@ def measure_dispatch(shapes, *, tile=(1024, 1024, 512), margin=0.02, seed=0, war
     ``native_matmul`` per ``(m, k, n)``, with calls interleaved per sample.
     A third arm, ``strassen_cached``, runs the same call with the
     packed-weight cache holding the weight (only the activation is packed
-    per call); it is recorded, not used for the table. A shape enters the
+    per call); it is recorded, not used for the table. The cache's capacity
+    is restored afterwards and its entries are dropped. A shape enters the
     table only when Strassen's mean is lower than native's by more than
     ``margin``. Each sample times ``batch`` back-to-back calls. Returns the
     table ``{"shapes": {"m,k,n": {"tile": [...], ...}}, ...}``."""

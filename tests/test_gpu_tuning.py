@@ -51,7 +51,8 @@ def test_dispatch_measurement_records():
     samples = records[0]["samples_ms"]
     # hipBLASLt is sampled in both phases (per-call packing, cached weight)
     assert len(samples["native"]) == 4 and len(samples["strassen"]) == 2 and len(samples["strassen_cached"]) == 2
-    assert smx.packed_weight_cache_info()["entries"] == 0  # the measurement leaves the cache as it found it
+    # the measurement restores the cache's capacity and leaves no entry of its own
+    assert smx.packed_weight_cache_info()["entries"] == 0
     assert records[1]["kind"] == "dispatch_skip"
     for key, entry in table["shapes"].items():
         assert entry["strassen_ms"] < entry["native_ms"]
