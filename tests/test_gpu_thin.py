@@ -205,3 +205,55 @@ def test_decode_sized_gate_up_swiglu():
         fn = smx.strassen_matmul if arm == "strassen" else smx.cubic_matmul
         got = host(fn(dev(a), pack(b_dev, bn, bk), bm=16, bn=bn, bk=bk, epilogue="swiglu"))
         assert_ulp_close(got, ref(a, laid, bm=16, bn=bn, bk=bk, epilogue="swiglu"), k=k)
+
+
+@pytest.mark.parametrize("out_f32,scale_f32", [(True, False), (False, True), (True, True)])
+def test_qk_norm_rope_pass_through_c_abi(out_f32, scale_f32):
+    """smx_qk_norm_rope on an FP32 product, through the C ABI, against the
+    oracle's per-head RMSNorm + RoPE on the same FP32 values: the float32
+    output agrees to float32 summation noise, the bf16 one to a bf16 ulp."""
+    import ctypes
+
+    from oracle import strassen_ref as ref
+    from strassen_tpu_amd import _lib
+
+    m, n, bn, hd, eps = 512, 1536, 768, 96, 1e-6
+    rng = np.random.default_rng(29)
+    x = rng.standard_normal((m, n)).astype(np.float32)
+    cos, sin = o.rope_values(m, hd, 1e6)
+    tcos, tsin = o.rope_layout_tables(cos, sin, bn // 2, hd)
+    scale = o.rope_scale_layout(o.bf16_round((1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)), bn, hd)
+    quads = ref._quadrants_of(x, 256, bn)
+    want = ref._qk_norm_rope(quads, m, n, 256, bn, tcos, tsin, scale, hd, eps)
+    x_dev = torch.from_numpy(x).to(DEV)
+    scale_dev = torch.from_numpy(scale).to(DEV)
+    scale_dev = scale_dev if scale_f32 else scale_dev.to(torch.bfloat16)
+    out = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=DEV)
+    dtypes = (_lib.SMX_QK_OUT_F32 if out_f32 else 0) | (_lib.SMX_QK_SCALE_F32 if scale_f32 else 0)
+    # the tables live in variables until the pass has read them
+    cos_dev, sin_dev = dev(tcos), dev(tsin)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(DEV).cuda_stream)
+    _lib.check(_lib.load().smx_qk_norm_rope(m, n, _lib.ptr(x_dev), n, _lib.ptr(cos_dev), _lib.ptr(sin_dev),
+                                            _lib.ptr(scale_dev), dtypes, bn, hd, eps, _lib.ptr(out), n, stream))
+    got = host(out)
+    if out_f32:
+        np.testing.assert_allclose(got, want, rtol=2e-6, atol=2e-6)
+    else:
+        assert_ulp_close(got, o.bf16_round(want), k=hd)
+
+
+def test_thin_tiling_fp32_inputs_highest_precision():
+    """A thin tiling with float32 inputs at HIGHEST precision (six bf16
+    passes per product): the packed A's padding rows stay zero in every
+    pass, and the FP32 result matches the oracle's."""
+    from test_gpu_parity import _gaussian32, assert_f32_close, dev32_weight
+
+    _, a, b = _gaussian32(7, 48, 1024, 512)
+    kw = dict(bm=16, bn=256, bk=512, dot_precision="highest")
+    for arm, fn, ref in (("strassen", smx.strassen_matmul, o.strassen_matmul),
+                         ("cubic", smx.cubic_matmul, o.cubic_blocked_matmul)):
+        say(f"  {arm}")
+        got = host(fn(dev32(a), dev32_weight(b), **kw))
+        okw = dict(kw, input_dtype="float32") if arm == "strassen" else dict(kw)
+        want = ref(a, b, output_dtype="float32", **okw)
+        assert_f32_close(got, want, 6 * 1024)
