@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SMX_VERSION 9
+#define SMX_VERSION 10
 
 /* Status codes. */
 #define SMX_OK 0
@@ -123,6 +123,14 @@ typedef struct smx_gemm_desc {
    * over the exact panels with that result as its partial. */
   const float* partial;
   int64_t ldp;
+  /* Optional device workspace (NULL, or workspace_bytes >= the
+   * smx_gemm_workspace_bytes of this descriptor, 16-byte aligned). With it,
+   * a packed launch whose last round of tiles would leave at least half the
+   * CUs idle runs those tiles as two K halves each into this FP32 buffer and
+   * a pass that sums the halves and applies the epilogue; without it every
+   * tile runs over full K. The result is the same up to FP32 summation order. */
+  void* workspace;
+  int64_t workspace_bytes;
 } smx_gemm_desc;
 
 /*
@@ -165,6 +173,15 @@ int smx_gemm(const smx_gemm_desc* desc, const void* a, const void* b, void* c, c
 int smx_gemm_noalloc(const smx_gemm_desc* desc, const void* a, const void* b, void* c, const void* residual,
                      const void* bias, const void* rope_cos, const void* rope_sin, const void* rope_scale,
                      void* stream);
+
+/* Bytes of device workspace (2 * M * N floats) with which smx_gemm splits
+ * the last round of tiles of this descriptor's launch over K, on the current
+ * device; 0 when no split applies: an unpacked or thin-tiled call, an FP32
+ * partial, K below 2048, or a tile count whose remainder on the device's
+ * CUs is zero or above half of them. Takes a descriptor smx_gemm accepts;
+ * no operand pointer is read. SMX_TAIL_SPLIT=0 in the environment turns the
+ * split off. No counterpart in the reference (a launch shape of gfx950). */
+int smx_gemm_workspace_bytes(const smx_gemm_desc* desc, int64_t* bytes);
 
 /* Tile granules of the kernels that serve (algo, epilogue, b_layout): bm
  * must be a multiple of 2*tm, bn of 2*tn, bk of 2*tk. Packed operands: 8, 128,

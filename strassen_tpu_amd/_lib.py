@@ -56,7 +56,7 @@ SMX_NRA_OUT_F32 = 4
 SMX_QK_SCALE_F32 = 1
 SMX_QK_OUT_F32 = 4
 
-EXPORTS = ("smx_gemm", "smx_gemm_noalloc", "smx_tile_requirements", "smx_packed_bytes", "smx_pack_operand",
+EXPORTS = ("smx_gemm", "smx_gemm_noalloc", "smx_gemm_workspace_bytes", "smx_tile_requirements", "smx_packed_bytes", "smx_pack_operand",
            "smx_norm_residual_add", "smx_qk_norm_rope", "smx_last_error", "smx_version")
 
 
@@ -73,6 +73,7 @@ class SmxGemmDesc(ctypes.Structure):
         ("flags", ctypes.c_int32),
         ("formula", ctypes.c_int32), ("block_permutation", ctypes.c_int32),
         ("partial", ctypes.c_void_p), ("ldp", ctypes.c_int64),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
     ]
 
 
@@ -94,6 +95,8 @@ def load():
     lib.smx_gemm.restype = ctypes.c_int
     lib.smx_gemm_noalloc.argtypes = [ctypes.POINTER(SmxGemmDesc), vp, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.smx_gemm_noalloc.restype = ctypes.c_int
+    lib.smx_gemm_workspace_bytes.argtypes = [ctypes.POINTER(SmxGemmDesc), ctypes.POINTER(ctypes.c_int64)]
+    lib.smx_gemm_workspace_bytes.restype = ctypes.c_int
     lib.smx_tile_requirements.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                           ctypes.POINTER(ctypes.c_int32),
                                           ctypes.POINTER(ctypes.c_int32),

@@ -294,7 +294,44 @@ struct Params {
   int32_t perm;              // block permutation bits: 1 rows, 2 K, 4 columns
   const float* partial;      // cubic: FP32 [M, N] added before the epilogue, or null
   int64_t ldp;
+  // Launch shape (packed kernels): grid workgroups (0: tiles_m * tiles_n).
+  // A K-split launch (ksplit 2, grid 2u) gives workgroups w and u + w the
+  // tile tile_base + w and the first floor(S/2), then the other, of its S K
+  // stages (S >= 2), and moves share h's output by h * split_stride
+  // elements.
+  int32_t grid;
+  int32_t ksplit;
+  int32_t tile_base;
+  int64_t split_stride;
 };
+
+// A workgroup's logical tile and its share of the K stages (see Params).
+struct WorkShare {
+  int tile;     // logical tile index, for tile_of
+  int stage0;   // first K stage
+  int nstages;  // K stages of this share
+  int share;    // 0 .. ksplit-1
+};
+
+__device__ __forceinline__ WorkShare work_share(const Params& p, int nstages_all) {
+  WorkShare w;
+  if (p.ksplit > 1) {
+    // Share h runs on workgroups h u .. h u + u - 1: with tile_base and u
+    // multiples of 8, workgroup w lands on the XCD that tile_of gathers
+    // tile tile_base + w on.
+    const int first = nstages_all >> 1, tiles = (int)(gridDim.x >> 1);
+    w.share = (int)blockIdx.x >= tiles ? 1 : 0;
+    w.tile = p.tile_base + (int)blockIdx.x - w.share * tiles;
+    w.nstages = w.share ? nstages_all - first : first;
+    w.stage0 = w.share ? first : 0;
+  } else {
+    w.share = 0;
+    w.tile = (int)blockIdx.x;
+    w.nstages = nstages_all;
+    w.stage0 = 0;
+  }
+  return w;
+}
 
 // Workgroup id -> product-space tile. Workgroups are dispatched round-robin
 // over the 8 XCDs; consecutive logical tiles are gathered on one XCD so that

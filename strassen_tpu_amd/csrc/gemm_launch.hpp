@@ -27,7 +27,7 @@ int launch_strassen_epilogue(const Params& p, hipStream_t stream) {
   } else {
     kern = split::gemm_split<kEpi, kQuadClassical, kThin>;
   }
-  return launch_kernel(kern, p, p.tiles_m * p.tiles_n, lds, stream);
+  return launch_kernel(kern, p, p.grid > 0 ? p.grid : p.tiles_m * p.tiles_n, lds, stream);
 }
 
 template <bool kThin, int kEpi>
@@ -36,7 +36,7 @@ int launch_cubic_epilogue(const Params& p, hipStream_t stream) {
   constexpr int lds = packed::Lay<8>::kLds > epi_lds ? packed::Lay<8>::kLds : epi_lds;
   void (*kern)(Params) = p.partial ? packed::gemm_packed<8, kEpi, kQuadCubicPartial, 3, kThin>
                                    : packed::gemm_packed<8, kEpi, kQuadCubic, 3, kThin>;
-  return launch_kernel(kern, p, p.tiles_m * p.tiles_n, lds, stream);
+  return launch_kernel(kern, p, p.grid > 0 ? p.grid : p.tiles_m * p.tiles_n, lds, stream);
 }
 
 template <bool kThin>

@@ -151,19 +151,24 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
   const int wave = tid >> 6, lane = tid & 63;
   const int wm = wave >> 1, wn = wave & 1;
 
+  const int nstages_all = (int)(p.k / (2 * TK));
+  const WorkShare ws = work_share(p, nstages_all);
+  if (ws.share) p.c = reinterpret_cast<float*>(p.c) + ws.share * p.split_stride;
   int tile_m, tile_n;
-  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tile_m, tile_n);
+  tile_of(ws.tile, p.tiles_m, p.tiles_n, p.group_m, tile_m, tile_n);
   const TileOrigin o = tile_origin<kThin>(p, (int64_t)tile_m * TM, (int64_t)tile_n * TN);
-  const int nstages = (int)(p.k / (2 * TK));
+  const int nstages = ws.nstages;
 
   // DMA sources: this workgroup's packed stages are contiguous runs of
   // L::kStage bytes; wave w moves fragments f = w + 4x of each.
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const uint32_t panel_bytes = (uint32_t)nstages * L::kStage - wave_u * kFrag;
   const __amdgpu_buffer_rsrc_t a_src = panel_rsrc(
-      reinterpret_cast<const uint8_t*>(p.a) + (int64_t)tile_m * nstages * L::kStage + wave_u * kFrag, panel_bytes);
+      reinterpret_cast<const uint8_t*>(p.a) + ((int64_t)tile_m * nstages_all + ws.stage0) * L::kStage + wave_u * kFrag,
+      panel_bytes);
   const __amdgpu_buffer_rsrc_t b_src = panel_rsrc(
-      reinterpret_cast<const uint8_t*>(p.b) + (int64_t)tile_n * nstages * L::kStage + wave_u * kFrag, panel_bytes);
+      reinterpret_cast<const uint8_t*>(p.b) + ((int64_t)tile_n * nstages_all + ws.stage0) * L::kStage + wave_u * kFrag,
+      panel_bytes);
   const uint32_t lane_off = lane * 16;
   uint8_t* const a_region = lds;
   uint8_t* const b_region = lds + L::kASlots * L::kStage;

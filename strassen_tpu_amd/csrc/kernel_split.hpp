@@ -308,21 +308,26 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
+  const int nstages_all = (int)(p.k / (2 * TK));
+  const WorkShare ws = work_share(p, nstages_all);
+  if (ws.share) p.c = reinterpret_cast<float*>(p.c) + ws.share * p.split_stride;
   int tile_m, tile_n;
-  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tile_m, tile_n);
+  tile_of(ws.tile, p.tiles_m, p.tiles_n, p.group_m, tile_m, tile_n);
   // The tile indices are uniform, but the integer divisions that produce
   // them run on VALU; readfirstlane moves them (and every operand address
   // derived from them) to SGPRs, which keeps VGPRs for the accumulators.
   tile_m = __builtin_amdgcn_readfirstlane(tile_m);
   tile_n = __builtin_amdgcn_readfirstlane(tile_n);
   const TileOrigin o = tile_origin<kThin>(p, (int64_t)tile_m * packed::TM, (int64_t)tile_n * packed::TN);
-  const int nstages = (int)(p.k / (2 * TK));
+  const int nstages = ws.nstages;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t panel_bytes = (uint32_t)nstages * L::kStage - wave * kFrag;
   const __amdgpu_buffer_rsrc_t a_src = packed::panel_rsrc(
-      reinterpret_cast<const uint8_t*>(p.a) + (int64_t)tile_m * nstages * L::kStage + wave * kFrag, panel_bytes);
+      reinterpret_cast<const uint8_t*>(p.a) + ((int64_t)tile_m * nstages_all + ws.stage0) * L::kStage + wave * kFrag,
+      panel_bytes);
   const __amdgpu_buffer_rsrc_t b_src = packed::panel_rsrc(
-      reinterpret_cast<const uint8_t*>(p.b) + (int64_t)tile_n * nstages * L::kStage + wave * kFrag, panel_bytes);
+      reinterpret_cast<const uint8_t*>(p.b) + ((int64_t)tile_n * nstages_all + ws.stage0) * L::kStage + wave * kFrag,
+      panel_bytes);
 
   // Prologue: stage 0 of everything, then stage 1 of A's long operands, of
   // B and of A's short operands (the loop's order); stage 0 has landed once

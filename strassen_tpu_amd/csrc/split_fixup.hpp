@@ -1,0 +1,132 @@
+// Second pass of a K-split tail (smx_gemm with a workspace): the last round
+// of a packed launch ran its tiles as two K halves, each writing its FP32
+// result, laid out as the [M, N] output, into one half of the workspace.
+// This pass sums the halves and applies the epilogue the fused kernels apply
+// (strassen_pallas.py:739-879), on the physical output positions.
+#pragma once
+
+#include "common.hpp"
+#include "kernel_packed.hpp"
+
+namespace smx {
+
+// Eight values of an [.., ld] array at element i (i % 8 == 0 for bf16,
+// i % 4 == 0 for float32 rows: 16-byte loads).
+__device__ __forceinline__ F8 load8(const void* base, int is_f32, int64_t i) {
+  if (is_f32) {
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(base) + i);
+    const f32x4 hi = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(base) + i + 4);
+    return F8{{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}};
+  }
+  return unpack8(*reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(base) + i));
+}
+
+__device__ __forceinline__ void store8(void* base, int out_f32, int64_t i, const F8& x) {
+  if (out_f32) {
+    float* const o = reinterpret_cast<float*>(base) + i;
+    *reinterpret_cast<f32x4*>(o) = f32x4{x.v[0], x.v[1], x.v[2], x.v[3]};
+    *reinterpret_cast<f32x4*>(o + 4) = f32x4{x.v[4], x.v[5], x.v[6], x.v[7]};
+  } else {
+    *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(base) + i) = pack8(x);
+  }
+}
+
+// One workgroup per tail tile u (tile tile_base + u of the launch's grid):
+// its 128 x 128 product-space block is 128 rows of each output row half by
+// 128 columns of each column half. Thread t takes columns 8 (t % 16) .. + 7
+// of both column halves (the a | b or gate | up pair of the epilogues) on
+// rows t / 16 + 16 i of the 256. `ws` holds the two halves, split_stride
+// floats apart, with row stride N. p is the fused call's Params.
+template <int kEpi>
+__global__ __launch_bounds__(256) void split_fixup(Params p, const float* __restrict__ ws) {
+  int tile_m, tile_n;
+  tile_of(p.tile_base + (int)blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tile_m, tile_n);
+  const TileOrigin o = tile_origin<false>(p, (int64_t)tile_m * packed::TM, (int64_t)tile_n * packed::TN);
+  const int64_t hm = p.bm / 2, hn = p.bn / 2;
+  const int t = (int)threadIdx.x;
+  const int64_t cin = o.tc + (t & 15) * 8;  // column inside a column half
+  const int64_t col_a = o.tj * p.bn + cin, col_b = col_a + hn;
+  const float* const ws1 = ws + p.split_stride;
+  F8 bias_a{}, bias_b{}, ga{}, gb{};
+  if constexpr (kEpi == SMX_EPI_BIAS_ADD) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      bias_a.v[e] = load_vec(p.bias, p.bias_f32, col_a + e);
+      bias_b.v[e] = load_vec(p.bias, p.bias_f32, col_b + e);
+    }
+  }
+  if constexpr (kEpi == SMX_EPI_QK_NORM_ROPE) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ga.v[e] = load_vec(p.rope_scale, p.scale_f32, cin + e);
+      gb.v[e] = load_vec(p.rope_scale, p.scale_f32, hn + cin + e);
+    }
+  }
+  const float inv_width = 1.0f / (float)p.head_dim;
+  for (int i = 0; i < 16; ++i) {
+    const int lr = (t >> 4) + 16 * i;  // row half lr / 128, row lr % 128 of the tile
+    const int64_t row = o.ti * p.bm + (lr >> 7) * hm + o.tr + (lr & 127);
+    F8 a = load8(ws, 1, row * p.n + col_a), b = load8(ws, 1, row * p.n + col_b);
+    const F8 a1 = load8(ws1, 1, row * p.n + col_a), b1 = load8(ws1, 1, row * p.n + col_b);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      a.v[e] += a1.v[e];
+      b.v[e] += b1.v[e];
+    }
+    if constexpr (kEpi == SMX_EPI_SWIGLU || kEpi == SMX_EPI_GEGLU) {
+      // gate | up: the tile's first and second column halves
+      F8 g;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) g.v[e] = gate_f32<kEpi>(a.v[e]) * b.v[e];
+      store8(p.c, p.out_f32, row * p.ldc + o.tj * hn + cin, g);
+      continue;
+    }
+    if constexpr (kEpi == SMX_EPI_RESIDUAL_ADD) {
+      const F8 ra = load8(p.residual, p.residual_f32, row * p.ldr + col_a);
+      const F8 rb = load8(p.residual, p.residual_f32, row * p.ldr + col_b);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        a.v[e] += ra.v[e];
+        b.v[e] += rb.v[e];
+      }
+    }
+    if constexpr (kEpi == SMX_EPI_BIAS_ADD) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        a.v[e] += bias_a.v[e];
+        b.v[e] += bias_b.v[e];
+      }
+    }
+    if constexpr (kEpi == SMX_EPI_QK_NORM_ROPE) {
+      // A head is 64 columns of each half: eight lanes (t % 8 equal
+      // neighbours) of a row. recip = 1 / sqrt((sum a^2 + sum b^2) /
+      // head_dim + eps); a' = (a recip) gamma_a, b' = (b recip) gamma_b;
+      // out_a = a' cos - b' sin, out_b = b' cos + a' sin (cos, sin at the
+      // output row and the column inside the half).
+      float ssa = 0.f, ssb = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        ssa += a.v[e] * a.v[e];
+        ssb += b.v[e] * b.v[e];
+      }
+#pragma unroll
+      for (int x = 1; x < 8; x <<= 1) {
+        ssa += __shfl_xor(ssa, x);
+        ssb += __shfl_xor(ssb, x);
+      }
+      const float recip = 1.0f / sqrtf((ssa + ssb) * inv_width + p.eps);
+      const F8 cs = unpack8(*reinterpret_cast<const u32x4*>(p.rope_cos + row * hn + cin));
+      const F8 sn = unpack8(*reinterpret_cast<const u32x4*>(p.rope_sin + row * hn + cin));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float na = (a.v[e] * recip) * ga.v[e], nb = (b.v[e] * recip) * gb.v[e];
+        a.v[e] = na * cs.v[e] - nb * sn.v[e];
+        b.v[e] = nb * cs.v[e] + na * sn.v[e];
+      }
+    }
+    store8(p.c, p.out_f32, row * p.ldc + col_a, a);
+    store8(p.c, p.out_f32, row * p.ldc + col_b, b);
+  }
+}
+
+}  // namespace smx

@@ -47,12 +47,14 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "common.hpp"
 #include "kernel_packed.hpp"
 #include "kernel_v1.hpp"
 #include "launch.hpp"
+#include "split_fixup.hpp"
 
 namespace smx {
 namespace {
@@ -253,6 +255,8 @@ int gemm_params(const smx_gemm_desc* d, const void* a, const void* b, void* c, c
   const bool out_f32 = (d->flags & SMX_FLAG_OUT_F32) != 0;
   if (!aligned16(c) || d->ldc % (out_f32 ? 4 : 8))
     return fail(SMX_ERR_INVALID, "C rows must be 16-byte aligned (C 16-byte aligned, ldc %% %d == 0)", out_f32 ? 4 : 8);
+  if (d->workspace_bytes < 0 || !aligned16(d->workspace))
+    return fail(SMX_ERR_INVALID, "the workspace must be 16-byte aligned with workspace_bytes >= 0");
   // The q/k epilogue addresses its RoPE tables ([M, bn/2] per tile half)
   // with 32-bit element offsets.
   if ((int64_t)hm * d->bn >= ((int64_t)1 << 31))
@@ -324,16 +328,128 @@ int gemm_params(const smx_gemm_desc* d, const void* a, const void* b, void* c, c
   return SMX_OK;
 }
 
-int launch_gemm(Params p, const smx_gemm_desc& d, hipStream_t s) {
-  if (d.b_layout != SMX_B_PACKED)
-    return d.algo == SMX_ALGO_STRASSEN ? dispatch_v1<7>(p, d.epilogue, s) : dispatch_v1<8>(p, d.epilogue, s);
+constexpr int kMaxDevices = 64;
+
+// Compute units of the current device, looked up once per device.
+int device_cus(int* cus) {
+  static std::atomic<int> known[kMaxDevices] = {};
+  int device = -1;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return fail(SMX_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (device < 0 || device >= kMaxDevices) return fail(SMX_ERR_UNSUPPORTED, "device %d out of range", device);
+  int v = known[device].load(std::memory_order_relaxed);
+  if (v <= 0) {
+    e = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device);
+    if (e != hipSuccess || v <= 0) return fail(SMX_ERR_LAUNCH, "compute unit count: %s", hipGetErrorString(e));
+    known[device].store(v, std::memory_order_relaxed);
+  }
+  *cus = v;
+  return SMX_OK;
+}
+
+// SMX_TAIL_SPLIT=0 keeps every tile of a launch over full K (for timing
+// the two launch shapes against each other).
+bool tail_split_setting() {
+  static const bool value = [] {
+    const char* env = getenv("SMX_TAIL_SPLIT");
+    return !(env && env[0] == '0');
+  }();
+  return value;
+}
+
+// Packed launch grid (p.tiles_m, p.tiles_n, p.group_m) of a checked call.
+void packed_grid(Params& p) {
   p.tiles_m = (int)(packed::padded_product_rows(p.m) / packed::TM);
   p.tiles_n = (int)((p.n / 2) / packed::TN);
   p.group_m = group_m_setting();
+}
+
+// Depth below which the tail round is short enough that the split's two
+// extra launches take much of its saving (a 128 x 128 Strassen product tile
+// over K = 2048 is 235 MFLOP: 24 us at one CU's peak).
+constexpr int64_t kTailSplitMinK = 2048;
+
+// Tiles of a packed launch's last round that run as two K halves (0: none).
+// The tiles fill whole rounds of one per CU and then a last round of r; when
+// r leaves at least half the CUs idle, those r tiles run as 2r half-K
+// workgroups, and the round takes about half as long. Thin tilings, FP32
+// partials and K below kTailSplitMinK keep every tile whole.
+int tail_split_tiles(const Params& p, int* tail) {
+  *tail = 0;
   const bool thin = (p.bm / 2) % packed::TM != 0;
-  if (d.algo == SMX_ALGO_STRASSEN)
-    return thin ? launch_strassen<true>(p, d.epilogue, s) : launch_strassen<false>(p, d.epilogue, s);
-  return thin ? launch_cubic<true>(p, d.epilogue, s) : launch_cubic<false>(p, d.epilogue, s);
+  if (thin || p.partial || !tail_split_setting() || p.k < kTailSplitMinK) return SMX_OK;
+  int cus = 0;
+  if (int rc = device_cus(&cus)) return rc;
+  const int r = (p.tiles_m * p.tiles_n) % cus;
+  if (r > 0 && 2 * r <= cus) *tail = r;
+  return SMX_OK;
+}
+
+int64_t tail_split_bytes(const Params& p) { return 2 * p.m * p.n * (int64_t)sizeof(float); }
+
+template <int kEpi>
+int launch_fixup(const Params& p, const float* ws, int tiles, hipStream_t s) {
+  hipLaunchKernelGGL(split_fixup<kEpi>, dim3((unsigned)tiles), dim3(256), 0, s, p, ws);
+  return check_launch();
+}
+
+int launch_split_fixup(const Params& p, int epilogue, const float* ws, int tiles, hipStream_t s) {
+  switch (epilogue) {
+    case SMX_EPI_NONE: return launch_fixup<SMX_EPI_NONE>(p, ws, tiles, s);
+    case SMX_EPI_SWIGLU: return launch_fixup<SMX_EPI_SWIGLU>(p, ws, tiles, s);
+    case SMX_EPI_GEGLU: return launch_fixup<SMX_EPI_GEGLU>(p, ws, tiles, s);
+    case SMX_EPI_RESIDUAL_ADD: return launch_fixup<SMX_EPI_RESIDUAL_ADD>(p, ws, tiles, s);
+    case SMX_EPI_BIAS_ADD: return launch_fixup<SMX_EPI_BIAS_ADD>(p, ws, tiles, s);
+    case SMX_EPI_QK_NORM_ROPE: return launch_fixup<SMX_EPI_QK_NORM_ROPE>(p, ws, tiles, s);
+  }
+  return fail(SMX_ERR_INVALID, "unknown epilogue %d", epilogue);
+}
+
+int launch_packed(const Params& p, int algo, int epilogue, hipStream_t s) {
+  const bool thin = (p.bm / 2) % packed::TM != 0;
+  if (algo == SMX_ALGO_STRASSEN)
+    return thin ? launch_strassen<true>(p, epilogue, s) : launch_strassen<false>(p, epilogue, s);
+  return thin ? launch_cubic<true>(p, epilogue, s) : launch_cubic<false>(p, epilogue, s);
+}
+
+// A packed call, with its last round split over K when a workspace is given
+// (smx_gemm_desc.workspace): the whole rounds with the fused epilogue, then
+// the last round's tiles as two K halves into the workspace (FP32, no
+// epilogue), then split_fixup, all on the caller's stream in that order.
+int launch_gemm(Params p, const smx_gemm_desc& d, hipStream_t s) {
+  if (d.b_layout != SMX_B_PACKED)
+    return d.algo == SMX_ALGO_STRASSEN ? dispatch_v1<7>(p, d.epilogue, s) : dispatch_v1<8>(p, d.epilogue, s);
+  packed_grid(p);
+  int tail = 0;
+  if (d.workspace) {
+    if (int rc = tail_split_tiles(p, &tail)) return rc;
+    if (tail && d.workspace_bytes < tail_split_bytes(p))
+      return fail(SMX_ERR_INVALID, "workspace_bytes %lld is below the %lld this call needs (smx_gemm_workspace_bytes)",
+                  (long long)d.workspace_bytes, (long long)tail_split_bytes(p));
+  }
+  if (!tail) return launch_packed(p, d.algo, d.epilogue, s);
+  const int tiles = p.tiles_m * p.tiles_n, whole = tiles - tail;
+  if (whole > 0) {
+    Params q = p;
+    q.grid = whole;
+    if (int rc = launch_packed(q, d.algo, d.epilogue, s)) return rc;
+  }
+  Params h = p;
+  h.c = d.workspace;
+  h.ldc = p.n;
+  h.out_f32 = 1;
+  h.residual = h.bias = nullptr;
+  h.rope_cos = h.rope_sin = nullptr;
+  h.rope_scale = nullptr;
+  h.grid = 2 * tail;
+  h.ksplit = 2;
+  h.tile_base = whole;
+  h.split_stride = p.m * p.n;
+  if (int rc = launch_packed(h, d.algo, SMX_EPI_NONE, s)) return rc;
+  Params f = p;
+  f.tile_base = whole;
+  f.split_stride = p.m * p.n;
+  return launch_split_fixup(f, d.epilogue, (const float*)d.workspace, tail, s);
 }
 
 // Device scratch of smx_gemm_noalloc: the packed activation of one call,
@@ -348,7 +464,6 @@ __device__ __attribute__((aligned(256))) uint8_t scratch[kNoAllocScratchBytes];
 // descriptor is checked (never dereferenced or launched with).
 const void* const kNoAllocScratchProbe = reinterpret_cast<const void*>((uintptr_t)256);
 
-constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxDevices] = {};
 
@@ -511,6 +626,23 @@ int smx_gemm(const smx_gemm_desc* d, const void* a, const void* b, void* c, cons
   Params p{};
   if (int rc = gemm_params(d, a, b, c, residual, bias, rope_cos, rope_sin, rope_scale, p)) return rc;
   return launch_gemm(p, *d, (hipStream_t)stream);
+}
+
+int smx_gemm_workspace_bytes(const smx_gemm_desc* d, int64_t* bytes) {
+  g_error[0] = 0;
+  if (!bytes) return fail(SMX_ERR_INVALID, "null output");
+  *bytes = 0;
+  // The descriptor is checked as smx_gemm checks it, with placeholders for
+  // the operand pointers (never dereferenced).
+  const void* x = kNoAllocScratchProbe;
+  Params p{};
+  if (int rc = gemm_params(d, x, x, const_cast<void*>(x), x, x, x, x, x, p)) return rc;
+  if (d->b_layout != SMX_B_PACKED) return SMX_OK;
+  packed_grid(p);
+  int tail = 0;
+  if (int rc = tail_split_tiles(p, &tail)) return rc;
+  if (tail) *bytes = tail_split_bytes(p);
+  return SMX_OK;
 }
 
 int smx_gemm_noalloc(const smx_gemm_desc* d, const void* a, const void* b, void* c, const void* residual,

@@ -57,6 +57,7 @@ Differences a caller can observe, all raised as exceptions (never silent):
 from __future__ import annotations
 
 import contextlib
+import ctypes
 import os
 import warnings
 
@@ -522,6 +523,14 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
         if rope_scale.dtype == torch.float32:
             aux |= _lib.SMX_AUX_SCALE_F32
     desc.aux_f32 = aux
+    # The last round of tiles runs as two K halves when the library asks
+    # for a workspace (FP32 halves of the output, summed by a second pass).
+    need = ctypes.c_int64()
+    _lib.check(lib.smx_gemm_workspace_bytes(desc, ctypes.byref(need)))
+    workspace = None
+    if need.value:
+        workspace = torch.empty(need.value, dtype=torch.uint8, device=a.device)
+        desc.workspace, desc.workspace_bytes = workspace.data_ptr(), need.value
     stream = torch.cuda.current_stream(a.device).cuda_stream
     rc = lib.smx_gemm(desc, _lib.ptr(a_ptr), _lib.ptr(b_ptr), _lib.ptr(c), _lib.ptr(residual),
                       _lib.ptr(bias), _lib.ptr(rope_cos), _lib.ptr(rope_sin),

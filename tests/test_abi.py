@@ -346,6 +346,25 @@ def test_epilogue_rows_are_16_byte_aligned(case, match):
     assert match in _lib.last_error()
 
 
+def test_workspace_arguments():
+    """The tail-split workspace: a misaligned pointer or a negative size is
+    refused before any launch, as is every descriptor smx_gemm refuses; an
+    unpacked call never needs one (both answered without a device)."""
+    lib = _lib.load()
+    buf = (ctypes.c_uint8 * 64)()
+    base = ctypes.addressof(buf)
+    p = ctypes.c_void_p(base + (-base) % 16)
+    for fields in (dict(workspace=p.value + 4, workspace_bytes=1 << 20), dict(workspace=p.value, workspace_bytes=-1)):
+        assert lib.smx_gemm(_desc(**fields), p, p, p, None, None, None, None, None, None) == _lib.SMX_ERR_INVALID
+        assert "workspace" in _lib.last_error()
+    need = ctypes.c_int64(-1)
+    assert lib.smx_gemm_workspace_bytes(_desc(k=4096, lda=4096, ldb=4096), ctypes.byref(need)) == _lib.SMX_OK
+    assert need.value == 0
+    assert lib.smx_gemm_workspace_bytes(_desc(bm=100), ctypes.byref(need)) == _lib.SMX_ERR_INVALID
+    assert lib.smx_gemm_workspace_bytes(None, ctypes.byref(need)) == _lib.SMX_ERR_INVALID
+    assert lib.smx_gemm_workspace_bytes(_desc(), None) == _lib.SMX_ERR_INVALID
+
+
 def test_inline_asm_kernel_check():
     """The build refuses device code that touches MFMA accumulators between
     the first inline-asm MFMA and the drain."""
