@@ -31,16 +31,23 @@ __device__ __forceinline__ void store8(void* base, int out_f32, int64_t i, const
   }
 }
 
-// One workgroup per tail tile u (tile tile_base + u of the launch's grid):
-// its 128 x 128 product-space block is 128 rows of each output row half by
-// 128 columns of each column half. Thread t takes columns 8 (t % 16) .. + 7
-// of both column halves (the a | b or gate | up pair of the epilogues) on
-// rows t / 16 + 16 i of the 256. `ws` holds the two halves, split_stride
-// floats apart, with row stride N. p is the fused call's Params.
+// Workgroups per split tile: each takes 32 of the tile's 256 output rows, so
+// a pass over r tiles runs 8 r workgroups and keeps enough loads in flight
+// to stream at HBM speed.
+constexpr int kFixupSlices = 8;
+
+// Workgroup w serves tail tile u = w / kFixupSlices (tile tile_base + u of
+// the launch's grid): its 128 x 128 product-space block is 128 rows of each
+// output row half by 128 columns of each column half. Thread t takes columns
+// 8 (t % 16) .. + 7 of both column halves (the a | b or gate | up pair of
+// the epilogues) on rows 32 (w % kFixupSlices) + t / 16 + 16 i, i < 2, of
+// the 256. `ws` holds the two halves, split_stride floats apart, with row
+// stride N. p is the fused call's Params.
 template <int kEpi>
 __global__ __launch_bounds__(256) void split_fixup(Params p, const float* __restrict__ ws) {
+  const int u = (int)blockIdx.x / kFixupSlices, slice = (int)blockIdx.x % kFixupSlices;
   int tile_m, tile_n;
-  tile_of(p.tile_base + (int)blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tile_m, tile_n);
+  tile_of(p.tile_base + u, p.tiles_m, p.tiles_n, p.group_m, tile_m, tile_n);
   const TileOrigin o = tile_origin<false>(p, (int64_t)tile_m * packed::TM, (int64_t)tile_n * packed::TN);
   const int64_t hm = p.bm / 2, hn = p.bn / 2;
   const int t = (int)threadIdx.x;
@@ -63,8 +70,9 @@ __global__ __launch_bounds__(256) void split_fixup(Params p, const float* __rest
     }
   }
   const float inv_width = 1.0f / (float)p.head_dim;
-  for (int i = 0; i < 16; ++i) {
-    const int lr = (t >> 4) + 16 * i;  // row half lr / 128, row lr % 128 of the tile
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int lr = 32 * slice + (t >> 4) + 16 * i;  // row half lr / 128, row lr % 128 of the tile
     const int64_t row = o.ti * p.bm + (lr >> 7) * hm + o.tr + (lr & 127);
     F8 a = load8(ws, 1, row * p.n + col_a), b = load8(ws, 1, row * p.n + col_b);
     const F8 a1 = load8(ws1, 1, row * p.n + col_a), b1 = load8(ws1, 1, row * p.n + col_b);

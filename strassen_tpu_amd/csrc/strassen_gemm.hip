@@ -389,7 +389,7 @@ int64_t tail_split_bytes(const Params& p) { return 2 * p.m * p.n * (int64_t)size
 
 template <int kEpi>
 int launch_fixup(const Params& p, const float* ws, int tiles, hipStream_t s) {
-  hipLaunchKernelGGL(split_fixup<kEpi>, dim3((unsigned)tiles), dim3(256), 0, s, p, ws);
+  hipLaunchKernelGGL(split_fixup<kEpi>, dim3((unsigned)(tiles * kFixupSlices)), dim3(256), 0, s, p, ws);
   return check_launch();
 }
 
