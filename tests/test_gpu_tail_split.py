@@ -24,7 +24,7 @@ import torch
 import oracle as o
 import strassen_tpu_amd as smx
 from strassen_tpu_amd import _lib
-from test_gpu_parity import DEV, _qk_problem, assert_ulp_close, dev, dev_weight, host, say
+from test_gpu_parity import DEV, _qk_problem, assert_ulp_close, dev, dev32, dev_weight, host, say
 
 pytestmark = pytest.mark.gpu
 
@@ -203,6 +203,33 @@ def test_split_formula_variants(formula, perm, epilogue):
     want = o.strassen_matmul(a, b, bm=TILE[0], bn=TILE[1], bk=TILE[2], epilogue=epilogue, formula_variant=formula,
                              block_permutation=perm, **aux)
     assert_ulp_close(got, want, k=k)
+
+
+# tile counts that are not multiples of 8 (the tile map does not gather
+# tiles by XCD then): 100 tiles (all split), 356 = one whole round + 100
+RAGGED = [(2560, 2048, 2560), (1024, 2048, 22784)]
+
+
+@pytest.mark.parametrize("shape", RAGGED)
+@pytest.mark.parametrize("algo", [7, 8])
+def test_ragged_tail_with_float32_operands(algo, shape):
+    """Ragged tile counts, and float32 residual and bias operands read by
+    the summing pass."""
+    m, k, n = shape
+    if not _split_tiles(m, n, k):
+        pytest.skip("this device's CU count leaves no half-empty last round at this shape")
+    rng, a, b = _problem(101 + algo, m, k, n)
+    pa, pb = _pack(algo, a, b, TILE)
+    cases = (("residual_add", dict(residual=rng.standard_normal((m, n)).astype(np.float32))),
+             ("bias_add", dict(bias=rng.standard_normal(n).astype(np.float32))))
+    for epilogue, aux in cases:
+        aux_dev = {key: dev32(v) for key, v in aux.items()}
+        split, need = abi_gemm(algo, pa, pb, m, n, k, TILE, epilogue, workspace=True, **aux_dev)
+        whole, _ = abi_gemm(algo, pa, pb, m, n, k, TILE, epilogue, workspace=False, **aux_dev)
+        assert need == 2 * m * n * 4
+        got = host(split)
+        assert_ulp_close(got, host(whole), k=k)
+        assert_ulp_close(got, _oracle(algo, a, b, TILE, epilogue=epilogue, **aux), k=k)
 
 
 def test_split_exact_panels_through_surface():
