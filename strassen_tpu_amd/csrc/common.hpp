@@ -441,12 +441,15 @@ __device__ __forceinline__ float load_vec(const void* v, int is_f32, int64_t i) 
 // Sum over the 32 lanes of a half-wave (lanes sharing lane>>5), the same
 // total in every lane. DPP adds within rows of 16 lanes (quad_perm
 // [1,0,3,2] and [2,3,0,1]: pairs and quads; row_half_mirror: lane i with
-// 7-i, halves of 8; row_mirror: lane i with 15-i, rows of 16), then
-// ds_swizzle in bit-mask mode (and 0x1f, xor 0x10: lane i with i ^ 16 within
-// each 32-lane group) adds the two rows. Every step adds two partial sums
-// that their partner lane adds in the other order, and float addition is
-// commutative, so all 32 lanes end with bit-identical totals. DPP steps are
-// plain VALU ops; only the last step uses the LDS crossbar.
+// 7-i, halves of 8; row_mirror: lane i with 15-i, rows of 16), after which
+// each row's lanes hold their row's total; then v_permlane16_swap (gfx950)
+// on two copies of the value swaps the odd rows of the first with the even
+// rows of the second, so that in both lanes i and i ^ 16 the first result
+// holds the lower row's total and the second the upper row's. Each DPP step
+// adds two partial sums that its partner lane adds in the other order (float
+// addition is commutative) and the last adds lower + upper in every lane, so
+// all 32 lanes end with bit-identical totals. Every step is a plain VALU op:
+// nothing waits on the LDS, and the sums of independent rows interleave.
 __device__ __forceinline__ float half_wave_sum(float x) {
   auto as_int = [](float v) __attribute__((always_inline)) { return __builtin_bit_cast(int, v); };
   auto as_float = [](int v) __attribute__((always_inline)) { return __builtin_bit_cast(float, v); };
@@ -454,8 +457,9 @@ __device__ __forceinline__ float half_wave_sum(float x) {
   x += as_float(__builtin_amdgcn_update_dpp(0, as_int(x), 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
   x += as_float(__builtin_amdgcn_update_dpp(0, as_int(x), 0x141, 0xF, 0xF, false));  // row_half_mirror
   x += as_float(__builtin_amdgcn_update_dpp(0, as_int(x), 0x140, 0xF, 0xF, false));  // row_mirror
-  x += as_float(__builtin_amdgcn_ds_swizzle(as_int(x), 0x401F));                     // lane ^ 16
-  return x;
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto rows = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (unsigned)rows[0]) + __builtin_bit_cast(float, (unsigned)rows[1]);
 }
 
 // One wave's epilogue staging tile in LDS: kRows x kCols floats, row stride
