@@ -228,22 +228,28 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
   // (i, 1) together), so the products of a finished block are dead before
   // the next round: holding all seven products of the whole 64x64 region
   // through the epilogue needed more than the register file and spilled.
-  // The epilogue stages its output in the wave's own receive slots, which
-  // are free from the moment their blocks are read until the barrier that
-  // ends the round (no wave writes them before it).
+  //
+  // Epilogues other than q/k stage their output in a tile of their own past
+  // the receive slots, so a wave sends the next round's blocks as soon as
+  // every wave has read the current round's, and that send overlaps the
+  // current block's epilogue. The q/k epilogue's two staging tiles per wave
+  // do not fit beside the slots: it stages in the wave's own receive slots,
+  // which are free from the moment their blocks are read until the barrier
+  // that ends the round (no wave writes them before it).
   constexpr int kBlockBytes = 64 * 16 * 4;
+  constexpr int kSlotBytes = 4 * 7 * kBlockBytes;
   constexpr bool kPairs = kEpi == SMX_EPI_QK_NORM_ROPE;
-  static_assert(kEpiTiles<kEpi> * StageTile<32, kPairs ? 64 : 32>::kBytes <= 7 * kBlockBytes,
-                "epilogue staging fits the wave's receive slots");
+  constexpr int kStageBytes = kEpiTiles<kEpi> * StageTile<32, kPairs ? 64 : 32>::kBytes;
+  static_assert(!kPairs || kStageBytes <= 7 * kBlockBytes, "q/k staging fits the wave's receive slots");
+  static_assert(kPairs || kSlotBytes + 4 * kStageBytes <= Ring::kBytes, "staging fits past the receive slots");
   const int wm = kWave >> 1, wn = kWave & 1;
   uint8_t* const mine = lds + kWave * 7 * kBlockBytes;
-  // q/k: the four quadrant sets of block (i, 0), formed on arrival, wait
-  // for block (i, 1).
-  f32x16 quads[4][1][2];
   // The rounds are spelled out with compile-time indices: a loop the
   // compiler declines to unroll (its body holds the inlined epilogue) would
   // index the block arrays at run time and move them to scratch.
-  auto round = [&](auto tc) __attribute__((always_inline)) {
+  //
+  // Round t's blocks of this wave's strips into their destination slots.
+  auto send = [&](auto tc) __attribute__((always_inline)) {
     constexpr int t = decltype(tc)::value, i = t >> 1, jj = t & 1;
     // the lane's byte offset, re-derived opaquely each round so that no copy
     // of it stays live through the epilogues
@@ -263,8 +269,10 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
         }
       }
     }
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    f32x16 blk[7][1][1];
+  };
+  // The seven products of the round's block from this wave's slots.
+  auto receive = [&](f32x16 (&blk)[7][1][1]) __attribute__((always_inline)) {
+    const uint32_t lane16 = opaque_lane_id() * 16;
 #pragma unroll
     for (int q = 0; q < 7; ++q) {
       const uint8_t* const slot = mine + q * kBlockBytes + lane16;
@@ -275,9 +283,19 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
         for (int e = 0; e < 4; ++e) blk[q][0][0][4 * g + e] = v[e];
       }
     }
-    // the block's reads complete before its slots turn into staging tiles
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if constexpr (kPairs) {
+  };
+  if constexpr (kPairs) {
+    // q/k: the four quadrant sets of block (i, 0), formed on arrival, wait
+    // for block (i, 1).
+    f32x16 quads[4][1][2];
+    auto round = [&](auto tc) __attribute__((always_inline)) {
+      constexpr int t = decltype(tc)::value, i = t >> 1, jj = t & 1;
+      send(tc);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      f32x16 blk[7][1][1];
+      receive(blk);
+      // the block's reads complete before its slots turn into staging tiles
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         quads[0][0][jj][r] = quadrant_value<kQuad, 0>(blk, 0, 0, r);
@@ -288,17 +306,35 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
       // the quadrant sets go through the epilogue as the cubic's would
       if constexpr (jj == 1)
         epilogue_body<1, 2, kEpi, 4, kQuadCubic, kThin>(p, o, wm * 64 + i * 32, wn * 64, quads, mine);
-    } else {
-      epilogue_body<1, 1, kEpi, 7, kQuad, kThin>(p, o, wm * 64 + i * 32, wn * 64 + jj * 32, blk, mine);
-    }
-    // every staging access has completed before the next round's blocks
-    // land in these slots
+      // every staging access has completed before the next round's blocks
+      // land in these slots
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    round(QuadC<0>{});
+    round(QuadC<1>{});
+    round(QuadC<2>{});
+    round(QuadC<3>{});
+  } else {
+    uint8_t* const stage = lds + kSlotBytes + kWave * kStageBytes;
+    // Round t: receive; once every wave has read its slots, send round
+    // t + 1 and run round t's epilogue; the barrier after both makes round
+    // t + 1's blocks visible.
+    auto step = [&](auto tc) __attribute__((always_inline)) {
+      constexpr int t = decltype(tc)::value, i = t >> 1, jj = t & 1;
+      f32x16 blk[7][1][1];
+      receive(blk);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if constexpr (t < 3) send(QuadC<t + 1>{});
+      epilogue_body<1, 1, kEpi, 7, kQuad, kThin>(p, o, wm * 64 + i * 32, wn * 64 + jj * 32, blk, stage);
+      if constexpr (t < 3) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    send(QuadC<0>{});
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  };
-  round(QuadC<0>{});
-  round(QuadC<1>{});
-  round(QuadC<2>{});
-  round(QuadC<3>{});
+    step(QuadC<0>{});
+    step(QuadC<1>{});
+    step(QuadC<2>{});
+    step(QuadC<3>{});
+  }
 }
 
 // kThin: a tiling whose bm/2 is not a multiple of 128 (ThinRows).
