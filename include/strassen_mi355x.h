@@ -125,10 +125,12 @@ typedef struct smx_gemm_desc {
   int64_t ldp;
   /* Optional device workspace (NULL, or workspace_bytes >= the
    * smx_gemm_workspace_bytes of this descriptor, 16-byte aligned). With it,
-   * a packed launch whose last round of tiles would leave at least half the
-   * CUs idle runs those tiles as two K halves each into this FP32 buffer and
-   * a pass that sums the halves and applies the epilogue; without it every
-   * tile runs over full K. The result is the same up to FP32 summation order. */
+   * a packed launch too small to fill the chip runs every tile as K shares
+   * (up to 16), and one whose last round of tiles would leave at least half
+   * the CUs idle runs that round as two K shares; the shares go into this
+   * FP32 buffer and a pass sums them and applies the epilogue. Without it
+   * every tile runs over full K. The result is the same up to FP32
+   * summation order. */
   void* workspace;
   int64_t workspace_bytes;
 } smx_gemm_desc;
@@ -174,13 +176,15 @@ int smx_gemm_noalloc(const smx_gemm_desc* desc, const void* a, const void* b, vo
                      const void* bias, const void* rope_cos, const void* rope_sin, const void* rope_scale,
                      void* stream);
 
-/* Bytes of device workspace (2 * M * N floats) with which smx_gemm splits
- * the last round of tiles of this descriptor's launch over K, on the current
- * device; 0 when no split applies: an unpacked or thin-tiled call, an FP32
- * partial, K below 2048, or a tile count whose remainder on the device's
- * CUs is zero or above half of them. Takes a descriptor smx_gemm accepts;
- * no operand pointer is read. SMX_TAIL_SPLIT=0 in the environment turns the
- * split off. No counterpart in the reference (a launch shape of gfx950). */
+/* Bytes of device workspace (s * M * N floats for s K shares) with which
+ * smx_gemm splits tiles of this descriptor's launch over K, on the current
+ * device; 0 when no split applies: an unpacked call, an FP32 partial, K
+ * below 2048, or a tile count T that neither leaves the device's C CUs at
+ * least half idle (T <= C / 2: every tile splits min(C / T, 16, K / 512)
+ * ways) nor ends in a last round of at most C / 2 tiles (those split two
+ * ways). Takes a descriptor smx_gemm accepts; no operand pointer is read.
+ * SMX_TAIL_SPLIT=0 in the environment turns the split off. No counterpart in
+ * the reference (a launch shape of gfx950). */
 int smx_gemm_workspace_bytes(const smx_gemm_desc* desc, int64_t* bytes);
 
 /* Tile granules of the kernels that serve (algo, epilogue, b_layout): bm

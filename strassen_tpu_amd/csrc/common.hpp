@@ -295,10 +295,10 @@ struct Params {
   const float* partial;      // cubic: FP32 [M, N] added before the epilogue, or null
   int64_t ldp;
   // Launch shape (packed kernels): grid workgroups (0: tiles_m * tiles_n).
-  // A K-split launch (ksplit 2, grid 2u) gives workgroups w and u + w the
-  // tile tile_base + w and the first floor(S/2), then the other, of its S K
-  // stages (S >= 2), and moves share h's output by h * split_stride
-  // elements.
+  // A K-split launch (ksplit s > 1, grid s u) gives workgroup h u + w the
+  // tile tile_base + w and share h of its S K stages, stages
+  // floor(h S / s) .. floor((h + 1) S / s) - 1 (S >= s), and moves share h's
+  // output by h * split_stride elements.
   int32_t grid;
   int32_t ksplit;
   int32_t tile_base;
@@ -317,13 +317,20 @@ __device__ __forceinline__ WorkShare work_share(const Params& p, int nstages_all
   WorkShare w;
   if (p.ksplit > 1) {
     // Share h runs on workgroups h u .. h u + u - 1: with tile_base and u
-    // multiples of 8, workgroup w lands on the XCD that tile_of gathers
-    // tile tile_base + w on.
-    const int first = nstages_all >> 1, tiles = (int)(gridDim.x >> 1);
-    w.share = (int)blockIdx.x >= tiles ? 1 : 0;
-    w.tile = p.tile_base + (int)blockIdx.x - w.share * tiles;
-    w.nstages = w.share ? nstages_all - first : first;
-    w.stage0 = w.share ? first : 0;
+    // multiples of 8, workgroup h u + w lands on the XCD that tile_of
+    // gathers tile tile_base + w on.
+    const uint32_t tiles = gridDim.x / (uint32_t)p.ksplit;
+    const uint32_t share = blockIdx.x / tiles;
+    w.share = (int)share;
+    w.tile = p.tile_base + (int)(blockIdx.x - share * tiles);
+    w.stage0 = (int)(share * (uint32_t)nstages_all / (uint32_t)p.ksplit);
+    w.nstages = (int)((share + 1) * (uint32_t)nstages_all / (uint32_t)p.ksplit) - w.stage0;
+    // The divisions run on VALU; the results are uniform, and in SGPRs they
+    // leave the VGPRs to the accumulators.
+    w.share = __builtin_amdgcn_readfirstlane(w.share);
+    w.tile = __builtin_amdgcn_readfirstlane(w.tile);
+    w.stage0 = __builtin_amdgcn_readfirstlane(w.stage0);
+    w.nstages = __builtin_amdgcn_readfirstlane(w.nstages);
   } else {
     w.share = 0;
     w.tile = (int)blockIdx.x;

@@ -1,8 +1,9 @@
-// Second pass of a K-split tail (smx_gemm with a workspace): the last round
-// of a packed launch ran its tiles as two K halves, each writing its FP32
-// result, laid out as the [M, N] output, into one half of the workspace.
-// This pass sums the halves and applies the epilogue the fused kernels apply
-// (strassen_pallas.py:739-879), on the physical output positions.
+// Second pass of a K-split launch (smx_gemm with a workspace): some tiles
+// of a packed launch ran as p.ksplit shares of their K stages, each share
+// writing its FP32 result, laid out as the [M, N] output, into its own part
+// of the workspace. This pass sums the shares in share order and applies the
+// epilogue the fused kernels apply (strassen_pallas.py:739-879), on the
+// physical output positions.
 #pragma once
 
 #include "common.hpp"
@@ -36,24 +37,28 @@ __device__ __forceinline__ void store8(void* base, int out_f32, int64_t i, const
 // to stream at HBM speed.
 constexpr int kFixupSlices = 8;
 
-// Workgroup w serves tail tile u = w / kFixupSlices (tile tile_base + u of
-// the launch's grid): its 128 x 128 product-space block is 128 rows of each
-// output row half by 128 columns of each column half. Thread t takes columns
-// 8 (t % 16) .. + 7 of both column halves (the a | b or gate | up pair of
-// the epilogues) on rows 32 (w % kFixupSlices) + t / 16 + 16 i, i < 2, of
-// the 256. `ws` holds the two halves, split_stride floats apart, with row
-// stride N. p is the fused call's Params.
+// Workgroup w serves split tile u = w / kFixupSlices (tile tile_base + u of
+// the launch's grid): its 128 x 128 product-space block is 128 product rows
+// in each output row half by 128 columns of each column half. Thread t takes
+// columns 8 (t % 16) .. + 7 of both column halves (the a | b or gate | up
+// pair of the epilogues) on rows 32 (w % kFixupSlices) + t / 16 + 16 i,
+// i < 2, of the 256. Product row P is output row (P / hm) bm + half hm +
+// P % hm (one row tile per product tile unless the tiling is thin); rows
+// past M/2 (a thin tiling's padding) are neither read nor written. `ws`
+// holds the p.ksplit shares, split_stride floats apart, with row stride N.
+// p is the fused call's Params.
 template <int kEpi>
 __global__ __launch_bounds__(256) void split_fixup(Params p, const float* __restrict__ ws) {
   const int u = (int)blockIdx.x / kFixupSlices, slice = (int)blockIdx.x % kFixupSlices;
   int tile_m, tile_n;
   tile_of(p.tile_base + u, p.tiles_m, p.tiles_n, p.group_m, tile_m, tile_n);
   const TileOrigin o = tile_origin<false>(p, (int64_t)tile_m * packed::TM, (int64_t)tile_n * packed::TN);
-  const int64_t hm = p.bm / 2, hn = p.bn / 2;
+  const ThinRows rows{(uint32_t)(p.bm / 2), (uint32_t)p.bm, (uint32_t)(p.m / 2)};
+  const uint32_t prow0 = (uint32_t)tile_m * packed::TM;
+  const int64_t hn = p.bn / 2;
   const int t = (int)threadIdx.x;
   const int64_t cin = o.tc + (t & 15) * 8;  // column inside a column half
   const int64_t col_a = o.tj * p.bn + cin, col_b = col_a + hn;
-  const float* const ws1 = ws + p.split_stride;
   F8 bias_a{}, bias_b{}, ga{}, gb{};
   if constexpr (kEpi == SMX_EPI_BIAS_ADD) {
 #pragma unroll
@@ -73,13 +78,18 @@ __global__ __launch_bounds__(256) void split_fixup(Params p, const float* __rest
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int lr = 32 * slice + (t >> 4) + 16 * i;  // row half lr / 128, row lr % 128 of the tile
-    const int64_t row = o.ti * p.bm + (lr >> 7) * hm + o.tr + (lr & 127);
+    const uint32_t prow = prow0 + (uint32_t)(lr & 127);
+    if (!rows.valid(prow)) continue;  // uniform over the 16 lanes of a row
+    const int64_t row = rows.row(prow, lr >> 7);
     F8 a = load8(ws, 1, row * p.n + col_a), b = load8(ws, 1, row * p.n + col_b);
-    const F8 a1 = load8(ws1, 1, row * p.n + col_a), b1 = load8(ws1, 1, row * p.n + col_b);
+    for (int h = 1; h < p.ksplit; ++h) {
+      const float* const wh = ws + h * p.split_stride;
+      const F8 ah = load8(wh, 1, row * p.n + col_a), bh = load8(wh, 1, row * p.n + col_b);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      a.v[e] += a1.v[e];
-      b.v[e] += b1.v[e];
+      for (int e = 0; e < 8; ++e) {
+        a.v[e] += ah.v[e];
+        b.v[e] += bh.v[e];
+      }
     }
     if constexpr (kEpi == SMX_EPI_SWIGLU || kEpi == SMX_EPI_GEGLU) {
       // gate | up: the tile's first and second column halves

@@ -348,8 +348,8 @@ int device_cus(int* cus) {
 }
 
 // SMX_TAIL_SPLIT=0 keeps every tile of a launch over full K (for timing
-// the two launch shapes against each other).
-bool tail_split_setting() {
+// the launch shapes against each other).
+bool split_setting() {
   static const bool value = [] {
     const char* env = getenv("SMX_TAIL_SPLIT");
     return !(env && env[0] == '0');
@@ -364,28 +364,49 @@ void packed_grid(Params& p) {
   p.group_m = group_m_setting();
 }
 
-// Depth below which the tail round is short enough that the split's two
-// extra launches take much of its saving (a 128 x 128 Strassen product tile
-// over K = 2048 is 235 MFLOP: 24 us at one CU's peak).
-constexpr int64_t kTailSplitMinK = 2048;
+// Depth below which a split's rounds are short enough that its two extra
+// launches take much of the saving (a 128 x 128 Strassen product tile over
+// K = 2048 is 235 MFLOP: 24 us at one CU's peak).
+constexpr int64_t kSplitMinK = 2048;
+// A K share keeps at least this many 32-deep K stages, and a launch splits
+// its tiles at most this many ways.
+constexpr int kSplitMinStages = 16;
+constexpr int kMaxKSplit = 16;
 
-// Tiles of a packed launch's last round that run as two K halves (0: none).
-// The tiles fill whole rounds of one per CU and then a last round of r; when
-// r leaves at least half the CUs idle, those r tiles run as 2r half-K
-// workgroups, and the round takes about half as long. Thin tilings, FP32
-// partials and K below kTailSplitMinK keep every tile whole.
-int tail_split_tiles(const Params& p, int* tail) {
-  *tail = 0;
-  const bool thin = (p.bm / 2) % packed::TM != 0;
-  if (thin || p.partial || !tail_split_setting() || p.k < kTailSplitMinK) return SMX_OK;
+// Which tiles of a packed launch run as K shares. A launch runs one tile per
+// CU and round: T tiles on C CUs make T / C whole rounds and a last round of
+// r = T mod C. With T <= C / 2 (a small launch: few output tiles, or a
+// decode-sized M) every tile runs as s = min(C / T, 16, stages / 16) shares
+// of its K stages, so that the launch fills the chip. Otherwise, when the
+// last round would leave at least half the CUs idle (0 < r <= C / 2), its r
+// tiles run as two shares each and the round takes about half as long. FP32
+// partials and K below kSplitMinK keep every tile whole.
+struct SplitPlan {
+  int whole;   // tiles 0 .. whole - 1 run over full K, with the epilogue
+  int split;   // tiles whole .. whole + split - 1 run as ksplit shares
+  int ksplit;
+};
+
+int split_plan(const Params& p, SplitPlan* plan) {
+  *plan = SplitPlan{p.tiles_m * p.tiles_n, 0, 1};
+  if (p.partial || !split_setting() || p.k < kSplitMinK) return SMX_OK;
   int cus = 0;
   if (int rc = device_cus(&cus)) return rc;
-  const int r = (p.tiles_m * p.tiles_n) % cus;
-  if (r > 0 && 2 * r <= cus) *tail = r;
+  const int tiles = p.tiles_m * p.tiles_n;
+  const int stages = (int)(p.k / (2 * packed::TK));
+  if (2 * tiles <= cus) {
+    const int s = min(min(cus / tiles, kMaxKSplit), stages / kSplitMinStages);
+    if (s >= 2) *plan = SplitPlan{0, tiles, s};
+    return SMX_OK;
+  }
+  const int r = tiles % cus;
+  if (r > 0 && 2 * r <= cus) *plan = SplitPlan{tiles - r, r, 2};
   return SMX_OK;
 }
 
-int64_t tail_split_bytes(const Params& p) { return 2 * p.m * p.n * (int64_t)sizeof(float); }
+int64_t split_bytes(const Params& p, const SplitPlan& plan) {
+  return (int64_t)plan.ksplit * p.m * p.n * (int64_t)sizeof(float);
+}
 
 template <int kEpi>
 int launch_fixup(const Params& p, const float* ws, int tiles, hipStream_t s) {
@@ -412,26 +433,25 @@ int launch_packed(const Params& p, int algo, int epilogue, hipStream_t s) {
   return thin ? launch_cubic<true>(p, epilogue, s) : launch_cubic<false>(p, epilogue, s);
 }
 
-// A packed call, with its last round split over K when a workspace is given
-// (smx_gemm_desc.workspace): the whole rounds with the fused epilogue, then
-// the last round's tiles as two K halves into the workspace (FP32, no
+// A packed call, with tiles split over K when a workspace is given
+// (smx_gemm_desc.workspace, split_plan): the whole tiles with the fused
+// epilogue, then the split tiles' K shares into the workspace (FP32, no
 // epilogue), then split_fixup, all on the caller's stream in that order.
 int launch_gemm(Params p, const smx_gemm_desc& d, hipStream_t s) {
   if (d.b_layout != SMX_B_PACKED)
     return d.algo == SMX_ALGO_STRASSEN ? dispatch_v1<7>(p, d.epilogue, s) : dispatch_v1<8>(p, d.epilogue, s);
   packed_grid(p);
-  int tail = 0;
+  SplitPlan plan{p.tiles_m * p.tiles_n, 0, 1};
   if (d.workspace) {
-    if (int rc = tail_split_tiles(p, &tail)) return rc;
-    if (tail && d.workspace_bytes < tail_split_bytes(p))
+    if (int rc = split_plan(p, &plan)) return rc;
+    if (plan.split && d.workspace_bytes < split_bytes(p, plan))
       return fail(SMX_ERR_INVALID, "workspace_bytes %lld is below the %lld this call needs (smx_gemm_workspace_bytes)",
-                  (long long)d.workspace_bytes, (long long)tail_split_bytes(p));
+                  (long long)d.workspace_bytes, (long long)split_bytes(p, plan));
   }
-  if (!tail) return launch_packed(p, d.algo, d.epilogue, s);
-  const int tiles = p.tiles_m * p.tiles_n, whole = tiles - tail;
-  if (whole > 0) {
+  if (!plan.split) return launch_packed(p, d.algo, d.epilogue, s);
+  if (plan.whole > 0) {
     Params q = p;
-    q.grid = whole;
+    q.grid = plan.whole;
     if (int rc = launch_packed(q, d.algo, d.epilogue, s)) return rc;
   }
   Params h = p;
@@ -441,15 +461,16 @@ int launch_gemm(Params p, const smx_gemm_desc& d, hipStream_t s) {
   h.residual = h.bias = nullptr;
   h.rope_cos = h.rope_sin = nullptr;
   h.rope_scale = nullptr;
-  h.grid = 2 * tail;
-  h.ksplit = 2;
-  h.tile_base = whole;
+  h.grid = plan.ksplit * plan.split;
+  h.ksplit = plan.ksplit;
+  h.tile_base = plan.whole;
   h.split_stride = p.m * p.n;
   if (int rc = launch_packed(h, d.algo, SMX_EPI_NONE, s)) return rc;
   Params f = p;
-  f.tile_base = whole;
+  f.ksplit = plan.ksplit;
+  f.tile_base = plan.whole;
   f.split_stride = p.m * p.n;
-  return launch_split_fixup(f, d.epilogue, (const float*)d.workspace, tail, s);
+  return launch_split_fixup(f, d.epilogue, (const float*)d.workspace, plan.split, s);
 }
 
 // Device scratch of smx_gemm_noalloc: the packed activation of one call,
@@ -639,9 +660,9 @@ int smx_gemm_workspace_bytes(const smx_gemm_desc* d, int64_t* bytes) {
   if (int rc = gemm_params(d, x, x, const_cast<void*>(x), x, x, x, x, x, p)) return rc;
   if (d->b_layout != SMX_B_PACKED) return SMX_OK;
   packed_grid(p);
-  int tail = 0;
-  if (int rc = tail_split_tiles(p, &tail)) return rc;
-  if (tail) *bytes = tail_split_bytes(p);
+  SplitPlan plan{};
+  if (int rc = split_plan(p, &plan)) return rc;
+  if (plan.split) *bytes = split_bytes(p, plan);
   return SMX_OK;
 }
 

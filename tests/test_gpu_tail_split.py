@@ -1,18 +1,20 @@
-"""GPU parity of the K-split tail of packed launches.
+"""GPU parity of the K splits of packed launches.
 
-A packed launch runs one 128 x 128 product tile per CU per round. When the
-last round would leave at least half the CUs idle (and K >= 2048), smx_gemm
-given a workspace runs the whole rounds with the fused epilogue, then the
-last round's tiles as two K halves each into the FP32 workspace, then a pass
-that sums the halves and applies the epilogue (strassen_pallas.py:739-879).
+A packed launch runs one 128 x 128 product tile per CU per round. Given a
+workspace (and K >= 2048), smx_gemm runs a launch too small to fill the chip
+(T tiles <= C / 2 CUs) as s = min(C / T, 16, K / 512) K shares of every tile,
+and a launch whose last round would leave at least half the CUs idle as its
+whole rounds with the fused epilogue plus that round's tiles as two K
+shares. The shares go into the FP32 workspace and a pass sums them and
+applies the epilogue (strassen_pallas.py:739-879), thin tilings included.
 strassen_matmul / cubic_matmul pass a workspace whenever the library asks for
 one. Checked against the oracle and against the same call without a
 workspace (every tile over full K): the two differ only in the order of FP32
 additions, so they agree within one bf16 ulp and are almost all bit-identical.
 
 Shapes: with bm = bn = 256 a launch has (M / 256) (N / 256) tiles; on the
-256 CUs of an MI355X, 2048 x 4096 is 128 tiles (one half-empty round, all of
-it split) and 3072 x 8192 is 384 (one whole round and a half-empty one).
+256 CUs of an MI355X, 2048 x 4096 is 128 tiles (every tile in two shares) and
+3072 x 8192 is 384 (one whole round, then 128 tiles in two shares).
 """
 
 import ctypes
@@ -40,11 +42,21 @@ def _announce(request):
     torch.cuda.synchronize()
 
 
-def _split_tiles(m, n, k):
-    """Tiles the library runs as two K halves (its rule, restated)."""
+def _plan(m, n, k, bm=256):
+    """(whole tiles, split tiles, shares) of the library's rule, restated."""
     cus = torch.cuda.get_device_properties(DEV).multi_processor_count
-    r = (m // 256) * (n // 256) % cus
-    return r if k >= 2048 and 0 < 2 * r <= cus else 0
+    tiles = -(-(m // 2) // 128) * (n // 256)
+    if k < 2048:
+        return tiles, 0, 1
+    if 2 * tiles <= cus:
+        s = min(cus // tiles, 16, (k // 32) // 16)
+        return (0, tiles, s) if s >= 2 else (tiles, 0, 1)
+    r = tiles % cus
+    return (tiles - r, r, 2) if 0 < 2 * r <= cus else (tiles, 0, 1)
+
+
+def _split_tiles(m, n, k, bm=256):
+    return _plan(m, n, k, bm)[1]
 
 
 def _stream():
@@ -133,7 +145,7 @@ def test_half_round_split_matches_whole_and_oracle(algo, epilogue):
     pa, pb = _pack(algo, a, b, TILE)
     split, need = abi_gemm(algo, pa, pb, m, n, k, TILE, epilogue, workspace=True, **aux_dev)
     whole, _ = abi_gemm(algo, pa, pb, m, n, k, TILE, epilogue, workspace=False, **aux_dev)
-    assert need == 2 * m * n * 4
+    assert need == _plan(m, n, k)[2] * m * n * 4
     got, ref = host(split), host(whole)
     assert_ulp_close(got, ref, k=k)
     assert_ulp_close(got, _oracle(algo, a, b, TILE, epilogue=epilogue, **aux), k=k)
@@ -226,7 +238,7 @@ def test_ragged_tail_with_float32_operands(algo, shape):
         aux_dev = {key: dev32(v) for key, v in aux.items()}
         split, need = abi_gemm(algo, pa, pb, m, n, k, TILE, epilogue, workspace=True, **aux_dev)
         whole, _ = abi_gemm(algo, pa, pb, m, n, k, TILE, epilogue, workspace=False, **aux_dev)
-        assert need == 2 * m * n * 4
+        assert need == _plan(m, n, k)[2] * m * n * 4
         got = host(split)
         assert_ulp_close(got, host(whole), k=k)
         assert_ulp_close(got, _oracle(algo, a, b, TILE, epilogue=epilogue, **aux), k=k)
@@ -254,10 +266,11 @@ def test_workspace_below_the_size_asked_for_is_refused():
         abi_gemm(7, pa, pb, m, n, k, TILE, workspace=True, workspace_bytes=2 * m * n * 4 - 16)
 
 
-@pytest.mark.parametrize("case", ["full_round", "short_k", "thin", "partial"])
+@pytest.mark.parametrize("case", ["full_round", "short_k", "full_last_round", "partial"])
 def test_no_workspace_asked_for(case):
-    """Whole rounds, K below 2048, thin tilings and FP32 partials keep every
-    tile over full K: the library asks for no workspace."""
+    """Whole rounds, K below 2048, a last round more than half full and FP32
+    partials keep every tile over full K: the library asks for no
+    workspace."""
     lib = _lib.load()
     d = _lib.SmxGemmDesc()
     m, k, n, tile = 2048, 2048, 4096, TILE
@@ -265,11 +278,10 @@ def test_no_workspace_asked_for(case):
         m, n = 4096, 4096  # 256 tiles
     elif case == "short_k":
         k = 1024
-    elif case == "thin":
-        tile = (32, 256, 512)
-    cus = torch.cuda.get_device_properties(DEV).multi_processor_count
-    if case == "full_round" and (m // 256) * (n // 256) % cus:
-        pytest.skip("256 tiles are not whole rounds on this device")
+    elif case == "full_last_round":
+        m, n = 6144, 5120  # 480 tiles: one round and 224
+    if _plan(m, n, k)[1] and case != "partial":
+        pytest.skip("this device's CU count splits this shape")
     d.m, d.n, d.k = m, n, k
     d.lda = d.ldb = k
     d.ldc = n
@@ -284,3 +296,55 @@ def test_no_workspace_asked_for(case):
     need = ctypes.c_int64(-1)
     _lib.check(lib.smx_gemm_workspace_bytes(d, ctypes.byref(need)))
     assert need.value == 0
+
+
+# Small launches: (m, k, n), tile. 20 tiles in 8 shares (one row tile; a
+# thin tiling with decode-sized M); 12 thin tiles over three product-row
+# tiles, the last partly padding, in 4 shares.
+SMALL = [
+    ((256, 4096, 5120), (256, 256, 512)),
+    ((16, 4096, 5120), (16, 256, 512)),
+    ((544, 2048, 1024), (272, 256, 256)),
+]
+
+
+@pytest.mark.parametrize("epilogue", [None, "swiglu", "residual_add"])
+@pytest.mark.parametrize("shape,tile", SMALL)
+@pytest.mark.parametrize("algo", [7, 8])
+def test_small_launch_split_every_tile(algo, shape, tile, epilogue):
+    (m, k, n), bm = shape, tile[0]
+    whole_tiles, split, s = _plan(m, n, k, bm)
+    if not split:
+        pytest.skip("this device's CU count does not split this shape")
+    rng, a, b = _problem(111 + algo, m, k, n)
+    aux = _aux(rng, epilogue, m, n)
+    aux_dev = {key: dev(v) for key, v in aux.items()}
+    pa, pb = _pack(algo, a, b, tile)
+    got_split, need = abi_gemm(algo, pa, pb, m, n, k, tile, epilogue, workspace=True, **aux_dev)
+    got_whole, _ = abi_gemm(algo, pa, pb, m, n, k, tile, epilogue, workspace=False, **aux_dev)
+    assert whole_tiles == 0 and need == s * m * n * 4
+    got = host(got_split)
+    assert_ulp_close(got, host(got_whole), k=k)
+    assert_ulp_close(got, _oracle(algo, a, b, tile, epilogue=epilogue, **aux), k=k)
+
+
+@pytest.mark.parametrize("algo", [7, 8])
+def test_small_thin_launch_qk_norm_rope(algo):
+    """Decode-sized q/k: 48 tokens (a thin tiling, bm = 16), 8 heads, every
+    tile in K shares; the summing pass maps rows as the thin epilogue does
+    and reads the tables at the output rows."""
+    batch, seq, heads, k, bn = 1, 48, 8, 2048, 256
+    m, n, tile = batch * seq, heads * 128, (16, bn, 512)
+    if not _split_tiles(m, n, k, 16):
+        pytest.skip("this device's CU count does not split this shape")
+    x, w, laid, tcos, tsin, scale = _qk_problem(17, batch, seq, heads, k, bn)
+    pa, pb = _pack(algo, x, laid, tile)
+    rope = (dev(tcos), dev(tsin), torch.from_numpy(scale).to(DEV).to(torch.bfloat16))
+    split, need = abi_gemm(algo, pa, pb, m, n, k, tile, "qk_norm_rope", workspace=True, rope=rope)
+    whole, _ = abi_gemm(algo, pa, pb, m, n, k, tile, "qk_norm_rope", workspace=False, rope=rope)
+    assert need == _plan(m, n, k, 16)[2] * m * n * 4
+    got = host(split)
+    assert_ulp_close(got, host(whole), k=k)
+    want = _oracle(algo, x, laid, tile, epilogue="qk_norm_rope", rope_cos=tcos, rope_sin=tsin, rope_scale=scale,
+                   rope_head_dim=128, rope_eps=1e-6)
+    assert_ulp_close(got, want, k=k)
