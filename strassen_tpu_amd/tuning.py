@@ -39,7 +39,8 @@ import torch
 
 from . import _lib
 from .layouts import swiglu_weight_layout
-from .packing import cache_packed_weights, cubic_weight_layout, pack_activation, strassen_weight_layout
+from .packing import (cache_packed_weights, cubic_weight_layout, pack_activation, packed_weight_cache_info,
+                      strassen_weight_layout)
 from .strassen import cubic_matmul, native_matmul, strassen_matmul
 
 __all__ = ["TILE_RULE", "enumerate_candidates", "time_calls", "screen_tiles", "measure_dispatch",
@@ -191,6 +192,25 @@ def screen_tiles(m, k, n, *, swiglu=True, seed=20260907, warmups=2, runs=5, devi
     return chosen
 
 
+# Row tiles a dispatched shape may use when M is not a multiple of the
+# default tile's bm (prefill chunks and decode batches; bm % 16, as the
+# reference allows).
+DISPATCH_BM = (1024, 512, 256, 128, 64, 32, 16)
+
+
+def dispatch_tile(m, k, n, tile=(1024, 1024, 512)):
+    """The tile ``measure_dispatch`` times for ``(m, k, n)``: ``tile``, with
+    bm lowered to the largest of ``DISPATCH_BM`` not above it that divides M
+    when ``tile``'s does not; None when no bm fits or bn, bk do not divide."""
+    bm, bn, bk = tile
+    if n % bn or k % bk:
+        return None
+    for b in (bm,) + tuple(v for v in DISPATCH_BM if v < bm):
+        if m % b == 0:
+            return (b, bn, bk)
+    return None
+
+
 def measure_dispatch(shapes, *, tile=(1024, 1024, 512), margin=0.02, seed=0, warmups=2, runs=10, batch=5,
                      device="cuda", emit=None):
     """Same-run comparison of ``strassen_matmul`` (plain weight, as
@@ -198,21 +218,26 @@ def measure_dispatch(shapes, *, tile=(1024, 1024, 512), margin=0.02, seed=0, war
     ``native_matmul`` per ``(m, k, n)``, with calls interleaved per sample.
     A third arm, ``strassen_cached``, runs the same call with the
     packed-weight cache holding the weight (only the activation is packed
-    per call); it is recorded, not used for the table. The cache's capacity
-    is restored afterwards and its entries are dropped. A shape enters the
-    table only when Strassen's mean is lower than native's by more than
-    ``margin``. Each sample times ``batch`` back-to-back calls. Returns the
-    table ``{"shapes": {"m,k,n": {"tile": [...], ...}}, ...}``."""
+    per call). The cache's capacity is restored afterwards and its entries
+    are dropped. A shape enters the table when either Strassen arm's mean is
+    lower than native's by more than ``margin``; the entry says which
+    (``per_call``, ``cached``), and ``tuned_matmul`` takes the cached win only
+    while the cache can hold the weight. Each shape runs on
+    ``dispatch_tile(m, k, n, tile)``. Each sample times ``batch``
+    back-to-back calls. Returns the table ``{"shapes": {"m,k,n": {"tile":
+    [...], ...}}, ...}``."""
     emit = emit or (lambda record: None)
     device = torch.device(device)
-    bm, bn, bk = tile
     table = {"device": _device_name(device), "tile": list(tile), "margin": margin,
-             "rule": "strassen mean below native mean by more than margin, same run, interleaved samples",
+             "rule": "a Strassen arm's mean below native's by more than margin, same run, interleaved samples; "
+                     "per_call: the weight packed for every call, cached: the packed-weight cache holding it",
              "shapes": {}}
     for m, k, n in shapes:
-        if m % bm or n % bn or k % bk:
+        shape_tile = dispatch_tile(m, k, n, tile)
+        if shape_tile is None:
             emit({"kind": "dispatch_skip", "shape": [m, k, n], "reason": f"does not tile by {tuple(tile)}"})
             continue
+        bm, bn, bk = shape_tile
         x, w = _inputs(m, k, n, seed, device)
 
         calls = {"native": lambda: native_matmul(x, w),
@@ -241,12 +266,15 @@ def measure_dispatch(shapes, *, tile=(1024, 1024, 512), margin=0.02, seed=0, war
         phase(("native", "strassen_cached"), 2 * k * n * 2)
         means = {arm: statistics.fmean(v) for arm, v in samples.items()}
         wins = means["strassen"] < (1.0 - margin) * means["native"]
-        record = {"kind": "dispatch", "shape": [m, k, n], "mean_ms": means, "samples_ms": samples,
-                  "strassen_wins": wins, "flops": 2 * m * k * n}
+        wins_cached = means["strassen_cached"] < (1.0 - margin) * means["native"]
+        record = {"kind": "dispatch", "shape": [m, k, n], "tile": list(shape_tile), "mean_ms": means,
+                  "samples_ms": samples, "strassen_wins": wins, "strassen_cached_wins": wins_cached,
+                  "flops": 2 * m * k * n}
         emit(record)
-        if wins:
-            table["shapes"][f"{m},{k},{n}"] = {"tile": list(tile), "strassen_ms": means["strassen"],
-                                               "native_ms": means["native"]}
+        if wins or wins_cached:
+            table["shapes"][f"{m},{k},{n}"] = {"tile": list(shape_tile), "strassen_ms": means["strassen"],
+                                               "strassen_cached_ms": means["strassen_cached"],
+                                               "native_ms": means["native"], "per_call": wins, "cached": wins_cached}
         del x, w
     return table
 
@@ -351,18 +379,30 @@ def load_table(path=None):
     return _TABLE[1]
 
 
+def _entry_wins(entry, k, n):
+    """Whether a table entry's measured win holds for this call: a win with
+    the weight packed per call always does; a win with the cached weight
+    only while the packed-weight cache can hold the packed weight (7/4 of
+    its bf16 bytes)."""
+    if entry.get("per_call", True):
+        return True
+    return bool(entry.get("cached")) and packed_weight_cache_info()["capacity"] >= 7 * k * n // 2
+
+
 def tuned_matmul(a, b, *, interpret=False):
     """Dispatch measured bf16 shapes to Strassen, everything else to the
     native GEMM (``strassen_pallas.py:1428-1461``). A shape goes to Strassen
-    only if it is in the measured table, both operands are 2-D bf16 with
-    matching K, and the table's tile divides it."""
+    only if it is in the measured table with a win that holds for the call
+    (per call, or with the packed-weight cache enabled), both operands are
+    2-D bf16 with matching K, and the table's tile divides it."""
     if a.dim() != 2 or b.dim() != 2:
         return native_matmul(a, b)
     m, k = a.shape
     k2, n = b.shape
     entry = load_table()["shapes"].get(f"{m},{k},{n}")
     use_strassen = (entry is not None and k == k2 and a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16
-                    and m % entry["tile"][0] == 0 and n % entry["tile"][1] == 0 and k % entry["tile"][2] == 0)
+                    and m % entry["tile"][0] == 0 and n % entry["tile"][1] == 0 and k % entry["tile"][2] == 0
+                    and _entry_wins(entry, k, n))
     if not use_strassen:
         return native_matmul(a, b)
     bm, bn, bk = entry["tile"]
@@ -370,14 +410,16 @@ def tuned_matmul(a, b, *, interpret=False):
 
 
 # Shapes timed for the shipped table: the reference's square crossover and
-# projection shapes (strassen_pallas.py:49-72) and the Qwen3-32B GEMM sites
-# at 8192 tokens.
+# projection shapes (strassen_pallas.py:49-72), the Qwen3-32B GEMM sites at
+# 8192 tokens, and its q, o, gate-or-up and down projections at 128, 256 and
+# 512 tokens (launches that the K split spreads over the chip).
 DISPATCH_SHAPES = (
     (4096, 4096, 4096), (8192, 8192, 8192), (16384, 16384, 16384),
     (8192, 4096, 8192), (8192, 4096, 12288), (8192, 4096, 28672), (8192, 14336, 4096),
     (8192, 5120, 8192), (8192, 5120, 1024), (8192, 8192, 5120), (8192, 5120, 25600), (8192, 5120, 51200),
     (8192, 25600, 5120),
-)
+) + tuple((m, k, n) for m in (128, 256, 512)
+          for k, n in ((5120, 8192), (8192, 5120), (5120, 25600), (25600, 5120)))
 
 
 def main(argv=None):

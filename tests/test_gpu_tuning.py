@@ -55,7 +55,8 @@ def test_dispatch_measurement_records():
     assert smx.packed_weight_cache_info()["entries"] == 0
     assert records[1]["kind"] == "dispatch_skip"
     for key, entry in table["shapes"].items():
-        assert entry["strassen_ms"] < entry["native_ms"]
+        assert entry["per_call"] or entry["cached"]
+        assert entry["strassen_ms"] < entry["native_ms"] or entry["strassen_cached_ms"] < entry["native_ms"]
 
 
 def test_occupancy_and_decode_measurements():
@@ -68,3 +69,28 @@ def test_occupancy_and_decode_measurements():
     assert dec[0]["shape"] == [16, 1024, 2048]
     assert dec[0]["weight_bytes"]["strassen"] == 7 * dec[0]["weight_bytes"]["hipblaslt"] // 4
     assert all(len(v) == 3 for v in dec[0]["samples_ms"].values())
+
+
+def test_shipped_cached_entry_routes_with_the_cache(monkeypatch):
+    """The shipped table's down projection at 256 tokens won with the
+    packed-weight cache: tuned_matmul sends it to Strassen (bit-identical to
+    the direct call on the entry's tile) while the cache can hold the
+    weight, and to the native GEMM without the cache."""
+    monkeypatch.delenv("SMX_TUNED_TABLE", raising=False)
+    entry = tuning.load_table(tuning.DEFAULT_TABLE)["shapes"].get("256,25600,5120")
+    if entry is None:
+        pytest.skip("the shipped table was measured without this shape")
+    g = torch.Generator(device="cuda").manual_seed(3)
+    a = torch.randn(256, 25600, device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn(5120, 25600, device="cuda", generator=g) * 0.02).to(torch.bfloat16).t()
+    previous = smx.cache_packed_weights(0)
+    try:
+        assert torch.equal(tuning.tuned_matmul(a, w), smx.native_matmul(a, w))
+        smx.cache_packed_weights(1 << 30)
+        bm, bn, bk = entry["tile"]
+        got = tuning.tuned_matmul(a, w)
+        assert torch.equal(got, smx.strassen_matmul(a, w, bm=bm, bn=bn, bk=bk))
+        assert smx.packed_weight_cache_info()["hits"] >= 1
+    finally:
+        smx.cache_packed_weights(0)
+        smx.cache_packed_weights(previous)

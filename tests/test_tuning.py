@@ -64,6 +64,32 @@ def test_tuned_matmul_dispatch_rules(table):
     assert tuning.tuned_matmul(z(512, 1024), z(1000, 512)) == "native"
 
 
+def test_cached_win_needs_the_cache(table, tmp_path, monkeypatch):
+    """An entry that won only with the packed-weight cache goes to Strassen
+    only while the cache can hold the packed weight (7/4 of 2 K N bytes)."""
+    path = tmp_path / "cached.json"
+    path.write_text(json.dumps({"shapes": {"128,1024,512": {"tile": [128, 256, 512], "per_call": False,
+                                                            "cached": True}}}))
+    monkeypatch.setenv("SMX_TUNED_TABLE", str(path))
+    capacity = {"capacity": 0}
+    monkeypatch.setattr(tuning, "packed_weight_cache_info", lambda: dict(capacity))
+    assert tuning.tuned_matmul(z(128, 1024), z(1024, 512)) == "native"
+    capacity["capacity"] = 7 * 1024 * 512 // 2 - 1
+    assert tuning.tuned_matmul(z(128, 1024), z(1024, 512)) == "native"
+    capacity["capacity"] = 7 * 1024 * 512 // 2
+    assert tuning.tuned_matmul(z(128, 1024), z(1024, 512)) == "strassen"
+    assert table[-1] == ("strassen", 128, 256, 512)
+
+
+def test_dispatch_tile():
+    assert tuning.dispatch_tile(8192, 5120, 25600) == (1024, 1024, 512)
+    assert tuning.dispatch_tile(256, 25600, 5120) == (256, 1024, 512)
+    assert tuning.dispatch_tile(384, 1024, 1024) == (128, 1024, 512)
+    assert tuning.dispatch_tile(48, 1024, 1024) == (16, 1024, 512)
+    assert tuning.dispatch_tile(500, 1024, 1024, (256, 256, 512)) is None  # no bm % 16 divides 500
+    assert tuning.dispatch_tile(1024, 1000, 1024) is None and tuning.dispatch_tile(1024, 1024, 1000) is None
+
+
 def test_shipped_table_is_well_formed():
     table = tuning.load_table(tuning.DEFAULT_TABLE)
     assert {"device", "tile", "margin", "rule", "shapes"} <= set(table)
@@ -71,4 +97,8 @@ def test_shipped_table_is_well_formed():
         m, k, n = (int(v) for v in key.split(","))
         bm, bn, bk = entry["tile"]
         assert m % bm == 0 and n % bn == 0 and k % bk == 0
-        assert entry["strassen_ms"] < entry["native_ms"]
+        assert entry["per_call"] or entry["cached"]
+        if entry["per_call"]:
+            assert entry["strassen_ms"] < entry["native_ms"]
+        if entry["cached"]:
+            assert entry["strassen_cached_ms"] < entry["native_ms"]
