@@ -125,12 +125,11 @@ typedef struct smx_gemm_desc {
   int64_t ldp;
   /* Optional device workspace (NULL, or workspace_bytes >= the
    * smx_gemm_workspace_bytes of this descriptor, 16-byte aligned). With it,
-   * a packed launch too small to fill the chip runs every tile as K shares
-   * (up to 16), and one whose last round of tiles would leave at least half
-   * the CUs idle runs that round as two K shares; the shares go into this
-   * FP32 buffer and a pass sums them and applies the epilogue. Without it
-   * every tile runs over full K. The result is the same up to FP32
-   * summation order. */
+   * the tiles of a packed launch's last, partly filled round (every tile of
+   * a launch under one round) run as K shares, up to 16, so that the round
+   * finishes soonest; the shares go into this FP32 buffer and a pass sums
+   * them and applies the epilogue. Without it every tile runs over full K.
+   * The result is the same up to FP32 summation order. */
   void* workspace;
   int64_t workspace_bytes;
 } smx_gemm_desc;
@@ -178,11 +177,14 @@ int smx_gemm_noalloc(const smx_gemm_desc* desc, const void* a, const void* b, vo
 
 /* Bytes of device workspace (s * M * N floats for s K shares) with which
  * smx_gemm splits tiles of this descriptor's launch over K, on the current
- * device; 0 when no split applies: an unpacked call, an FP32 partial, K
- * below 2048, or a tile count T that neither leaves the device's C CUs at
- * least half idle (T <= C / 2: every tile splits min(C / T, 16, K / 512)
- * ways) nor ends in a last round of at most C / 2 tiles (those split two
- * ways). Takes a descriptor smx_gemm accepts; no operand pointer is read.
+ * device. T tiles on the device's C CUs make T / C whole rounds and a last
+ * round of r = T mod C tiles; those r tiles split into the s shares,
+ * 2 <= s <= min(16, K / 512, 2^30 / (4 M N)), that minimise
+ * ceil(s r / C) (1/s + f) + s r g (f = 400 / K, g = (5/3) / K: a workgroup's
+ * fixed time and the summing pass's traffic, in units of a full-K tile's
+ * time), when that is under 0.95 (1 + f). 0 when no split applies: an
+ * unpacked call, an FP32 partial, K below 2048, r = 0, or no s that shortens
+ * the round. Takes a descriptor smx_gemm accepts; no operand pointer is read.
  * SMX_TAIL_SPLIT=0 in the environment turns the split off. No counterpart in
  * the reference (a launch shape of gfx950). */
 int smx_gemm_workspace_bytes(const smx_gemm_desc* desc, int64_t* bytes);

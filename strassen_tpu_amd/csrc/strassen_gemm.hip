@@ -47,6 +47,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 
@@ -368,24 +369,38 @@ void packed_grid(Params& p) {
 // launches take much of the saving (a 128 x 128 Strassen product tile over
 // K = 2048 is 235 MFLOP: 24 us at one CU's peak).
 constexpr int64_t kSplitMinK = 2048;
-// A K share keeps at least this many 32-deep K stages, and a launch splits
-// its tiles at most this many ways.
+// A K share keeps at least this many 32-deep K stages; a launch splits its
+// tiles at most this many ways, and into no more shares than keep the
+// workspace (shares x M x N floats) within kSplitMaxBytes.
 constexpr int kSplitMinStages = 16;
 constexpr int kMaxKSplit = 16;
+constexpr int64_t kSplitMaxBytes = (int64_t)1 << 30;
 
 // Which tiles of a packed launch run as K shares. A launch runs one tile per
 // CU and round: T tiles on C CUs make T / C whole rounds and a last round of
-// r = T mod C. With T <= C / 2 (a small launch: few output tiles, or a
-// decode-sized M) every tile runs as s = min(C / T, 16, stages / 16) shares
-// of its K stages, so that the launch fills the chip. Otherwise, when the
-// last round would leave at least half the CUs idle (0 < r <= C / 2), its r
-// tiles run as two shares each and the round takes about half as long. FP32
-// partials and K below kSplitMinK keep every tile whole.
+// r = T mod C (r = T for a launch under one round). Those r tiles can run as
+// s shares of their K stages, s r workgroups in ceil(s r / C) rounds. In
+// units of one full-K tile's time (about 0.03 K us on MI355X), the split
+// round costs
+//   ceil(s r / C) (1/s + f) + s r g,   f = 400 / K,  g = (5/3) / K:
+// f is a workgroup's fixed prologue and epilogue (about 12 us), g the
+// summing pass's read of one share of one tile (256 KB at about 5 TB/s).
+// The cheapest s of 2 .. s_max splits when it costs under 0.95 of the
+// unsplit round (1 + f). On 256 CUs a launch of 20 tiles over K = 25600
+// splits 12 ways, 128 tiles two ways, a last round of 32 tiles at K = 8192
+// five ways (the workspace bound), one of 224 tiles not at all. FP32
+// partials, K below kSplitMinK and a whole last round keep every tile whole.
 struct SplitPlan {
   int whole;   // tiles 0 .. whole - 1 run over full K, with the epilogue
   int split;   // tiles whole .. whole + split - 1 run as ksplit shares
   int ksplit;
 };
+
+double split_cost(int s, int r, int cus, int64_t k) {
+  const double f = 400.0 / (double)k, g = (5.0 / 3.0) / (double)k;
+  const int rounds = (s * r + cus - 1) / cus;
+  return (double)rounds * (1.0 / (double)s + f) + (double)(s * r) * g;
+}
 
 int split_plan(const Params& p, SplitPlan* plan) {
   *plan = SplitPlan{p.tiles_m * p.tiles_n, 0, 1};
@@ -393,14 +408,21 @@ int split_plan(const Params& p, SplitPlan* plan) {
   int cus = 0;
   if (int rc = device_cus(&cus)) return rc;
   const int tiles = p.tiles_m * p.tiles_n;
-  const int stages = (int)(p.k / (2 * packed::TK));
-  if (2 * tiles <= cus) {
-    const int s = min(min(cus / tiles, kMaxKSplit), stages / kSplitMinStages);
-    if (s >= 2) *plan = SplitPlan{0, tiles, s};
-    return SMX_OK;
-  }
   const int r = tiles % cus;
-  if (r > 0 && 2 * r <= cus) *plan = SplitPlan{tiles - r, r, 2};
+  if (r == 0) return SMX_OK;
+  const int stages = (int)(p.k / (2 * packed::TK));
+  const int64_t share_bytes = p.m * p.n * (int64_t)sizeof(float);
+  const int s_max = (int)std::min<int64_t>(std::min(kMaxKSplit, stages / kSplitMinStages), kSplitMaxBytes / share_bytes);
+  int best_s = 1;
+  double best = 0.95 * split_cost(1, r, cus, p.k);
+  for (int s = 2; s <= s_max; ++s) {
+    const double c = split_cost(s, r, cus, p.k);
+    if (c < best) {
+      best = c;
+      best_s = s;
+    }
+  }
+  if (best_s > 1) *plan = SplitPlan{tiles - r, r, best_s};
   return SMX_OK;
 }
 

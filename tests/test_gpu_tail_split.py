@@ -1,16 +1,16 @@
 """GPU parity of the K splits of packed launches.
 
-A packed launch runs one 128 x 128 product tile per CU per round. Given a
-workspace (and K >= 2048), smx_gemm runs a launch too small to fill the chip
-(T tiles <= C / 2 CUs) as s = min(C / T, 16, K / 512) K shares of every tile,
-and a launch whose last round would leave at least half the CUs idle as its
-whole rounds with the fused epilogue plus that round's tiles as two K
-shares. The shares go into the FP32 workspace and a pass sums them and
-applies the epilogue (strassen_pallas.py:739-879), thin tilings included.
-strassen_matmul / cubic_matmul pass a workspace whenever the library asks for
-one. Checked against the oracle and against the same call without a
-workspace (every tile over full K): the two differ only in the order of FP32
-additions, so they agree within one bf16 ulp and are almost all bit-identical.
+A packed launch runs one 128 x 128 product tile per CU per round: T tiles on
+C CUs make T / C whole rounds and a last round of r = T mod C tiles. Given a
+workspace (and K >= 2048), smx_gemm runs those r tiles (every tile of a
+launch under one round) as s K shares, s chosen so that the s r workgroups
+finish soonest, after the whole rounds with the fused epilogue. The shares
+go into the FP32 workspace and a pass sums them and applies the epilogue
+(strassen_pallas.py:739-879), thin tilings included. strassen_matmul /
+cubic_matmul pass a workspace whenever the library asks for one. Checked
+against the oracle and against the same call without a workspace (every tile
+over full K): the two differ only in the order of FP32 additions, so they
+agree within one bf16 ulp and are almost all bit-identical.
 
 Shapes: with bm = bn = 256 a launch has (M / 256) (N / 256) tiles; on the
 256 CUs of an MI355X, 2048 x 4096 is 128 tiles (every tile in two shares) and
@@ -43,16 +43,27 @@ def _announce(request):
 
 
 def _plan(m, n, k, bm=256):
-    """(whole tiles, split tiles, shares) of the library's rule, restated."""
+    """(whole tiles, split tiles, shares) of the library's rule, restated:
+    the last round's r tiles (all T of a launch under one round) split into
+    the s <= min(16, K / 512, 2^30 / (4 M N)) shares that minimise
+    ceil(s r / C) (1/s + f) + s r g (f = 400 / K, g = (5/3) / K), when that
+    is under 0.95 of the unsplit 1 + f."""
     cus = torch.cuda.get_device_properties(DEV).multi_processor_count
     tiles = -(-(m // 2) // 128) * (n // 256)
-    if k < 2048:
-        return tiles, 0, 1
-    if 2 * tiles <= cus:
-        s = min(cus // tiles, 16, (k // 32) // 16)
-        return (0, tiles, s) if s >= 2 else (tiles, 0, 1)
     r = tiles % cus
-    return (tiles - r, r, 2) if 0 < 2 * r <= cus else (tiles, 0, 1)
+    if k < 2048 or r == 0:
+        return tiles, 0, 1
+    s_max = min(16, (k // 32) // 16, (1 << 30) // (4 * m * n))
+
+    def cost(s):
+        f, g = 400.0 / k, (5.0 / 3.0) / k
+        return ((s * r + cus - 1) // cus) * (1.0 / s + f) + (s * r) * g
+
+    best_s, best = 1, 0.95 * cost(1)
+    for s in range(2, s_max + 1):
+        if cost(s) < best:
+            best_s, best = s, cost(s)
+    return (tiles - r, r, best_s) if best_s > 1 else (tiles, 0, 1)
 
 
 def _split_tiles(m, n, k, bm=256):
