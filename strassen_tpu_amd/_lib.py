@@ -145,3 +145,19 @@ def check(rc):
 
 def ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def k_shares(m, k, n, tile, algo=SMX_ALGO_STRASSEN):
+    """K shares smx_gemm gives the split tiles of a packed (m, k, n) launch
+    on the current device (1: no split), from smx_gemm_workspace_bytes."""
+    lib = load()
+    d = SmxGemmDesc()
+    d.m, d.n, d.k = m, n, k
+    d.lda, d.ldb, d.ldc = k, k, n
+    d.bm, d.bn, d.bk = tile
+    d.algo = algo
+    d.a_layout, d.b_layout = SMX_A_PACKED, SMX_B_PACKED
+    d.rope_head_dim, d.rope_eps = 128, 1e-6
+    need = ctypes.c_int64()
+    check(lib.smx_gemm_workspace_bytes(d, ctypes.byref(need)))
+    return max(1, need.value // (m * n * 4))

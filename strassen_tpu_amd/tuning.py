@@ -365,6 +365,51 @@ def measure_decode(tokens=DECODE_TOKENS, *, k=5120, n=51200, bn=1024, bk=512, se
     return results
 
 
+# Launches with few tiles: the Qwen3-32B down and o projections and the k
+# projection at decode-sized and prefill-chunk M ((m, k, n, bm): 20-40 tiles
+# on 256 CUs), and the k/v projection at 8192 tokens (128 tiles).
+SMALL_LAUNCH_SHAPES = ((16, 25600, 5120, 16), (16, 8192, 5120, 16), (128, 25600, 5120, 128),
+                       (256, 25600, 5120, 256), (512, 25600, 5120, 512), (16, 5120, 1024, 16),
+                       (8192, 5120, 1024, 256))
+
+
+def measure_small_launches(shapes=SMALL_LAUNCH_SHAPES, *, bn=256, bk=512, seed=0, warmups=3, runs=10, batch=10,
+                           device="cuda", emit=None):
+    """Strassen and the cubic on operands packed once (outside the timing),
+    no epilogue, against hipBLASLt, on launches whose few tiles leave most
+    CUs idle unless the K split spreads them; the arms rotate per sample of
+    ``batch`` back-to-back calls. The split's share count comes from the
+    library (``smx_gemm_workspace_bytes``); run once as is and once with
+    SMX_TAIL_SPLIT=0 to time the whole tiles."""
+    emit = emit or (lambda record: None)
+    device = torch.device(device)
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    results = []
+    for m, k, n, bm in shapes:
+        x, w = _inputs(m, k, n, seed, device)
+        packed = {algo: (pack_activation(x, algo, bm, bk),
+                         (strassen_weight_layout if algo == _lib.SMX_ALGO_STRASSEN else cubic_weight_layout)(w, bn, bk))
+                  for algo in (_lib.SMX_ALGO_STRASSEN, _lib.SMX_ALGO_CUBIC)}
+        calls = {"strassen": lambda: strassen_matmul(*packed[_lib.SMX_ALGO_STRASSEN], bm=bm, bn=bn, bk=bk),
+                 "cubic": lambda: cubic_matmul(*packed[_lib.SMX_ALGO_CUBIC], bm=bm, bn=bn, bk=bk),
+                 "hipblaslt": lambda: native_matmul(x, w)}
+        for call in calls.values():
+            time_calls(call, warmups, 0)
+        samples = {arm: [] for arm in calls}
+        names = list(calls)
+        for r in range(runs):
+            for arm in names[r % 3:] + names[:r % 3]:
+                samples[arm] += time_calls(calls[arm], 0, 1, batch=batch)
+        tiles = -(-(m // 2) // 128) * (n // 256)
+        record = {"kind": "small_launch", "shape": [m, k, n], "tile": [bm, bn, bk], "tiles": tiles, "cus": cus,
+                  "k_shares": _lib.k_shares(m, k, n, (bm, bn, bk)),
+                  "median_ms": {arm: statistics.median(v) for arm, v in samples.items()}, "samples_ms": samples}
+        emit(record)
+        results.append(record)
+        del x, w, packed
+    return results
+
+
 _TABLE = None
 
 
@@ -437,7 +482,9 @@ def main(argv=None):
     occupancy.add_argument("--runs", type=int, default=20)
     decode = sub.add_parser("decode", help="the gate|up site with SwiGLU at decode-sized M (thin tiling)")
     decode.add_argument("--runs", type=int, default=30)
-    for p in (screen, dispatch, occupancy, decode):
+    small = sub.add_parser("small", help="Strassen, cubic and hipBLASLt on launches with few tiles (the K split)")
+    small.add_argument("--runs", type=int, default=10)
+    for p in (screen, dispatch, occupancy, decode, small):
         p.add_argument("--out", default=None, help="also append the JSON records to this file")
     args = ap.parse_args(argv)
     sink = open(args.out, "a") if args.out else None
@@ -457,6 +504,8 @@ def main(argv=None):
         measure_occupancy(runs=args.runs, emit=emit)
     elif args.command == "decode":
         measure_decode(runs=args.runs, emit=emit)
+    elif args.command == "small":
+        measure_small_launches(runs=args.runs, emit=emit)
     else:
         table = measure_dispatch(DISPATCH_SHAPES, runs=args.runs, emit=emit)
         emit({"kind": "table", **table})

@@ -94,3 +94,12 @@ def test_shipped_cached_entry_routes_with_the_cache(monkeypatch):
     finally:
         smx.cache_packed_weights(0)
         smx.cache_packed_weights(previous)
+
+
+def test_small_launch_measurement():
+    """The small-launch measurement records the library's share count (at
+    least two for 20 tiles over K = 4096) and samples every arm."""
+    rec = tuning.measure_small_launches([(16, 4096, 5120, 16)], warmups=1, runs=3, batch=2)[0]
+    assert rec["tiles"] == 20 and rec["k_shares"] >= 2
+    assert set(rec["median_ms"]) == {"strassen", "cubic", "hipblaslt"}
+    assert all(len(v) == 3 for v in rec["samples_ms"].values())
