@@ -523,8 +523,9 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
         if rope_scale.dtype == torch.float32:
             aux |= _lib.SMX_AUX_SCALE_F32
     desc.aux_f32 = aux
-    # The last round of tiles runs as two K halves when the library asks
-    # for a workspace (FP32 halves of the output, summed by a second pass).
+    # The tiles of a partly filled last round run as K shares when the
+    # library asks for a workspace (FP32 shares of the output, summed by a
+    # second pass).
     need = ctypes.c_int64()
     _lib.check(lib.smx_gemm_workspace_bytes(desc, ctypes.byref(need)))
     workspace = None
