@@ -45,6 +45,12 @@ struct Plan {
   __device__ __forceinline__ static constexpr int row(int j) { return (kFirst + j) % 4; }
   // Whether strip j starts a product (its B fragments must be read).
   __device__ __forceinline__ static constexpr bool opens(int j) { return j == 0 || product(j) != product(j - 1); }
+  // The strip of product q and block row r, or -1 if another wave owns it.
+  __device__ __forceinline__ static constexpr int strip_of(int q, int r) {
+    for (int j = 0; j < 7; ++j)
+      if (product(j) == q && row(j) == r) return j;
+    return -1;
+  }
 };
 
 // Accumulators of strips 0-3 live in AGPRs, strips 4-6 in VGPRs.
@@ -248,7 +254,11 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
   // compiler declines to unroll (its body holds the inlined epilogue) would
   // index the block arrays at run time and move them to scratch.
   //
-  // Round t's blocks of this wave's strips into their destination slots.
+  // Round t's blocks of this wave's strips into their destination slots;
+  // outside q/k, a block this wave receives itself stays in its registers
+  // (receive). The q/k kernels, whose epilogue holds two blocks' quadrant
+  // sets, spill when those registers stay live, so they move every block.
+  constexpr bool kKeepOwn = !kPairs;
   auto send = [&](auto tc) __attribute__((always_inline)) {
     constexpr int t = decltype(tc)::value, i = t >> 1, jj = t & 1;
     // the lane's byte offset, re-derived opaquely each round so that no copy
@@ -261,6 +271,7 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
 #pragma unroll
       for (int c = jj; c < 4; c += 2) {
         const int dest = 2 * (r / 2) + c / 2;
+        if (kKeepOwn && dest == kWave) continue;
         uint8_t* const slot = lds + (dest * 7 + P::product(j)) * kBlockBytes + lane16;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -270,11 +281,19 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
       }
     }
   };
-  // The seven products of the round's block from this wave's slots.
-  auto receive = [&](f32x16 (&blk)[7][1][1]) __attribute__((always_inline)) {
+  // The seven products of round t's block: from this wave's own strips where
+  // it owns them, else from its slots.
+  auto receive = [&](auto tc, f32x16 (&blk)[7][1][1]) __attribute__((always_inline)) {
+    constexpr int t = decltype(tc)::value, i = t >> 1, jj = t & 1;
     const uint32_t lane16 = opaque_lane_id() * 16;
 #pragma unroll
     for (int q = 0; q < 7; ++q) {
+      const int own = kKeepOwn ? P::strip_of(q, 2 * (kWave >> 1) + i) : -1;
+      if (own >= 0) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) blk[q][0][0][e] = acc[own][2 * (kWave & 1) + jj][e];
+        continue;
+      }
       const uint8_t* const slot = mine + q * kBlockBytes + lane16;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -293,7 +312,7 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
       send(tc);
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       f32x16 blk[7][1][1];
-      receive(blk);
+      receive(tc, blk);
       // the block's reads complete before its slots turn into staging tiles
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
@@ -322,7 +341,7 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
     auto step = [&](auto tc) __attribute__((always_inline)) {
       constexpr int t = decltype(tc)::value, i = t >> 1, jj = t & 1;
       f32x16 blk[7][1][1];
-      receive(blk);
+      receive(tc, blk);
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       if constexpr (t < 3) send(QuadC<t + 1>{});
       epilogue_body<1, 1, kEpi, 7, kQuad, kThin>(p, o, wm * 64 + i * 32, wn * 64 + jj * 32, blk, stage);
