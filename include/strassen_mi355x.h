@@ -144,7 +144,7 @@ typedef struct smx_gemm_desc {
  * (SMX_AUX_RESIDUAL_F32). bias: [n] bf16 or f32. rope_cos / rope_sin: bf16 [m, bn/2] tables
  * indexed by output row (rope_layout_tables). rope_scale: [bn] bf16 or f32
  * (rope_scale_layout). Unused pointers may be NULL. The epilogue moves C,
- * residual and partial rows, and reads the RoPE tables, in 16-byte chunks:
+ * residual and partial rows, and reads the RoPE tables and scale, in 16-byte chunks:
  * those pointers must be 16-byte aligned and their row strides keep every
  * row 16-byte aligned (ldc, ldr a multiple of 8 elements for bf16, 4 for
  * float32; ldp a multiple of 4).

@@ -445,6 +445,27 @@ __device__ __forceinline__ float load_vec(const void* v, int is_f32, int64_t i) 
   return is_f32 ? reinterpret_cast<const float*>(v)[i] : bf16_to_f32(reinterpret_cast<const uint16_t*>(v)[i]);
 }
 
+// Eight values of an [.., ld] array at element i (i % 8 == 0 for bf16,
+// i % 4 == 0 for float32 rows: 16-byte loads).
+__device__ __forceinline__ F8 load8(const void* base, int is_f32, int64_t i) {
+  if (is_f32) {
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(base) + i);
+    const f32x4 hi = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(base) + i + 4);
+    return F8{{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}};
+  }
+  return unpack8(*reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(base) + i));
+}
+
+__device__ __forceinline__ void store8(void* base, int out_f32, int64_t i, const F8& x) {
+  if (out_f32) {
+    float* const o = reinterpret_cast<float*>(base) + i;
+    *reinterpret_cast<f32x4*>(o) = f32x4{x.v[0], x.v[1], x.v[2], x.v[3]};
+    *reinterpret_cast<f32x4*>(o + 4) = f32x4{x.v[4], x.v[5], x.v[6], x.v[7]};
+  } else {
+    *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(base) + i) = pack8(x);
+  }
+}
+
 // Sum over the 32 lanes of a half-wave (lanes sharing lane>>5), the same
 // total in every lane. DPP adds within rows of 16 lanes (quad_perm
 // [1,0,3,2] and [2,3,0,1]: pairs and quads; row_half_mirror: lane i with
@@ -797,8 +818,8 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
     // Rotation and store by 16-byte row chunks (the staging tile's store
     // pattern). A lane always takes the same chunk column, eight columns c0..
     // of the tile half: it reads their scale (gamma) once per row half, and
-    // the RoPE tables ([M, hn] bf16, by output row and column inside the
-    // half) eight values per load. out_a = a' cos - b' sin and out_b =
+    // the scale and the RoPE tables ([M, hn] bf16, by output row and column
+    // inside the half) eight values per 16-byte-aligned load. out_a = a' cos - b' sin and out_b =
     // b' cos + a' sin with a' = (a * recip) * gamma_a, b' = (b * recip) *
     // gamma_b, as the reference orders them (strassen_pallas.py:821-827).
     constexpr int kChunks = T::kCols / 8;
@@ -807,12 +828,7 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
     const int64_t c0 = cc_base + ch * 8;
     auto rotate_store = [&](int half) __attribute__((always_inline)) {
       fence();
-      float ga[8], gb[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        ga[e] = load_vec(p.rope_scale, p.scale_f32, c0 + e);
-        gb[e] = load_vec(p.rope_scale, p.scale_f32, hn + c0 + e);
-      }
+      const F8 ga = load8(p.rope_scale, p.scale_f32, c0), gb = load8(p.rope_scale, p.scale_f32, hn + c0);
       const int es = p.out_f32 ? 4 : 2;
       char* const out_cols = reinterpret_cast<char*>(p.c) + (col_base + ch * 8) * es;
 #pragma unroll
@@ -836,8 +852,8 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
         F8 oa, ob;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float na = (e < 4 ? a_lo[e & 3] : a_hi[e & 3]) * ga[e];
-          const float nb = (e < 4 ? b_lo[e & 3] : b_hi[e & 3]) * gb[e];
+          const float na = (e < 4 ? a_lo[e & 3] : a_hi[e & 3]) * ga.v[e];
+          const float nb = (e < 4 ? b_lo[e & 3] : b_hi[e & 3]) * gb.v[e];
           oa.v[e] = na * cs.v[e] - nb * sn.v[e];
           ob.v[e] = nb * cs.v[e] + na * sn.v[e];
         }
@@ -877,7 +893,9 @@ __device__ __forceinline__ void epilogue_body(const Params& p, const TileOrigin&
             const float b0 = qb(i, 2 * h, r), b1 = qb(i, 2 * h + 1, r);
             const float ssa = half_wave_sum(a0 * a0 + a1 * a1);
             const float ssb = half_wave_sum(b0 * b0 + b1 * b1);
-            const float recip = 1.0f / sqrtf((ssa + ssb) * inv_width + p.eps);
+            // the reference's jax.lax.rsqrt (strassen_pallas.py:818) as the
+            // hardware reciprocal square root, within 1 ulp of 1 / sqrt
+            const float recip = __builtin_amdgcn_rsqf((ssa + ssb) * inv_width + p.eps);
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj) {
               const int j = 2 * h + jj;

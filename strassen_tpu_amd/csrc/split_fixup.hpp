@@ -11,27 +11,6 @@
 
 namespace smx {
 
-// Eight values of an [.., ld] array at element i (i % 8 == 0 for bf16,
-// i % 4 == 0 for float32 rows: 16-byte loads).
-__device__ __forceinline__ F8 load8(const void* base, int is_f32, int64_t i) {
-  if (is_f32) {
-    const f32x4 lo = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(base) + i);
-    const f32x4 hi = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(base) + i + 4);
-    return F8{{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}};
-  }
-  return unpack8(*reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(base) + i));
-}
-
-__device__ __forceinline__ void store8(void* base, int out_f32, int64_t i, const F8& x) {
-  if (out_f32) {
-    float* const o = reinterpret_cast<float*>(base) + i;
-    *reinterpret_cast<f32x4*>(o) = f32x4{x.v[0], x.v[1], x.v[2], x.v[3]};
-    *reinterpret_cast<f32x4*>(o + 4) = f32x4{x.v[4], x.v[5], x.v[6], x.v[7]};
-  } else {
-    *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(base) + i) = pack8(x);
-  }
-}
-
 // Workgroups per split tile: each takes 32 of the tile's 256 output rows, so
 // a pass over r tiles runs 8 r workgroups and keeps enough loads in flight
 // to stream at HBM speed.
@@ -117,8 +96,8 @@ __global__ __launch_bounds__(256) void split_fixup(Params p, const float* __rest
     }
     if constexpr (kEpi == SMX_EPI_QK_NORM_ROPE) {
       // A head is 64 columns of each half: eight lanes (t % 8 equal
-      // neighbours) of a row. recip = 1 / sqrt((sum a^2 + sum b^2) /
-      // head_dim + eps); a' = (a recip) gamma_a, b' = (b recip) gamma_b;
+      // neighbours) of a row. recip = rsqrt((sum a^2 + sum b^2) /
+      // head_dim + eps) (v_rsq_f32, as in the fused epilogue); a' = (a recip) gamma_a, b' = (b recip) gamma_b;
       // out_a = a' cos - b' sin, out_b = b' cos + a' sin (cos, sin at the
       // output row and the column inside the half).
       float ssa = 0.f, ssb = 0.f;
@@ -132,7 +111,7 @@ __global__ __launch_bounds__(256) void split_fixup(Params p, const float* __rest
         ssa += __shfl_xor(ssa, x);
         ssb += __shfl_xor(ssb, x);
       }
-      const float recip = 1.0f / sqrtf((ssa + ssb) * inv_width + p.eps);
+      const float recip = __builtin_amdgcn_rsqf((ssa + ssb) * inv_width + p.eps);
       const F8 cs = unpack8(*reinterpret_cast<const u32x4*>(p.rope_cos + row * hn + cin));
       const F8 sn = unpack8(*reinterpret_cast<const u32x4*>(p.rope_sin + row * hn + cin));
 #pragma unroll

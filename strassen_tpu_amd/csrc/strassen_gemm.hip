@@ -309,9 +309,9 @@ int gemm_params(const smx_gemm_desc* d, const void* a, const void* b, void* c, c
     case SMX_EPI_QK_NORM_ROPE:
       if (!rope_cos || !rope_sin || !rope_scale)
         return fail(SMX_ERR_INVALID, "qk_norm_rope requires rope_cos, rope_sin and rope_scale");
-      // the epilogue reads the tables eight values (16 bytes) at a time
-      if (!aligned16(rope_cos) || !aligned16(rope_sin))
-        return fail(SMX_ERR_INVALID, "rope_cos and rope_sin must be 16-byte aligned");
+      // the epilogue reads the tables and the scale 16 bytes at a time
+      if (!aligned16(rope_cos) || !aligned16(rope_sin) || !aligned16(rope_scale))
+        return fail(SMX_ERR_INVALID, "rope_cos, rope_sin and rope_scale must be 16-byte aligned");
       if (d->rope_head_dim != 128)
         return fail(SMX_ERR_UNSUPPORTED,
                     "the fused qk_norm_rope takes head_dim 128, got %d: run smx_gemm with SMX_FLAG_OUT_F32 and no "

@@ -516,10 +516,11 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
         # float32 tables are rounded to bf16 here.
         rope_cos = rope_cos.to(torch.bfloat16).contiguous()
         rope_sin = rope_sin.to(torch.bfloat16).contiguous()
-        # the kernels read the tables 16 bytes at a time
+        # the kernels read the tables and the scale 16 bytes at a time
         rope_cos = rope_cos if rope_cos.data_ptr() % 16 == 0 else rope_cos.clone()
         rope_sin = rope_sin if rope_sin.data_ptr() % 16 == 0 else rope_sin.clone()
         rope_scale = _aux_tensor(rope_scale.contiguous())
+        rope_scale = rope_scale if rope_scale.data_ptr() % 16 == 0 else rope_scale.clone()
         if rope_scale.dtype == torch.float32:
             aux |= _lib.SMX_AUX_SCALE_F32
     desc.aux_f32 = aux

@@ -346,6 +346,23 @@ def test_epilogue_rows_are_16_byte_aligned(case, match):
     assert match in _lib.last_error()
 
 
+@pytest.mark.parametrize("odd_arg", ["rope_cos", "rope_sin", "rope_scale"])
+def test_qk_tables_and_scale_are_16_byte_aligned(odd_arg):
+    """The q/k epilogue reads the RoPE tables and the per-column scale eight
+    values (16 bytes) at a time: a misaligned pointer to any of them is
+    refused before any launch."""
+    lib = _lib.load()
+    buf = (ctypes.c_uint8 * 256)()
+    base = (ctypes.addressof(buf) + 15) & ~15
+    good, odd = ctypes.c_void_p(base), ctypes.c_void_p(base + 2)
+    rope = {"rope_cos": good, "rope_sin": good, "rope_scale": good}
+    rope[odd_arg] = odd
+    d = _desc(epilogue=_lib.SMX_EPI["qk_norm_rope"])
+    rc = lib.smx_gemm(d, good, good, good, None, None, rope["rope_cos"], rope["rope_sin"], rope["rope_scale"], None)
+    assert rc == _lib.SMX_ERR_INVALID
+    assert "must be 16-byte aligned" in _lib.last_error() and "rope_scale" in _lib.last_error()
+
+
 def test_workspace_arguments():
     """The tail-split workspace: a misaligned pointer or a negative size is
     refused before any launch, as is every descriptor smx_gemm refuses; an
