@@ -40,6 +40,7 @@ __global__ __launch_bounds__(256) void split_fixup(Params p, const float* __rest
   const int64_t col_a = o.tj * p.bn + cin, col_b = col_a + hn;
   F8 bias_a{}, bias_b{}, ga{}, gb{};
   if constexpr (kEpi == SMX_EPI_BIAS_ADD) {
+    // the bias has no alignment requirement: element loads
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       bias_a.v[e] = load_vec(p.bias, p.bias_f32, col_a + e);
@@ -47,11 +48,8 @@ __global__ __launch_bounds__(256) void split_fixup(Params p, const float* __rest
     }
   }
   if constexpr (kEpi == SMX_EPI_QK_NORM_ROPE) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      ga.v[e] = load_vec(p.rope_scale, p.scale_f32, cin + e);
-      gb.v[e] = load_vec(p.rope_scale, p.scale_f32, hn + cin + e);
-    }
+    ga = load8(p.rope_scale, p.scale_f32, cin);
+    gb = load8(p.rope_scale, p.scale_f32, hn + cin);
   }
   const float inv_width = 1.0f / (float)p.head_dim;
 #pragma unroll
