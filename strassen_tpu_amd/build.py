@@ -117,28 +117,20 @@ def verify_inline_asm_kernels(asm_text):
 # Scratch (private segment) per GEMM kernel, in bytes per lane. The Strassen
 # kernels and the matched cubic keep their accumulators, fragments and
 # addresses in registers: a spill there is reloaded on every tile, so the
-# build refuses it. Two exceptions carry a stated cap: the q/k epilogue of the
-# Strassen kernel (20 bytes, in full and thin tilings: its first exchange
-# round holds the register file's peak) and the cubic that adds an FP32
-# partial product before its epilogue (the exact-panel path, off the hot
-# path).
+# build refuses it. One exception carries a stated cap: the cubic that adds
+# an FP32 partial product before its epilogue (the exact-panel path, off the
+# hot path).
 _KERNEL_DESC = re.compile(r"\.amdhsa_kernel (\S+)(.*?)\.end_amdhsa_kernel", re.S)
 _SPLIT = re.compile(r"gemm_splitILi(\d+)ELi(\d+)ELb(\d)E")
 _PACKED = re.compile(r"gemm_packedILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb(\d)E")
-_EPI_QK = 4
 _QUAD_CUBIC_PARTIAL = 1
-QK_SCRATCH_CAP = 32
-THIN_QK_SCRATCH_CAP = 32
 PARTIAL_SCRATCH_CAP = 1024
 
 
 def scratch_limit(name):
     """Allowed scratch bytes per lane of a kernel (None: not a GEMM kernel)."""
-    m = _SPLIT.search(name)
-    if m:
-        if int(m.group(1)) != _EPI_QK:
-            return 0
-        return THIN_QK_SCRATCH_CAP if m.group(3) == "1" else QK_SCRATCH_CAP
+    if _SPLIT.search(name):
+        return 0
     m = _PACKED.search(name)
     if m:
         return PARTIAL_SCRATCH_CAP if int(m.group(3)) == _QUAD_CUBIC_PARTIAL else 0

@@ -430,18 +430,18 @@ def test_kernel_scratch_check():
     thin_cubic = "_ZN3smx6packed11gemm_packedILi8ELi2ELi0ELi3ELb1EEEvNS_6ParamsE"
     other = "_ZN3smx6packed9pack_rowsILi7ELi0EEEvPKtlliiiiPKiiPh"
     assert build.scratch_limit(split_swiglu) == 0
-    assert build.scratch_limit(split_qk) == build.QK_SCRATCH_CAP
+    assert build.scratch_limit(split_qk) == 0
     assert build.scratch_limit(thin_swiglu) == 0
-    assert build.scratch_limit(thin_qk) == build.THIN_QK_SCRATCH_CAP
+    assert build.scratch_limit(thin_qk) == 0
     assert build.scratch_limit(cubic) == 0
     assert build.scratch_limit(cubic_partial) == build.PARTIAL_SCRATCH_CAP
     assert build.scratch_limit(thin_cubic) == 0
     assert build.scratch_limit(other) is None
-    clean = (desc(split_swiglu, 0) + desc(split_qk, 20) + desc(thin_qk, 20) + desc(cubic, 0)
+    clean = (desc(split_swiglu, 0) + desc(split_qk, 0) + desc(thin_qk, 0) + desc(cubic, 0)
              + desc(cubic_partial, 792) + desc(other, 64))
     assert build.verify_kernel_scratch(clean) == 5
-    for name, size in ((split_swiglu, 8), (split_qk, build.QK_SCRATCH_CAP + 4), (thin_swiglu, 4),
-                       (thin_qk, build.THIN_QK_SCRATCH_CAP + 4), (cubic, 4), (thin_cubic, 4),
+    for name, size in ((split_swiglu, 8), (split_qk, 4), (thin_swiglu, 4),
+                       (thin_qk, 4), (cubic, 4), (thin_cubic, 4),
                        (cubic_partial, build.PARTIAL_SCRATCH_CAP + 4)):
         with pytest.raises(RuntimeError, match="scratch per lane"):
             build.verify_kernel_scratch(clean + desc(name, size))
