@@ -289,6 +289,7 @@ struct Params {
   float eps;
   int32_t tiles_m, tiles_n;  // product-space workgroup grid
   int32_t group_m;           // tile rows per rasterization group
+  int32_t raster;            // tile order (kRaster*, tile_of)
   int32_t out_f32;           // store float32 instead of bf16
   int32_t formula;           // kFormula* (Strassen family)
   int32_t perm;              // block permutation bits: 1 rows, 2 K, 4 columns
@@ -341,15 +342,54 @@ __device__ __forceinline__ WorkShare work_share(const Params& p, int nstages_all
 }
 
 // Workgroup id -> product-space tile. Workgroups are dispatched round-robin
-// over the 8 XCDs; consecutive logical tiles are gathered on one XCD so that
-// neighbouring tiles share its L2, and inside an XCD tiles walk column groups
-// of group_m rows (an A row panel is reused across the group's columns).
-__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
-  const int total = tiles_m * tiles_n;
-  int logical = bid;
-  if (total % 8 == 0) {
-    const int per_xcd = total / 8;
-    logical = (bid % 8) * per_xcd + bid / 8;
+// over the 8 XCDs (bid % 8), and an XCD's 32 CUs run its workgroups in the
+// order bid / 8, 32 at a time. Tiles walk column groups of group_m rows, so
+// that 32 concurrent tiles on an XCD are group_m rows x 32 / group_m
+// columns (8 A and 4 B panels for group_m = 8: the fewest for 32 tiles)
+// and share them in its L2. Where the 8 XCDs' concurrent tiles sit decides
+// how often an L2 miss is served by the MALL (memory-side cache, 256 MB)
+// rather than HBM, which the Strassen kernel's operand stream feels:
+//   kRasterSpread: XCD x takes the x-th eighth of the order. All tile rows
+//     run at once and each B panel is shared by several XCDs: the order for
+//     a packed A that stays in the MALL;
+//   kRasterChunks: XCD x takes chunks x, x + 8, ... of 32 tiles of the
+//     order, so a round is 8 consecutive chunks: few tile rows, each shared
+//     by several XCDs, and all B columns of a narrow launch, which then stay
+//     in the MALL;
+//   kRasterBlocks: chunks as above over super-blocks of 2 group_m rows x
+//     4 chunk widths, so a round is a 2 x 4 grid of XCD blocks that shares
+//     each A panel 4 ways and each B panel 2 ways, for launches where
+//     neither operand stays in the MALL.
+constexpr int kRasterSpread = 0, kRasterChunks = 1, kRasterBlocks = 2;
+constexpr int kXcds = 8, kXcdTiles = 32;
+
+__host__ __device__ inline int xcd_order(int bid, int total, int raster) {
+  if (total % kXcds) return bid;
+  const int per_xcd = total / kXcds, x = bid % kXcds, slot = bid / kXcds;
+  if (raster == kRasterSpread) return x * per_xcd + slot;
+  const int full = per_xcd / kXcdTiles * kXcdTiles;
+  return slot < full ? ((slot / kXcdTiles) * kXcds + x) * kXcdTiles + slot % kXcdTiles
+                     : full * kXcds + x * (per_xcd - full) + (slot - full);
+}
+
+__host__ __device__ inline void tile_of(int bid, int tiles_m, int tiles_n, int group_m, int raster, int& tm,
+                                        int& tn) {
+  const int logical = xcd_order(bid, tiles_m * tiles_n, raster);
+  if (raster == kRasterBlocks) {
+    const int chunk_cols = kXcdTiles / group_m > 0 ? kXcdTiles / group_m : 1;
+    const int sg_rows = 2 * group_m, strip = 4 * chunk_cols;
+    const int sg = logical / (sg_rows * tiles_n);
+    const int h = min(sg_rows, tiles_m - sg * sg_rows);
+    const int in_sg = logical - sg * sg_rows * tiles_n;
+    const int t = in_sg / (h * strip);
+    const int w = min(strip, tiles_n - t * strip);
+    const int in_strip = in_sg - t * h * strip;
+    const int h1 = min(group_m, h);
+    const bool second = in_strip >= h1 * w;
+    const int k = second ? in_strip - h1 * w : in_strip, rows = second ? h - h1 : h1;
+    tm = sg * sg_rows + (second ? h1 : 0) + k % rows;
+    tn = t * strip + k / rows;
+    return;
   }
   const int group_size = group_m * tiles_n;
   const int group = logical / group_size;

@@ -155,7 +155,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
   const WorkShare ws = work_share(p, nstages_all);
   if (ws.share) p.c = reinterpret_cast<float*>(p.c) + ws.share * p.split_stride;
   int tile_m, tile_n;
-  tile_of(ws.tile, p.tiles_m, p.tiles_n, p.group_m, tile_m, tile_n);
+  tile_of(ws.tile, p.tiles_m, p.tiles_n, p.group_m, p.raster, tile_m, tile_n);
   const TileOrigin o = tile_origin<kThin>(p, (int64_t)tile_m * TM, (int64_t)tile_n * TN);
   const int nstages = ws.nstages;
 

@@ -367,7 +367,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
   const WorkShare ws = work_share(p, nstages_all);
   if (ws.share) p.c = reinterpret_cast<float*>(p.c) + ws.share * p.split_stride;
   int tile_m, tile_n;
-  tile_of(ws.tile, p.tiles_m, p.tiles_n, p.group_m, tile_m, tile_n);
+  tile_of(ws.tile, p.tiles_m, p.tiles_n, p.group_m, p.raster, tile_m, tile_n);
   // The tile indices are uniform, but the integer divisions that produce
   // them run on VALU; readfirstlane moves them (and every operand address
   // derived from them) to SGPRs, which keeps VGPRs for the accumulators.

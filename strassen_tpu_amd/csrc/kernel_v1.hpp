@@ -182,7 +182,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_v1(Params p) {
   const int wave_n = wave % C::wn;
 
   int tile_m, tile_n;
-  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tile_m, tile_n);
+  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, p.raster, tile_m, tile_n);
   const TileOrigin o = tile_origin(p, (int64_t)tile_m * C::TM, (int64_t)tile_n * C::TN);
   const int hm = p.bm / 2, hn = p.bn / 2;
   const int64_t a_row0[2] = {o.ti * p.bm + o.tr, o.ti * p.bm + hm + o.tr};

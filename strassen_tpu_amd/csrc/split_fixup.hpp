@@ -30,7 +30,7 @@ template <int kEpi>
 __global__ __launch_bounds__(256) void split_fixup(Params p, const float* __restrict__ ws) {
   const int u = (int)blockIdx.x / kFixupSlices, slice = (int)blockIdx.x % kFixupSlices;
   int tile_m, tile_n;
-  tile_of(p.tile_base + u, p.tiles_m, p.tiles_n, p.group_m, tile_m, tile_n);
+  tile_of(p.tile_base + u, p.tiles_m, p.tiles_n, p.group_m, p.raster, tile_m, tile_n);
   const TileOrigin o = tile_origin<false>(p, (int64_t)tile_m * packed::TM, (int64_t)tile_n * packed::TN);
   const ThinRows rows{(uint32_t)(p.bm / 2), (uint32_t)p.bm, (uint32_t)(p.m / 2)};
   const uint32_t prow0 = (uint32_t)tile_m * packed::TM;

@@ -85,7 +85,21 @@ int group_m_setting() {
   static const int value = [] {
     const char* env = getenv("SMX_GROUP_M");
     const int v = env ? atoi(env) : 0;
-    return v > 0 ? v : 8;
+    return v > 0 && v <= 64 ? v : 8;
+  }();
+  return value;
+}
+
+// Tile order of a packed launch (tile_of): SMX_RASTER=spread, chunks or
+// blocks forces one; unset (-1), packed_grid chooses.
+int raster_setting() {
+  static const int value = [] {
+    const char* env = getenv("SMX_RASTER");
+    if (!env) return -1;
+    if (!strcmp(env, "spread")) return (int)kRasterSpread;
+    if (!strcmp(env, "chunks")) return (int)kRasterChunks;
+    if (!strcmp(env, "blocks")) return (int)kRasterBlocks;
+    return -1;
   }();
   return value;
 }
@@ -358,11 +372,37 @@ bool split_setting() {
   return value;
 }
 
-// Packed launch grid (p.tiles_m, p.tiles_n, p.group_m) of a checked call.
-void packed_grid(Params& p) {
+// Bytes of packed operand the MALL (the 256 MB memory-side cache shared by
+// the XCDs) keeps across a launch's rounds next to the streaming operand.
+constexpr int64_t kMallResident = (int64_t)192 << 20;
+
+// Tile order (tile_of) of a packed launch, from its packed operand sizes.
+// Measured on MI355X (whole rounds, Strassen): a packed A that the MALL
+// holds runs fastest spread over all tile rows (8192 x 5120 x 20480: 1.47 ms
+// spread, 1.55 chunks); a larger A with a B that fits runs fastest in chunks
+// (16384 x 5120 x 10240: 1.63 ms spread, 1.51 chunks); when neither fits
+// but a round's 32 panels do, in blocks (8192 x 8192 x 20480: 2.47 ms
+// spread, 2.35 blocks); with panels beyond that no order gains (8192 x 25600
+// x 5120: 2.09-2.11 ms).
+int raster_for(const Params& p, int algo) {
+  const int64_t nops = packed::nops_of(algo), depth = p.k / 2;
+  const int64_t panel = (int64_t)packed::TM * depth * nops * 2;
+  const int64_t a_bytes = (int64_t)p.tiles_m * panel, b_bytes = (int64_t)p.tiles_n * panel;
+  if (a_bytes <= kMallResident) return kRasterSpread;
+  if (b_bytes <= kMallResident) return kRasterChunks;
+  // a blocks round reads 16 A and 16 B panels
+  if (32 * panel <= ((int64_t)256 << 20)) return kRasterBlocks;
+  return kRasterSpread;
+}
+
+// Packed launch grid (p.tiles_m, p.tiles_n, p.group_m, p.raster) of a
+// checked call.
+void packed_grid(Params& p, int algo) {
   p.tiles_m = (int)(packed::padded_product_rows(p.m) / packed::TM);
   p.tiles_n = (int)((p.n / 2) / packed::TN);
   p.group_m = group_m_setting();
+  const int forced = raster_setting();
+  p.raster = forced >= 0 ? forced : raster_for(p, algo);
 }
 
 // Depth below which a split's rounds are short enough that its two extra
@@ -462,7 +502,7 @@ int launch_packed(const Params& p, int algo, int epilogue, hipStream_t s) {
 int launch_gemm(Params p, const smx_gemm_desc& d, hipStream_t s) {
   if (d.b_layout != SMX_B_PACKED)
     return d.algo == SMX_ALGO_STRASSEN ? dispatch_v1<7>(p, d.epilogue, s) : dispatch_v1<8>(p, d.epilogue, s);
-  packed_grid(p);
+  packed_grid(p, d.algo);
   SplitPlan plan{p.tiles_m * p.tiles_n, 0, 1};
   if (d.workspace) {
     if (int rc = split_plan(p, &plan)) return rc;
@@ -681,7 +721,7 @@ int smx_gemm_workspace_bytes(const smx_gemm_desc* d, int64_t* bytes) {
   Params p{};
   if (int rc = gemm_params(d, x, x, const_cast<void*>(x), x, x, x, x, x, p)) return rc;
   if (d->b_layout != SMX_B_PACKED) return SMX_OK;
-  packed_grid(p);
+  packed_grid(p, d->algo);
   SplitPlan plan{};
   if (int rc = split_plan(p, &plan)) return rc;
   if (plan.split) *bytes = split_bytes(p, plan);

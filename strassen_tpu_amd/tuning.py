@@ -316,6 +316,7 @@ def measure_occupancy(shapes=OCCUPANCY_SHAPES, *, tile=(1024, 1024, 512), seed=0
         tiles = (m // 256) * (n // 256)
         rounds = tiles / cus
         record = {"kind": "occupancy", "shape": [m, k, n], "tile": list(tile), "tiles": tiles, "cus": cus,
+                  "settings": {name: os.environ.get(name) for name in ("SMX_RASTER", "SMX_TAIL_SPLIT")},
                   "rounds": rounds, "mean_ms": means, "ms_per_round_of_work": {a: v / rounds for a, v in means.items()},
                   "strassen_speed_over_cubic": means["cubic"] / means["strassen"], "samples_ms": samples}
         emit(record)
@@ -480,6 +481,8 @@ def main(argv=None):
     dispatch.add_argument("--table", default=None, help="write the dispatch table here")
     occupancy = sub.add_parser("occupancy", help="Strassen and cubic on launches that fill part of the chip")
     occupancy.add_argument("--runs", type=int, default=20)
+    occupancy.add_argument("--shapes", default=None,
+                           help="M,K,N shapes separated by ';' (default: OCCUPANCY_SHAPES)")
     decode = sub.add_parser("decode", help="the gate|up site with SwiGLU at decode-sized M (thin tiling)")
     decode.add_argument("--runs", type=int, default=30)
     small = sub.add_parser("small", help="Strassen, cubic and hipBLASLt on launches with few tiles (the K split)")
@@ -501,7 +504,10 @@ def main(argv=None):
         m, k, n = (int(v) for v in args.shape.split(","))
         screen_tiles(m, k, n, swiglu=not args.no_swiglu, warmups=args.warmups, runs=args.runs, emit=emit)
     elif args.command == "occupancy":
-        measure_occupancy(runs=args.runs, emit=emit)
+        shapes = OCCUPANCY_SHAPES
+        if args.shapes:
+            shapes = tuple(tuple(int(v) for v in shape.split(",")) for shape in args.shapes.split(";"))
+        measure_occupancy(shapes, runs=args.runs, emit=emit)
     elif args.command == "decode":
         measure_decode(runs=args.runs, emit=emit)
     elif args.command == "small":
