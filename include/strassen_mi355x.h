@@ -147,7 +147,10 @@ typedef struct smx_gemm_desc {
  * residual and partial rows, and reads the RoPE tables and scale, in 16-byte chunks:
  * those pointers must be 16-byte aligned and their row strides keep every
  * row 16-byte aligned (ldc, ldr a multiple of 8 elements for bf16, 4 for
- * float32; ldp a multiple of 4).
+ * float32; ldp a multiple of 4). The packed kernel orders its tiles over the
+ * XCDs by the packed operand sizes (what of them the 256 MB MALL keeps across
+ * rounds); SMX_RASTER=spread|chunks|blocks in the environment, read once per
+ * process, forces an order. Every order gives the same result.
  * Returns SMX_OK or an SMX_ERR_* code; smx_last_error() describes it.
  */
 int smx_gemm(const smx_gemm_desc* desc, const void* a, const void* b, void* c, const void* residual,
