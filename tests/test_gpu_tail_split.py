@@ -18,6 +18,7 @@ Shapes: with bm = bn = 256 a launch has (M / 256) (N / 256) tiles; on the
 """
 
 import ctypes
+import os
 
 import numpy as np
 import pytest
@@ -47,11 +48,12 @@ def _plan(m, n, k, bm=256):
     the last round's r tiles (all T of a launch under one round) split into
     the s <= min(16, K / 512, 2^30 / (4 M N)) shares that minimise
     ceil(s r / C) (1/s + f) + s r g (f = 400 / K, g = (5/3) / K), when that
-    is under 0.95 of the unsplit 1 + f."""
+    is under 0.95 of the unsplit 1 + f. SMX_TAIL_SPLIT starting with 0 in
+    the environment turns the split off."""
     cus = torch.cuda.get_device_properties(DEV).multi_processor_count
     tiles = -(-(m // 2) // 128) * (n // 256)
     r = tiles % cus
-    if k < 2048 or r == 0:
+    if os.environ.get("SMX_TAIL_SPLIT", "").startswith("0") or k < 2048 or r == 0:
         return tiles, 0, 1
     s_max = min(16, (k // 32) // 16, (1 << 30) // (4 * m * n))
 
@@ -149,7 +151,7 @@ def _oracle(algo, a, b, tile, **kw):
 def test_half_round_split_matches_whole_and_oracle(algo, epilogue):
     m, k, n = HALF_ROUND
     if not _split_tiles(m, n, k):
-        pytest.skip("this device's CU count leaves no half-empty round at this shape")
+        pytest.skip("no split at this shape: this device's CU count leaves no half-empty round, or SMX_TAIL_SPLIT=0")
     rng, a, b = _problem(61 + algo, m, k, n)
     aux = _aux(rng, epilogue, m, n)
     aux_dev = {key: dev(v) for key, v in aux.items()}
@@ -171,7 +173,7 @@ def test_whole_rounds_then_split_tail(algo):
     """384 tiles: 256 over full K with the fused epilogue, 128 split."""
     m, k, n = ROUND_AND_HALF
     if not _split_tiles(m, n, k):
-        pytest.skip("this device's CU count leaves no half-empty last round at this shape")
+        pytest.skip("no split at this shape: this device's CU count leaves no half-empty last round, or SMX_TAIL_SPLIT=0")
     rng, a, b = _problem(71 + algo, m, k, n)
     aux = _aux(rng, "residual_add", m, n)
     pa, pb = _pack(algo, a, b, TILE)
@@ -191,7 +193,7 @@ def test_split_qk_norm_rope(algo, scale_dtype, out_f32):
     batch, seq, heads, k, bn = 2, 1024, 32, 2048, 512
     m, n, tile = batch * seq, heads * 128, (256, bn, 512)
     if not _split_tiles(m, n, k):
-        pytest.skip("this device's CU count leaves no half-empty round at this shape")
+        pytest.skip("no split at this shape: this device's CU count leaves no half-empty round, or SMX_TAIL_SPLIT=0")
     x, w, laid, tcos, tsin, scale = _qk_problem(13, batch, seq, heads, k, bn)
     pa, pb = _pack(algo, x, laid, tile)
     rope = (dev(tcos), dev(tsin), torch.from_numpy(scale).to(DEV).to(scale_dtype))
@@ -211,7 +213,7 @@ def test_split_qk_norm_rope(algo, scale_dtype, out_f32):
 def test_split_formula_variants(formula, perm, epilogue):
     m, k, n = HALF_ROUND
     if not _split_tiles(m, n, k):
-        pytest.skip("this device's CU count leaves no half-empty round at this shape")
+        pytest.skip("no split at this shape: this device's CU count leaves no half-empty round, or SMX_TAIL_SPLIT=0")
     rng, a, b = _problem(81, m, k, n)
     aux = _aux(rng, epilogue, m, n)
     aux_dev = {key: dev(v) for key, v in aux.items()}
@@ -240,7 +242,7 @@ def test_ragged_tail_with_float32_operands(algo, shape):
     the summing pass."""
     m, k, n = shape
     if not _split_tiles(m, n, k):
-        pytest.skip("this device's CU count leaves no half-empty last round at this shape")
+        pytest.skip("no split at this shape: this device's CU count leaves no half-empty last round, or SMX_TAIL_SPLIT=0")
     rng, a, b = _problem(101 + algo, m, k, n)
     pa, pb = _pack(algo, a, b, TILE)
     cases = (("residual_add", dict(residual=rng.standard_normal((m, n)).astype(np.float32))),
@@ -270,7 +272,7 @@ def test_split_exact_panels_through_surface():
 def test_workspace_below_the_size_asked_for_is_refused():
     m, k, n = HALF_ROUND
     if not _split_tiles(m, n, k):
-        pytest.skip("this device's CU count leaves no half-empty round at this shape")
+        pytest.skip("no split at this shape: this device's CU count leaves no half-empty round, or SMX_TAIL_SPLIT=0")
     _, a, b = _problem(5, m, k, n)
     pa, pb = _pack(7, a, b, TILE)
     with pytest.raises(ValueError, match="workspace_bytes"):
@@ -326,7 +328,7 @@ def test_small_launch_split_every_tile(algo, shape, tile, epilogue):
     (m, k, n), bm = shape, tile[0]
     whole_tiles, split, s = _plan(m, n, k, bm)
     if not split:
-        pytest.skip("this device's CU count does not split this shape")
+        pytest.skip("no split at this shape: this device's CU count, or SMX_TAIL_SPLIT=0")
     rng, a, b = _problem(111 + algo, m, k, n)
     aux = _aux(rng, epilogue, m, n)
     aux_dev = {key: dev(v) for key, v in aux.items()}
@@ -347,7 +349,7 @@ def test_small_thin_launch_qk_norm_rope(algo):
     batch, seq, heads, k, bn = 1, 48, 8, 2048, 256
     m, n, tile = batch * seq, heads * 128, (16, bn, 512)
     if not _split_tiles(m, n, k, 16):
-        pytest.skip("this device's CU count does not split this shape")
+        pytest.skip("no split at this shape: this device's CU count, or SMX_TAIL_SPLIT=0")
     x, w, laid, tcos, tsin, scale = _qk_problem(17, batch, seq, heads, k, bn)
     pa, pb = _pack(algo, x, laid, tile)
     rope = (dev(tcos), dev(tsin), torch.from_numpy(scale).to(DEV).to(torch.bfloat16))

@@ -4,6 +4,7 @@ kept tile; tuned_matmul sends a tabled shape to Strassen (bit-identical to a
 direct call) and anything else to the native GEMM."""
 
 import json
+import os
 
 import pytest
 import torch
@@ -100,6 +101,7 @@ def test_small_launch_measurement():
     """The small-launch measurement records the library's share count (at
     least two for 20 tiles over K = 4096) and samples every arm."""
     rec = tuning.measure_small_launches([(16, 4096, 5120, 16)], warmups=1, runs=3, batch=2)[0]
-    assert rec["tiles"] == 20 and rec["k_shares"] >= 2
+    split_off = os.environ.get("SMX_TAIL_SPLIT", "").startswith("0")
+    assert rec["tiles"] == 20 and (rec["k_shares"] == 1 if split_off else rec["k_shares"] >= 2)
     assert set(rec["median_ms"]) == {"strassen", "cubic", "hipblaslt"}
     assert all(len(v) == 3 for v in rec["samples_ms"].values())
