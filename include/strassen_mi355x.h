@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SMX_VERSION 10
+#define SMX_VERSION 11
 
 /* Status codes. */
 #define SMX_OK 0
@@ -81,6 +81,16 @@ extern "C" {
 
 /* desc.flags bits. */
 #define SMX_FLAG_OUT_F32 1 /* C is float32 (the unrounded FP32 result, output_dtype=float32, :1048-1057) */
+/* Strassen on packed operands: run the product-major kernel, which takes the
+ * seven products of a 128 x 256 product-space tile one after another over
+ * the whole K range into three FP32 register sets (the default kernel keeps
+ * seven sets of a 128 x 128 tile), parking two partial sets per workgroup in
+ * the workspace (smx_gemm_workspace_bytes). It streams 384 operand bytes per
+ * MFMA instead of 512. Calls it cannot take run the default kernel: another
+ * formula, the qk_norm_rope epilogue, an FP32 partial, bm/2 not a multiple of
+ * 128, bn/2 not a multiple of 256, or K not a multiple of 128. No counterpart
+ * in the reference (a kernel choice of gfx950). */
+#define SMX_FLAG_PRODUCT_MAJOR 2
 
 /* aux_f32 bits: element type of the small auxiliary vectors. */
 #define SMX_AUX_BIAS_F32 1  /* bias is float32 (else bf16) */
@@ -178,7 +188,11 @@ int smx_gemm_noalloc(const smx_gemm_desc* desc, const void* a, const void* b, vo
                      const void* bias, const void* rope_cos, const void* rope_sin, const void* rope_scale,
                      void* stream);
 
-/* Bytes of device workspace (s * M * N floats for s K shares) with which
+/* Bytes of device workspace with which smx_gemm runs this descriptor's
+ * call: for a call on the product-major kernel (SMX_FLAG_PRODUCT_MAJOR),
+ * 256 KB per 128 x 256 product tile, (M/2 / 128) (N/2 / 256) tiles, which
+ * the call then requires. Otherwise the bytes (s * M * N floats for s K
+ * shares) with which
  * smx_gemm splits tiles of this descriptor's launch over K, on the current
  * device. T tiles on the device's C CUs make T / C whole rounds and a last
  * round of r = T mod C tiles; those r tiles split into the s shares,

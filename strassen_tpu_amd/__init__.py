@@ -12,7 +12,8 @@ from .layouts import (  # noqa: F401
 )
 from .strassen import (  # noqa: F401
     PROFILE_INFO, TUNED_BK, TUNED_BM, TUNED_BN, VMEM_PROFILE, check_tiling,
-    cubic_matmul, native_matmul, plain_weight_kernel, strassen_matmul, strassen_matmul_lhs_transposed,
+    cubic_matmul, native_matmul, plain_weight_kernel, strassen_kernel, strassen_matmul,
+    strassen_matmul_lhs_transposed,
 )
 
 from .packing import (  # noqa: F401

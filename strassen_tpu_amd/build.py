@@ -20,7 +20,8 @@ import tempfile
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
 SOURCES = tuple(os.path.join(HERE, "csrc", name) for name in (
-    "strassen_gemm.hip", "gemm_strassen.hip", "gemm_strassen_thin.hip", "gemm_cubic.hip", "gemm_cubic_thin.hip"))
+    "strassen_gemm.hip", "gemm_strassen.hip", "gemm_strassen_thin.hip", "gemm_strassen_pm.hip", "gemm_cubic.hip",
+    "gemm_cubic_thin.hip"))
 LIBRARY = os.path.join(HERE, "libstrassen_mi355x.so")
 INCLUDE = os.path.join(REPO, "include")
 
@@ -122,6 +123,7 @@ def verify_inline_asm_kernels(asm_text):
 # hot path).
 _KERNEL_DESC = re.compile(r"\.amdhsa_kernel (\S+)(.*?)\.end_amdhsa_kernel", re.S)
 _SPLIT = re.compile(r"gemm_splitILi(\d+)ELi(\d+)ELb(\d)E")
+_PM = re.compile(r"gemm_pmILi(\d+)EE")
 _PACKED = re.compile(r"gemm_packedILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb(\d)E")
 _QUAD_CUBIC_PARTIAL = 1
 PARTIAL_SCRATCH_CAP = 1024
@@ -129,7 +131,7 @@ PARTIAL_SCRATCH_CAP = 1024
 
 def scratch_limit(name):
     """Allowed scratch bytes per lane of a kernel (None: not a GEMM kernel)."""
-    if _SPLIT.search(name):
+    if _SPLIT.search(name) or _PM.search(name):
         return 0
     m = _PACKED.search(name)
     if m:

@@ -304,6 +304,9 @@ struct Params {
   int32_t ksplit;
   int32_t tile_base;
   int64_t split_stride;
+  // Product-major Strassen kernel (kernel_pm.hpp): FP32 space for one parked
+  // quadrant set per workgroup (pm::kParkBytes each).
+  void* park;
 };
 
 // A workgroup's logical tile and its share of the K stages (see Params).

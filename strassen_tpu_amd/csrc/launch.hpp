@@ -36,6 +36,10 @@ int launch_strassen(const Params& p, int epilogue, hipStream_t stream);
 template <bool kThin>
 int launch_cubic(const Params& p, int epilogue, hipStream_t stream);
 
+// The product-major Strassen kernel (kernel_pm.hpp) on packed operands:
+// 128 x 256 product-space tiles, p.tiles_n counted in those, p.park set.
+int launch_strassen_pm(const Params& p, int epilogue, hipStream_t stream);
+
 extern template int launch_strassen<false>(const Params&, int, hipStream_t);
 extern template int launch_strassen<true>(const Params&, int, hipStream_t);
 extern template int launch_cubic<false>(const Params&, int, hipStream_t);

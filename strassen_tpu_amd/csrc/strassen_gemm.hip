@@ -53,6 +53,7 @@
 
 #include "common.hpp"
 #include "kernel_packed.hpp"
+#include "kernel_pm.hpp"
 #include "kernel_v1.hpp"
 #include "launch.hpp"
 #include "split_fixup.hpp"
@@ -232,7 +233,8 @@ int gemm_params(const smx_gemm_desc* d, const void* a, const void* b, void* c, c
   const bool packed_path = d->b_layout == SMX_B_PACKED;
   if (packed_path != (d->a_layout == SMX_A_PACKED))
     return fail(SMX_ERR_UNSUPPORTED, "A and B must both be packed (smx_pack_operand) or both unpacked");
-  if (d->flags & ~SMX_FLAG_OUT_F32) return fail(SMX_ERR_INVALID, "unknown flags 0x%x", d->flags);
+  if (d->flags & ~(SMX_FLAG_OUT_F32 | SMX_FLAG_PRODUCT_MAJOR))
+    return fail(SMX_ERR_INVALID, "unknown flags 0x%x", d->flags);
   if (int rc = check_variant(d->algo, d->formula, d->block_permutation)) return rc;
   if ((d->formula || d->block_permutation) && !packed_path)
     return fail(SMX_ERR_UNSUPPORTED, "formula variants and block permutations run on packed operands");
@@ -384,14 +386,15 @@ constexpr int64_t kMallResident = (int64_t)192 << 20;
 // but a round's 32 panels do, in blocks (8192 x 8192 x 20480: 2.47 ms
 // spread, 2.35 blocks); with panels beyond that no order gains (8192 x 25600
 // x 5120: 2.09-2.11 ms).
-int raster_for(const Params& p, int algo) {
+int raster_for(const Params& p, int algo, int tile_cols) {
   const int64_t nops = packed::nops_of(algo), depth = p.k / 2;
   const int64_t panel = (int64_t)packed::TM * depth * nops * 2;
-  const int64_t a_bytes = (int64_t)p.tiles_m * panel, b_bytes = (int64_t)p.tiles_n * panel;
+  const int64_t b_panel = panel * (tile_cols / packed::TN);
+  const int64_t a_bytes = (int64_t)p.tiles_m * panel, b_bytes = (int64_t)p.tiles_n * b_panel;
   if (a_bytes <= kMallResident) return kRasterSpread;
   if (b_bytes <= kMallResident) return kRasterChunks;
   // a blocks round reads 16 A and 16 B panels
-  if (32 * panel <= ((int64_t)256 << 20)) return kRasterBlocks;
+  if (16 * (panel + b_panel) <= ((int64_t)256 << 20)) return kRasterBlocks;
   return kRasterSpread;
 }
 
@@ -402,7 +405,7 @@ void packed_grid(Params& p, int algo) {
   p.tiles_n = (int)((p.n / 2) / packed::TN);
   p.group_m = group_m_setting();
   const int forced = raster_setting();
-  p.raster = forced >= 0 ? forced : raster_for(p, algo);
+  p.raster = forced >= 0 ? forced : raster_for(p, algo, packed::TN);
 }
 
 // Depth below which a split's rounds are short enough that its two extra
@@ -495,6 +498,32 @@ int launch_packed(const Params& p, int algo, int epilogue, hipStream_t s) {
   return thin ? launch_cubic<true>(p, epilogue, s) : launch_cubic<false>(p, epilogue, s);
 }
 
+// Whether a checked packed Strassen call asks for (SMX_FLAG_PRODUCT_MAJOR)
+// and can take the product-major kernel (kernel_pm.hpp): the classical formula, no FP32 partial, whole 128 x 256
+// product tiles inside every (bm, bn) tile, K a multiple of 128, and an
+// epilogue it fuses.
+bool pm_eligible(const Params& p, const smx_gemm_desc& d) {
+  if (!(d.flags & SMX_FLAG_PRODUCT_MAJOR)) return false;
+  if (d.algo != SMX_ALGO_STRASSEN || d.b_layout != SMX_B_PACKED || p.partial) return false;
+  if (p.formula != SMX_FORMULA_CLASSICAL || (p.bm / 2) % pm::TM || (p.bn / 2) % pm::TN) return false;
+  if ((p.k / 32) % pm::kQuarters) return false;  // whole pipeline stages of 64 product-space k
+  return d.epilogue == SMX_EPI_NONE || d.epilogue == SMX_EPI_SWIGLU || d.epilogue == SMX_EPI_GEGLU ||
+         d.epilogue == SMX_EPI_RESIDUAL_ADD || d.epilogue == SMX_EPI_BIAS_ADD;
+}
+
+// Grid of a product-major launch: 128 x 256 product tiles, the tile order
+// chosen from its packed operands as for the other packed kernels.
+void pm_grid(Params& p) {
+  p.tiles_m = (int)((p.m / 2) / pm::TM);
+  p.tiles_n = (int)((p.n / 2) / pm::TN);
+  p.group_m = group_m_setting();
+  const int forced = raster_setting();
+  p.raster = forced >= 0 ? forced : raster_for(p, SMX_ALGO_STRASSEN, pm::TN);
+}
+
+// Workspace of a product-major launch: two parked FP32 sets per workgroup.
+int64_t pm_park_bytes(const Params& p) { return (int64_t)p.tiles_m * p.tiles_n * pm::kParkBytes; }
+
 // A packed call, with tiles split over K when a workspace is given
 // (smx_gemm_desc.workspace, split_plan): the whole tiles with the fused
 // epilogue, then the split tiles' K shares into the workspace (FP32, no
@@ -502,6 +531,18 @@ int launch_packed(const Params& p, int algo, int epilogue, hipStream_t s) {
 int launch_gemm(Params p, const smx_gemm_desc& d, hipStream_t s) {
   if (d.b_layout != SMX_B_PACKED)
     return d.algo == SMX_ALGO_STRASSEN ? dispatch_v1<7>(p, d.epilogue, s) : dispatch_v1<8>(p, d.epilogue, s);
+  if (pm_eligible(p, d)) {
+    Params q = p;
+    pm_grid(q);
+    // The product-major kernel parks two partial sets per workgroup in the
+    // workspace.
+    if (!d.workspace || d.workspace_bytes < pm_park_bytes(q))
+      return fail(SMX_ERR_INVALID,
+                  "the product-major kernel needs workspace_bytes >= %lld (smx_gemm_workspace_bytes), got %lld",
+                  (long long)pm_park_bytes(q), (long long)(d.workspace ? d.workspace_bytes : 0));
+    q.park = d.workspace;
+    return launch_strassen_pm(q, d.epilogue, s);
+  }
   packed_grid(p, d.algo);
   SplitPlan plan{p.tiles_m * p.tiles_n, 0, 1};
   if (d.workspace) {
@@ -721,6 +762,11 @@ int smx_gemm_workspace_bytes(const smx_gemm_desc* d, int64_t* bytes) {
   Params p{};
   if (int rc = gemm_params(d, x, x, const_cast<void*>(x), x, x, x, x, x, p)) return rc;
   if (d->b_layout != SMX_B_PACKED) return SMX_OK;
+  if (pm_eligible(p, *d)) {
+    pm_grid(p);
+    *bytes = pm_park_bytes(p);
+    return SMX_OK;
+  }
   packed_grid(p, d->algo);
   SplitPlan plan{};
   if (int rc = split_plan(p, &plan)) return rc;

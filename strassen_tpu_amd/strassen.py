@@ -71,7 +71,7 @@ from .packing import (PackedOperand, SplitOperand, exact_schedule, pack_operand,
 
 __all__ = [
     "strassen_matmul", "strassen_matmul_lhs_transposed", "cubic_matmul", "native_matmul", "check_tiling",
-    "TUNED_BM", "TUNED_BN", "TUNED_BK", "VMEM_PROFILE", "PROFILE_INFO", "plain_weight_kernel",
+    "TUNED_BM", "TUNED_BN", "TUNED_BK", "VMEM_PROFILE", "PROFILE_INFO", "plain_weight_kernel", "strassen_kernel",
 ]
 
 LANE = 128
@@ -136,6 +136,27 @@ def plain_weight_kernel(kind):
         yield
     finally:
         PLAIN_WEIGHTS = previous
+
+
+# Strassen kernel for packed operands: "split" (the seven products of a
+# 128 x 128 product tile in registers, gemm_split) or "product_major" (the
+# products of a 128 x 256 tile one after another into three register sets,
+# SMX_FLAG_PRODUCT_MAJOR; calls that kernel cannot take run "split").
+STRASSEN_KERNEL = "split"
+
+
+@contextlib.contextmanager
+def strassen_kernel(kind):
+    """Run packed Strassen calls inside the block on ``kind`` ("split" or
+    "product_major"). Process-wide; not for concurrent use."""
+    global STRASSEN_KERNEL
+    if kind not in ("split", "product_major"):
+        raise ValueError("Strassen kernel must be 'split' or 'product_major'")
+    previous, STRASSEN_KERNEL = STRASSEN_KERNEL, kind
+    try:
+        yield
+    finally:
+        STRASSEN_KERNEL = previous
 
 
 def _fits(algo, epilogue, bm, bn, bk, b_layout):
@@ -492,6 +513,8 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
     desc.a_layout = _lib.SMX_A_PACKED if packed else _lib.SMX_A_ROWMAJOR
     desc.b_layout = b_layout
     desc.flags = _lib.SMX_FLAG_OUT_F32 if out_dtype == torch.float32 else 0
+    if algo == 7 and packed and STRASSEN_KERNEL == "product_major":
+        desc.flags |= _lib.SMX_FLAG_PRODUCT_MAJOR
     desc.formula = _lib.SMX_FORMULA[formula]
     desc.block_permutation = block_permutation
     if partial is not None:
