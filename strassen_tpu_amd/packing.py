@@ -28,6 +28,7 @@ from __future__ import annotations
 import collections
 import ctypes
 import os
+import weakref
 
 import torch
 
@@ -35,7 +36,7 @@ from . import _lib
 
 __all__ = ["PackedOperand", "SplitOperand", "ExactSchedule", "exact_schedule", "pack_operand", "precision_passes",
            "strassen_weight_layout", "cubic_weight_layout", "pack_activation", "cache_packed_weights",
-           "packed_weight_cache_info", "pack_weight_for_call"]
+           "packed_weight_cache_info", "pack_weight_for_call", "default_cache_bytes", "weight_cached_or_fits"]
 
 _ALGOS = {_lib.SMX_ALGO_STRASSEN: "strassen", _lib.SMX_ALGO_CUBIC: "cubic"}
 
@@ -281,76 +282,135 @@ class _WeightCache:
 
     A call that passes an ordinary ``[K, N]`` weight packs it (the seven
     Strassen operand sums, 7/4 of its bytes, or the cubic's quadrants) before
-    the GEMM; with the cache enabled the packed form of the same weight is
-    reused on later calls. Key: the weight's data address, view geometry,
-    dtype and device, and the packing (algorithm, tile, formula, block
-    permutation, exact panels, bf16 passes). An entry keeps the weight tensor
-    alive, so its storage cannot be freed and its address taken by another
-    tensor while the entry lives, and records torch's version counter at
-    packing: an in-place update of the weight through it or any view of it
-    bumps the counter and the next call packs again. Writes that bypass the
-    counter (through ``.data``, or from outside torch) are not seen.
-    Least-recently used entries are dropped beyond the capacity (bytes of
-    packed data); an operand larger than the capacity is not kept. Not
+    the GEMM; the packed form of the same weight is reused on later calls.
+    Key: the weight's data address, view geometry, dtype and device, and the
+    packing (algorithm, tile, formula, block permutation, exact panels, bf16
+    passes). An entry holds a weak reference to the tensor whose storage the
+    weight is (the view's base, else the weight itself), never the weight:
+    when that tensor is freed the entry goes with it, so neither the plain
+    weight nor a stale packed form outlives the caller's weight, and a new
+    tensor at the same address cannot match. It also records torch's version
+    counter at packing (shared by a tensor and its views): an in-place update
+    of the weight through it or any view of it bumps the counter and the next
+    call packs again. Writes that bypass the counter (through ``.data``, or
+    from outside torch) are not seen. Least-recently used entries are dropped
+    beyond the capacity (bytes of packed data, the only device memory the
+    cache holds); an operand larger than the capacity is not kept. Not
     thread-safe."""
 
     def __init__(self, capacity):
-        self.capacity = int(capacity)
+        # None: default_cache_bytes(), resolved at first use (it reads the
+        # device's memory size, which initialises the GPU runtime)
+        self._capacity = None if capacity is None else int(capacity)
         self.entries = collections.OrderedDict()
         self.bytes = 0
         self.hits = self.misses = self.stale = 0
+
+    @property
+    def capacity(self):
+        if self._capacity is None:
+            self._capacity = default_cache_bytes()
+        return self._capacity
 
     @staticmethod
     def _nbytes(packed):
         parts = [packed.ordinary, packed.exact] if isinstance(packed, SplitOperand) else [packed]
         return sum(p.data.numel() * p.data.element_size() for p in parts if p is not None)
 
+    @staticmethod
+    def _key(x, packing):
+        return (x.data_ptr(), tuple(x.shape), tuple(x.stride()), x.dtype, str(x.device), packing)
+
     def resize(self, capacity):
-        self.capacity = int(capacity)
+        self._capacity = int(capacity)
         self._evict()
+
+    def _drop(self, key):
+        entry = self.entries.pop(key, None)
+        if entry is not None:
+            self.bytes -= entry[3]
 
     def _evict(self):
         while self.entries and self.bytes > self.capacity:
             _, (_, _, _, nbytes) = self.entries.popitem(last=False)
             self.bytes -= nbytes
 
+    def _valid(self, key):
+        entry = self.entries.get(key)
+        if entry is None:
+            return None
+        owner, version, packed, _ = entry
+        base = owner()
+        if base is None:  # freed (its weak-reference callback drops the entry)
+            self._drop(key)
+            return None
+        if base._version != version:
+            self.stale += 1
+            self._drop(key)
+            return None
+        return packed
+
+    def contains(self, x, packing):
+        """Whether the packed form of ``x`` is held and current (packs nothing)."""
+        return self.capacity > 0 and self._valid(self._key(x, packing)) is not None
+
+    def has_room(self, nbytes):
+        """Whether ``nbytes`` more would fit without evicting an entry."""
+        return self.bytes + nbytes <= self.capacity
+
     def lookup(self, x, packing, make):
         if self.capacity <= 0:
             return make()
-        key = (x.data_ptr(), tuple(x.shape), tuple(x.stride()), x.dtype, str(x.device), packing)
-        entry = self.entries.get(key)
-        if entry is not None:
-            tensor, version, packed, nbytes = entry
-            if tensor._version == version:
-                self.entries.move_to_end(key)
-                self.hits += 1
-                return packed
-            self.stale += 1
-            del self.entries[key]
-            self.bytes -= nbytes
+        key = self._key(x, packing)
+        packed = self._valid(key)
+        if packed is not None:
+            self.entries.move_to_end(key)
+            self.hits += 1
+            return packed
         self.misses += 1
-        version = x._version
+        base = x._base if x._base is not None else x
+        version = base._version
         packed = make()
         nbytes = self._nbytes(packed)
         if nbytes <= self.capacity:
-            self.entries[key] = (x, version, packed, nbytes)
+            entries = self.entries
+
+            def forget(_, key=key, entries=entries, cache=self):
+                if key in entries and entries[key][0]() is None:
+                    cache._drop(key)
+
+            self.entries[key] = (weakref.ref(base, forget), version, packed, nbytes)
             self.bytes += nbytes
             self._evict()
         return packed
 
 
-_WEIGHT_CACHE = _WeightCache(int(os.environ.get("SMX_WEIGHT_CACHE_BYTES", "0") or 0))
+def default_cache_bytes():
+    """The packed-weight cache's default capacity: ``SMX_WEIGHT_CACHE_BYTES``
+    when set (0 turns the cache off), else the smaller of 16 GiB and 1/16 of
+    the current device's memory (18 GB of an MI355X's 288 GB: the packed
+    Strassen weights of ten Qwen3-32B layers)."""
+    env = os.environ.get("SMX_WEIGHT_CACHE_BYTES")
+    if env is not None and env.strip() != "":
+        return int(env)
+    if not torch.cuda.is_available():
+        return 16 << 30
+    total = torch.cuda.get_device_properties(torch.cuda.current_device()).total_memory
+    return int(min(16 << 30, total // 16))
+
+
+_WEIGHT_CACHE = _WeightCache(None)
 
 
 def cache_packed_weights(capacity_bytes):
     """Keep the packed forms of plain weights that ``strassen_matmul`` /
-    ``cubic_matmul`` calls pack, up to ``capacity_bytes`` of packed data
-    (0, the default unless ``SMX_WEIGHT_CACHE_BYTES`` sets one, packs on
-    every call and empties the cache). Returns the previous capacity. Size it
-    to hold every weight of the working set (a Strassen weight packs to 7/4
-    of its bytes); a cache that evicts before reuse only adds bookkeeping.
-    Packing weights once with ``strassen_weight_layout`` /
-    ``cubic_weight_layout`` needs no cache."""
+    ``cubic_matmul`` calls pack, up to ``capacity_bytes`` of packed data (0
+    packs on every call and empties the cache; the default is
+    ``default_cache_bytes()``). Returns the previous capacity. The cache
+    holds no plain weight: an entry goes when its weight is freed. A working
+    set larger than the capacity evicts before reuse and then only adds
+    bookkeeping to the per-call packing; packing weights once with
+    ``strassen_weight_layout`` / ``cubic_weight_layout`` needs no cache."""
     previous = _WEIGHT_CACHE.capacity
     _WEIGHT_CACHE.resize(capacity_bytes)
     return previous
@@ -362,6 +422,19 @@ def packed_weight_cache_info():
     c = _WEIGHT_CACHE
     return {"hits": c.hits, "misses": c.misses, "stale": c.stale, "entries": len(c.entries), "bytes": c.bytes,
             "capacity": c.capacity}
+
+
+def _weight_packing(algo, bn, bk, formula="classical", block_permutation=0, classical_panels=(), exact=None,
+                    dot_precision=None):
+    return (algo, bn, bk, formula, block_permutation, tuple(classical_panels), exact, dot_precision)
+
+
+def weight_cached_or_fits(b, *, algo, bn, bk, packed_bytes):
+    """Whether a call on the plain weight ``b`` (default packing) finds its
+    packed form in the cache, or can add it (``packed_bytes``) without
+    evicting another entry."""
+    packing = _weight_packing(algo, bn, bk)
+    return _WEIGHT_CACHE.contains(b, packing) or (_WEIGHT_CACHE.capacity > 0 and _WEIGHT_CACHE.has_room(packed_bytes))
 
 
 def pack_weight_for_call(b, *, algo, bn, bk, formula="classical", block_permutation=0, classical_panels=(),
@@ -377,7 +450,7 @@ def pack_weight_for_call(b, *, algo, bn, bk, formula="classical", block_permutat
     if panel_schedule is not None and not isinstance(panel_schedule, ExactSchedule):
         return make()  # a schedule still to be read from the device: packed per call
     exact = panel_schedule.exact if panel_schedule is not None else None
-    packing = (algo, bn, bk, formula, block_permutation, tuple(classical_panels), exact, dot_precision)
+    packing = _weight_packing(algo, bn, bk, formula, block_permutation, classical_panels, exact, dot_precision)
     return _WEIGHT_CACHE.lookup(b, packing, make)
 
 

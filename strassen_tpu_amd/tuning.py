@@ -40,7 +40,7 @@ import torch
 from . import _lib
 from .layouts import swiglu_weight_layout
 from .packing import (cache_packed_weights, cubic_weight_layout, pack_activation, packed_weight_cache_info,
-                      strassen_weight_layout)
+                      strassen_weight_layout, weight_cached_or_fits)
 from .strassen import cubic_matmul, native_matmul, strassen_matmul
 
 __all__ = ["TILE_RULE", "enumerate_candidates", "time_calls", "screen_tiles", "measure_dispatch",
@@ -425,21 +425,29 @@ def load_table(path=None):
     return _TABLE[1]
 
 
-def _entry_wins(entry, k, n):
-    """Whether a table entry's measured win holds for this call: a win with
-    the weight packed per call always does; a win with the cached weight
-    only while the packed-weight cache can hold the packed weight (7/4 of
-    its bf16 bytes)."""
+def _entry_wins(entry, b):
+    """Whether a table entry's measured win holds for a call on the weight
+    ``b [K, N]``: a win with the weight packed per call always does; a win
+    measured with the packed weight cached holds only when the cache has
+    this weight's packed form (7/4 of its bf16 bytes) or can add it without
+    evicting another. A working set the cache cannot hold therefore stays on
+    the native GEMM for the weights beyond it, instead of packing them on
+    every call (the per-call arm, which lost)."""
     if entry.get("per_call", True):
         return True
-    return bool(entry.get("cached")) and packed_weight_cache_info()["capacity"] >= 7 * k * n // 2
+    if not entry.get("cached"):
+        return False
+    k, n = b.shape
+    _, bn, bk = entry["tile"]
+    return weight_cached_or_fits(b, algo=_lib.SMX_ALGO_STRASSEN, bn=bn, bk=bk, packed_bytes=7 * k * n // 2)
 
 
 def tuned_matmul(a, b, *, interpret=False):
     """Dispatch measured bf16 shapes to Strassen, everything else to the
     native GEMM (``strassen_pallas.py:1428-1461``). A shape goes to Strassen
     only if it is in the measured table with a win that holds for the call
-    (per call, or with the packed-weight cache enabled), both operands are
+    (per call, or with the weight's packed form cached or fitting in the
+    packed-weight cache), both operands are
     2-D bf16 with matching K, and the table's tile divides it."""
     if a.dim() != 2 or b.dim() != 2:
         return native_matmul(a, b)
@@ -448,7 +456,7 @@ def tuned_matmul(a, b, *, interpret=False):
     entry = load_table()["shapes"].get(f"{m},{k},{n}")
     use_strassen = (entry is not None and k == k2 and a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16
                     and m % entry["tile"][0] == 0 and n % entry["tile"][1] == 0 and k % entry["tile"][2] == 0
-                    and _entry_wins(entry, k, n))
+                    and _entry_wins(entry, b))
     if not use_strassen:
         return native_matmul(a, b)
     bm, bn, bk = entry["tile"]

@@ -66,19 +66,78 @@ def test_tuned_matmul_dispatch_rules(table):
 
 def test_cached_win_needs_the_cache(table, tmp_path, monkeypatch):
     """An entry that won only with the packed-weight cache goes to Strassen
-    only while the cache can hold the packed weight (7/4 of 2 K N bytes)."""
+    only while the cache holds the weight's packed form (7/4 of 2 K N bytes)
+    or can add it without evicting another: with room for one packed weight
+    and calls cycling over two weights, the first weight stays on Strassen
+    and the second goes native, instead of both missing and repacking on
+    every call."""
+    from strassen_tpu_amd import packing
+
     path = tmp_path / "cached.json"
     path.write_text(json.dumps({"shapes": {"128,1024,512": {"tile": [128, 256, 512], "per_call": False,
                                                             "cached": True}}}))
     monkeypatch.setenv("SMX_TUNED_TABLE", str(path))
-    capacity = {"capacity": 0}
-    monkeypatch.setattr(tuning, "packed_weight_cache_info", lambda: dict(capacity))
-    assert tuning.tuned_matmul(z(128, 1024), z(1024, 512)) == "native"
-    capacity["capacity"] = 7 * 1024 * 512 // 2 - 1
-    assert tuning.tuned_matmul(z(128, 1024), z(1024, 512)) == "native"
-    capacity["capacity"] = 7 * 1024 * 512 // 2
-    assert tuning.tuned_matmul(z(128, 1024), z(1024, 512)) == "strassen"
+    packed_bytes = 7 * 1024 * 512 // 2
+    cache = packing._WeightCache(0)
+    monkeypatch.setattr(packing, "_WEIGHT_CACHE", cache)
+
+    class Packed:  # stands in for a PackedOperand of packed_bytes
+        data = torch.zeros(packed_bytes, dtype=torch.uint8)
+
+    def strassen(a, b, **kw):
+        # what strassen_matmul does with a plain weight: the cached lookup
+        cache.lookup(b, packing._weight_packing(7, kw["bn"], kw["bk"]), Packed)
+        table.append(("strassen", kw["bm"], kw["bn"], kw["bk"]))
+        return "strassen"
+
+    monkeypatch.setattr(tuning, "strassen_matmul", strassen)
+    w1, w2 = z(1024, 512), z(1024, 512)
+    assert tuning.tuned_matmul(z(128, 1024), w1) == "native"  # cache off
+    cache.resize(packed_bytes - 1)
+    assert tuning.tuned_matmul(z(128, 1024), w1) == "native"  # no room
+    cache.resize(packed_bytes)
+    assert tuning.tuned_matmul(z(128, 1024), w1) == "strassen"  # room: packed and kept
     assert table[-1] == ("strassen", 128, 256, 512)
+    for _ in range(3):
+        assert tuning.tuned_matmul(z(128, 1024), w2) == "native"  # would evict w1
+        assert tuning.tuned_matmul(z(128, 1024), w1) == "strassen"  # cached
+    assert cache.misses == 1 and cache.hits == 3
+    assert tuning.tuned_matmul(z(128, 1024), w1.t().contiguous().t()) == "native"  # another tensor, no room
+
+
+def test_weight_cache_entries_follow_their_weights():
+    """Entries hold weak references: freeing a weight (or the base of the
+    view passed) drops its entry and its packed bytes; an in-place update
+    (the shared version counter) makes the next lookup pack again; contains()
+    packs nothing; views of one base share an entry per geometry."""
+    from strassen_tpu_amd import packing
+
+    cache = packing._WeightCache(1 << 20)
+    made = []
+
+    def make():
+        made.append(1)
+
+        class Packed:
+            data = torch.zeros(1000, dtype=torch.uint8)
+        return Packed
+
+    key = ("k",)
+    base = torch.zeros(64, 32, dtype=torch.bfloat16)  # stored [out, in]; the call passes base.t()
+    assert not cache.contains(base.t(), key)
+    cache.lookup(base.t(), key, make)
+    assert cache.contains(base.t(), key) and len(made) == 1
+    cache.lookup(base.t(), key, make)  # a fresh view of the same base: a hit
+    assert len(made) == 1 and cache.hits == 1 and cache.bytes == 1000
+    base.add_(1)  # in place, through the base: the view's entry is stale
+    assert not cache.contains(base.t(), key) and cache.stale == 1 and cache.bytes == 0
+    cache.lookup(base.t(), key, make)
+    assert len(made) == 2 and cache.bytes == 1000
+    del base
+    import gc
+    gc.collect()
+    assert len(cache.entries) == 0 and cache.bytes == 0
+    assert cache.has_room(1 << 20) and not cache.has_room((1 << 20) + 1)
 
 
 def test_dispatch_tile():
