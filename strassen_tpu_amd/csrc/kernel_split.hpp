@@ -288,11 +288,13 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
     const uint32_t lane16 = opaque_lane_id() * 16;
 #pragma unroll
     for (int q = 0; q < 7; ++q) {
-      const int own = kKeepOwn ? P::strip_of(q, 2 * (kWave >> 1) + i) : -1;
-      if (own >= 0) {
+      if constexpr (kKeepOwn) {
+        const int own = P::strip_of(q, 2 * (kWave >> 1) + i);
+        if (own >= 0) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) blk[q][0][0][e] = acc[own][2 * (kWave & 1) + jj][e];
-        continue;
+          for (int e = 0; e < 16; ++e) blk[q][0][0][e] = acc[own][2 * (kWave & 1) + jj][e];
+          continue;
+        }
       }
       const uint8_t* const slot = mine + q * kBlockBytes + lane16;
 #pragma unroll
