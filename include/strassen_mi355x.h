@@ -180,7 +180,10 @@ int smx_gemm(const smx_gemm_desc* desc, const void* a, const void* b, void* c, c
  * A needs smx_packed_bytes(algo, M, K) bytes (about M/2 * K/2 * nops * 2, nops
  * 7 for Strassen, 4 for the cubic), so M * K must stay at or below about
  * 76,695,844 (Strassen) or 134,217,728 (cubic); larger calls fail with SMX_ERR_UNSUPPORTED before any launch. No
- * FP32 partial (desc->partial must be null). Calls allocate nothing. Every
+ * FP32 partial (desc->partial must be null). A workspace in the descriptor
+ * (smx_gemm_workspace_bytes sizes this descriptor as the packed call it
+ * becomes) is checked, with every other argument, before anything is
+ * launched. Calls allocate nothing. Every
  * call on one GPU shares that GPU's scratch: calls that overlap on one GPU
  * (different streams, or another thread) race, so a caller serialises them.
  */
@@ -203,7 +206,8 @@ int smx_gemm_noalloc(const smx_gemm_desc* desc, const void* a, const void* b, vo
  * unpacked call, an FP32 partial, K below 2048, r = 0, or no s that shortens
  * the round. Takes a descriptor smx_gemm accepts; no operand pointer is read.
  * SMX_TAIL_SPLIT=0 in the environment turns the split off. No counterpart in
- * the reference (a launch shape of gfx950). */
+ * the reference (a launch shape of gfx950). A row-major A with a packed B
+ * (smx_gemm_noalloc's descriptor) is sized as the packed call it becomes. */
 int smx_gemm_workspace_bytes(const smx_gemm_desc* desc, int64_t* bytes);
 
 /* Tile granules of the kernels that serve (algo, epilogue, b_layout): bm

@@ -524,6 +524,31 @@ void pm_grid(Params& p) {
 // Workspace of a product-major launch: two parked FP32 sets per workgroup.
 int64_t pm_park_bytes(const Params& p) { return (int64_t)p.tiles_m * p.tiles_n * pm::kParkBytes; }
 
+// The workspace checks of a checked call, run before anything is launched
+// (launch_gemm, and smx_gemm_noalloc before its packing pass): the
+// product-major kernel's parked sets, or a K split's shares.
+int check_workspace(const Params& p, const smx_gemm_desc& d) {
+  if (d.b_layout != SMX_B_PACKED) return SMX_OK;
+  if (pm_eligible(p, d)) {
+    Params q = p;
+    pm_grid(q);
+    if (!d.workspace || d.workspace_bytes < pm_park_bytes(q))
+      return fail(SMX_ERR_INVALID,
+                  "the product-major kernel needs workspace_bytes >= %lld (smx_gemm_workspace_bytes), got %lld",
+                  (long long)pm_park_bytes(q), (long long)(d.workspace ? d.workspace_bytes : 0));
+    return SMX_OK;
+  }
+  if (!d.workspace) return SMX_OK;
+  Params q = p;
+  packed_grid(q, d.algo);
+  SplitPlan plan{};
+  if (int rc = split_plan(q, &plan)) return rc;
+  if (plan.split && d.workspace_bytes < split_bytes(q, plan))
+    return fail(SMX_ERR_INVALID, "workspace_bytes %lld is below the %lld this call needs (smx_gemm_workspace_bytes)",
+                (long long)d.workspace_bytes, (long long)split_bytes(q, plan));
+  return SMX_OK;
+}
+
 // A packed call, with tiles split over K when a workspace is given
 // (smx_gemm_desc.workspace, split_plan): the whole tiles with the fused
 // epilogue, then the split tiles' K shares into the workspace (FP32, no
@@ -531,26 +556,19 @@ int64_t pm_park_bytes(const Params& p) { return (int64_t)p.tiles_m * p.tiles_n *
 int launch_gemm(Params p, const smx_gemm_desc& d, hipStream_t s) {
   if (d.b_layout != SMX_B_PACKED)
     return d.algo == SMX_ALGO_STRASSEN ? dispatch_v1<7>(p, d.epilogue, s) : dispatch_v1<8>(p, d.epilogue, s);
+  if (int rc = check_workspace(p, d)) return rc;
   if (pm_eligible(p, d)) {
-    Params q = p;
-    pm_grid(q);
     // The product-major kernel parks two partial sets per workgroup in the
     // workspace.
-    if (!d.workspace || d.workspace_bytes < pm_park_bytes(q))
-      return fail(SMX_ERR_INVALID,
-                  "the product-major kernel needs workspace_bytes >= %lld (smx_gemm_workspace_bytes), got %lld",
-                  (long long)pm_park_bytes(q), (long long)(d.workspace ? d.workspace_bytes : 0));
+    Params q = p;
+    pm_grid(q);
     q.park = d.workspace;
     return launch_strassen_pm(q, d.epilogue, s);
   }
   packed_grid(p, d.algo);
   SplitPlan plan{p.tiles_m * p.tiles_n, 0, 1};
-  if (d.workspace) {
+  if (d.workspace)
     if (int rc = split_plan(p, &plan)) return rc;
-    if (plan.split && d.workspace_bytes < split_bytes(p, plan))
-      return fail(SMX_ERR_INVALID, "workspace_bytes %lld is below the %lld this call needs (smx_gemm_workspace_bytes)",
-                  (long long)d.workspace_bytes, (long long)split_bytes(p, plan));
-  }
   if (!plan.split) return launch_packed(p, d.algo, d.epilogue, s);
   if (plan.whole > 0) {
     Params q = p;
@@ -756,8 +774,13 @@ int smx_gemm_workspace_bytes(const smx_gemm_desc* d, int64_t* bytes) {
   g_error[0] = 0;
   if (!bytes) return fail(SMX_ERR_INVALID, "null output");
   *bytes = 0;
+  if (!d) return fail(SMX_ERR_INVALID, "null descriptor");
   // The descriptor is checked as smx_gemm checks it, with placeholders for
-  // the operand pointers (never dereferenced).
+  // the operand pointers (never dereferenced). A row-major A with a packed B
+  // (smx_gemm_noalloc's descriptor) is sized as the packed call it becomes.
+  smx_gemm_desc desc = *d;
+  if (desc.a_layout == SMX_A_ROWMAJOR && desc.b_layout == SMX_B_PACKED) desc.a_layout = SMX_A_PACKED;
+  d = &desc;
   const void* x = kNoAllocScratchProbe;
   Params p{};
   if (int rc = gemm_params(d, x, x, const_cast<void*>(x), x, x, x, x, x, p)) return rc;
@@ -800,6 +823,7 @@ int smx_gemm_noalloc(const smx_gemm_desc* d, const void* a, const void* b, void*
                 "(M*K <= %lld for algo %d)",
                 (long long)kNoAllocScratchBytes, (long long)bytes,
                 (long long)(kNoAllocScratchBytes / (packed::nops_of(d->algo) / 2.0)), d->algo);
+  if (int rc = check_workspace(p, packed)) return rc;
   void* scratch_ptr = nullptr;
   if (int rc = scratch_address(&scratch_ptr)) return rc;
   if (int rc = smx_pack_operand(d->algo, d->formula, d->block_permutation, SMX_SIDE_LHS, d->m, d->k, a,

@@ -100,3 +100,52 @@ def test_noalloc_refuses_calls_beyond_its_scratch():
     rc = lib.smx_gemm_noalloc(d, _lib.ptr(a), _lib.ptr(a), _lib.ptr(a), None, None, None, None, None, stream())
     assert rc == _lib.SMX_ERR_UNSUPPORTED
     assert "scratch" in _lib.last_error()
+
+
+def workspace_bytes(lib, d):
+    need = ctypes.c_int64()
+    _lib.check(lib.smx_gemm_workspace_bytes(d, ctypes.byref(need)))
+    return need.value
+
+
+@pytest.mark.parametrize("flags", [0, _lib.SMX_FLAG_PRODUCT_MAJOR])
+def test_noalloc_with_the_workspace_it_asks_for(flags):
+    """smx_gemm_workspace_bytes sizes the noalloc descriptor (row-major A,
+    packed B) as the packed call it becomes: a launch of 128 product tiles
+    split over K (flags 0) or the product-major kernel's parked sets. With
+    that workspace the result is bit-identical to smx_gemm with the same
+    workspace; with 16 bytes less the call is refused before anything is
+    launched (the output keeps its NaNs)."""
+    lib = _lib.load()
+    algo, m, n, k, tile = _lib.SMX_ALGO_STRASSEN, 2048, 4096, 2048, (256, 512, 512)
+    g = torch.Generator(device=DEV).manual_seed(11)
+    a = torch.randn(m, k, device=DEV, generator=g).to(torch.bfloat16)
+    bt = (torch.randn(n, k, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
+    b_packed = pack(lib, algo, _lib.SMX_SIDE_RHS, bt, tile[1], tile[2])
+    d = desc(m, n, k, tile, algo, None, _lib.SMX_A_ROWMAJOR)
+    d.flags = flags
+    need = workspace_bytes(lib, d)
+    dp = desc(m, n, k, tile, algo, None, _lib.SMX_A_PACKED)
+    dp.flags = flags
+    assert need > 0 and need == workspace_bytes(lib, dp)
+    say(f"  smx_gemm_noalloc flags={flags} workspace={need}")
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    got = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=DEV)
+    d.workspace, d.workspace_bytes = ws.data_ptr(), need - 16
+    rc = lib.smx_gemm_noalloc(d, _lib.ptr(a), _lib.ptr(b_packed), _lib.ptr(got), None, None, None, None, None,
+                              stream())
+    torch.cuda.synchronize()
+    assert rc == _lib.SMX_ERR_INVALID and "workspace" in _lib.last_error()
+    assert torch.isnan(got.float()).all()
+    d.workspace_bytes = need
+    _lib.check(lib.smx_gemm_noalloc(d, _lib.ptr(a), _lib.ptr(b_packed), _lib.ptr(got), None, None, None, None, None,
+                                    stream()))
+    a_packed = pack(lib, algo, _lib.SMX_SIDE_LHS, a, tile[0], tile[2])
+    ws2 = torch.empty(need, dtype=torch.uint8, device=DEV)
+    dp.workspace, dp.workspace_bytes = ws2.data_ptr(), need
+    want = torch.full_like(got, float("nan"))
+    _lib.check(lib.smx_gemm(dp, _lib.ptr(a_packed), _lib.ptr(b_packed), _lib.ptr(want), None, None, None, None, None,
+                            stream()))
+    torch.cuda.synchronize()
+    assert torch.isfinite(got.float()).all()
+    assert torch.equal(got, want)
