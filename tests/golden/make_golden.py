@@ -17,6 +17,10 @@ Fixtures:
   (``Strassen_MM_Focus/data/qwen3-0.6b-real-v001/tensors/layer0_q_proj.bf16``,
   Apache-2.0), after checking the file's SHA-256 against the reference's
   manifest. Stored as raw bf16 bit patterns (uint16).
+* ``qwen3_0p6b_down_proj_slice.npz`` -- a [256, 1024] slice (output features x
+  input features) of the layer-0 down_proj weight the reference ships beside
+  it (``.../tensors/layer0_down_proj.bf16``, [1024, 3072]), SHA-256 checked
+  against its manifest the same way.
 """
 
 from __future__ import annotations
@@ -57,22 +61,25 @@ def accuracy_gate():
         stream.write("\n")
 
 
-def q_proj_slice():
-    meta_path = os.path.join(REFERENCE, TENSOR_DIR, "layer0_q_proj.json")
+def weight_slice(name, rows, cols):
+    """A [rows, cols] slice of a reference tensor, after checking the whole
+    file's SHA-256 against its manifest entry."""
+    meta_path = os.path.join(REFERENCE, TENSOR_DIR, f"layer0_{name}.json")
     with open(meta_path, encoding="utf-8") as stream:
         meta = json.load(stream)
-    raw = open(os.path.join(REFERENCE, TENSOR_DIR, "layer0_q_proj.bf16"), "rb").read()
+    raw = open(os.path.join(REFERENCE, TENSOR_DIR, f"layer0_{name}.bf16"), "rb").read()
     digest = hashlib.sha256(raw).hexdigest()
-    assert digest == meta["sha256"], "q_proj tensor does not match the reference manifest"
-    rows, cols = meta["shape"]
-    weight = np.frombuffer(raw, dtype="<u2").reshape(rows, cols)
-    piece = np.ascontiguousarray(weight[:256, :512])
-    np.savez(os.path.join(HERE, "qwen3_0p6b_q_proj_slice.npz"), weight_bits=piece,
-             source=np.array(f"{TENSOR_DIR}/layer0_q_proj.bf16[:256, :512]"),
+    assert digest == meta["sha256"], f"{name} tensor does not match the reference manifest"
+    full_rows, full_cols = meta["shape"]
+    weight = np.frombuffer(raw, dtype="<u2").reshape(full_rows, full_cols)
+    piece = np.ascontiguousarray(weight[:rows, :cols])
+    np.savez(os.path.join(HERE, f"qwen3_0p6b_{name}_slice.npz"), weight_bits=piece,
+             source=np.array(f"{TENSOR_DIR}/layer0_{name}.bf16[:{rows}, :{cols}]"),
              source_sha256=np.array(digest))
 
 
 if __name__ == "__main__":
     accuracy_gate()
-    q_proj_slice()
+    weight_slice("q_proj", 256, 512)
+    weight_slice("down_proj", 256, 1024)
     print("golden fixtures written to", HERE)

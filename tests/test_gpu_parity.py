@@ -294,6 +294,31 @@ def test_real_qwen3_weight_slice():
         assert rel_l2(got, ref) <= 1.5 * max(rel_l2(want, ref), 1e-4)
 
 
+def test_real_qwen3_down_proj_slice_residual_add():
+    """Real Qwen3-0.6B layer-0 down_proj weights (a [256 out, 1024 in] slice
+    of the reference's test data, SHA-checked when the fixture was written)
+    as B of the residual_add site: H [512, 1024] SwiGLU-sized activations
+    (silu(g) u of unit normals) and a unit-normal residual, every arm within
+    one bf16 ulp of the oracle and within 1.5x the oracle's error against
+    FP32."""
+    data = np.load(os.path.join(GOLDEN, "qwen3_0p6b_down_proj_slice.npz"))
+    w_bits = data["weight_bits"]  # [out=256, in=1024]
+    w = o.bits_to_f32(w_bits)
+    b = np.ascontiguousarray(w.T)  # [K=1024, N=256]
+    rng = np.random.default_rng(2027)
+    g, u = rng.standard_normal((2, 512, 1024)).astype(np.float32)
+    h = o.bf16_round(g / (1.0 + np.exp(-g)) * u)
+    r = o.bf16_round(rng.standard_normal((512, 256)).astype(np.float32))
+    b_dev = torch.from_numpy(w_bits.view(np.int16)).view(torch.bfloat16).to(DEV).t()
+    ref = (o.high_precision_reference(h, b) + r).astype(np.float64)
+    kw = dict(bm=256, bn=256, bk=512, epilogue="residual_add")
+    for arm in ARMS:
+        got = host(run_arm(arm, h, b_dev, residual=dev(r), **kw))
+        want = oracle_arm(arm, h, b, residual=r, **kw)
+        assert_ulp_close(got, want, k=1024)
+        assert rel_l2(got, ref) <= 1.5 * max(rel_l2(want, ref), 1e-4), arm
+
+
 @pytest.mark.slow
 def test_published_accuracy_gate_on_gpu():
     """The reference's accuracy gate, regenerated: Strassen error vs FP32 on

@@ -767,3 +767,115 @@ def test_torch_cpu_restatement_matches_numpy_oracle():
     e_got = np.linalg.norm(got - ref) / np.linalg.norm(ref)
     e_want = np.linalg.norm(want - ref) / np.linalg.norm(ref)
     assert abs(e_got - e_want) < 0.02 * e_want
+
+
+# ---------------------------------------------------------------------------
+# Closed-form pins of the unfused RMSNorm / RoPE helpers
+# (benchmark_qwen3_32b_layer.py:258-284), independent of the block's copies.
+# ---------------------------------------------------------------------------
+
+def test_rope_values_closed_form():
+    """cos / sin [p, i] = cos / sin(p theta^(-2 (i mod D/2) / D)), both halves
+    equal, position 0 the identity; the float32 angle computation and the one
+    bf16 rounding stay within one bf16 ulp of the float64 value."""
+    seq, hd, theta = 64, 128, 1e6
+    cos, sin = o.rope_values(seq, hd, theta)
+    i = np.arange(hd) % (hd // 2)
+    angles = np.arange(seq, dtype=np.float64)[:, None] * theta ** (-2.0 * i[None, :] / hd)
+    for got, want in ((cos, np.cos(angles)), (sin, np.sin(angles))):
+        assert got.shape == (seq, hd)
+        assert np.array_equal(got[:, : hd // 2], got[:, hd // 2:])
+        assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.maximum(np.abs(want), 2.0 ** -8) + 1e-7)
+    assert np.array_equal(cos[0], np.ones(hd)) and np.array_equal(sin[0], np.zeros(hd))
+    # a planted mistake (the inverse frequency over D/2 instead of D) fails it
+    wrong = np.cos(np.arange(seq, dtype=np.float64)[:, None] * theta ** (-2.0 * i[None, :] / (hd // 2)))
+    assert np.max(np.abs(cos - wrong)) > 0.5
+
+
+def test_apply_rope_closed_forms():
+    """Position 0 is the identity; a basis vector e_i (i < D/2) maps to
+    cos e_i + sin e_{i+D/2} and e_{i+D/2} to -sin e_i + cos e_{i+D/2} (the
+    reference's x cos + concat(-x2, x1) sin); each (i, i + D/2) pair keeps
+    its norm; rotating by p then by q is rotating by p + q (float64 tables,
+    so only the bf16 output rounding remains)."""
+    rng = np.random.default_rng(41)
+    hd, seq = 128, 8
+    x = o.bf16_round(rng.standard_normal((1, seq, 2, hd)).astype(np.float32))
+    cos, sin = o.rope_values(seq, hd, 1e6)
+    assert np.array_equal(o.apply_rope(x[:, :1], cos[:1], sin[:1]), x[:, :1])
+    angle = 0.75
+    c = np.full((1, hd), np.cos(angle), np.float32)
+    s = np.full((1, hd), np.sin(angle), np.float32)
+    for i in (0, 5, hd // 2 - 1):
+        e = np.zeros((1, 1, 1, hd), np.float32)
+        e[..., i] = 1.0
+        out = o.apply_rope(e, c, s)[0, 0, 0]
+        want = np.zeros(hd, np.float32)
+        want[i], want[i + hd // 2] = np.cos(angle), np.sin(angle)
+        assert np.allclose(out, o.bf16_round(want), atol=0), i
+        e2 = np.zeros((1, 1, 1, hd), np.float32)
+        e2[..., i + hd // 2] = 1.0
+        out2 = o.apply_rope(e2, c, s)[0, 0, 0]
+        want2 = np.zeros(hd, np.float32)
+        want2[i], want2[i + hd // 2] = -np.sin(angle), np.cos(angle)
+        assert np.allclose(out2, o.bf16_round(want2), atol=0), i
+    # norm of each pair, and composition, with exact (float64-derived) tables
+    p, q = 3.0, 11.0
+    freq = 1e6 ** (-2.0 * (np.arange(hd) % (hd // 2)) / hd)
+    tables = {a: (np.cos(a * freq)[None].astype(np.float32), np.sin(a * freq)[None].astype(np.float32))
+              for a in (p, q, p + q)}
+    y = x[:, :1]
+    once = o.apply_rope(y, *tables[p])
+    pair = lambda v: v[..., : hd // 2] ** 2 + v[..., hd // 2:] ** 2  # noqa: E731
+    assert np.allclose(pair(once), pair(y), rtol=2 ** -6, atol=1e-3)
+    twice = o.apply_rope(once, *tables[q])
+    direct = o.apply_rope(y, *tables[p + q])
+    assert np.allclose(twice, direct, rtol=2 ** -6, atol=2 ** -6)
+
+
+def test_rms_norm_closed_forms():
+    """Under unit gamma a normalised row has unit RMS (to bf16 rounding);
+    gamma scales the output elementwise; with eps = 0 the map is invariant
+    to scaling a row by a power of two (every step scales exactly); a
+    constant row maps to +-1."""
+    rng = np.random.default_rng(42)
+    x = o.bf16_round(rng.standard_normal((16, 512)).astype(np.float32) * 3.0)
+    y = o.rms_norm(x, np.ones(512, np.float32), 1e-6)
+    rms = np.sqrt(np.mean(y.astype(np.float64) ** 2, axis=-1))
+    assert np.all(np.abs(rms - 1.0) < 2 ** -8)
+    g = o.bf16_round((1 + 0.1 * rng.standard_normal(512)).astype(np.float32))
+    unscaled = o.rms_norm(x, np.ones(512, np.float32), 0.0)
+    assert np.allclose(o.rms_norm(x, g, 0.0), o.bf16_round(unscaled * g), rtol=2 ** -7, atol=0)
+    assert np.array_equal(o.rms_norm(4.0 * x, g, 0.0), o.rms_norm(x, g, 0.0))
+    const = np.full((2, 64), -2.5, np.float32)
+    assert np.array_equal(o.rms_norm(const, np.ones(64, np.float32), 0.0), -np.ones((2, 64), np.float32))
+
+
+# SHA-256 of the reference's real-weight test tensors, from its manifest
+# (Strassen_MM_Focus/data/qwen3-0.6b-real-v001/manifest.json, "tensors" list).
+REAL_WEIGHT_SHA256 = {
+    "q_proj": "7592f6e783c400f502653f77d9b483cb03e96c3061af16f538da0d695d21bc53",
+    "down_proj": "01cc5c354c8ac9cf4917157d74beceb0b3ce3f38d9bdec271ae691bded0b2e3b",
+}
+
+
+@pytest.mark.parametrize("name,shape", [("q_proj", (256, 512)), ("down_proj", (256, 1024))])
+def test_real_weight_slices(name, shape):
+    """The committed slices come from the manifest-checked reference tensors
+    (tests/golden/make_golden.py) and hold finite, weight-sized bf16 values;
+    the oracle's Strassen product on them lands in the reference's published
+    error band against FP32 (a few 1e-3, strassen_v5e_classical_comparison.jsonl:3)."""
+    data = np.load(os.path.join(GOLDEN, f"qwen3_0p6b_{name}_slice.npz"))
+    assert str(data["source_sha256"]) == REAL_WEIGHT_SHA256[name]
+    assert str(data["source"]).endswith(f"layer0_{name}.bf16[:{shape[0]}, :{shape[1]}]")
+    bits = data["weight_bits"]
+    assert bits.shape == shape and bits.dtype == np.uint16
+    w = o.bits_to_f32(bits)
+    assert np.isfinite(w).all() and 1e-3 < float(np.std(w)) < 0.2
+    b = np.ascontiguousarray(w.T)  # [K, N]
+    rng = np.random.default_rng(77)
+    a = o.bf16_round(rng.standard_normal((256, b.shape[0])).astype(np.float32))
+    ref = o.high_precision_reference(a, b).astype(np.float64)
+    got = o.strassen_matmul(a, b, bm=256, bn=256, bk=256)
+    err = float(np.linalg.norm(got - ref) / np.linalg.norm(ref))
+    assert 1e-3 < err < 1e-2
