@@ -477,7 +477,9 @@ def main():
     if os.path.exists(measured):
         rec = json.load(open(measured))["strassen"]
         traffic = round(rec["traffic_bytes"])
-        traffic_note = (f"HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE passes scaled by a copy-kernel "
+        traffic_note = (f"L2-miss bytes per launch (reads and writes between the XCDs' L2 and the memory side, "
+                        f"which the 256 MB MALL or HBM serves: rocprofv3 exposes no counter that tells them apart on "
+                        f"this image) from rocprofv3 FETCH_SIZE/WRITE_SIZE passes scaled by a copy-kernel "
                         f"calibration (profiles/gemm_split_strassen_swiglu_qwen3_32b_gate_up.md); algorithmic "
                         f"{rec['algorithmic_bytes']} B")
     roofline = {

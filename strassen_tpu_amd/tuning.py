@@ -39,9 +39,9 @@ import torch
 
 from . import _lib
 from .layouts import swiglu_weight_layout
-from .packing import (cache_packed_weights, cubic_weight_layout, pack_activation, packed_weight_cache_info,
-                      strassen_weight_layout, weight_cached_or_fits)
-from .strassen import cubic_matmul, native_matmul, strassen_matmul
+from .packing import (cache_packed_weights, cubic_weight_layout, pack_activation, pack_operand,
+                      packed_weight_cache_info, strassen_weight_layout, weight_cached_or_fits)
+from .strassen import cubic_matmul, native_matmul, per_call_packing_expected, strassen_matmul
 
 __all__ = ["TILE_RULE", "enumerate_candidates", "time_calls", "screen_tiles", "measure_dispatch",
            "load_table", "tuned_matmul", "DEFAULT_TABLE"]
@@ -247,15 +247,17 @@ def measure_dispatch(shapes, *, tile=(1024, 1024, 512), margin=0.02, seed=0, war
 
         def phase(arms, cache_bytes):
             """Interleaved samples of ``arms`` with the packed-weight cache at
-            ``cache_bytes`` (0: the weight packed on every call)."""
+            ``cache_bytes`` (0: the weight packed on every call, on purpose,
+            so the plain-weight warning is held back)."""
             previous = cache_packed_weights(cache_bytes)
             try:
-                for _ in range(warmups):
-                    for arm in arms:
-                        calls[arm]()
-                for r in range(runs):
-                    for arm in (arms if r % 2 == 0 else arms[::-1]):
-                        samples[arm] += time_calls(calls[arm], 0, 1, batch=batch)
+                with per_call_packing_expected():
+                    for _ in range(warmups):
+                        for arm in arms:
+                            calls[arm]()
+                    for r in range(runs):
+                        for arm in (arms if r % 2 == 0 else arms[::-1]):
+                            samples[arm] += time_calls(calls[arm], 0, 1, batch=batch)
             finally:
                 cache_packed_weights(0)
                 cache_packed_weights(previous)
@@ -411,6 +413,68 @@ def measure_small_launches(shapes=SMALL_LAUNCH_SHAPES, *, bn=256, bk=512, seed=0
     return results
 
 
+# Kernels one pure GEMM launch can run on (measure_launches).
+LAUNCH_ARMS = ("hipblaslt", "cubic", "strassen", "product_major")
+
+
+def measure_launches(arm, m, k, n, *, tile=(1024, 1024, 512), calls=10, seed=0, device="cuda:0", emit=None):
+    """``calls`` timed launches of one pure bf16 GEMM (no epilogue) on one
+    kernel, for counter runs under a profiler: ``hipblaslt`` (torch.matmul
+    on an ``[in, out]`` view of an ``[out, in]`` weight), or ``cubic`` /
+    ``strassen`` / ``product_major`` through ``smx_gemm`` on operands packed
+    beforehand (the product-major kernel with SMX_FLAG_PRODUCT_MAJOR). One
+    untimed launch first; returns the per-launch milliseconds (HIP events)."""
+    import ctypes
+
+    if arm not in LAUNCH_ARMS:
+        raise ValueError(f"arm must be one of {LAUNCH_ARMS}")
+    emit = emit or (lambda record: None)
+    dev = torch.device(device)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    a = torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn(n, k, device=dev, generator=g) * 0.02).to(torch.bfloat16).t()
+    if arm == "hipblaslt":
+        call = lambda: torch.matmul(a, w)  # noqa: E731
+    else:
+        algo = _lib.SMX_ALGO_CUBIC if arm == "cubic" else _lib.SMX_ALGO_STRASSEN
+        bm, bn, bk = tile
+        pa = pack_operand(a, algo=algo, side="lhs", tile_rows=bm, bk=bk)
+        pb = pack_operand(w, algo=algo, side="rhs", tile_rows=bn, bk=bk)
+        lib = _lib.load()
+        d = _lib.SmxGemmDesc()
+        d.m, d.n, d.k = m, n, k
+        d.lda, d.ldb, d.ldc = k, k, n
+        d.bm, d.bn, d.bk = tile
+        d.algo, d.epilogue = algo, _lib.SMX_EPI[None]
+        d.a_layout, d.b_layout = _lib.SMX_A_PACKED, _lib.SMX_B_PACKED
+        d.flags = _lib.SMX_FLAG_PRODUCT_MAJOR if arm == "product_major" else 0
+        need = ctypes.c_int64()
+        _lib.check(lib.smx_gemm_workspace_bytes(d, ctypes.byref(need)))
+        workspace = None
+        if need.value:
+            workspace = torch.empty(need.value, dtype=torch.uint8, device=dev)
+            d.workspace, d.workspace_bytes = workspace.data_ptr(), need.value
+        out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+        def call():
+            _lib.check(lib.smx_gemm(d, _lib.ptr(pa.data), _lib.ptr(pb.data), _lib.ptr(out), None, None, None, None,
+                                    None, stream))
+    call()
+    torch.cuda.synchronize(dev)
+    times = []
+    for _ in range(calls):
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        call()
+        stop.record()
+        torch.cuda.synchronize(dev)
+        times.append(start.elapsed_time(stop))
+    emit({"kind": "launches", "arm": arm, "shape": [m, k, n], "tile": list(tile), "ms": times,
+          "tflops": 2.0 * m * n * k / (statistics.fmean(times) * 1e-3) / 1e12})
+    return times
+
+
 _TABLE = None
 
 
@@ -495,7 +559,11 @@ def main(argv=None):
     decode.add_argument("--runs", type=int, default=30)
     small = sub.add_parser("small", help="Strassen, cubic and hipBLASLt on launches with few tiles (the K split)")
     small.add_argument("--runs", type=int, default=10)
-    for p in (screen, dispatch, occupancy, decode, small):
+    launches = sub.add_parser("launches", help="timed launches of one pure GEMM on one kernel (for counter runs)")
+    launches.add_argument("--arm", choices=LAUNCH_ARMS, required=True)
+    launches.add_argument("--shape", default="8192,5120,25600", help="m,k,n (default: a Qwen3-32B gate or up)")
+    launches.add_argument("--calls", type=int, default=10)
+    for p in (screen, dispatch, occupancy, decode, small, launches):
         p.add_argument("--out", default=None, help="also append the JSON records to this file")
     args = ap.parse_args(argv)
     sink = open(args.out, "a") if args.out else None
@@ -520,6 +588,9 @@ def main(argv=None):
         measure_decode(runs=args.runs, emit=emit)
     elif args.command == "small":
         measure_small_launches(runs=args.runs, emit=emit)
+    elif args.command == "launches":
+        m, k, n = (int(v) for v in args.shape.split(","))
+        measure_launches(args.arm, m, k, n, calls=args.calls, emit=emit)
     else:
         table = measure_dispatch(DISPATCH_SHAPES, runs=args.runs, emit=emit)
         emit({"kind": "table", **table})
