@@ -173,6 +173,19 @@ class PlainWeightPackWarning(UserWarning):
 
 
 _PLAIN_PACK_WARNED = False
+_PLAIN_PACK_EXPECTED = 0
+
+
+@contextlib.contextmanager
+def per_call_packing_expected():
+    """Calls inside pack plain weights per call on purpose (a measurement of
+    that cost): they neither warn nor use up the once-per-process warning."""
+    global _PLAIN_PACK_EXPECTED
+    _PLAIN_PACK_EXPECTED += 1
+    try:
+        yield
+    finally:
+        _PLAIN_PACK_EXPECTED -= 1
 
 
 def _plain_weight(b, **packing):
@@ -180,7 +193,8 @@ def _plain_weight(b, **packing):
     packed-weight cache when enabled). The first per-call pack of a process
     without a cache warns once: it repeats on every call."""
     global _PLAIN_PACK_WARNED
-    if not _PLAIN_PACK_WARNED and packed_weight_cache_info()["capacity"] <= 0:
+    if (not _PLAIN_PACK_WARNED and not _PLAIN_PACK_EXPECTED
+            and packed_weight_cache_info()["capacity"] <= 0):
         _PLAIN_PACK_WARNED = True
         warnings.warn("a plain weight is packed on every call (a Strassen weight packs to 7/4 of its bytes): "
                       "pack it once with strassen_weight_layout / cubic_weight_layout, or keep packed weights "

@@ -3,6 +3,8 @@ strassen_matmul / cubic_matmul is packed once and reused while unchanged,
 with results bit-identical to packing it for every call, and an in-place
 update of the weight is seen on the next call."""
 
+import warnings
+
 import numpy as np
 import pytest
 import torch
@@ -74,6 +76,25 @@ def test_per_call_packing_warns_once():
         with pytest.warns(smx.PlainWeightPackWarning, match="packed on every call"):
             smx.strassen_matmul(dev(a), dev_weight(b), bm=256, bn=256, bk=512)
         assert surface._PLAIN_PACK_WARNED
+    finally:
+        smx.cache_packed_weights(previous)
+    torch.cuda.synchronize(DEV)
+
+
+def test_expected_per_call_packing_keeps_the_warning():
+    """A measurement that packs per call on purpose neither warns nor uses
+    up the warning of a later per-call pack."""
+    a, b = _problem()
+    previous = smx.cache_packed_weights(0)
+    surface._PLAIN_PACK_WARNED = False
+    try:
+        with warnings.catch_warnings():
+            warnings.simplefilter("error", smx.PlainWeightPackWarning)
+            with surface.per_call_packing_expected():
+                smx.strassen_matmul(dev(a), dev_weight(b), bm=256, bn=256, bk=512)
+        assert not surface._PLAIN_PACK_WARNED
+        with pytest.warns(smx.PlainWeightPackWarning, match="packed on every call"):
+            smx.strassen_matmul(dev(a), dev_weight(b), bm=256, bn=256, bk=512)
     finally:
         smx.cache_packed_weights(previous)
     torch.cuda.synchronize(DEV)
