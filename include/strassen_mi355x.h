@@ -194,12 +194,12 @@ int smx_gemm_noalloc(const smx_gemm_desc* desc, const void* a, const void* b, vo
 /* Bytes of device workspace with which smx_gemm runs this descriptor's
  * call: for a call on the product-major kernel (SMX_FLAG_PRODUCT_MAJOR),
  * 256 KB per 128 x 256 product tile, (M/2 / 128) (N/2 / 256) tiles, which
- * the call then requires. Otherwise the bytes (s * M * N floats for s K
- * shares) with which
+ * the call then requires. Otherwise the bytes (s * r * 256 KB: one dense
+ * 256 x 256 FP32 block per K share and split tile) with which
  * smx_gemm splits tiles of this descriptor's launch over K, on the current
  * device. T tiles on the device's C CUs make T / C whole rounds and a last
  * round of r = T mod C tiles; those r tiles split into the s shares,
- * 2 <= s <= min(16, K / 512, 2^30 / (4 M N)), that minimise
+ * 2 <= s <= min(16, K / 512, 2^30 / (r * 256 KB)), that minimise
  * ceil(s r / C) (1/s + f) + s r g (f = 400 / K, g = (5/3) / K: a workgroup's
  * fixed time and the summing pass's traffic, in units of a full-K tile's
  * time), when that is under 0.95 (1 + f). 0 when no split applies: an

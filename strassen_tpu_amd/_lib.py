@@ -161,4 +161,12 @@ def k_shares(m, k, n, tile, algo=SMX_ALGO_STRASSEN):
     d.rope_head_dim, d.rope_eps = 128, 1e-6
     need = ctypes.c_int64()
     check(lib.smx_gemm_workspace_bytes(d, ctypes.byref(need)))
-    return max(1, need.value // (m * n * 4))
+    if not need.value:
+        return 1
+    # The workspace holds one 256 x 256 FP32 block per share and split tile;
+    # the split tiles are the last round's (128 x 128 product tiles, one per CU
+    # and round).
+    cus = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
+    tiles = -(-(m // 2) // 128) * ((n // 2) // 128)
+    split = tiles % cus or cus
+    return need.value // (split * 256 * 256 * 4)

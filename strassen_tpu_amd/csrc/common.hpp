@@ -298,8 +298,10 @@ struct Params {
   // Launch shape (packed kernels): grid workgroups (0: tiles_m * tiles_n).
   // A K-split launch (ksplit s > 1, grid s u) gives workgroup h u + w the
   // tile tile_base + w and share h of its S K stages, stages
-  // floor(h S / s) .. floor((h + 1) S / s) - 1 (S >= s), and moves share h's
-  // output by h * split_stride elements.
+  // floor(h S / s) .. floor((h + 1) S / s) - 1 (S >= s), and stores that
+  // share as a dense FP32 block (dense_share_output): share h of split tile
+  // w at h * split_stride + w * kSplitTileFloats floats, split_stride =
+  // u * kSplitTileFloats.
   int32_t grid;
   int32_t ksplit;
   int32_t tile_base;
@@ -432,6 +434,24 @@ __device__ __forceinline__ TileOrigin tile_origin(const Params& p, int64_t prow0
   o.tj = uniform(c / hn);
   o.tc = uniform(c % hn);
   return o;
+}
+
+// FP32 elements of one K share of one split tile: its 256 x 256 outputs.
+constexpr int64_t kSplitTileFloats = 256 * 256;
+
+// A K share's output (the no-epilogue FP32 store of a K-split launch) goes to
+// the workspace as a dense 256 x 256 block per split tile: the tile's four
+// 128 x 128 quadrant blocks at row and column offsets 0 and 128, row stride
+// 256, in the order the block permutation stores them. The store code is the
+// ordinary epilogue's, on the geometry of a 256 x 256 tiling whose only tile
+// sits at the origin (a thin tiling then maps every product row straight to
+// a row of its half). split_fixup reads the blocks back.
+__device__ __forceinline__ void dense_share_output(Params& p, TileOrigin& o, const WorkShare& ws) {
+  p.c = reinterpret_cast<float*>(p.c) + ws.share * p.split_stride + (int64_t)(ws.tile - p.tile_base) * kSplitTileFloats;
+  p.bm = p.bn = 256;
+  p.m = p.n = 256;
+  p.ldc = 256;
+  o = TileOrigin{0, 0, 0, 0};
 }
 
 // Output rows of a thin tiling. Product row P (of M/2) is row P % hm of row

@@ -153,10 +153,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
 
   const int nstages_all = (int)(p.k / (2 * TK));
   const WorkShare ws = work_share(p, nstages_all);
-  if (ws.share) p.c = reinterpret_cast<float*>(p.c) + ws.share * p.split_stride;
   int tile_m, tile_n;
   tile_of(ws.tile, p.tiles_m, p.tiles_n, p.group_m, p.raster, tile_m, tile_n);
-  const TileOrigin o = tile_origin<kThin>(p, (int64_t)tile_m * TM, (int64_t)tile_n * TN);
+  TileOrigin o = tile_origin<kThin>(p, (int64_t)tile_m * TM, (int64_t)tile_n * TN);
+  // K-split shares run without an epilogue and store dense FP32 blocks.
+  if constexpr (kEpi == SMX_EPI_NONE)
+    if (p.ksplit > 1) dense_share_output(p, o, ws);
   const int nstages = ws.nstages;
 
   // DMA sources: this workgroup's packed stages are contiguous runs of

@@ -367,7 +367,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
   const int lane = tid & 63;
   const int nstages_all = (int)(p.k / (2 * TK));
   const WorkShare ws = work_share(p, nstages_all);
-  if (ws.share) p.c = reinterpret_cast<float*>(p.c) + ws.share * p.split_stride;
   int tile_m, tile_n;
   tile_of(ws.tile, p.tiles_m, p.tiles_n, p.group_m, p.raster, tile_m, tile_n);
   // The tile indices are uniform, but the integer divisions that produce
@@ -375,7 +374,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
   // derived from them) to SGPRs, which keeps VGPRs for the accumulators.
   tile_m = __builtin_amdgcn_readfirstlane(tile_m);
   tile_n = __builtin_amdgcn_readfirstlane(tile_n);
-  const TileOrigin o = tile_origin<kThin>(p, (int64_t)tile_m * packed::TM, (int64_t)tile_n * packed::TN);
+  TileOrigin o = tile_origin<kThin>(p, (int64_t)tile_m * packed::TM, (int64_t)tile_n * packed::TN);
+  // K-split shares run without an epilogue and store dense FP32 blocks.
+  if constexpr (kEpi == SMX_EPI_NONE)
+    if (p.ksplit > 1) dense_share_output(p, o, ws);
   const int nstages = ws.nstages;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t panel_bytes = (uint32_t)nstages * L::kStage - wave * kFrag;

@@ -1,9 +1,9 @@
 // Second pass of a K-split launch (smx_gemm with a workspace): some tiles
 // of a packed launch ran as p.ksplit shares of their K stages, each share
-// writing its FP32 result, laid out as the [M, N] output, into its own part
-// of the workspace. This pass sums the shares in share order and applies the
-// epilogue the fused kernels apply (strassen_pallas.py:739-879), on the
-// physical output positions.
+// writing its FP32 result into the workspace as one dense 256 x 256 block per
+// split tile (dense_share_output). This pass sums the shares in share order
+// and applies the epilogue the fused kernels apply
+// (strassen_pallas.py:739-879), on the physical output positions.
 #pragma once
 
 #include "common.hpp"
@@ -24,8 +24,10 @@ constexpr int kFixupSlices = 8;
 // i < 2, of the 256. Product row P is output row (P / hm) bm + half hm +
 // P % hm (one row tile per product tile unless the tiling is thin); rows
 // past M/2 (a thin tiling's padding) are neither read nor written. `ws`
-// holds the p.ksplit shares, split_stride floats apart, with row stride N.
-// p is the fused call's Params.
+// holds the p.ksplit shares, split_stride floats apart; in a share, split
+// tile u's block starts at u * kSplitTileFloats and holds the tile's row
+// lr (row half lr / 128) and column half c at lr * 256 + 128 c. p is the
+// fused call's Params.
 template <int kEpi>
 __global__ __launch_bounds__(256) void split_fixup(Params p, const float* __restrict__ ws) {
   const int u = (int)blockIdx.x / kFixupSlices, slice = (int)blockIdx.x % kFixupSlices;
@@ -58,10 +60,11 @@ __global__ __launch_bounds__(256) void split_fixup(Params p, const float* __rest
     const uint32_t prow = prow0 + (uint32_t)(lr & 127);
     if (!rows.valid(prow)) continue;  // uniform over the 16 lanes of a row
     const int64_t row = rows.row(prow, lr >> 7);
-    F8 a = load8(ws, 1, row * p.n + col_a), b = load8(ws, 1, row * p.n + col_b);
+    const int64_t at = (int64_t)u * kSplitTileFloats + lr * 256 + (t & 15) * 8;
+    F8 a = load8(ws, 1, at), b = load8(ws, 1, at + 128);
     for (int h = 1; h < p.ksplit; ++h) {
       const float* const wh = ws + h * p.split_stride;
-      const F8 ah = load8(wh, 1, row * p.n + col_a), bh = load8(wh, 1, row * p.n + col_b);
+      const F8 ah = load8(wh, 1, at), bh = load8(wh, 1, at + 128);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         a.v[e] += ah.v[e];

@@ -414,7 +414,7 @@ void packed_grid(Params& p, int algo) {
 constexpr int64_t kSplitMinK = 2048;
 // A K share keeps at least this many 32-deep K stages; a launch splits its
 // tiles at most this many ways, and into no more shares than keep the
-// workspace (shares x M x N floats) within kSplitMaxBytes.
+// workspace (shares x split tiles x 256 KB) within kSplitMaxBytes.
 constexpr int kSplitMinStages = 16;
 constexpr int kMaxKSplit = 16;
 constexpr int64_t kSplitMaxBytes = (int64_t)1 << 30;
@@ -454,7 +454,7 @@ int split_plan(const Params& p, SplitPlan* plan) {
   const int r = tiles % cus;
   if (r == 0) return SMX_OK;
   const int stages = (int)(p.k / (2 * packed::TK));
-  const int64_t share_bytes = p.m * p.n * (int64_t)sizeof(float);
+  const int64_t share_bytes = (int64_t)r * kSplitTileFloats * (int64_t)sizeof(float);
   const int s_max = (int)std::min<int64_t>(std::min(kMaxKSplit, stages / kSplitMinStages), kSplitMaxBytes / share_bytes);
   int best_s = 1;
   double best = 0.95 * split_cost(1, r, cus, p.k);
@@ -469,8 +469,8 @@ int split_plan(const Params& p, SplitPlan* plan) {
   return SMX_OK;
 }
 
-int64_t split_bytes(const Params& p, const SplitPlan& plan) {
-  return (int64_t)plan.ksplit * p.m * p.n * (int64_t)sizeof(float);
+int64_t split_bytes(const Params&, const SplitPlan& plan) {
+  return (int64_t)plan.ksplit * plan.split * kSplitTileFloats * (int64_t)sizeof(float);
 }
 
 template <int kEpi>
@@ -577,7 +577,6 @@ int launch_gemm(Params p, const smx_gemm_desc& d, hipStream_t s) {
   }
   Params h = p;
   h.c = d.workspace;
-  h.ldc = p.n;
   h.out_f32 = 1;
   h.residual = h.bias = nullptr;
   h.rope_cos = h.rope_sin = nullptr;
@@ -585,12 +584,12 @@ int launch_gemm(Params p, const smx_gemm_desc& d, hipStream_t s) {
   h.grid = plan.ksplit * plan.split;
   h.ksplit = plan.ksplit;
   h.tile_base = plan.whole;
-  h.split_stride = p.m * p.n;
+  h.split_stride = (int64_t)plan.split * kSplitTileFloats;
   if (int rc = launch_packed(h, d.algo, SMX_EPI_NONE, s)) return rc;
   Params f = p;
   f.ksplit = plan.ksplit;
   f.tile_base = plan.whole;
-  f.split_stride = p.m * p.n;
+  f.split_stride = (int64_t)plan.split * kSplitTileFloats;
   return launch_split_fixup(f, d.epilogue, (const float*)d.workspace, plan.split, s);
 }
 

@@ -43,10 +43,20 @@ def _announce(request):
     torch.cuda.synchronize()
 
 
+# Workspace of one K share of one split tile: its 256 x 256 FP32 outputs.
+SPLIT_TILE_BYTES = 256 * 256 * 4
+
+
+def _workspace_bytes(m, n, k, bm=256):
+    """The workspace the library asks for: s shares of the r split tiles."""
+    _, split, s = _plan(m, n, k, bm)
+    return s * split * SPLIT_TILE_BYTES if split else 0
+
+
 def _plan(m, n, k, bm=256):
     """(whole tiles, split tiles, shares) of the library's rule, restated:
     the last round's r tiles (all T of a launch under one round) split into
-    the s <= min(16, K / 512, 2^30 / (4 M N)) shares that minimise
+    the s <= min(16, K / 512, 2^30 / (r 256 KB)) shares that minimise
     ceil(s r / C) (1/s + f) + s r g (f = 400 / K, g = (5/3) / K), when that
     is under 0.95 of the unsplit 1 + f. SMX_TAIL_SPLIT starting with 0 in
     the environment turns the split off."""
@@ -55,7 +65,7 @@ def _plan(m, n, k, bm=256):
     r = tiles % cus
     if os.environ.get("SMX_TAIL_SPLIT", "").startswith("0") or k < 2048 or r == 0:
         return tiles, 0, 1
-    s_max = min(16, (k // 32) // 16, (1 << 30) // (4 * m * n))
+    s_max = min(16, (k // 32) // 16, (1 << 30) // (r * SPLIT_TILE_BYTES))
 
     def cost(s):
         f, g = 400.0 / k, (5.0 / 3.0) / k
@@ -158,7 +168,7 @@ def test_half_round_split_matches_whole_and_oracle(algo, epilogue):
     pa, pb = _pack(algo, a, b, TILE)
     split, need = abi_gemm(algo, pa, pb, m, n, k, TILE, epilogue, workspace=True, **aux_dev)
     whole, _ = abi_gemm(algo, pa, pb, m, n, k, TILE, epilogue, workspace=False, **aux_dev)
-    assert need == _plan(m, n, k)[2] * m * n * 4
+    assert need == _workspace_bytes(m, n, k)
     got, ref = host(split), host(whole)
     assert_ulp_close(got, ref, k=k)
     assert_ulp_close(got, _oracle(algo, a, b, TILE, epilogue=epilogue, **aux), k=k)
@@ -251,7 +261,7 @@ def test_ragged_tail_with_float32_operands(algo, shape):
         aux_dev = {key: dev32(v) for key, v in aux.items()}
         split, need = abi_gemm(algo, pa, pb, m, n, k, TILE, epilogue, workspace=True, **aux_dev)
         whole, _ = abi_gemm(algo, pa, pb, m, n, k, TILE, epilogue, workspace=False, **aux_dev)
-        assert need == _plan(m, n, k)[2] * m * n * 4
+        assert need == _workspace_bytes(m, n, k)
         got = host(split)
         assert_ulp_close(got, host(whole), k=k)
         assert_ulp_close(got, _oracle(algo, a, b, TILE, epilogue=epilogue, **aux), k=k)
@@ -276,7 +286,7 @@ def test_workspace_below_the_size_asked_for_is_refused():
     _, a, b = _problem(5, m, k, n)
     pa, pb = _pack(7, a, b, TILE)
     with pytest.raises(ValueError, match="workspace_bytes"):
-        abi_gemm(7, pa, pb, m, n, k, TILE, workspace=True, workspace_bytes=2 * m * n * 4 - 16)
+        abi_gemm(7, pa, pb, m, n, k, TILE, workspace=True, workspace_bytes=_workspace_bytes(m, n, k) - 16)
 
 
 @pytest.mark.parametrize("case", ["full_round", "short_k", "full_last_round", "partial"])
@@ -335,7 +345,7 @@ def test_small_launch_split_every_tile(algo, shape, tile, epilogue):
     pa, pb = _pack(algo, a, b, tile)
     got_split, need = abi_gemm(algo, pa, pb, m, n, k, tile, epilogue, workspace=True, **aux_dev)
     got_whole, _ = abi_gemm(algo, pa, pb, m, n, k, tile, epilogue, workspace=False, **aux_dev)
-    assert whole_tiles == 0 and need == s * m * n * 4
+    assert whole_tiles == 0 and need == s * split * SPLIT_TILE_BYTES
     got = host(got_split)
     assert_ulp_close(got, host(got_whole), k=k)
     assert_ulp_close(got, _oracle(algo, a, b, tile, epilogue=epilogue, **aux), k=k)
@@ -355,7 +365,7 @@ def test_small_thin_launch_qk_norm_rope(algo):
     rope = (dev(tcos), dev(tsin), torch.from_numpy(scale).to(DEV).to(torch.bfloat16))
     split, need = abi_gemm(algo, pa, pb, m, n, k, tile, "qk_norm_rope", workspace=True, rope=rope)
     whole, _ = abi_gemm(algo, pa, pb, m, n, k, tile, "qk_norm_rope", workspace=False, rope=rope)
-    assert need == _plan(m, n, k, 16)[2] * m * n * 4
+    assert need == _workspace_bytes(m, n, k, 16)
     got = host(split)
     assert_ulp_close(got, host(whole), k=k)
     want = _oracle(algo, x, laid, tile, epilogue="qk_norm_rope", rope_cos=tcos, rope_sin=tsin, rope_scale=scale,
