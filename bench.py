@@ -41,6 +41,8 @@ BATCH, SEQ = 8, 1024
 THETA, EPS = 1e6, 1e-6
 TILE = (1024, 1024, 512)
 COPY_BYTES = 256 << 20
+# The default Strassen arm's packed weights on the opt-in product-major kernel.
+PM_ARM = "strassen_product_major"
 
 
 def log(*args):
@@ -374,7 +376,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default=None,
                     help="profiling runs: time only ARM:SITE (ARM strassen|cubic|strassen_plain|cubic_plain|"
-                         "hipblaslt; SITE q|k|v|o|gate_up|down|pure_gate_up|pure_down|pure_o, or gate_up_gemm "
+                         "hipblaslt|strassen_product_major; SITE q|k|v|o|gate_up|down|pure_gate_up|pure_down|pure_o, or gate_up_gemm "
                          "for the packed GEMM launch alone), or \"copy\" (a 256 MiB copy, counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -412,6 +414,13 @@ def main():
 
     if args.only:
         arm, site = args.only.split(":")
+        if arm == PM_ARM:
+            with smx.strassen_kernel("product_major"):
+                fn = arms["strassen"][site] if not site.startswith("pure_") else \
+                    pure_sites(torch, d, "strassen")[site.replace("pure_", "")]
+                _, ev = time_steps(torch, fn, args.steps, args.warmup)
+            log(f"{args.only}: {statistics.mean(ev):.3f} ms/call")
+            return
         if site == "gate_up_gemm":
             fn = gate_up_gemm(d, 7 if arm == "strassen" else 8)
             _, ev = time_steps(torch, fn, args.steps, args.warmup)
@@ -458,6 +467,18 @@ def main():
         for name, fn in table.items():
             _, ev = time_steps(torch, fn, args.steps, 2)
             pure[arm][name] = statistics.median(ev)
+    # The opt-in product-major Strassen kernel on the same packed weights.
+    # It does not take the q/k epilogue: the q and k sites run the default
+    # kernel.
+    with smx.strassen_kernel("product_major"):
+        per_site[PM_ARM] = {}
+        for name in ("q", "k", "v", "o", "gate_up", "down"):
+            _, ev = time_steps(torch, arms["strassen"][name], args.steps, 2)
+            per_site[PM_ARM][name] = statistics.median(ev)
+        pure[PM_ARM] = {}
+        for name, fn in pure_sites(torch, d, "strassen").items():
+            _, ev = time_steps(torch, fn, args.steps, 2)
+            pure[PM_ARM][name] = statistics.median(ev)
     pure_shapes = {"gate_up": (TOKENS, HIDDEN, FFN), "down": (TOKENS, FFN, HIDDEN),
                    "o": (TOKENS, HEADS * HEAD_DIM, HIDDEN)}
 
