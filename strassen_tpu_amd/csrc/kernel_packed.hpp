@@ -260,33 +260,43 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
     auto body = [&](const Stage& cur) {
       // Slot of stage s+1, and of stage s+kSlots-1 (the one read at s-1).
       const int slot1 = slot == kSlots - 1 ? 0 : slot + 1, refill = slot == 0 ? kSlots - 1 : slot - 1;
-      // The stage's DMA fragments (A then B) go out two at a time between
-      // the first half's MFMA groups rather than as one burst ahead of them;
-      // all are issued before the mid-stage barrier, so its vmcnt
-      // accounting is unchanged.
+      // The stage's DMA fragments (A then B) go out one at a time between the
+      // first half's MFMAs, after the second and fourth of each group of
+      // four, rather than in bursts: a DMA issued right after another holds
+      // back the next MFMA's issue (measured 5% on the gate|up launch). All
+      // are issued before the mid-stage barrier, so its vmcnt accounting is
+      // unchanged.
       const uint32_t from = (uint32_t)min(s + kSlots - 1, nstages - 1) * L::kStage;
       uint8_t* const a_to = a_region + refill * L::kStage + wave_u * kFrag;
       uint8_t* const b_to = b_region + refill * L::kStage + wave_u * kFrag;
-      auto dma_pair = [&](int g) {
-#pragma unroll
-        for (int q = 2 * g; q < 2 * g + 2; ++q) {
-          const bool is_a = q < L::kDmaPerWave;
-          const int x = is_a ? q : q - L::kDmaPerWave;
-          dma_frag(is_a ? a_src : b_src, lane_off, from + x * 4 * kFrag, (is_a ? a_to : b_to) + 4 * x * kFrag);
-        }
+      auto dma_one = [&](int q) __attribute__((always_inline)) {
+        const bool is_a = q < L::kDmaPerWave;
+        const int x = is_a ? q : q - L::kDmaPerWave;
+        dma_frag(is_a ? a_src : b_src, lane_off, from + x * 4 * kFrag, (is_a ? a_to : b_to) + 4 * x * kFrag);
       };
+      // Group g's four MFMAs on quadrant set g, with DMAs 2g and 2g + 1.
+      auto mfma4_dma = [&](const Frags& f, int g) __attribute__((always_inline)) {
+        auto step = [&](f32x16& c, const bf16x8& a, const bf16x8& b, int k) __attribute__((always_inline)) {
+          mfma_agpr(c, a, b);
+          __builtin_amdgcn_sched_barrier(0);
+          if (k == 1) dma_one(2 * g);
+          if (k == 3) dma_one(2 * g + 1);
+          __builtin_amdgcn_sched_barrier(0);
+        };
+        step(acc[g][0][0], f.a0, f.b0, 0);
+        step(acc[g][0][1], f.a0, f.b1, 1);
+        step(acc[g][1][0], f.a1, f.b0, 2);
+        step(acc[g][1][1], f.a1, f.b1, 3);
+      };
+      static_assert(2 * L::kDmaPerWave == 8, "two DMAs per MFMA group");
       __builtin_amdgcn_sched_barrier(0);
       {
         const Frags& t = cur.h0t;
         const Frags& b = cur.h0b;
-        mfma4(Frags{t.a0, t.a1, t.b0, t.b1}, 0);
-        dma_pair(0);
-        mfma4(Frags{t.a0, t.a1, b.b0, b.b1}, 1);
-        dma_pair(1);
-        mfma4(Frags{b.a0, b.a1, t.b0, t.b1}, 2);
-        dma_pair(2);
-        mfma4(Frags{b.a0, b.a1, b.b0, b.b1}, 3);
-        dma_pair(3);
+        mfma4_dma(Frags{t.a0, t.a1, t.b0, t.b1}, 0);
+        mfma4_dma(Frags{t.a0, t.a1, b.b0, b.b1}, 1);
+        mfma4_dma(Frags{b.a0, b.a1, t.b0, t.b1}, 2);
+        mfma4_dma(Frags{b.a0, b.a1, b.b0, b.b1}, 3);
       }
       __builtin_amdgcn_sched_barrier(0);
       stage_barrier<L::kPending>();

@@ -40,10 +40,12 @@
 // "quarters") of one product, 16 KB of A and 32 KB of B; a ring of three
 // stages is refilled two stages ahead, and the DMA stream runs on across
 // product boundaries. One barrier per stage, before its last quarter's
-// MFMAs: it sees the next stage landed and every wave done with the slot
-// the next refill overwrites. Per wave and stage: 24 fragment reads, 12
-// DMAs (three after each of the first three quarters' first MFMAs) and 32
-// MFMAs.
+// MFMAs: it sees the next stage landed and every wave done reading the
+// stage, whose slot the refill then starts on. Per wave and stage: 24
+// fragment reads, 32 MFMAs and 12 DMAs, three per quarter, each issued
+// between two MFMAs (after the second, fifth and eighth of the quarter):
+// DMAs issued back to back hold back the next MFMA's issue (4% on the
+// gate|up launch).
 //
 // Waves: wave (wm, wn) owns product rows 64 wm .. + 63 and columns
 // 128 wn .. + 127 of the tile, 2 x 4 blocks of 32 x 32 per set; per 16 k it
@@ -137,6 +139,36 @@ __device__ __forceinline__ void mfma8(Set& acc, const Set& from, const Frags& f)
             : "=&a"(acc[i][j])
             : "v"(f.a[i]), "v"(f.b[j]), "a"(from[i][j]));
       }
+    }
+}
+
+// mfma8 with hook(k) after MFMA k (k = 0..7), each hook between scheduling
+// barriers.
+template <int kSet, int kStart, class Hook>
+__device__ __forceinline__ void mfma8_dma(Set& acc, const Set& from, const Frags& f, Hook hook) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (kStart == 0) {
+        if constexpr (in_agprs(kSet))
+          packed::mfma_agpr(acc[i][j], f.a[i], f.b[j]);
+        else
+          packed::mfma_vgpr(acc[i][j], f.a[i], f.b[j]);
+      } else if constexpr (kStart == 1) {
+        if constexpr (in_agprs(kSet))
+          asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&a"(acc[i][j]) : "v"(f.a[i]), "v"(f.b[j]));
+        else
+          asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(acc[i][j]) : "v"(f.a[i]), "v"(f.b[j]));
+      } else {
+        static_assert(in_agprs(kSet), "only the AGPR sets start from another set");
+        asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %3"
+            : "=&a"(acc[i][j])
+            : "v"(f.a[i]), "v"(f.b[j]), "a"(from[i][j]));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      hook(4 * i + j);
+      __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -307,19 +339,31 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_pm(Params p) {
       reinterpret_cast<const uint8_t*>(p.park) + (int64_t)blockIdx.x * kParkBytes, (uint32_t)kParkBytes);
   uint8_t* const tile = lds + kRingBytes + wave * Tile::kBytes;
 
-  // DMA of quarter q of stage (ph, s) into ring slot `slot`: wave w moves
-  // block w of A and of both B tiles. Stages past the last one re-load it
-  // (in bounds, never read).
-  auto dma_quarter = [&](int ph, int s, int q, int slot, uint32_t lane_off) __attribute__((always_inline)) {
+  // DMA x of quarter q of stage (ph, s) into ring slot `slot`: wave w moves
+  // block w of A (x = 0) and of each B tile (x = 1, 2). Stages past the
+  // last one re-load it (in bounds, never read).
+  auto dma_one = [&](int ph, int s, int q, int slot, uint32_t lane_off, int x) __attribute__((always_inline)) {
     if (ph >= kOps) {
       ph = kOps - 1;
       s = nstages - 1;
     }
     const uint32_t off = (uint32_t)((kQuarters * s + q) * kOps + product_of(ph)) * kOpStage;
     uint8_t* const to = lds + slot * kStageBytes + q * kQuarterBytes + wave * kFrag;
-    packed::dma_frag(a_src, lane_off, off, to);
-    packed::dma_frag(b_src, lane_off, off, to + kOpStage);
-    packed::dma_frag(b_src, lane_off, off + panel, to + 2 * kOpStage);
+    if (x == 0) packed::dma_frag(a_src, lane_off, off, to);
+    if (x == 1) packed::dma_frag(b_src, lane_off, off, to + kOpStage);
+    if (x == 2) packed::dma_frag(b_src, lane_off, off + panel, to + 2 * kOpStage);
+  };
+  auto dma_quarter = [&](int ph, int s, int q, int slot, uint32_t lane_off) __attribute__((always_inline)) {
+#pragma unroll
+    for (int x = 0; x < 3; ++x) dma_one(ph, s, q, slot, lane_off, x);
+  };
+  // Hook for mfma8_dma: the three DMAs of quarter q after MFMAs 1, 4 and 7.
+  auto dma_hook = [&](int ph, int s, int q, int slot, uint32_t lane_off) __attribute__((always_inline)) {
+    return [=, &dma_one](int k) __attribute__((always_inline)) {
+      if (k == 1) dma_one(ph, s, q, slot, lane_off, 0);
+      if (k == 4) dma_one(ph, s, q, slot, lane_off, 1);
+      if (k == 7) dma_one(ph, s, q, slot, lane_off, 2);
+    };
   };
   auto load = [&](int slot, int q) __attribute__((always_inline)) {
     const int lo = opaque_lane_id() * 16;
@@ -332,27 +376,33 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_pm(Params p) {
     return f;
   };
 
-  // Prologue: stages 0 .. kDist-1 of the stream.
+  // Prologue: stages 0 .. kDist-1 of the stream, and quarter 0 of stage
+  // kDist (the stage loop refills quarters 1-3 of the slot it reads, and
+  // quarter 0 of the next refill after its barrier).
+  int dph = kDist / nstages, ds = kDist % nstages;
   {
     const uint32_t lane_off = opaque_lane_id() * 16;
 #pragma unroll
     for (int st = 0; st < kDist; ++st)
 #pragma unroll
       for (int q = 0; q < kQuarters; ++q) dma_quarter(st / nstages, st % nstages, q, st, lane_off);
+    dma_quarter(dph, ds, 0, kDist, lane_off);
   }
-  // The DMA stream's next stage.
-  int dph = kDist / nstages, ds = kDist % nstages;
-  packed::stage_barrier<kPending>();
+  packed::stage_barrier<kPending + 3>();
 
   Set V, A1, A2;
   int slot = 0;
   Frags cur = load(0, 0);
 
   // One pipeline stage: each quarter's fragments read under the previous
-  // quarter's MFMAs, the refill of the slot read at the previous stage
-  // spread over the first three quarters, the barrier, then the next
-  // stage's first quarter read under the last quarter's MFMAs. kStart
-  // applies to the first quarter (the product's first stage).
+  // quarter's MFMAs; quarters 1-3 of the refill of the slot read at the
+  // previous stage under the first three quarters' MFMAs; the barrier; then
+  // the next stage's first quarter read, and quarter 0 of the refill of the
+  // slot this stage read, under the last quarter's MFMAs. Every wave has
+  // read all of that slot by the barrier (its quarter 0 before the previous
+  // one), and at the barrier a wave leaves only the current refill's 12
+  // DMAs in flight, so the previous refill (the next stage) has landed.
+  // kStart applies to the first quarter (the product's first stage).
   auto stage = [&](auto setc, auto startc, Set& acc, const Set& from) __attribute__((always_inline)) {
     constexpr int kSet = decltype(setc)::value, kStart = decltype(startc)::value;
     const int next = slot == kSlots - 1 ? 0 : slot + 1;
@@ -364,12 +414,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_pm(Params p) {
       const Frags nxt = load(slot, q + 1);
       __builtin_amdgcn_sched_barrier(0);
       if (q == 0)
-        mfma8<kSet, kStart>(acc, from, cur);
+        mfma8_dma<kSet, kStart>(acc, from, cur, dma_hook(dph, ds, q + 1, fill, lane_off));
       else
-        mfma8<kSet, 0>(acc, from, cur);
-      __builtin_amdgcn_sched_barrier(0);
-      dma_quarter(dph, ds, q, fill, lane_off);
-      if (q == kQuarters - 2) dma_quarter(dph, ds, q + 1, fill, lane_off);
+        mfma8_dma<kSet, 0>(acc, from, cur, dma_hook(dph, ds, q + 1, fill, lane_off));
       __builtin_amdgcn_sched_barrier(0);
       cur = nxt;
     }
@@ -380,7 +427,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_pm(Params p) {
     packed::stage_barrier<kPending>();
     const Frags h0 = load(next, 0);  // past the last stage: a re-loaded copy, unused
     __builtin_amdgcn_sched_barrier(0);
-    mfma8<kSet, 0>(acc, from, cur);
+    mfma8_dma<kSet, 0>(acc, from, cur, dma_hook(dph, ds, 0, slot, lane_off));
     __builtin_amdgcn_sched_barrier(0);
     cur = h0;
     slot = next;

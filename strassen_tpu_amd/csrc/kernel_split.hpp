@@ -139,14 +139,31 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
         packed::mfma_vgpr(acc[j][c], a, b[c]);
     }
   };
+  // The same with hook(c) after MFMA c between scheduling barriers: the
+  // stage's DMAs go out one at a time in the MFMAs' shadow.
+  auto mfma_strip_dma = [&](int j, const bf16x8& a, const bf16x8 (&b)[4], auto hook) __attribute__((always_inline)) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (j < 4)
+        packed::mfma_agpr(acc[j][c], a, b[c]);
+      else
+        packed::mfma_vgpr(acc[j][c], a, b[c]);
+      __builtin_amdgcn_sched_barrier(0);
+      hook(c);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
 
   // Stage s: the 12 long-distance prefetch DMAs spread over strips 0-5 (two
-  // after each strip's MFMAs), with the next strip's fragments read under
-  // the current strip's MFMAs; barrier; the short-distance A prefetch of
-  // stage s+2; the next stage's strip-0 fragments read under strip 6's
-  // MFMAs. The barrier sees every read of stage s complete and every wave's
-  // DMA of stage s+1 landed. Issuing the short-distance prefetch right
-  // after the barrier, instead of with the others, gave 0.7%.
+  // per strip, after its second and fourth MFMA), with the next strip's
+  // fragments read under the current strip's MFMAs; barrier; the
+  // short-distance A prefetch of stage s+2; the next stage's strip-0
+  // fragments read under strip 6's MFMAs. The barrier sees every read of
+  // stage s complete and every wave's DMA of stage s+1 landed. Issuing the
+  // short-distance prefetch right after the barrier, instead of with the
+  // others, gave 0.7%. A DMA issued between two MFMAs, rather than two in a
+  // row after a strip, keeps the wave from stalling the MFMA pipe on the
+  // second DMA's issue (1.5% on the gate|up launch).
   int s = 0, l_slot = 0, s_slot = 0;
   bf16x8 a_cur = load_a(a_long, a_short, 0);
   bf16x8 b_cur[4];
@@ -180,17 +197,20 @@ __device__ __forceinline__ void run_wave(const Params& p, const TileOrigin& o, i
 #pragma unroll
     for (int j = 0; j < 6; ++j) {
       const bf16x8 a_next = load_a(sal, sas, j + 1);
+      static_assert(Ring::kLoopDma == 2 * 6, "two DMAs per strip");
+      auto hook = [&](int c) __attribute__((always_inline)) {
+        if (c == 1) dma_op(2 * j);
+        if (c == 3) dma_op(2 * j + 1);
+      };
       if (P::opens(j + 1)) {
         bf16x8 b_next_frags[4];
         load_b(sb, j + 1, b_next_frags);
-        mfma_strip(j, a_cur, b_cur);
+        mfma_strip_dma(j, a_cur, b_cur, hook);
 #pragma unroll
         for (int c = 0; c < 4; ++c) b_cur[c] = b_next_frags[c];
       } else {
-        mfma_strip(j, a_cur, b_cur);
+        mfma_strip_dma(j, a_cur, b_cur, hook);
       }
-#pragma unroll
-      for (int q = (Ring::kLoopDma * j) / 6; q < (Ring::kLoopDma * (j + 1)) / 6; ++q) dma_op(q);
       __builtin_amdgcn_sched_barrier(0);
       a_cur = a_next;
     }
