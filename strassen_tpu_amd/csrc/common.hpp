@@ -445,11 +445,15 @@ constexpr int64_t kSplitTileFloats = 256 * 256;
 // 256, in the order the block permutation stores them. The store code is the
 // ordinary epilogue's, on the geometry of a 256 x 256 tiling whose only tile
 // sits at the origin (a thin tiling then maps every product row straight to
-// a row of its half). split_fixup reads the blocks back.
-__device__ __forceinline__ void dense_share_output(Params& p, TileOrigin& o, const WorkShare& ws) {
+// a row of its half). Its M keeps the tile's real product rows (prow0 is
+// the tile's first): a thin tiling's padding rows, past M/2, are not stored.
+// split_fixup reads the blocks back.
+__device__ __forceinline__ void dense_share_output(Params& p, TileOrigin& o, const WorkShare& ws, int64_t prow0) {
+  const int64_t rows = p.m / 2 - prow0;
   p.c = reinterpret_cast<float*>(p.c) + ws.share * p.split_stride + (int64_t)(ws.tile - p.tile_base) * kSplitTileFloats;
   p.bm = p.bn = 256;
-  p.m = p.n = 256;
+  p.m = 2 * (rows < 128 ? rows : 128);
+  p.n = 256;
   p.ldc = 256;
   o = TileOrigin{0, 0, 0, 0};
 }

@@ -158,7 +158,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_packed(Params p) {
   TileOrigin o = tile_origin<kThin>(p, (int64_t)tile_m * TM, (int64_t)tile_n * TN);
   // K-split shares run without an epilogue and store dense FP32 blocks.
   if constexpr (kEpi == SMX_EPI_NONE)
-    if (p.ksplit > 1) dense_share_output(p, o, ws);
+    if (p.ksplit > 1) dense_share_output(p, o, ws, (int64_t)tile_m * TM);
   const int nstages = ws.nstages;
 
   // DMA sources: this workgroup's packed stages are contiguous runs of

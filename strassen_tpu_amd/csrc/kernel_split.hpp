@@ -397,7 +397,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_split(Params p) {
   TileOrigin o = tile_origin<kThin>(p, (int64_t)tile_m * packed::TM, (int64_t)tile_n * packed::TN);
   // K-split shares run without an epilogue and store dense FP32 blocks.
   if constexpr (kEpi == SMX_EPI_NONE)
-    if (p.ksplit > 1) dense_share_output(p, o, ws);
+    if (p.ksplit > 1) dense_share_output(p, o, ws, (int64_t)tile_m * packed::TM);
   const int nstages = ws.nstages;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t panel_bytes = (uint32_t)nstages * L::kStage - wave * kFrag;

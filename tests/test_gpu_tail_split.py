@@ -102,9 +102,11 @@ def _pack(algo, a, b, tile, formula="classical", block_permutation=0):
 
 
 def abi_gemm(algo, pa, pb, m, n, k, tile, epilogue=None, *, workspace, out_f32=False, residual=None, bias=None,
-             rope=None, formula=0, block_permutation=0, workspace_bytes=None):
+             rope=None, formula=0, block_permutation=0, workspace_bytes=None, keep_workspace=False):
     """smx_gemm on packed operands, with the workspace the library asks for
-    (workspace=True) or none. Returns (output, bytes asked for)."""
+    (workspace=True) or none. Returns (output, bytes asked for), and with
+    keep_workspace the workspace too, filled with 0xff bytes before the call
+    (a NaN in every float)."""
     lib = _lib.load()
     d = _lib.SmxGemmDesc()
     d.m, d.n, d.k = m, n, k
@@ -133,13 +135,15 @@ def abi_gemm(algo, pa, pb, m, n, k, tile, epilogue=None, *, workspace, out_f32=F
     if workspace and need.value:
         nbytes = need.value if workspace_bytes is None else workspace_bytes
         ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=DEV)
+        if keep_workspace:
+            ws.fill_(0xFF)
         d.workspace, d.workspace_bytes = ws.data_ptr(), nbytes
     out = torch.full((m, d.ldc), float("nan"), dtype=torch.float32 if out_f32 else torch.bfloat16, device=DEV)
     say(f"  smx_gemm algo={algo} m={m} n={n} k={k} tile={tile} epilogue={epilogue} workspace={need.value if ws is not None else 0}")
     _lib.check(lib.smx_gemm(d, _lib.ptr(pa.data), _lib.ptr(pb.data), _lib.ptr(out), _lib.ptr(residual), _lib.ptr(bias),
                             _lib.ptr(cos), _lib.ptr(sin), _lib.ptr(scale), _stream()))
     torch.cuda.synchronize()
-    return out, need.value
+    return (out, need.value, ws) if keep_workspace else (out, need.value)
 
 
 def _aux(rng, epilogue, m, n):
@@ -349,6 +353,30 @@ def test_small_launch_split_every_tile(algo, shape, tile, epilogue):
     got = host(got_split)
     assert_ulp_close(got, host(got_whole), k=k)
     assert_ulp_close(got, _oracle(algo, a, b, tile, epilogue=epilogue, **aux), k=k)
+
+
+@pytest.mark.parametrize("algo", [7, 8])
+def test_thin_split_stores_only_real_rows(algo):
+    """A thin tiling's K shares store only the tile's real product rows in
+    their dense 256 x 256 workspace blocks (rows r and 128 + r for the M/2
+    real product rows r): 16 tokens make 8 of the 128, and the padding rows'
+    stores would cost 15 times the bytes. The sentinel the workspace is
+    filled with survives in every padding row."""
+    m, k, n, tile = 16, 25600, 5120, (16, 256, 512)
+    _, split, s = _plan(m, n, k, 16)
+    if not split:
+        pytest.skip("no split at this shape: this device's CU count, or SMX_TAIL_SPLIT=0")
+    _, a, b = _problem(131 + algo, m, k, n)
+    pa, pb = _pack(algo, a, b, tile)
+    out, need, ws = abi_gemm(algo, pa, pb, m, n, k, tile, workspace=True, keep_workspace=True)
+    assert need == s * split * SPLIT_TILE_BYTES
+    blocks = ws[:need].view(torch.int32).view(s * split, 256, 256).cpu()
+    real = torch.zeros(256, dtype=torch.bool)
+    real[: m // 2] = True
+    real[128: 128 + m // 2] = True
+    assert (blocks[:, ~real, :] == -1).all(), "a padding row of a share was stored"
+    assert not (blocks[:, real, :] == -1).any(), "a real row of a share was not stored"
+    assert torch.isfinite(out.float()).all()
 
 
 @pytest.mark.parametrize("algo", [7, 8])
