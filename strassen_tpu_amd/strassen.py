@@ -561,9 +561,10 @@ def _run(algo, a, b, *, bm, bn, bk, epilogue=None, residual=None, bias=None,
         if rope_scale.dtype == torch.float32:
             aux |= _lib.SMX_AUX_SCALE_F32
     desc.aux_f32 = aux
-    # The tiles of a partly filled last round run as K shares when the
-    # library asks for a workspace (FP32 shares of the output, summed by a
-    # second pass).
+    # The library asks for a workspace when the tiles of a partly filled last
+    # round run as K shares (FP32 shares of the output, summed by a second
+    # pass) or when the product-major kernel takes the call (its two parked
+    # FP32 sets per tile).
     need = ctypes.c_int64()
     _lib.check(lib.smx_gemm_workspace_bytes(desc, ctypes.byref(need)))
     workspace = None
