@@ -14,7 +14,12 @@ Mirrors the reference's layer (``experiments/qwen3/benchmark_qwen3_32b_layer.py`
 v runs on hipBLASLt (``torch.matmul``), and attention on torch's fused SDPA
 kernels. The ``"hipblaslt"`` arm is the reference's unfused native layer:
 ``torch.matmul`` GEMMs with the norms, RoPE, SwiGLU and residual adds as
-separate torch ops. Weights are random-init (there is no network to fetch
+separate torch ops. The ``"cubic_unfused"`` arm is the cubic arm of the
+reference's published block run (``cubic_pallas`` with extended sites o and
+down, :63-76, :146-170): the cubic kernel for o, gate|up and down with no
+fused epilogue (the reference's ``cubic_matmul`` takes none), SwiGLU and the
+residual adds as torch ops, and q, k and v on hipBLASLt with torch's norms
+and RoPE. Weights are random-init (there is no network to fetch
 checkpoints); a caller may supply real ones through ``BlockWeights``.
 """
 
@@ -33,7 +38,7 @@ from .strassen import cubic_matmul, strassen_matmul
 __all__ = ["Qwen3Dims", "QWEN3_32B", "BlockWeights", "PreparedBlock", "rms_norm", "apply_rope", "rope_values",
            "attention", "block_forward", "ARMS"]
 
-ARMS = ("strassen", "cubic", "hipblaslt")
+ARMS = ("strassen", "cubic", "hipblaslt", "cubic_unfused")
 
 
 @dataclasses.dataclass(frozen=True)
@@ -146,6 +151,12 @@ class PreparedBlock:
         bm, bn, bk = self.tile
         self.algo = _lib.SMX_ALGO_STRASSEN if arm == "strassen" else _lib.SMX_ALGO_CUBIC
         pack = strassen_weight_layout if arm == "strassen" else cubic_weight_layout
+        if arm == "cubic_unfused":
+            # plain [gate | up] columns: SwiGLU runs on the GEMM's output
+            self.attention_output = pack(weights.attention_output, bn, bk)
+            self.gate_up = pack(weights.gate_up, bn, bk)
+            self.mlp_down = pack(weights.mlp_down, bn, bk)
+            return
         self.query = pack(rope_weight_layout(weights.query, bn, dims.head_dim), bn, bk)
         self.key = pack(rope_weight_layout(weights.key, bn, dims.head_dim), bn, bk)
         self.attention_output = pack(weights.attention_output, bn, bk)
@@ -169,7 +180,7 @@ def block_forward(x, block):
     d, w = block.dims, block.weights
     batch, seq = block.batch, block.seq
     normalized = rms_norm(x, w.attention_norm, d.eps)
-    if block.arm == "hipblaslt":
+    if block.arm in ("hipblaslt", "cubic_unfused"):
         query = torch.matmul(normalized, w.query).view(batch, seq, d.heads, d.head_dim)
         key = torch.matmul(normalized, w.key).view(batch, seq, d.kv_heads, d.head_dim)
         query = apply_rope(rms_norm(query, w.query_norm, d.eps), block.cos, block.sin)
@@ -191,6 +202,12 @@ def block_forward(x, block):
         gate, up = torch.matmul(normalized, w.gate_up).chunk(2, dim=-1)
         activated = (torch.nn.functional.silu(gate.float()) * up.float()).to(torch.bfloat16)
         return (residual.float() + torch.matmul(activated, w.mlp_down).float()).to(torch.bfloat16)
+    if block.arm == "cubic_unfused":
+        residual = (x.float() + block.gemm(attended, block.attention_output).float()).to(torch.bfloat16)
+        normalized = rms_norm(residual, w.mlp_norm, d.eps)
+        gate, up = block.gemm(normalized, block.gate_up).chunk(2, dim=-1)
+        activated = (torch.nn.functional.silu(gate.float()) * up.float()).to(torch.bfloat16)
+        return (residual.float() + block.gemm(activated, block.mlp_down).float()).to(torch.bfloat16)
     residual = block.gemm(attended, block.attention_output, epilogue="residual_add", residual=x)
     normalized = rms_norm(residual, w.mlp_norm, d.eps)
     activated = block.gemm(normalized, block.gate_up, epilogue="swiglu")
