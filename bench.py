@@ -224,6 +224,9 @@ def pure_sites(torch, d, algo):
         "gate_up": lambda: fn(d["y"], "wup"),
         "down": lambda: fn(d["h_any"], "wd"),
         "o": lambda: fn(d["attn"], "wo"),
+        # the whole gate|up weight (a column permutation of [gate | up]), no
+        # epilogue: the shape of the reference's pure-GEMM confirmation run
+        "gate_up_full": lambda: fn(d["y"], "wgu_laid"),
     }
 
 
@@ -379,7 +382,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default=None,
                     help="profiling runs: time only ARM:SITE (ARM strassen|cubic|strassen_plain|cubic_plain|"
-                         "hipblaslt|strassen_product_major; SITE q|k|v|o|gate_up|down|pure_gate_up|pure_down|pure_o, or gate_up_gemm "
+                         "hipblaslt|strassen_product_major; SITE q|k|v|o|gate_up|down|pure_gate_up|pure_down|pure_o|pure_gate_up_full, or gate_up_gemm "
                          "for the packed GEMM launch alone), or \"copy\" (a 256 MiB copy, counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -483,7 +486,7 @@ def main():
             _, ev = time_steps(torch, fn, args.steps, 2)
             pure[PM_ARM][name] = statistics.median(ev)
     pure_shapes = {"gate_up": (TOKENS, HIDDEN, FFN), "down": (TOKENS, FFN, HIDDEN),
-                   "o": (TOKENS, HEADS * HEAD_DIM, HIDDEN)}
+                   "o": (TOKENS, HEADS * HEAD_DIM, HIDDEN), "gate_up_full": (TOKENS, HIDDEN, 2 * FFN)}
 
     # Roofline of the dominant kernel: the fused gate|up SwiGLU Strassen GEMM
     # launch alone (activation already packed), timed with events on the
@@ -556,6 +559,11 @@ def main():
         "pure_gemm_ms": {arm: {k: round(v, 4) for k, v in s.items()} for arm, s in pure.items()},
         "pure_gemm_tflops": {arm: {k: round(flops(pure_shapes[k]) / (v * 1e-3) / 1e12, 1) for k, v in s.items()}
                              for arm, s in pure.items()},
+        # The reference's pure-GEMM confirmation shape, 8192 x 5120 x 51200
+        # with no epilogue (strassen_qwen3_32b_v6e_pure_gemm.jsonl:17).
+        "pure_gate_up_full_speedup": {"vs_cubic": round(pure["cubic"]["gate_up_full"] / pure["strassen"]["gate_up_full"], 4),
+                                      "vs_hipblaslt": round(pure["hipblaslt"]["gate_up_full"]
+                                                            / pure["strassen"]["gate_up_full"], 4)},
         "roofline": roofline,
         "full_block_ms": {k: round(v, 4) for k, v in full_block.items()},
         "full_block_speedup_vs_cubic": round(full_block["cubic"] / full_block["strassen"], 4),
