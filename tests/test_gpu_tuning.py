@@ -105,3 +105,17 @@ def test_small_launch_measurement():
     assert rec["tiles"] == 20 and (rec["k_shares"] == 1 if split_off else rec["k_shares"] >= 2)
     assert set(rec["median_ms"]) == {"strassen", "cubic", "hipblaslt"}
     assert all(len(v) == 3 for v in rec["samples_ms"].values())
+
+
+@pytest.mark.parametrize("arm", tuning.LAUNCH_ARMS)
+def test_measure_launches_every_arm(arm):
+    """`tuning launches` (the driver of the hipBLASLt comparison's counter
+    runs) times each kernel on a pure GEMM: one untimed launch, then the
+    asked-for number of positive times, in one emitted record."""
+    records = []
+    times = tuning.measure_launches(arm, 1024, 1024, 2048, calls=3, emit=records.append)
+    assert len(times) == 3 and all(t > 0 for t in times)
+    assert len(records) == 1 and records[0]["kind"] == "launches" and records[0]["arm"] == arm
+    assert records[0]["shape"] == [1024, 1024, 2048] and records[0]["tflops"] > 0
+    with pytest.raises(ValueError, match="arm must be one of"):
+        tuning.measure_launches("xla", 1024, 1024, 2048)
