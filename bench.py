@@ -41,8 +41,10 @@ BATCH, SEQ = 8, 1024
 THETA, EPS = 1e6, 1e-6
 TILE = (1024, 1024, 512)
 COPY_BYTES = 256 << 20
-# The default Strassen arm's packed weights on the opt-in product-major kernel.
-PM_ARM = "strassen_product_major"
+# The default Strassen arm's packed weights on the library's other Strassen
+# kernels (the default runs the product-major kernel on whole rounds of its
+# tiles and the split kernel on the rest).
+KERNEL_ARMS = {"strassen_split": "split", "strassen_product_major": "product_major"}
 
 
 def log(*args):
@@ -243,6 +245,37 @@ def gate_up_gemm(d, algo):
     return lambda: smx.cubic_matmul(packed, d["wgu_laid_cw"], bm=bm, bn=bn, bk=bk, epilogue="swiglu")
 
 
+def head_columns(m, n, bn, cus):
+    """Columns of an (m, n) Strassen call that the default kernel choice runs
+    on the product-major kernel: its 128 x 256 product tiles in whole rounds
+    of the CUs, ending on a bn tile boundary (the library's
+    pm_round_columns)."""
+    tiles_m, tiles_n = (m // 2) // 128, (n // 2) // 256
+    per_round = cus // math.gcd(tiles_m, cus)
+    per_bn = (bn // 2) // 256
+    step = per_round * per_bn // math.gcd(per_round, per_bn)
+    return 2 * 256 * (tiles_n // step * step)
+
+
+def gate_up_head_gemm(d, cus):
+    """The dominant kernel alone: the product-major head of the fused gate|up
+    SwiGLU call (the columns head_columns gives), on an activation packed
+    beforehand. Returns (head columns, callable)."""
+    import strassen_tpu_amd as smx
+    from strassen_tpu_amd.packing import PackedOperand
+
+    bm, bn, bk = TILE
+    n = head_columns(TOKENS, 2 * FFN, bn, cus)
+    w = d["wgu_laid_sw"]
+    # A packed weight's leading n columns are its first n/2 / 128 packed
+    # tiles: (n/2) (K/2) seven operands of bf16.
+    head = PackedOperand(w.data[:(n // 2) * (w.k // 2) * 7], algo=7, side="rhs", rows=n, k=w.k,
+                         tile_rows=w.tile_rows, bk=w.bk)
+    packed = smx.pack_activation(d["y"], 7, bm, bk)
+    return n, lambda: smx.strassen_matmul(packed, head, bm=bm, bn=bn, bk=bk, epilogue="swiglu",
+                                          interleave_products=True)
+
+
 def full_block_times(torch, dev, steps, warmup):
     """Median ms of one whole Qwen3-32B decoder block (RMSNorms, q/k with
     fused qk_norm_rope, v on hipBLASLt, causal SDPA attention, o + residual,
@@ -382,8 +415,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default=None,
                     help="profiling runs: time only ARM:SITE (ARM strassen|cubic|strassen_plain|cubic_plain|"
-                         "hipblaslt|strassen_product_major; SITE q|k|v|o|gate_up|down|pure_gate_up|pure_down|pure_o|pure_gate_up_full, or gate_up_gemm "
-                         "for the packed GEMM launch alone), or \"copy\" (a 256 MiB copy, counter calibration)")
+                         "hipblaslt|strassen_split|strassen_product_major; SITE q|k|v|o|gate_up|down|pure_gate_up|pure_down|pure_o|pure_gate_up_full, gate_up_gemm "
+                         "for the packed GEMM call alone, or gate_up_head for its product-major head alone), or \"copy\" (a 256 MiB copy, counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: the Strassen GEMM path runs on one MI355X "
@@ -420,11 +453,16 @@ def main():
 
     if args.only:
         arm, site = args.only.split(":")
-        if arm == PM_ARM:
-            with smx.strassen_kernel("product_major"):
+        if arm in KERNEL_ARMS:
+            with smx.strassen_kernel(KERNEL_ARMS[arm]):
                 fn = arms["strassen"][site] if not site.startswith("pure_") else \
                     pure_sites(torch, d, "strassen")[site.replace("pure_", "")]
                 _, ev = time_steps(torch, fn, args.steps, args.warmup)
+            log(f"{args.only}: {statistics.mean(ev):.3f} ms/call")
+            return
+        if site == "gate_up_head":
+            _, fn = gate_up_head_gemm(d, torch.cuda.get_device_properties(0).multi_processor_count)
+            _, ev = time_steps(torch, fn, args.steps, args.warmup)
             log(f"{args.only}: {statistics.mean(ev):.3f} ms/call")
             return
         if site == "gate_up_gemm":
@@ -473,28 +511,35 @@ def main():
         for name, fn in table.items():
             _, ev = time_steps(torch, fn, args.steps, 2)
             pure[arm][name] = statistics.median(ev)
-    # The opt-in product-major Strassen kernel on the same packed weights.
-    # It does not take the q/k epilogue: the q and k sites run the default
-    # kernel.
-    with smx.strassen_kernel("product_major"):
-        per_site[PM_ARM] = {}
-        for name in ("q", "k", "v", "o", "gate_up", "down"):
-            _, ev = time_steps(torch, arms["strassen"][name], args.steps, 2)
-            per_site[PM_ARM][name] = statistics.median(ev)
-        pure[PM_ARM] = {}
-        for name, fn in pure_sites(torch, d, "strassen").items():
-            _, ev = time_steps(torch, fn, args.steps, 2)
-            pure[PM_ARM][name] = statistics.median(ev)
+    # The other Strassen kernels on the same packed weights: the split kernel
+    # alone, and the product-major kernel on every tile (it does not take the
+    # q/k epilogue: the q and k sites then run the split kernel).
+    for kernel_arm, kind in KERNEL_ARMS.items():
+        with smx.strassen_kernel(kind):
+            per_site[kernel_arm] = {}
+            for name in ("q", "k", "v", "o", "gate_up", "down"):
+                _, ev = time_steps(torch, arms["strassen"][name], args.steps, 2)
+                per_site[kernel_arm][name] = statistics.median(ev)
+            pure[kernel_arm] = {}
+            for name, fn in pure_sites(torch, d, "strassen").items():
+                _, ev = time_steps(torch, fn, args.steps, 2)
+                pure[kernel_arm][name] = statistics.median(ev)
     pure_shapes = {"gate_up": (TOKENS, HIDDEN, FFN), "down": (TOKENS, FFN, HIDDEN),
                    "o": (TOKENS, HEADS * HEAD_DIM, HIDDEN), "gate_up_full": (TOKENS, HIDDEN, 2 * FFN)}
 
-    # Roofline of the dominant kernel: the fused gate|up SwiGLU Strassen GEMM
-    # launch alone (activation already packed), timed with events on the
-    # stream it is launched on.
+    # Roofline of the dominant kernel: the product-major head of the fused
+    # gate|up SwiGLU Strassen call (its whole rounds of 128 x 256 product
+    # tiles) alone, activation already packed, timed with events on the
+    # stream it is launched on. The whole call adds the split kernel's rest.
     bm, bn, bk = TILE
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    head_n, head_fn = gate_up_head_gemm(d, cus)
+    head_tiles = (TOKENS // 2 // 128) * (head_n // 2 // 256)
+    _, ev = time_steps(torch, head_fn, args.steps, 2)
+    head_ms = statistics.mean(ev)
+    head_tflops = 2.0 * TOKENS * HIDDEN * head_n / (head_ms * 1e-3) / 1e12
     _, ev = time_steps(torch, gate_up_gemm(d, 7), args.steps, 2)
     gu_ms = statistics.mean(ev)
-    gu_tflops = flops(shapes["gate_up"]) / (gu_ms * 1e-3) / 1e12
     _, ev = time_steps(torch, gate_up_gemm(d, 8), args.steps, 2)
     gu_cubic_ms = statistics.mean(ev)
     _, ev = time_steps(torch, lambda: smx.pack_activation(d["y"], 7, bm, bk), args.steps, 2)
@@ -503,19 +548,23 @@ def main():
     measured = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gate_up_swiglu_qwen3_32b_traffic.json")
     if os.path.exists(measured):
         rec = json.load(open(measured))["strassen"]
-        traffic = round(rec["traffic_bytes"])
-        traffic_note = (f"L2-miss bytes per launch (reads and writes between the XCDs' L2 and the memory side, "
-                        f"which the 256 MB MALL or HBM serves: rocprofv3 exposes no counter that tells them apart on "
-                        f"this image) from rocprofv3 FETCH_SIZE/WRITE_SIZE passes scaled by a copy-kernel "
-                        f"calibration (profiles/gemm_split_strassen_swiglu_qwen3_32b_gate_up.md); algorithmic "
-                        f"{rec['algorithmic_bytes']} B")
+        if rec.get("columns") == head_n:
+            traffic = round(rec["traffic_bytes"])
+            traffic_note = (f"L2-miss bytes per launch (reads and writes between the XCDs' L2 and the memory side, "
+                            f"which the 256 MB MALL or HBM serves: rocprofv3 exposes no counter that tells them "
+                            f"apart on this image) from rocprofv3 FETCH_SIZE/WRITE_SIZE passes scaled by a "
+                            f"copy-kernel calibration (profiles/gemm_pm_strassen_swiglu_qwen3_32b_gate_up_head.md); "
+                            f"algorithmic {rec['algorithmic_bytes']} B")
     roofline = {
-        "bound": "mfma", "achieved": round(gu_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-        "frac": round(gu_tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic, "traffic_note": traffic_note,
-        "kernel": "smx::split::gemm_split<SMX_EPI_SWIGLU> (product-split Strassen; gate|up, M=8192 K=5120 N=51200, "
-                  "packed operands)",
-        "mfma_executed_frac": round(gu_tflops * 7 / 8 / PEAK_BF16_TFLOPS, 4),
-        "avg_launch_ms": round(gu_ms, 4),
+        "bound": "mfma", "achieved": round(head_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+        "frac": round(head_tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic, "traffic_note": traffic_note,
+        "kernel": f"smx::pm::gemm_pm<SMX_EPI_SWIGLU> (product-major Strassen): the head of the gate|up call, "
+                  f"M=8192 K=5120 N={head_n} of 51200, {head_tiles} tiles of 128 x 256 product space "
+                  f"({head_tiles // cus} whole rounds on {cus} CUs), packed operands",
+        "mfma_executed_frac": round(head_tflops * 7 / 8 / PEAK_BF16_TFLOPS, 4),
+        "avg_launch_ms": round(head_ms, 4),
+        "gate_up_call_ms": round(gu_ms, 4),
+        "gate_up_call_tflops": round(flops(shapes["gate_up"]) / (gu_ms * 1e-3) / 1e12, 2),
         "cubic_same_site_ms": round(gu_cubic_ms, 4),
         "activation_pack_ms": round(pack_ms, 4),
     }

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SMX_VERSION 11
+#define SMX_VERSION 12
 
 /* Status codes. */
 #define SMX_OK 0
@@ -91,6 +91,20 @@ extern "C" {
  * 128, bn/2 not a multiple of 256, or K not a multiple of 128. No counterpart
  * in the reference (a kernel choice of gfx950). */
 #define SMX_FLAG_PRODUCT_MAJOR 2
+/* Strassen on packed operands: the product-major kernel for the leading
+ * tile columns whose tiles fill whole rounds of the device's CUs, the
+ * default kernel (with its K split of a partly filled last round) for the
+ * columns after them. The product-major kernel streams fewer operand bytes
+ * per MFMA but has no K split, so a partly filled last round of its tiles
+ * (twice the default kernel's size) runs as long as a full one: this flag
+ * keeps it to whole rounds. The head's columns end on a bn tile boundary.
+ * A call whose product-major tiles fill no whole round, or that the
+ * product-major kernel cannot take (as for SMX_FLAG_PRODUCT_MAJOR), runs on
+ * the default kernel alone. The workspace (smx_gemm_workspace_bytes) then
+ * serves both parts, one after the other. Not together with
+ * SMX_FLAG_PRODUCT_MAJOR. No counterpart in the reference (a kernel choice
+ * of gfx950). */
+#define SMX_FLAG_PRODUCT_MAJOR_ROUNDS 4
 
 /* aux_f32 bits: element type of the small auxiliary vectors. */
 #define SMX_AUX_BIAS_F32 1  /* bias is float32 (else bf16) */
@@ -194,7 +208,9 @@ int smx_gemm_noalloc(const smx_gemm_desc* desc, const void* a, const void* b, vo
 /* Bytes of device workspace with which smx_gemm runs this descriptor's
  * call: for a call on the product-major kernel (SMX_FLAG_PRODUCT_MAJOR),
  * 256 KB per 128 x 256 product tile, (M/2 / 128) (N/2 / 256) tiles, which
- * the call then requires. Otherwise the bytes (s * r * 256 KB: one dense
+ * the call then requires. With SMX_FLAG_PRODUCT_MAJOR_ROUNDS, the larger of
+ * that for the product-major head and the K split's bytes below for the
+ * rest (required when a head runs). Otherwise the bytes (s * r * 256 KB: one dense
  * 256 x 256 FP32 block per K share and split tile) with which
  * smx_gemm splits tiles of this descriptor's launch over K, on the current
  * device. T tiles on the device's C CUs make T / C whole rounds and a last

@@ -42,6 +42,7 @@ SMX_SIDE_RHS = 1
 SMX_SIDE_LHS_T = 2
 SMX_FLAG_OUT_F32 = 1
 SMX_FLAG_PRODUCT_MAJOR = 2
+SMX_FLAG_PRODUCT_MAJOR_ROUNDS = 4
 SMX_FORMULA = {"classical": 0, "dual": 1, "powers": 2}
 SMX_AUX_BIAS_F32 = 1
 SMX_AUX_SCALE_F32 = 2

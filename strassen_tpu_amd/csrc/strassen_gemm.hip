@@ -50,6 +50,7 @@
 #include <algorithm>
 #include <atomic>
 #include <mutex>
+#include <numeric>
 
 #include "common.hpp"
 #include "kernel_packed.hpp"
@@ -233,8 +234,10 @@ int gemm_params(const smx_gemm_desc* d, const void* a, const void* b, void* c, c
   const bool packed_path = d->b_layout == SMX_B_PACKED;
   if (packed_path != (d->a_layout == SMX_A_PACKED))
     return fail(SMX_ERR_UNSUPPORTED, "A and B must both be packed (smx_pack_operand) or both unpacked");
-  if (d->flags & ~(SMX_FLAG_OUT_F32 | SMX_FLAG_PRODUCT_MAJOR))
+  if (d->flags & ~(SMX_FLAG_OUT_F32 | SMX_FLAG_PRODUCT_MAJOR | SMX_FLAG_PRODUCT_MAJOR_ROUNDS))
     return fail(SMX_ERR_INVALID, "unknown flags 0x%x", d->flags);
+  if ((d->flags & SMX_FLAG_PRODUCT_MAJOR) && (d->flags & SMX_FLAG_PRODUCT_MAJOR_ROUNDS))
+    return fail(SMX_ERR_INVALID, "SMX_FLAG_PRODUCT_MAJOR and SMX_FLAG_PRODUCT_MAJOR_ROUNDS exclude each other");
   if (int rc = check_variant(d->algo, d->formula, d->block_permutation)) return rc;
   if ((d->formula || d->block_permutation) && !packed_path)
     return fail(SMX_ERR_UNSUPPORTED, "formula variants and block permutations run on packed operands");
@@ -498,12 +501,13 @@ int launch_packed(const Params& p, int algo, int epilogue, hipStream_t s) {
   return thin ? launch_cubic<true>(p, epilogue, s) : launch_cubic<false>(p, epilogue, s);
 }
 
-// Whether a checked packed Strassen call asks for (SMX_FLAG_PRODUCT_MAJOR)
-// and can take the product-major kernel (kernel_pm.hpp): the classical formula, no FP32 partial, whole 128 x 256
+// Whether a checked packed Strassen call asks for (SMX_FLAG_PRODUCT_MAJOR or
+// SMX_FLAG_PRODUCT_MAJOR_ROUNDS) and can take the product-major kernel
+// (kernel_pm.hpp): the classical formula, no FP32 partial, whole 128 x 256
 // product tiles inside every (bm, bn) tile, K a multiple of 128, and an
 // epilogue it fuses.
 bool pm_eligible(const Params& p, const smx_gemm_desc& d) {
-  if (!(d.flags & SMX_FLAG_PRODUCT_MAJOR)) return false;
+  if (!(d.flags & (SMX_FLAG_PRODUCT_MAJOR | SMX_FLAG_PRODUCT_MAJOR_ROUNDS))) return false;
   if (d.algo != SMX_ALGO_STRASSEN || d.b_layout != SMX_B_PACKED || p.partial) return false;
   if (p.formula != SMX_FORMULA_CLASSICAL || (p.bm / 2) % pm::TM || (p.bn / 2) % pm::TN) return false;
   if ((p.k / 32) % pm::kQuarters) return false;  // whole pipeline stages of 64 product-space k
@@ -524,48 +528,137 @@ void pm_grid(Params& p) {
 // Workspace of a product-major launch: two parked FP32 sets per workgroup.
 int64_t pm_park_bytes(const Params& p) { return (int64_t)p.tiles_m * p.tiles_n * pm::kParkBytes; }
 
-// The workspace checks of a checked call, run before anything is launched
-// (launch_gemm, and smx_gemm_noalloc before its packing pass): the
-// product-major kernel's parked sets, or a K split's shares.
-int check_workspace(const Params& p, const smx_gemm_desc& d) {
-  if (d.b_layout != SMX_B_PACKED) return SMX_OK;
+// Product-major tile columns that a SMX_FLAG_PRODUCT_MAJOR_ROUNDS call runs on
+// the product-major kernel (q on its grid, pm_grid): the most whose tiles
+// fill whole rounds of `cus` CUs (tiles_m columns a multiple of cus) and
+// end on a bn tile boundary (a multiple of bn/2 / 256 columns).
+int pm_round_columns(const Params& q, int cus) {
+  const int per_bn = (int)((q.bn / 2) / pm::TN);
+  const int per_round = cus / std::gcd(q.tiles_m, cus);
+  const int step = std::lcm(per_bn, per_round);
+  return q.tiles_n / step * step;
+}
+
+// The product-space columns pcol0 .. pcol0 + pcols - 1 of a checked packed
+// Strassen call as a call of its own (pcol0 and pcols multiples of bn/2):
+// B's packed tiles from pcol0 / 128 on, and C, residual and bias from
+// physical column 2 pcol0 on (C from pcol0 for SwiGLU / GeGLU, whose output
+// has N/2 columns). A tile's physical columns relative to its part are
+// those it has in the whole call, so the parts store what the whole does.
+Params column_part(const Params& p, int epilogue, int64_t pcol0, int64_t pcols) {
+  Params q = p;
+  q.n = 2 * pcols;
+  // One packed B tile (128 product columns) is K/32 stages of the seven
+  // operands' fragments (packed::Lay<7>::kStage bytes each).
+  const int64_t tile_bytes = (p.k / (2 * packed::TK)) * packed::Lay<7>::kStage;
+  q.b = reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(p.b) + pcol0 / packed::TN * tile_bytes);
+  const int64_t col = 2 * pcol0;
+  const bool gated = epilogue == SMX_EPI_SWIGLU || epilogue == SMX_EPI_GEGLU;
+  q.c = reinterpret_cast<uint8_t*>(p.c) + (gated ? pcol0 : col) * (p.out_f32 ? 4 : 2);
+  if (p.residual) q.residual = reinterpret_cast<const uint8_t*>(p.residual) + col * (p.residual_f32 ? 4 : 2);
+  if (p.bias) q.bias = reinterpret_cast<const uint8_t*>(p.bias) + col * (p.bias_f32 ? 4 : 2);
+  return q;
+}
+
+// How a checked packed call runs: a head of product-major tile columns on the
+// product-major kernel (every column with SMX_FLAG_PRODUCT_MAJOR, whole
+// rounds with SMX_FLAG_PRODUCT_MAJOR_ROUNDS), then the rest on the split
+// (or cubic) kernel, with that part's K split when a workspace is given.
+struct Parts {
+  int pm_cols = 0;    // product-major tile columns (0: no head)
+  bool rest = true;   // whether a split-kernel part follows
+  Params head{};      // on pm_grid
+  Params rest_p{};    // on packed_grid
+};
+
+int plan_parts(const Params& p, const smx_gemm_desc& d, Parts* out) {
+  Parts t;
+  t.rest_p = p;
   if (pm_eligible(p, d)) {
     Params q = p;
     pm_grid(q);
-    if (!d.workspace || d.workspace_bytes < pm_park_bytes(q))
-      return fail(SMX_ERR_INVALID,
-                  "the product-major kernel needs workspace_bytes >= %lld (smx_gemm_workspace_bytes), got %lld",
-                  (long long)pm_park_bytes(q), (long long)(d.workspace ? d.workspace_bytes : 0));
-    return SMX_OK;
+    int cols = q.tiles_n;
+    if (d.flags & SMX_FLAG_PRODUCT_MAJOR_ROUNDS) {
+      int cus = 0;
+      if (int rc = device_cus(&cus)) return rc;
+      cols = pm_round_columns(q, cus);
+    }
+    if (cols == q.tiles_n) {
+      t.pm_cols = cols;
+      t.head = q;
+      t.rest = false;
+    } else if (cols > 0) {
+      const int64_t pcols = (int64_t)cols * pm::TN;
+      t.pm_cols = cols;
+      t.head = column_part(p, d.epilogue, 0, pcols);
+      pm_grid(t.head);
+      t.rest_p = column_part(p, d.epilogue, pcols, p.n / 2 - pcols);
+    }
   }
-  if (!d.workspace) return SMX_OK;
-  Params q = p;
-  packed_grid(q, d.algo);
-  SplitPlan plan{};
-  if (int rc = split_plan(q, &plan)) return rc;
-  if (plan.split && d.workspace_bytes < split_bytes(q, plan))
-    return fail(SMX_ERR_INVALID, "workspace_bytes %lld is below the %lld this call needs (smx_gemm_workspace_bytes)",
-                (long long)d.workspace_bytes, (long long)split_bytes(q, plan));
+  if (t.rest) packed_grid(t.rest_p, d.algo);
+  *out = t;
   return SMX_OK;
 }
 
-// A packed call, with tiles split over K when a workspace is given
-// (smx_gemm_desc.workspace, split_plan): the whole tiles with the fused
-// epilogue, then the split tiles' K shares into the workspace (FP32, no
-// epilogue), then split_fixup, all on the caller's stream in that order.
+// Workspace bytes of a planned call: the head's parked sets and the rest's
+// K shares (split_plan), which run one after the other on one stream and
+// share the buffer.
+int parts_workspace(const Parts& t, int64_t* bytes) {
+  int64_t need = t.pm_cols ? pm_park_bytes(t.head) : 0;
+  if (t.rest) {
+    SplitPlan plan{};
+    if (int rc = split_plan(t.rest_p, &plan)) return rc;
+    if (plan.split) need = std::max(need, split_bytes(t.rest_p, plan));
+  }
+  *bytes = need;
+  return SMX_OK;
+}
+
+// The workspace checks of a checked call, run before anything is launched
+// (launch_gemm, and smx_gemm_noalloc before its packing pass): a
+// product-major head needs its parked sets (and then the whole call's
+// workspace); otherwise a given workspace must hold the K split's shares.
+int check_workspace(const Params& p, const smx_gemm_desc& d) {
+  if (d.b_layout != SMX_B_PACKED) return SMX_OK;
+  Parts t;
+  if (int rc = plan_parts(p, d, &t)) return rc;
+  if (!t.pm_cols && !d.workspace) return SMX_OK;
+  int64_t need = 0;
+  if (int rc = parts_workspace(t, &need)) return rc;
+  if (t.pm_cols && (!d.workspace || d.workspace_bytes < need))
+    return fail(SMX_ERR_INVALID,
+                "the product-major kernel needs workspace_bytes >= %lld (smx_gemm_workspace_bytes), got %lld",
+                (long long)need, (long long)(d.workspace ? d.workspace_bytes : 0));
+  if (d.workspace_bytes < need)
+    return fail(SMX_ERR_INVALID, "workspace_bytes %lld is below the %lld this call needs (smx_gemm_workspace_bytes)",
+                (long long)d.workspace_bytes, (long long)need);
+  return SMX_OK;
+}
+
+int launch_rest(Params p, const smx_gemm_desc& d, hipStream_t s);
+
+// A packed call: a product-major head (plan_parts) parks two partial sets
+// per workgroup in the workspace; the rest runs as launch_rest says.
 int launch_gemm(Params p, const smx_gemm_desc& d, hipStream_t s) {
   if (d.b_layout != SMX_B_PACKED)
     return d.algo == SMX_ALGO_STRASSEN ? dispatch_v1<7>(p, d.epilogue, s) : dispatch_v1<8>(p, d.epilogue, s);
   if (int rc = check_workspace(p, d)) return rc;
-  if (pm_eligible(p, d)) {
-    // The product-major kernel parks two partial sets per workgroup in the
-    // workspace.
-    Params q = p;
-    pm_grid(q);
+  Parts t;
+  if (int rc = plan_parts(p, d, &t)) return rc;
+  if (t.pm_cols) {
+    Params q = t.head;
     q.park = d.workspace;
-    return launch_strassen_pm(q, d.epilogue, s);
+    if (int rc = launch_strassen_pm(q, d.epilogue, s)) return rc;
   }
-  packed_grid(p, d.algo);
+  return t.rest ? launch_rest(t.rest_p, d, s) : SMX_OK;
+}
+
+// The split (or cubic) kernel's part of a packed call (on packed_grid), with
+// tiles split over K when a workspace is given (smx_gemm_desc.workspace,
+// split_plan): the whole tiles with the fused epilogue, then the split
+// tiles' K shares into the workspace (FP32, no epilogue), then split_fixup,
+// all on the caller's stream in that order.
+int launch_rest(Params p, const smx_gemm_desc& d, hipStream_t s) {
   SplitPlan plan{p.tiles_m * p.tiles_n, 0, 1};
   if (d.workspace)
     if (int rc = split_plan(p, &plan)) return rc;
@@ -784,16 +877,9 @@ int smx_gemm_workspace_bytes(const smx_gemm_desc* d, int64_t* bytes) {
   Params p{};
   if (int rc = gemm_params(d, x, x, const_cast<void*>(x), x, x, x, x, x, p)) return rc;
   if (d->b_layout != SMX_B_PACKED) return SMX_OK;
-  if (pm_eligible(p, *d)) {
-    pm_grid(p);
-    *bytes = pm_park_bytes(p);
-    return SMX_OK;
-  }
-  packed_grid(p, d->algo);
-  SplitPlan plan{};
-  if (int rc = split_plan(p, &plan)) return rc;
-  if (plan.split) *bytes = split_bytes(p, plan);
-  return SMX_OK;
+  Parts t;
+  if (int rc = plan_parts(p, *d, &t)) return rc;
+  return parts_workspace(t, bytes);
 }
 
 int smx_gemm_noalloc(const smx_gemm_desc* d, const void* a, const void* b, void* c, const void* residual,

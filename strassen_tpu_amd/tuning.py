@@ -414,15 +414,17 @@ def measure_small_launches(shapes=SMALL_LAUNCH_SHAPES, *, bn=256, bk=512, seed=0
 
 
 # Kernels one pure GEMM launch can run on (measure_launches).
-LAUNCH_ARMS = ("hipblaslt", "cubic", "strassen", "product_major")
+LAUNCH_ARMS = ("hipblaslt", "cubic", "strassen", "product_major", "product_major_rounds")
 
 
 def measure_launches(arm, m, k, n, *, tile=(1024, 1024, 512), calls=10, seed=0, device="cuda:0", emit=None):
     """``calls`` timed launches of one pure bf16 GEMM (no epilogue) on one
     kernel, for counter runs under a profiler: ``hipblaslt`` (torch.matmul
     on an ``[in, out]`` view of an ``[out, in]`` weight), or ``cubic`` /
-    ``strassen`` / ``product_major`` through ``smx_gemm`` on operands packed
-    beforehand (the product-major kernel with SMX_FLAG_PRODUCT_MAJOR). One
+    ``strassen`` / ``product_major`` / ``product_major_rounds`` through
+    ``smx_gemm`` on operands packed beforehand (the product-major kernel with
+    SMX_FLAG_PRODUCT_MAJOR, or on whole rounds with
+    SMX_FLAG_PRODUCT_MAJOR_ROUNDS). One
     untimed launch first; returns the per-launch milliseconds (HIP events)."""
     import ctypes
 
@@ -447,7 +449,8 @@ def measure_launches(arm, m, k, n, *, tile=(1024, 1024, 512), calls=10, seed=0, 
         d.bm, d.bn, d.bk = tile
         d.algo, d.epilogue = algo, _lib.SMX_EPI[None]
         d.a_layout, d.b_layout = _lib.SMX_A_PACKED, _lib.SMX_B_PACKED
-        d.flags = _lib.SMX_FLAG_PRODUCT_MAJOR if arm == "product_major" else 0
+        d.flags = {"product_major": _lib.SMX_FLAG_PRODUCT_MAJOR,
+                   "product_major_rounds": _lib.SMX_FLAG_PRODUCT_MAJOR_ROUNDS}.get(arm, 0)
         need = ctypes.c_int64()
         _lib.check(lib.smx_gemm_workspace_bytes(d, ctypes.byref(need)))
         workspace = None

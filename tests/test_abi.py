@@ -39,7 +39,7 @@ def test_version_and_macros_match_header():
     for name in ("SMX_OK", "SMX_ERR_INVALID", "SMX_ERR_UNSUPPORTED", "SMX_ERR_LAUNCH",
                  "SMX_ALGO_STRASSEN", "SMX_ALGO_CUBIC", "SMX_A_ROWMAJOR", "SMX_A_PACKED",
                  "SMX_B_KCONTIG", "SMX_B_PACKED", "SMX_SIDE_LHS", "SMX_SIDE_RHS", "SMX_SIDE_LHS_T",
-                 "SMX_FLAG_OUT_F32", "SMX_FLAG_PRODUCT_MAJOR",
+                 "SMX_FLAG_OUT_F32", "SMX_FLAG_PRODUCT_MAJOR", "SMX_FLAG_PRODUCT_MAJOR_ROUNDS",
                  "SMX_AUX_BIAS_F32", "SMX_AUX_SCALE_F32"):
         value = int(re.search(rf"#define {name} (\d+)", header).group(1))
         assert getattr(_lib, name) == value, name
@@ -100,7 +100,8 @@ def _desc(**kw):
     ("b_layout", _lib.SMX_B_PACKED, _lib.SMX_ERR_UNSUPPORTED),  # and vice versa
     ("lda", 100, _lib.SMX_ERR_INVALID),
     ("epilogue", 9, _lib.SMX_ERR_INVALID),
-    ("flags", 4, _lib.SMX_ERR_INVALID),
+    ("flags", 8, _lib.SMX_ERR_INVALID),
+    ("flags", _lib.SMX_FLAG_PRODUCT_MAJOR | _lib.SMX_FLAG_PRODUCT_MAJOR_ROUNDS, _lib.SMX_ERR_INVALID),
     ("formula", 3, _lib.SMX_ERR_INVALID),
     ("block_permutation", 8, _lib.SMX_ERR_INVALID),
     ("formula", 1, _lib.SMX_ERR_UNSUPPORTED),            # variants need packed operands

@@ -1,0 +1,201 @@
+"""GPU parity of SMX_FLAG_PRODUCT_MAJOR_ROUNDS: the product-major kernel on
+the leading tile columns whose 128 x 256 product tiles fill whole rounds of
+the CUs, the default (split) kernel on the columns after them.
+
+The two parts are column ranges of one call: the head's tiles are the ones
+the product-major kernel computes on its own (bit-identical), the rest's
+are the default kernel's on a call of those columns (its K split included),
+so every output matches the oracle within one bf16 ulp and integer operands
+are bit-exact. Checked through the surface (strassen_kernel(
+"product_major_rounds")) on shapes whose head fills exactly one round of the
+device's CUs and leaves a rest: every epilogue the product-major kernel
+fuses, FP32 output and auxiliaries, a block permutation, the workspace the
+call asks for (the larger of the head's parked sets and the rest's K
+shares), and the calls with no whole round or nothing left over.
+"""
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as o
+import strassen_tpu_amd as smx
+from strassen_tpu_amd import _lib
+from test_gpu_parity import DEV, _gaussian, assert_ulp_close, dev, dev_weight, host, say
+
+pytestmark = pytest.mark.gpu
+
+PARK_PER_TILE = 256 * 1024  # two parked FP32 sets of a 128 x 256 product tile
+TILE = dict(bm=1024, bn=1024, bk=512)
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    say(f"\n[gpu] {request.node.nodeid}")
+    yield
+    torch.cuda.synchronize()
+
+
+def _cus():
+    return torch.cuda.get_device_properties(DEV).multi_processor_count
+
+
+def head_columns(m, n, bn=1024):
+    """Output columns of the product-major head (the C library's
+    pm_round_columns, restated): the most 256-column product tiles per row
+    whose tiles fill whole rounds and end on a bn tile boundary."""
+    tiles_m, tiles_n = (m // 2) // 128, (n // 2) // 256
+    per_round = _cus() // math.gcd(tiles_m, _cus())
+    step = math.lcm(per_round, (bn // 2) // 256)
+    return 2 * 256 * (tiles_n // step * step)
+
+
+def hybrid_shape(k):
+    """M = 1024 (4 product-major tile rows): the head fills one round of the
+    CUs with cus / 4 tile columns; two more bn tiles form the rest."""
+    m = 1024
+    n = 2 * 256 * (_cus() // 4) + 2 * 1024
+    return m, k, n
+
+
+def _workspace_bytes(m, n, k, flags, epilogue=None, tile=(1024, 1024, 512)):
+    d = _lib.SmxGemmDesc()
+    d.m, d.n, d.k = m, n, k
+    d.lda, d.ldb = k, k
+    d.ldc = n // 2 if epilogue in ("swiglu", "geglu") else n
+    d.bm, d.bn, d.bk = tile
+    d.algo, d.epilogue = 7, _lib.SMX_EPI[epilogue]
+    d.a_layout, d.b_layout = _lib.SMX_A_PACKED, _lib.SMX_B_PACKED
+    d.flags = flags
+    d.rope_head_dim, d.rope_eps = 128, 1e-6
+    need = ctypes.c_int64()
+    _lib.check(_lib.load().smx_gemm_workspace_bytes(d, ctypes.byref(need)))
+    return need.value
+
+
+def rounds_matmul(a, b, **kw):
+    with smx.strassen_kernel("product_major_rounds"):
+        return smx.strassen_matmul(a, b, **kw)
+
+
+def pm_matmul(a, b, **kw):
+    with smx.strassen_kernel("product_major"):
+        return smx.strassen_matmul(a, b, **kw)
+
+
+def test_workspace_covers_both_parts():
+    rounds = _lib.SMX_FLAG_PRODUCT_MAJOR_ROUNDS
+    m, k, n = hybrid_shape(2048)
+    head = head_columns(m, n)
+    assert 0 < head < n
+    head_tiles = (m // 256) * (head // 512)
+    assert head_tiles == _cus()
+    rest = _workspace_bytes(m, n - head, k, 0)  # the rest as a call of its own
+    assert rest > 0  # its 32 split-kernel tiles split over K
+    assert _workspace_bytes(m, n, k, rounds) == max(head_tiles * PARK_PER_TILE, rest)
+    # Every column in whole rounds: the product-major kernel alone.
+    assert _workspace_bytes(m, head, k, rounds) == head_tiles * PARK_PER_TILE
+    # No whole round: the default kernel alone.
+    for shape in ((1024, 2048, 2048), (2048, 4096, 4096)):
+        assert _workspace_bytes(*shape, rounds) == _workspace_bytes(*shape, 0)
+    # A q/k epilogue is never the product-major kernel's.
+    assert _workspace_bytes(m, n, k, rounds, epilogue="qk_norm_rope") == _workspace_bytes(
+        m, n, k, 0, epilogue="qk_norm_rope")
+
+
+@pytest.mark.parametrize("k", [1024, 2048])
+def test_integer_kat_bit_exact(k):
+    """K = 2048 splits the rest's tiles over K as well."""
+    m, k, n = hybrid_shape(k)
+    rng = np.random.default_rng(960 + k // 1024)
+    a = rng.integers(-2, 3, (m, k)).astype(np.float32)
+    b = rng.integers(-2, 3, (k, n)).astype(np.float32)
+    w = smx.strassen_weight_layout(dev_weight(b), 1024, 512)
+    exact = a @ b
+    got32 = host(rounds_matmul(dev(a), w, output_dtype=torch.float32, **TILE))
+    assert np.array_equal(got32, exact)
+    got = host(rounds_matmul(dev(a), w, **TILE))
+    assert np.array_equal(got, o.bf16_round(exact))
+
+
+def _sample_columns(n, head, width):
+    """Column blocks (one bn tile of output each) at both ends of the head
+    and of the rest."""
+    return sorted({0, head - width, head, n - width})
+
+
+@pytest.mark.parametrize("epilogue,perm", [(None, 0), ("swiglu", 0), ("geglu", 5), ("residual_add", 3),
+                                           ("bias_add", 6)])
+def test_epilogues_match_oracle_and_both_kernels(epilogue, perm):
+    m, k, n = hybrid_shape(1024)
+    head = head_columns(m, n)
+    rng, a, b = _gaussian(970 + perm, m, k, n)
+    gated = epilogue in ("swiglu", "geglu")
+    b_use = o.swiglu_weight_layout(b, 1024) if gated else b
+    kw = dict(TILE, epilogue=epilogue, block_permutation=perm)
+    okw = dict(TILE, epilogue=epilogue, block_permutation=perm)
+    res = bias = None
+    if epilogue == "residual_add":
+        res = o.bf16_round(rng.standard_normal((m, n)).astype(np.float32))
+        kw["residual"] = dev(res)
+    if epilogue == "bias_add":
+        bias = o.bf16_round(rng.standard_normal(n).astype(np.float32))
+        kw["bias"] = dev(bias)
+    w = smx.strassen_weight_layout(dev_weight(b_use), 1024, 512, block_permutation=perm)
+    a_dev = dev(a)
+    got = host(rounds_matmul(a_dev, w, **kw))
+    # The head is the product-major kernel's own result, the rest the
+    # default kernel's (K = 1024: no K split on either side).
+    out_head = head // 2 if gated else head
+    assert np.array_equal(got[:, :out_head], host(pm_matmul(a_dev, w, **kw))[:, :out_head])
+    assert np.array_equal(got[:, out_head:], host(smx.strassen_matmul(a_dev, w, **kw))[:, out_head:])
+    # The oracle on one bn tile of columns at each end of both parts (a
+    # tile depends only on its own rows and columns).
+    for c0 in _sample_columns(n, head, 1024):
+        sub = dict(okw)
+        if res is not None:
+            sub["residual"] = res[:, c0:c0 + 1024]
+        if bias is not None:
+            sub["bias"] = bias[c0:c0 + 1024]
+        want = o.strassen_matmul(a, b_use[:, c0:c0 + 1024], **sub)
+        oc = c0 // 2 if gated else c0
+        assert_ulp_close(got[:, oc:oc + want.shape[1]], want, k=k)
+
+
+def test_fp32_output_and_fp32_auxiliaries():
+    m, k, n = hybrid_shape(1024)
+    head = head_columns(m, n)
+    rng, a, b = _gaussian(980, m, k, n)
+    w = smx.strassen_weight_layout(dev_weight(b), 1024, 512)
+    a_dev = dev(a)
+    r = rng.standard_normal((m, n)).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    for extra in (dict(output_dtype=torch.float32),
+                  dict(epilogue="residual_add", residual=torch.from_numpy(r).to(DEV)),
+                  dict(epilogue="bias_add", bias=torch.from_numpy(bias).to(DEV))):
+        got = host(rounds_matmul(a_dev, w, **TILE, **extra))
+        assert np.array_equal(got[:, :head], host(pm_matmul(a_dev, w, **TILE, **extra))[:, :head])
+        # K = 1024: the rest's tiles run over full K, as in the default call.
+        assert np.array_equal(got[:, head:], host(smx.strassen_matmul(a_dev, w, **TILE, **extra))[:, head:])
+    c0 = head
+    want = o.strassen_matmul(a, b[:, c0:c0 + 1024], **TILE, epilogue="residual_add", residual=r[:, c0:c0 + 1024])
+    got = host(rounds_matmul(a_dev, w, **TILE, epilogue="residual_add", residual=torch.from_numpy(r).to(DEV)))
+    assert_ulp_close(got[:, c0:c0 + 1024], want, k=k)
+
+
+def test_both_product_major_flags_are_refused():
+    m, k, n = 1024, 1024, 2048
+    d = _lib.SmxGemmDesc()
+    d.m, d.n, d.k = m, n, k
+    d.lda, d.ldb, d.ldc = k, k, n
+    d.bm, d.bn, d.bk = 1024, 1024, 512
+    d.algo, d.epilogue = 7, _lib.SMX_EPI[None]
+    d.a_layout, d.b_layout = _lib.SMX_A_PACKED, _lib.SMX_B_PACKED
+    d.flags = _lib.SMX_FLAG_PRODUCT_MAJOR | _lib.SMX_FLAG_PRODUCT_MAJOR_ROUNDS
+    need = ctypes.c_int64()
+    lib = _lib.load()
+    assert lib.smx_gemm_workspace_bytes(d, ctypes.byref(need)) == _lib.SMX_ERR_INVALID
+    assert b"exclude each other" in lib.smx_last_error()

@@ -7,6 +7,7 @@ import pytest
 import torch
 
 import strassen_tpu_amd as smx
+from strassen_tpu_amd import strassen as surface
 
 
 def t(*shape, dtype=torch.bfloat16):
@@ -429,3 +430,32 @@ def test_cache_packed_weights_api():
     finally:
         smx.cache_packed_weights(previous)
     assert smx.packed_weight_cache_info()["capacity"] == previous
+
+
+def test_strassen_kernel_choice():
+    """The packed Strassen kernel is chosen per process: the product-major
+    kernel on whole rounds by default, or one of the two kernels alone."""
+    assert surface.STRASSEN_KERNEL == "product_major_rounds"
+    for kind in surface.STRASSEN_KERNELS:
+        with smx.strassen_kernel(kind):
+            assert surface.STRASSEN_KERNEL == kind
+        assert surface.STRASSEN_KERNEL == "product_major_rounds"
+    with pytest.raises(ValueError, match="Strassen kernel must be one of"):
+        with smx.strassen_kernel("fastest"):
+            pass
+
+
+def test_bench_head_columns():
+    """bench.py's head_columns restates the library's pm_round_columns: the
+    most 256-column product tiles per tile row that fill whole rounds of the
+    CUs and end on a bn tile boundary."""
+    import bench
+
+    # gate|up at 8 x 1024 tokens on 256 CUs: 32 tile rows, 8 columns a round.
+    assert bench.head_columns(8192, 51200, 1024, 256) == 49152
+    assert bench.head_columns(8192, 5120, 1024, 256) == 4096  # o and down: one round
+    assert bench.head_columns(8192, 1024, 1024, 256) == 0     # v: under one round
+    assert bench.head_columns(1024, 34816, 1024, 256) == 32768
+    # bn / 2 = 1024: whole bn tiles of 4 columns; 24 tile rows: 32 a round.
+    assert bench.head_columns(6144, 2 * 256 * 72, 2048, 256) == 2 * 256 * 64
+    assert bench.head_columns(8192, 51200, 1024, 304) == 2 * 256 * 76  # 38 columns a round
