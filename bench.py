@@ -245,11 +245,13 @@ def gate_up_gemm(d, algo):
     return lambda: smx.cubic_matmul(packed, d["wgu_laid_cw"], bm=bm, bn=bn, bk=bk, epilogue="swiglu")
 
 
-def head_columns(m, n, bn, cus):
-    """Columns of an (m, n) Strassen call that the default kernel choice runs
-    on the product-major kernel: its 128 x 256 product tiles in whole rounds
-    of the CUs, ending on a bn tile boundary (the library's
-    pm_round_columns)."""
+def head_columns(m, k, n, bn, cus):
+    """Columns of an (m, k, n) Strassen call that the default kernel choice
+    runs on the product-major kernel: its 128 x 256 product tiles in whole
+    rounds of the CUs, ending on a bn tile boundary, and none below K = 4096
+    (the library's pm_round_columns)."""
+    if k < 4096:
+        return 0
     tiles_m, tiles_n = (m // 2) // 128, (n // 2) // 256
     per_round = cus // math.gcd(tiles_m, cus)
     per_bn = (bn // 2) // 256
@@ -265,7 +267,7 @@ def gate_up_head_gemm(d, cus):
     from strassen_tpu_amd.packing import PackedOperand
 
     bm, bn, bk = TILE
-    n = head_columns(TOKENS, 2 * FFN, bn, cus)
+    n = head_columns(TOKENS, HIDDEN, 2 * FFN, bn, cus)
     w = d["wgu_laid_sw"]
     # A packed weight's leading n columns are its first n/2 / 128 packed
     # tiles: (n/2) (K/2) seven operands of bf16.

@@ -98,9 +98,10 @@ extern "C" {
  * per MFMA but has no K split, so a partly filled last round of its tiles
  * (twice the default kernel's size) runs as long as a full one: this flag
  * keeps it to whole rounds. The head's columns end on a bn tile boundary.
- * A call whose product-major tiles fill no whole round, or that the
- * product-major kernel cannot take (as for SMX_FLAG_PRODUCT_MAJOR), runs on
- * the default kernel alone. The workspace (smx_gemm_workspace_bytes) then
+ * A call whose product-major tiles fill no whole round, with K below 4096
+ * (where the product-major kernel's per-tile costs outweigh its lead), or
+ * that the product-major kernel cannot take (as for SMX_FLAG_PRODUCT_MAJOR),
+ * runs on the default kernel alone. The workspace (smx_gemm_workspace_bytes) then
  * serves both parts, one after the other. Not together with
  * SMX_FLAG_PRODUCT_MAJOR. No counterpart in the reference (a kernel choice
  * of gfx950). */

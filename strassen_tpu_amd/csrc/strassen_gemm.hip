@@ -528,11 +528,21 @@ void pm_grid(Params& p) {
 // Workspace of a product-major launch: two parked FP32 sets per workgroup.
 int64_t pm_park_bytes(const Params& p) { return (int64_t)p.tiles_m * p.tiles_n * pm::kParkBytes; }
 
+// Depth below which a SMX_FLAG_PRODUCT_MAJOR_ROUNDS call runs on the split
+// kernel alone. The product-major kernel's per-tile costs (two mid-kernel
+// epilogues, two parked sets) are fixed while its lead per unit of K is
+// small: on whole rounds (8192 x K x 16384, one MI355X) it takes 15% longer
+// than the split kernel at K = 1024, 3% at 2048, the same at 3072, 1% less
+// at 4096, 1-2% at 5120 and 10% at 25600.
+constexpr int64_t kPmRoundsMinK = 4096;
+
 // Product-major tile columns that a SMX_FLAG_PRODUCT_MAJOR_ROUNDS call runs on
 // the product-major kernel (q on its grid, pm_grid): the most whose tiles
 // fill whole rounds of `cus` CUs (tiles_m columns a multiple of cus) and
-// end on a bn tile boundary (a multiple of bn/2 / 256 columns).
+// end on a bn tile boundary (a multiple of bn/2 / 256 columns); none below
+// kPmRoundsMinK.
 int pm_round_columns(const Params& q, int cus) {
+  if (q.k < kPmRoundsMinK) return 0;
   const int per_bn = (int)((q.bn / 2) / pm::TN);
   const int per_round = cus / std::gcd(q.tiles_m, cus);
   const int step = std::lcm(per_bn, per_round);

@@ -11,7 +11,8 @@ are bit-exact. Checked through the surface (strassen_kernel(
 device's CUs and leaves a rest: every epilogue the product-major kernel
 fuses, FP32 output and auxiliaries, a block permutation, the workspace the
 call asks for (the larger of the head's parked sets and the rest's K
-shares), and the calls with no whole round or nothing left over.
+shares), and the calls with no whole round, nothing left over, or K below
+4096 (the split kernel alone).
 """
 
 import ctypes
@@ -24,7 +25,7 @@ import torch
 import oracle as o
 import strassen_tpu_amd as smx
 from strassen_tpu_amd import _lib
-from test_gpu_parity import DEV, _gaussian, assert_ulp_close, dev, dev_weight, host, say
+from test_gpu_parity import DEV, _gaussian, assert_ulp_close, dev, dev_weight, fp32_floor, host, say
 
 pytestmark = pytest.mark.gpu
 
@@ -43,10 +44,13 @@ def _cus():
     return torch.cuda.get_device_properties(DEV).multi_processor_count
 
 
-def head_columns(m, n, bn=1024):
+def head_columns(m, k, n, bn=1024):
     """Output columns of the product-major head (the C library's
     pm_round_columns, restated): the most 256-column product tiles per row
-    whose tiles fill whole rounds and end on a bn tile boundary."""
+    whose tiles fill whole rounds and end on a bn tile boundary; none below
+    K = 4096."""
+    if k < 4096:
+        return 0
     tiles_m, tiles_n = (m // 2) // 128, (n // 2) // 256
     per_round = _cus() // math.gcd(tiles_m, _cus())
     step = math.lcm(per_round, (bn // 2) // 256)
@@ -88,8 +92,8 @@ def pm_matmul(a, b, **kw):
 
 def test_workspace_covers_both_parts():
     rounds = _lib.SMX_FLAG_PRODUCT_MAJOR_ROUNDS
-    m, k, n = hybrid_shape(2048)
-    head = head_columns(m, n)
+    m, k, n = hybrid_shape(4096)
+    head = head_columns(m, k, n)
     assert 0 < head < n
     head_tiles = (m // 256) * (head // 512)
     assert head_tiles == _cus()
@@ -104,11 +108,14 @@ def test_workspace_covers_both_parts():
     # A q/k epilogue is never the product-major kernel's.
     assert _workspace_bytes(m, n, k, rounds, epilogue="qk_norm_rope") == _workspace_bytes(
         m, n, k, 0, epilogue="qk_norm_rope")
+    # Below K = 4096 the split kernel runs alone.
+    assert head_columns(m, 2048, n) == 0
+    assert _workspace_bytes(m, n, 2048, rounds) == _workspace_bytes(m, n, 2048, 0)
 
 
-@pytest.mark.parametrize("k", [1024, 2048])
+@pytest.mark.parametrize("k", [4096, 6144])
 def test_integer_kat_bit_exact(k):
-    """K = 2048 splits the rest's tiles over K as well."""
+    """The rest's tiles split over K as well."""
     m, k, n = hybrid_shape(k)
     rng = np.random.default_rng(960 + k // 1024)
     a = rng.integers(-2, 3, (m, k)).astype(np.float32)
@@ -130,8 +137,8 @@ def _sample_columns(n, head, width):
 @pytest.mark.parametrize("epilogue,perm", [(None, 0), ("swiglu", 0), ("geglu", 5), ("residual_add", 3),
                                            ("bias_add", 6)])
 def test_epilogues_match_oracle_and_both_kernels(epilogue, perm):
-    m, k, n = hybrid_shape(1024)
-    head = head_columns(m, n)
+    m, k, n = hybrid_shape(4096)
+    head = head_columns(m, k, n)
     rng, a, b = _gaussian(970 + perm, m, k, n)
     gated = epilogue in ("swiglu", "geglu")
     b_use = o.swiglu_weight_layout(b, 1024) if gated else b
@@ -147,11 +154,14 @@ def test_epilogues_match_oracle_and_both_kernels(epilogue, perm):
     w = smx.strassen_weight_layout(dev_weight(b_use), 1024, 512, block_permutation=perm)
     a_dev = dev(a)
     got = host(rounds_matmul(a_dev, w, **kw))
-    # The head is the product-major kernel's own result, the rest the
-    # default kernel's (K = 1024: no K split on either side).
+    # The head is the product-major kernel's own result, the rest the split
+    # kernel's (its last round split over K, as the whole call's on the split
+    # kernel alone splits other tiles: up to the order of FP32 additions).
     out_head = head // 2 if gated else head
     assert np.array_equal(got[:, :out_head], host(pm_matmul(a_dev, w, **kw))[:, :out_head])
-    assert np.array_equal(got[:, out_head:], host(smx.strassen_matmul(a_dev, w, **kw))[:, out_head:])
+    with smx.strassen_kernel("split"):
+        split = host(smx.strassen_matmul(a_dev, w, **kw))
+    assert_ulp_close(got[:, out_head:], split[:, out_head:], k=k)
     # The oracle on one bn tile of columns at each end of both parts (a
     # tile depends only on its own rows and columns).
     for c0 in _sample_columns(n, head, 1024):
@@ -166,8 +176,8 @@ def test_epilogues_match_oracle_and_both_kernels(epilogue, perm):
 
 
 def test_fp32_output_and_fp32_auxiliaries():
-    m, k, n = hybrid_shape(1024)
-    head = head_columns(m, n)
+    m, k, n = hybrid_shape(4096)
+    head = head_columns(m, k, n)
     rng, a, b = _gaussian(980, m, k, n)
     w = smx.strassen_weight_layout(dev_weight(b), 1024, 512)
     a_dev = dev(a)
@@ -178,8 +188,14 @@ def test_fp32_output_and_fp32_auxiliaries():
                   dict(epilogue="bias_add", bias=torch.from_numpy(bias).to(DEV))):
         got = host(rounds_matmul(a_dev, w, **TILE, **extra))
         assert np.array_equal(got[:, :head], host(pm_matmul(a_dev, w, **TILE, **extra))[:, :head])
-        # K = 1024: the rest's tiles run over full K, as in the default call.
-        assert np.array_equal(got[:, head:], host(smx.strassen_matmul(a_dev, w, **TILE, **extra))[:, head:])
+        # The rest against the split kernel alone: the same tiles, their K
+        # split in another place, so the FP32 sums differ only in order.
+        with smx.strassen_kernel("split"):
+            split = host(smx.strassen_matmul(a_dev, w, **TILE, **extra))[:, head:]
+        if extra.get("output_dtype") is torch.float32:
+            assert np.all(np.abs(got[:, head:] - split) <= 8 * np.abs(split) * 2.0 ** -23 + fp32_floor(split, k))
+        else:
+            assert_ulp_close(got[:, head:], split, k=k)
     c0 = head
     want = o.strassen_matmul(a, b[:, c0:c0 + 1024], **TILE, epilogue="residual_add", residual=r[:, c0:c0 + 1024])
     got = host(rounds_matmul(a_dev, w, **TILE, epilogue="residual_add", residual=torch.from_numpy(r).to(DEV)))

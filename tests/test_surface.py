@@ -448,14 +448,16 @@ def test_strassen_kernel_choice():
 def test_bench_head_columns():
     """bench.py's head_columns restates the library's pm_round_columns: the
     most 256-column product tiles per tile row that fill whole rounds of the
-    CUs and end on a bn tile boundary."""
+    CUs and end on a bn tile boundary, none below K = 4096."""
     import bench
 
     # gate|up at 8 x 1024 tokens on 256 CUs: 32 tile rows, 8 columns a round.
-    assert bench.head_columns(8192, 51200, 1024, 256) == 49152
-    assert bench.head_columns(8192, 5120, 1024, 256) == 4096  # o and down: one round
-    assert bench.head_columns(8192, 1024, 1024, 256) == 0     # v: under one round
-    assert bench.head_columns(1024, 34816, 1024, 256) == 32768
+    assert bench.head_columns(8192, 5120, 51200, 1024, 256) == 49152
+    assert bench.head_columns(8192, 8192, 5120, 1024, 256) == 4096   # o: one round
+    assert bench.head_columns(8192, 25600, 5120, 1024, 256) == 4096  # down
+    assert bench.head_columns(8192, 5120, 1024, 1024, 256) == 0      # v: under one round
+    assert bench.head_columns(8192, 2048, 51200, 1024, 256) == 0     # K below 4096
+    assert bench.head_columns(1024, 4096, 34816, 1024, 256) == 32768
     # bn / 2 = 1024: whole bn tiles of 4 columns; 24 tile rows: 32 a round.
-    assert bench.head_columns(6144, 2 * 256 * 72, 2048, 256) == 2 * 256 * 64
-    assert bench.head_columns(8192, 51200, 1024, 304) == 2 * 256 * 76  # 38 columns a round
+    assert bench.head_columns(6144, 4096, 2 * 256 * 72, 2048, 256) == 2 * 256 * 64
+    assert bench.head_columns(8192, 5120, 51200, 1024, 304) == 2 * 256 * 76  # 38 columns a round
