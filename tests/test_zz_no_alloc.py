@@ -108,16 +108,23 @@ def workspace_bytes(lib, d):
     return need.value
 
 
-@pytest.mark.parametrize("flags", [0, _lib.SMX_FLAG_PRODUCT_MAJOR])
-def test_noalloc_with_the_workspace_it_asks_for(flags):
+@pytest.mark.parametrize("flags,shape,tile", [
+    (0, (2048, 4096, 2048), (256, 512, 512)),
+    (_lib.SMX_FLAG_PRODUCT_MAJOR, (2048, 4096, 2048), (256, 512, 512)),
+    # a head of one round of product-major tiles (4 rows x 64 columns on 256
+    # CUs), then the split kernel's 32 tiles split over K
+    (_lib.SMX_FLAG_PRODUCT_MAJOR_ROUNDS, (1024, 34816, 4096), (1024, 1024, 512)),
+])
+def test_noalloc_with_the_workspace_it_asks_for(flags, shape, tile):
     """smx_gemm_workspace_bytes sizes the noalloc descriptor (row-major A,
     packed B) as the packed call it becomes: a launch of 128 product tiles
-    split over K (flags 0) or the product-major kernel's parked sets. With
-    that workspace the result is bit-identical to smx_gemm with the same
-    workspace; with 16 bytes less the call is refused before anything is
-    launched (the output keeps its NaNs)."""
+    split over K (flags 0), the product-major kernel's parked sets, or both
+    (a product-major head and a split rest). With that workspace the result
+    is bit-identical to smx_gemm with the same workspace; with 16 bytes less
+    the call is refused before anything is launched (the output keeps its
+    NaNs)."""
     lib = _lib.load()
-    algo, m, n, k, tile = _lib.SMX_ALGO_STRASSEN, 2048, 4096, 2048, (256, 512, 512)
+    algo, (m, n, k) = _lib.SMX_ALGO_STRASSEN, shape
     g = torch.Generator(device=DEV).manual_seed(11)
     a = torch.randn(m, k, device=DEV, generator=g).to(torch.bfloat16)
     bt = (torch.randn(n, k, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
