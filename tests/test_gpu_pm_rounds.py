@@ -128,6 +128,27 @@ def test_integer_kat_bit_exact(k):
     assert np.array_equal(got, o.bf16_round(exact))
 
 
+@pytest.mark.parametrize("bn", [512, 2048])
+def test_other_bn_tiles_bit_exact(bn):
+    """bn = 512 (one product-major tile column per bn tile) and bn = 2048
+    (four): the head ends on a bn tile boundary and the rest starts on one,
+    with integer operands and an integer residual bit-exact."""
+    m, k = 1024, 4096
+    n = 2 * 256 * (_cus() // 4) + bn
+    head = head_columns(m, k, n, bn=bn)
+    assert head == 2 * 256 * (_cus() // 4)
+    rng = np.random.default_rng(990 + bn)
+    a = rng.integers(-2, 3, (m, k)).astype(np.float32)
+    b = rng.integers(-2, 3, (k, n)).astype(np.float32)
+    r = rng.integers(-8, 9, (m, n)).astype(np.float32)
+    w = smx.strassen_weight_layout(dev_weight(b), bn, 512)
+    tile = dict(bm=1024, bn=bn, bk=512)
+    exact = a @ b
+    assert np.array_equal(host(rounds_matmul(dev(a), w, output_dtype=torch.float32, **tile)), exact)
+    got = host(rounds_matmul(dev(a), w, epilogue="residual_add", residual=dev(r), **tile))
+    assert np.array_equal(got, o.bf16_round(exact + r))
+
+
 def _sample_columns(n, head, width):
     """Column blocks (one bn tile of output each) at both ends of the head
     and of the rest."""
