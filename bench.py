@@ -13,11 +13,13 @@ already resident in HBM:
   down  H[8192,25600] . Wd[25600,5120]  + residual (residual_add)
 
 7.989 TFLOP per step (2*M*N*K summed over the sites, the classical count for
-every arm). Arms: "strassen" (7-product kernel), "cubic" (matched 8-product
-kernel, identical tiling and epilogues) and "hipblaslt" (torch.matmul, with
-the epilogues as separate torch ops). Printed value: effective TFLOP/s of the
-Strassen arm. The pure GEMMs at the same shapes (no epilogue) are reported in
-"pure_gemm".
+every arm). Arms: "strassen" (the 7-product kernels: the product-major
+kernel on the whole rounds of a call's tiles, the split kernel on the rest),
+"cubic" (matched 8-product kernel, identical tiling and epilogues) and
+"hipblaslt" (torch.matmul, with the epilogues as separate torch ops);
+"strassen_split" and "strassen_product_major" are the Strassen weights on one
+of its kernels alone. Printed value: effective TFLOP/s of the Strassen arm.
+The pure GEMMs at the same shapes (no epilogue) are reported in "pure_gemm".
 
 One JSON line on stdout; progress on stderr.
 """
