@@ -72,17 +72,18 @@ def test_occupancy_and_decode_measurements():
     assert all(len(v) == 3 for v in dec[0]["samples_ms"].values())
 
 
-def test_shipped_cached_entry_routes_with_the_cache(monkeypatch):
-    """The shipped table's down projection at 256 tokens won with the
-    packed-weight cache: tuned_matmul sends it to Strassen (bit-identical to
-    the direct call on the entry's tile) while the cache can hold the
+@pytest.mark.parametrize("m", [256, 8192])
+def test_shipped_cached_entry_routes_with_the_cache(monkeypatch, m):
+    """The shipped table's down projection at 256 and 8192 tokens won with
+    the packed-weight cache: tuned_matmul sends it to Strassen (bit-identical
+    to the direct call on the entry's tile) while the cache can hold the
     weight, and to the native GEMM without the cache."""
     monkeypatch.delenv("SMX_TUNED_TABLE", raising=False)
-    entry = tuning.load_table(tuning.DEFAULT_TABLE)["shapes"].get("256,25600,5120")
+    entry = tuning.load_table(tuning.DEFAULT_TABLE)["shapes"].get(f"{m},25600,5120")
     if entry is None:
         pytest.skip("the shipped table was measured without this shape")
     g = torch.Generator(device="cuda").manual_seed(3)
-    a = torch.randn(256, 25600, device="cuda", generator=g).to(torch.bfloat16)
+    a = torch.randn(m, 25600, device="cuda", generator=g).to(torch.bfloat16)
     w = (torch.randn(5120, 25600, device="cuda", generator=g) * 0.02).to(torch.bfloat16).t()
     previous = smx.cache_packed_weights(0)
     try:
