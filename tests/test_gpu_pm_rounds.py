@@ -149,6 +149,27 @@ def test_other_bn_tiles_bit_exact(bn):
     assert np.array_equal(got, o.bf16_round(exact + r))
 
 
+def test_exact_panels_transposed_lhs_and_fp32_inputs_take_the_head():
+    """The paths built on the packed Strassen call keep their results when
+    it splits into a product-major head and a split rest, with integer
+    operands bit-exact: exact panels (the Strassen part over 14 of 16 bk
+    panels, FP32, then the cubic over the other two), a transposed A, and
+    FP32 inputs at HIGHEST precision (six bf16 passes, packed K = 6 K)."""
+    m, n = 1024, 2 * 256 * (_cus() // 4) + 1024
+    rng = np.random.default_rng(995)
+    a = rng.integers(-2, 3, (m, 8192)).astype(np.float32)
+    b = rng.integers(-2, 3, (8192, n)).astype(np.float32)
+    got = smx.strassen_matmul(dev(a), dev_weight(b), classical_panels=(1, 3), **TILE)
+    assert np.array_equal(host(got), o.bf16_round(a @ b))
+    a4, b4 = a[:, :4096], b[:4096]
+    got = smx.strassen_matmul_lhs_transposed(dev(np.ascontiguousarray(a4.T)), dev(b4), **TILE)
+    assert np.array_equal(host(got), o.bf16_round(a4 @ b4))
+    a1, b1 = a[:, :1024], b[:1024]
+    got = smx.strassen_matmul(torch.from_numpy(a1).to(DEV), torch.from_numpy(b1).to(DEV), dot_precision="HIGHEST",
+                              output_dtype=torch.float32, **TILE)
+    assert np.array_equal(host(got), a1 @ b1)
+
+
 def _sample_columns(n, head, width):
     """Column blocks (one bn tile of output each) at both ends of the head
     and of the rest."""
