@@ -82,8 +82,12 @@ def test_bench_sites_full_size(block, arm):
     torch.cuda.synchronize()
     rng = np.random.default_rng(5)
 
-    def tiles(m, n, count=2):
-        return [(int(rng.integers(m // BM)), int(rng.integers(n // BN))) for _ in range(count)]
+    def tiles(m, n):
+        """The first and the last column tile (the ends of a product-major
+        head and of the split kernel's rest, where the call has both), and
+        one at random, each in a random row."""
+        cols = [0, n // BN - 1, int(rng.integers(n // BN))]
+        return [(int(rng.integers(m // BM)), j) for j in cols]
 
     # q and k: qk_norm_rope on the relaid weight, tables [tokens, bn/2]
     for name, w, scale, heads in (("q", "wq_laid", "scale_q", bench.HEADS), ("k", "wk_laid", "scale_k",
