@@ -257,3 +257,18 @@ def test_both_product_major_flags_are_refused():
     lib = _lib.load()
     assert lib.smx_gemm_workspace_bytes(d, ctypes.byref(need)) == _lib.SMX_ERR_INVALID
     assert b"exclude each other" in lib.smx_last_error()
+
+
+def test_bench_head_columns_match_the_library():
+    """bench.py times the gate|up call's product-major head alone on the
+    columns its head_columns names: those must be the library's head. At
+    8192 x 5120 x 51200 the rest (256 split tiles, one whole round) splits
+    nothing over K, so the workspace is the head's parked sets alone."""
+    import bench
+
+    m, k, n = bench.TOKENS, bench.HIDDEN, 2 * bench.FFN
+    head = bench.head_columns(m, k, n, 1024, _cus())
+    assert 0 < head <= n
+    assert head == head_columns(m, k, n)
+    need = _workspace_bytes(m, n, k, _lib.SMX_FLAG_PRODUCT_MAJOR_ROUNDS, epilogue="swiglu")
+    assert need == (m // 256) * (head // 512) * PARK_PER_TILE
